@@ -1,0 +1,25 @@
+"""MI355X-native (gfx950) backend for Channel's Q4 inference hot path.
+
+The compute path is libchannel_hip.so: hand-written HIP kernels behind the
+C-ABI declared in include/channel_hip.h.  This package only binds it
+(ctypes) for tests, benchmarks and Python callers.
+"""
+from ._abi import HEADER_PATH, LIB_PATH, PROTOTYPES, ChannelError, lib
+from .device import Buffer, Context, device_count
+
+Q4_BLOCK_BYTES = 20
+Q8_BLOCK_BYTES = 36
+
+
+def q4_bytes(rows, K):
+    """getQuantizedSizeBytes(rows, K, .q4) (src/quant.zig:181-183)."""
+    return rows * ((K + 31) // 32) * Q4_BLOCK_BYTES
+
+
+def q8_bytes(rows, K):
+    """getQuantizedSizeBytes(rows, K, .q8) (src/quant.zig:181-183)."""
+    return rows * ((K + 31) // 32) * Q8_BLOCK_BYTES
+
+
+__all__ = ["Buffer", "ChannelError", "Context", "HEADER_PATH", "LIB_PATH", "PROTOTYPES",
+           "device_count", "lib", "q4_bytes", "q8_bytes"]

@@ -1,0 +1,77 @@
+"""ctypes binding of include/channel_hip.h (libchannel_hip.so).
+
+The library is the product: every compute call goes to hand-written gfx950
+HIP kernels behind the C-ABI.  There is no fallback; if the shared library is
+missing, importing this module raises.
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libchannel_hip.so")
+HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "channel_hip.h")
+
+c_void_p = ctypes.c_void_p
+c_u32 = ctypes.c_uint32
+c_u64 = ctypes.c_uint64
+c_int = ctypes.c_int
+c_f32 = ctypes.c_float
+c_size = ctypes.c_size_t
+P = ctypes.POINTER
+
+STATUS_NAMES = {
+    0: "OK",
+    -1: "Invalid",
+    -2: "HipError",
+    -3: "NoDevice",
+    -4: "OutOfMemory",
+    -5: "BatchTooLarge",
+    -6: "Unsupported",
+}
+
+# name -> (restype, argtypes)
+PROTOTYPES = {
+    "chn_device_count": (c_int, [P(c_int)]),
+    "chn_init": (c_int, [c_int, P(c_void_p)]),
+    "chn_destroy": (None, [c_void_p]),
+    "chn_last_error": (ctypes.c_char_p, [c_void_p]),
+    "chn_alloc": (c_int, [c_void_p, c_size, P(c_void_p)]),
+    "chn_free": (c_int, [c_void_p, c_void_p]),
+    "chn_upload": (c_int, [c_void_p, c_void_p, c_void_p, c_size]),
+    "chn_download": (c_int, [c_void_p, c_void_p, c_void_p, c_size]),
+    "chn_copy": (c_int, [c_void_p, c_void_p, c_void_p, c_size]),
+    "chn_fill_u32": (c_int, [c_void_p, c_void_p, c_u32, c_size]),
+    "chn_sync": (c_int, [c_void_p]),
+    "chn_timer_start": (c_int, [c_void_p]),
+    "chn_timer_stop": (c_int, [c_void_p, P(c_f32)]),
+    "chn_gemv_q4": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_u32, c_u32]),
+    "chn_fused_qkv_q4": (c_int, [c_void_p] + [c_void_p] * 7 + [c_u32, c_u32, c_u32]),
+    "chn_fused_mlp_q4": (c_int, [c_void_p] + [c_void_p] * 4 + [c_u32, c_u32]),
+    "chn_synth_q4": (c_int, [c_void_p, c_void_p, c_u32, c_u32, c_u64, c_f32, c_f32]),
+    "chn_synth_q8": (c_int, [c_void_p, c_void_p, c_u32, c_u32, c_u64, c_f32, c_f32]),
+    "chn_synth_normal": (c_int, [c_void_p, c_void_p, c_size, c_u64, c_f32]),
+}
+
+
+class ChannelError(RuntimeError):
+    """A negative status from the C-ABI, with chn_last_error()'s text."""
+
+    def __init__(self, fn, code, msg):
+        self.code = code
+        self.status = STATUS_NAMES.get(code, str(code))
+        super().__init__(f"{fn} -> {self.status} ({code}): {msg}")
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'`")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in PROTOTYPES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load()

@@ -1,0 +1,90 @@
+// Internal definitions shared by the gfx950 kernels and the C-ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/channel_hip.h"
+
+struct chn_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+    std::string err;
+    // Workspace for kernels that need partials (split-K attention, ...).
+    // Grown on demand outside graph capture; owned by the context.
+    void *ws = nullptr;
+    size_t ws_bytes = 0;
+};
+
+namespace chn {
+
+int set_err(chn_ctx *ctx, int code, const char *fmt, ...);
+int hip_fail(chn_ctx *ctx, hipError_t e, const char *what);
+// Make sure ctx->ws holds at least `bytes`; returns a status code.
+int ensure_workspace(chn_ctx *ctx, size_t bytes);
+
+#define CHN_HIP(ctx, call)                                   \
+    do {                                                     \
+        hipError_t e_ = (call);                              \
+        if (e_ != hipSuccess) return chn::hip_fail((ctx), e_, #call); \
+    } while (0)
+
+// Check the launch that was just enqueued.
+#define CHN_LAUNCHED(ctx, what)                              \
+    do {                                                     \
+        hipError_t e_ = hipGetLastError();                   \
+        if (e_ != hipSuccess) return chn::hip_fail((ctx), e_, what); \
+    } while (0)
+
+#define CHN_REQUIRE(ctx, cond, ...)                          \
+    do {                                                     \
+        if (!(cond)) return chn::set_err((ctx), CHN_E_INVALID, __VA_ARGS__); \
+    } while (0)
+
+inline bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+// ---------------------------------------------------------------------
+// Device helpers
+// ---------------------------------------------------------------------
+
+// Hides known bits from the optimiser so that byte extraction from a
+// masked nibble word lowers to v_cvt_f32_ubyte{0..3} (one op per weight)
+// instead of a bitfield extract followed by a convert.
+__device__ __forceinline__ uint32_t opaque_u32(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+__device__ __forceinline__ float f16_lo_to_f32(uint32_t w) {
+    _Float16 h = __builtin_bit_cast(_Float16, (unsigned short)(w & 0xffffu));
+    return (float)h;
+}
+
+// Dword-aligned 16-byte vector: global_load_dwordx4 accepts 4-byte
+// alignment on gfx950, which lets one load take words 1..4 of a 20-byte
+// Q4 block.
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+// splitmix64 output function over a counter (same constants as the host
+// restatement used to check generated inputs).
+__device__ __forceinline__ uint64_t mix64(uint64_t seed, uint64_t idx) {
+    uint64_t z = seed + (idx + 1ull) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+    float c = 0.044715f * x;
+    c = c * x;
+    c = c * x;
+    float inner = 0.7978845608f * (x + c);
+    return (0.5f * x) * (1.0f + tanhf(inner));
+}
+
+}  // namespace chn

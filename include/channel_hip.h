@@ -1,0 +1,139 @@
+/*
+ * channel_hip.h -- C-ABI of the MI355X (gfx950) backend for Channel's
+ * quantized inference hot path.
+ *
+ * Plain C: opaque handles, raw pointers and sizes, no C++ or torch types.
+ * Device pointers come from chn_alloc().  Every compute entry point only
+ * enqueues work on the context's single HIP stream and returns; results are
+ * visible after chn_sync() or a blocking chn_download().  A context, like the
+ * reference's GpuEngine, is not thread-safe: one thread drives it.
+ *
+ * Status codes: 0 = OK, negative = error; chn_last_error() describes the
+ * last failure on a context.  Each declaration names the reference
+ * interface (Sullux/channel, file:line) it replaces.
+ *
+ * Q4 weight layout (src/quant.zig:54-98, kept bit-for-bit): each row of K
+ * weights is K/32 blocks of 5 little-endian u32 words (20 bytes); word 0 =
+ * f16 scale | f16 min << 16, words 1..4 = 32 nibbles, element 8w+n in bits
+ * 4n..4n+3 of word 1+w.  Every kernel dequantizes scale*(q-8) and ignores
+ * the min half, as the reference's live shaders do.  K % 32 == 0 is
+ * required (shaders/gemv_q4.wgsl:37).
+ */
+#ifndef CHANNEL_HIP_H
+#define CHANNEL_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes: mirror the reference's Zig error names ------------- */
+#define CHN_OK 0
+#define CHN_E_INVALID (-1)          /* bad argument / shape                 */
+#define CHN_E_HIP (-2)              /* HIP runtime failure (VkQueueSubmitFailed, ...) */
+#define CHN_E_NO_DEVICE (-3)        /* error.NoVulkanDevices (src/gpu/context.zig:29) */
+#define CHN_E_OUT_OF_MEMORY (-4)    /* error.VkMemoryAllocFailed (src/gpu/buffer.zig:82) */
+#define CHN_E_BATCH_TOO_LARGE (-5)  /* error.BatchTooLarge (src/gpu/batch_dispatch.zig:42) */
+#define CHN_E_UNSUPPORTED (-6)      /* shape outside what the kernels support */
+
+typedef struct chn_ctx chn_ctx;
+
+/* ======================================================================
+ * Runtime (replaces the Vulkan runtime, src/gpu/context.zig,
+ * src/gpu/buffer.zig)
+ * ==================================================================== */
+
+/* Number of visible HIP devices (context.zig:25-29 device enumeration). */
+int chn_device_count(int *count);
+
+/* GpuContext.init (src/gpu/context.zig:17-107): bind device `device`,
+ * create one stream.  CHN_E_NO_DEVICE when no device is visible. */
+int chn_init(int device, chn_ctx **out);
+
+/* GpuContext.deinit (src/gpu/context.zig:109). Waits for queued work. */
+void chn_destroy(chn_ctx *ctx);
+
+/* Text of the last error on `ctx` ("" if none).  With ctx == NULL: the last
+ * error of a failed chn_init on this thread. */
+const char *chn_last_error(const chn_ctx *ctx);
+
+/* GpuBuffer.init (src/gpu/buffer.zig:57-97): device allocation, 256-byte
+ * aligned.  Unlike the reference's host-visible UMA buffers the memory is
+ * device-local; host access goes through chn_upload/chn_download. */
+int chn_alloc(chn_ctx *ctx, size_t bytes, void **dptr);
+
+/* GpuBuffer.deinit (src/gpu/buffer.zig:99-106). */
+int chn_free(chn_ctx *ctx, void *dptr);
+
+/* Writes through GpuBuffer.asSlice (src/gpu/buffer.zig:108-111), made
+ * explicit: host -> device copy, ordered on the context stream, returns
+ * once the source may be reused. */
+int chn_upload(chn_ctx *ctx, void *dst_dev, const void *src_host, size_t bytes);
+
+/* Reads through GpuBuffer.asSlice, made explicit: waits for queued work,
+ * then device -> host copy. */
+int chn_download(chn_ctx *ctx, void *dst_host, const void *src_dev, size_t bytes);
+
+/* Device -> device copy on the stream (vkCmdCopyBuffer,
+ * src/gpu/batch_dispatch.zig:146). */
+int chn_copy(chn_ctx *ctx, void *dst_dev, const void *src_dev, size_t bytes);
+
+/* Fill `count` u32 words with `value` by a kernel (graph-capture safe). */
+int chn_fill_u32(chn_ctx *ctx, void *dst_dev, uint32_t value, size_t count);
+
+/* vkWaitForFences on the context's queue (src/gpu/kernels.zig:193). */
+int chn_sync(chn_ctx *ctx);
+
+/* Stream timer: chn_timer_start records an event, chn_timer_stop records a
+ * second one, waits for it and returns the elapsed milliseconds.  Has no
+ * reference counterpart (the reference has no GPU timers); it times work on
+ * the stream the kernels run on. */
+int chn_timer_start(chn_ctx *ctx);
+int chn_timer_stop(chn_ctx *ctx, float *ms);
+
+/* ======================================================================
+ * Decode matvecs (GpuEngine.record*, src/gpu/kernels.zig:89-126)
+ * ==================================================================== */
+
+/* y[M] = W[M x K] (Q4) . x[K], fp32 accumulate.
+ * recordGemv / recordGemvMlp (src/gpu/kernels.zig:89-92,107-110) +
+ * shaders/gemv_q4.wgsl.  x must be 16-byte aligned. */
+int chn_gemv_q4(chn_ctx *ctx, const uint32_t *W, const float *x, float *y,
+                uint32_t M, uint32_t K);
+
+/* q = Wq.x, k = Wk.x, v = Wv.x in one launch over the concatenated row
+ * space [q_dim | kv_dim | kv_dim].  recordFusedQkv
+ * (src/gpu/kernels.zig:93-100) + shaders/fused_qkv_q4.wgsl. */
+int chn_fused_qkv_q4(chn_ctx *ctx, const uint32_t *Wq, const uint32_t *Wk,
+                     const uint32_t *Wv, const float *x, float *q, float *k,
+                     float *v, uint32_t q_dim, uint32_t kv_dim, uint32_t K);
+
+/* act[r] = gelu_tanh(Wg[r].x) * (Wu[r].x), r < M.  recordGateUpSwiGlu
+ * (src/gpu/kernels.zig:123-126) + shaders/fused_mlp_q4.wgsl. */
+int chn_fused_mlp_q4(chn_ctx *ctx, const uint32_t *Wg, const uint32_t *Wu,
+                     const float *x, float *act, uint32_t M, uint32_t K);
+
+/* ======================================================================
+ * Seeded synthetic inputs (no reference counterpart: benchmark and test
+ * inputs generated in place on the device; the same counter-based hash is
+ * restated on the host, so any block can be regenerated for checking)
+ * ==================================================================== */
+
+/* Q4 matrix [rows x K], codes uniform 0..15, f16 scales U(smin, smax). */
+int chn_synth_q4(chn_ctx *ctx, uint32_t *W, uint32_t rows, uint32_t K,
+                 uint64_t seed, float smin, float smax);
+
+/* Q8_0 matrix [rows x K], int8 uniform, f32 scales U(smin, smax). */
+int chn_synth_q8(chn_ctx *ctx, uint32_t *W, uint32_t rows, uint32_t K,
+                 uint64_t seed, float smin, float smax);
+
+/* n floats ~ N(0, stddev^2) (Box-Muller on one hash per element). */
+int chn_synth_normal(chn_ctx *ctx, float *dst, size_t n, uint64_t seed,
+                     float stddev);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CHANNEL_HIP_H */

@@ -1,0 +1,114 @@
+"""GPU parity of the decode matvecs (gemv_q4, fused_qkv_q4, fused_mlp_q4)
+against the oracle, through the C-ABI.  Inputs are generated on the device,
+downloaded, and fed to the oracle, so both sides see identical bits.
+Tolerance: normwise relative error <= 1e-3 (fp32 accumulation)."""
+import numpy as np
+import pytest
+
+import oracle
+from gpu_util import f32_host, q4_host, rel_err, say, synth_normal_dev, synth_q4_dev
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def test_synth_q4_matches_host_generator(ctx):
+    say("synth_q4 64x1024")
+    W = synth_q4_dev(ctx, 64, 1024, 0xC4A77E1)
+    assert np.array_equal(q4_host(ctx, W, 64, 1024), oracle.synth_q4(64, 1024, 0xC4A77E1))
+
+
+def test_gemv_q4_reference_kat(ctx):
+    """src/gpu.zig:38-60 on the GPU: every row is exactly 55.34375."""
+    import oracle as o
+    w = np.full((64, 128), 0x3F80, dtype=np.uint16)
+    W = ctx.upload(o.quantize_q4(w))
+    x = ctx.upload((np.arange(128) % 5).astype(np.float32) * 0.25)
+    y = ctx.alloc(64 * 4)
+    say("gemv_q4 KAT 64x128")
+    ctx.call("chn_gemv_q4", W, x, y, 64, 128)
+    assert np.all(f32_host(ctx, y, 64) == np.float32(55.34375))
+
+
+@pytest.mark.parametrize("M,K", [
+    (8192, 2048),    # config: single Q4 matvec, N=8192 x K=2048
+    (3840, 4096),    # o_proj at 12B dims
+    (3840, 15360),   # down_proj at 12B dims
+    (100, 640),      # 20 blocks: partial pass, rows not a tile multiple
+    (33, 2080),      # 65 blocks: second pass has one live lane
+    (7, 32),         # one block
+    (1, 8192),
+])
+def test_gemv_q4_parity(ctx, M, K):
+    seed = 1000 + M + K
+    W = synth_q4_dev(ctx, M, K, seed)
+    x = synth_normal_dev(ctx, K, seed + 1)
+    y = ctx.alloc(M * 4)
+    say(f"gemv_q4 M={M} K={K}")
+    ctx.call("chn_gemv_q4", W, x, y, M, K)
+    got = f32_host(ctx, y, M)
+    want = oracle.gemv_q4(q4_host(ctx, W, M, K), f32_host(ctx, x, K), M, K)
+    assert rel_err(got, want) < TOL
+
+
+def test_gemv_q4_zero_codes_and_single_weight(ctx):
+    """All codes 8 -> exactly 0; one code 15 -> s * 7 * x[k] exactly."""
+    M, K = 16, 256
+    Wh = oracle.synth_q4(M, K, 5).reshape(M, K // 32, 5).copy()
+    Wh[:, :, 1:] = 0x88888888
+    Wh[9, 3, 4] = 0x8F888888          # block 3, word 4 (elements 24..31), nibble 6
+    W = ctx.upload(Wh)
+    xh = oracle.synth_normal(K, 6)
+    x = ctx.upload(xh)
+    y = ctx.alloc(M * 4)
+    say("gemv_q4 zero/single")
+    ctx.call("chn_gemv_q4", W, x, y, M, K)
+    got = f32_host(ctx, y, M)
+    s = np.uint16(Wh[9, 3, 0] & 0xFFFF).view(np.float16).astype(np.float32)
+    assert got[9] == np.float32(s * np.float32(7.0 * xh[3 * 32 + 24 + 6]))
+    assert np.all(np.delete(got, 9) == 0.0)
+
+
+@pytest.mark.parametrize("q_dim,kv_dim,K", [(4096, 2048, 3840), (96, 40, 256)])
+def test_fused_qkv_q4_parity(ctx, q_dim, kv_dim, K):
+    seed = 2000 + q_dim
+    Wq = synth_q4_dev(ctx, q_dim, K, seed)
+    Wk = synth_q4_dev(ctx, kv_dim, K, seed + 1)
+    Wv = synth_q4_dev(ctx, kv_dim, K, seed + 2)
+    x = synth_normal_dev(ctx, K, seed + 3)
+    q, k, v = ctx.alloc(q_dim * 4), ctx.alloc(kv_dim * 4), ctx.alloc(kv_dim * 4)
+    say(f"fused_qkv_q4 q={q_dim} kv={kv_dim} K={K}")
+    ctx.call("chn_fused_qkv_q4", Wq, Wk, Wv, x, q, k, v, q_dim, kv_dim, K)
+    rq, rk, rv = oracle.fused_qkv_q4(q4_host(ctx, Wq, q_dim, K), q4_host(ctx, Wk, kv_dim, K),
+                                     q4_host(ctx, Wv, kv_dim, K), f32_host(ctx, x, K),
+                                     q_dim, kv_dim, K)
+    assert rel_err(f32_host(ctx, q, q_dim), rq) < TOL
+    assert rel_err(f32_host(ctx, k, kv_dim), rk) < TOL
+    assert rel_err(f32_host(ctx, v, kv_dim), rv) < TOL
+
+
+@pytest.mark.parametrize("M,K", [(15360, 3840), (50, 96)])
+def test_fused_mlp_q4_parity(ctx, M, K):
+    seed = 3000 + M
+    Wg = synth_q4_dev(ctx, M, K, seed)
+    Wu = synth_q4_dev(ctx, M, K, seed + 1)
+    x = synth_normal_dev(ctx, K, seed + 2)
+    act = ctx.alloc(M * 4)
+    say(f"fused_mlp_q4 M={M} K={K}")
+    ctx.call("chn_fused_mlp_q4", Wg, Wu, x, act, M, K)
+    want = oracle.fused_mlp_q4(q4_host(ctx, Wg, M, K), q4_host(ctx, Wu, M, K),
+                               f32_host(ctx, x, K), M, K)
+    assert rel_err(f32_host(ctx, act, M), want) < TOL
+
+
+def test_rejects_bad_shapes(ctx):
+    import channel_amd as ca
+    W = synth_q4_dev(ctx, 4, 64, 1)
+    x = synth_normal_dev(ctx, 64, 2)
+    y = ctx.alloc(16)
+    with pytest.raises(ca.ChannelError) as e:
+        ctx.call("chn_gemv_q4", W, x, y, 4, 48)      # K % 32 != 0
+    assert e.value.status == "Invalid"
+    with pytest.raises(ca.ChannelError):
+        ctx.call("chn_gemv_q4", W, x.ptr + 4, y, 4, 32)  # x not 16-byte aligned
