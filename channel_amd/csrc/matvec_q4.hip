@@ -2,31 +2,88 @@
 // gemv_q4 (shaders/gemv_q4.wgsl), fused_qkv_q4 (shaders/fused_qkv_q4.wgsl)
 // and fused_mlp_q4 (shaders/fused_mlp_q4.wgsl).
 //
-// Design (HBM-bound, no MFMA):
-//  * lane <-> one 32-weight block: a wave covers 64 consecutive blocks of
-//    a row, so the wave's weight loads are one contiguous run of 64*20
-//    bytes (one dwordx4 + one dword per lane, dword-aligned);
-//  * the lane keeps its 32 activations in registers and reuses them for
-//    RPW rows (and for the gate and up matrices), so x is read once per
-//    RPW rows instead of once per row;
-//  * the dot uses sum (q-8)x = sum q*x - 8*sum x per block: a nibble word
-//    is masked twice (low / high nibbles of each byte) and each byte goes
-//    through v_cvt_f32_ubyteN, i.e. ~2.3 VALU ops per weight; the high
-//    nibbles come out multiplied by 16, so the odd-position activations are
-//    pre-scaled by 1/16 (an exact power-of-two scaling);
-//  * WPR waves of a workgroup split the column passes of the same rows
-//    (split-K inside the workgroup), and the partial sums are reduced
-//    through LDS in a fixed order, so results are deterministic.
+// The weight stream is HBM-bound; the design keeps the VALU cost per weight
+// near one instruction so that the issue rate never caps the stream:
+//
+//  * Activations are turned once per call into "digit planes": per 32-block
+//    b, X_i = rint(x_i * 2^(22-e_b)) with |x_i| < 2^e_b, written as six
+//    balanced base-16 digits D_p in [-8, 7] (X = sum_p D_p 16^p), and each
+//    digit plane packed as signed 4-bit lanes in the same nibble order as
+//    the weights.  The quantisation error is <= 2^-22 of the block maximum,
+//    i.e. fp32-grade.
+//  * A Q4 word XOR 0x88888888 is exactly the eight signed 4-bit values
+//    (q - 8), so sum_i (q_i - 8) X_i is an exact integer computed with
+//    v_dot8c_i32_i4 (8 MACs per instruction), plane by plane in Horner
+//    form; the block result is (float)T * scale_b * 2^(e_b - 22).
+//  * Weights are streamed with coalesced non-temporal 16-byte loads of whole
+//    row segments (prefetching the next row group into VGPRs while the
+//    current one is computed), transposed through LDS to one lane per
+//    20-byte block.  Waves are persistent and walk row groups with a
+//    grid-wide stride, so the chip reads W as one contiguous front.
+//  * WPR waves of a workgroup may split K; their partials meet in LDS in a
+//    fixed order, so results are deterministic.
 #include "chn_internal.h"
 
 namespace chn {
+
+constexpr int XP_PLANES = 6;      // digit planes per activation block
+constexpr int XP_FRAC = 22;       // fixed-point bits below the block exponent
+constexpr int XP_WORDS = XP_PLANES * 4;
+
+// Planes for K/32 blocks: u32 plane words in SoA order [(p*4 + w) * nb + b],
+// followed by nb float scales 2^(e_b - 22).
+__host__ __device__ inline size_t xplanes_bytes(uint32_t nb) { return (size_t)nb * (XP_WORDS + 1) * 4; }
+
+// Four threads per 32-block, one per 8-element weight word: block maximum
+// over the four (two xor-shuffles), quantise, split into balanced hex digits
+// and pack this word's six plane words.
+__global__ __launch_bounds__(256) void k_xplanes(const float *__restrict__ x, uint32_t *__restrict__ xp,
+                                                 uint32_t nb) {
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t b = t >> 2, w = t & 3;
+    const bool ok = b < nb;
+    float v[8];
+    if (ok) {
+        const float4 *xv = (const float4 *)(x + (size_t)b * 32 + w * 8);
+        const float4 t0 = xv[0], t1 = xv[1];
+        v[0] = t0.x; v[1] = t0.y; v[2] = t0.z; v[3] = t0.w;
+        v[4] = t1.x; v[5] = t1.y; v[6] = t1.z; v[7] = t1.w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
+    m = fmaxf(m, __shfl_xor(m, 1, 64));
+    m = fmaxf(m, __shfl_xor(m, 2, 64));
+    int e = 0;
+    (void)frexpf(m, &e);           // m = f * 2^e, f in [0.5, 1): |x_i| < 2^e
+    float scale = 0.0f, inv = 0.0f;
+    if (m > 0.0f && e > -100) {
+        scale = ldexpf(1.0f, XP_FRAC - e);
+        inv = ldexpf(1.0f, e - XP_FRAC);
+    }
+    uint32_t u[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) u[i] = (uint32_t)((int)rintf(v[i] * scale) + 0x888888);
+    if (!ok) return;
+#pragma unroll
+    for (int p = 0; p < XP_PLANES; ++p) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int n = 0; n < 8; ++n) word |= ((u[n] >> (4 * p)) & 15u) << (4 * n);
+        xp[(size_t)(p * 4 + w) * nb + b] = word ^ 0x88888888u;
+    }
+    if (w == 0) ((float *)(xp + (size_t)XP_WORDS * nb))[b] = inv;
+}
 
 enum MatvecMode { MV_GEMV = 0, MV_QKV = 1, MV_MLP = 2 };
 
 struct MatvecArgs {
     const uint32_t *W0, *W1, *W2;  // GEMV: W0. QKV: Wq, Wk, Wv. MLP: Wg, Wu.
     float *y0, *y1, *y2;           // GEMV: y0. QKV: q, k, v. MLP: act.
-    const float *x;
+    const uint32_t *xp;            // activation digit planes
     uint32_t M;                    // output rows (QKV: q_dim + 2 kv_dim)
     uint32_t seg1, seg2;           // QKV: q_dim, q_dim + kv_dim
     uint32_t nb;                   // K / 32
@@ -34,6 +91,265 @@ struct MatvecArgs {
 
 template <int MODE>
 __device__ __forceinline__ const uint32_t *row_base(const MatvecArgs &a, uint32_t row, int mat) {
+    const size_t rw = (size_t)a.nb * 5;
+    if (MODE == MV_QKV) {
+        if (row < a.seg1) return a.W0 + (size_t)row * rw;
+        if (row < a.seg2) return a.W1 + (size_t)(row - a.seg1) * rw;
+        return a.W2 + (size_t)(row - a.seg2) * rw;
+    }
+    if (MODE == MV_MLP && mat == 1) return a.W1 + (size_t)row * rw;
+    return a.W0 + (size_t)row * rw;
+}
+
+template <int MODE>
+__device__ __forceinline__ void store_row(const MatvecArgs &a, uint32_t row, float v) {
+    if (MODE == MV_QKV) {
+        if (row < a.seg1) a.y0[row] = v;
+        else if (row < a.seg2) a.y1[row - a.seg1] = v;
+        else a.y2[row - a.seg2] = v;
+    } else {
+        a.y0[row] = v;
+    }
+}
+
+// sum_i (q_i - 8) X_i for one block: q words XOR 8 per nibble, Horner over
+// the digit planes (top plane first).
+__device__ __forceinline__ int block_idot(const uint32_t *q, const uint32_t (&P)[XP_WORDS]) {
+    uint32_t s[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) s[w] = q[w] ^ 0x88888888u;
+    int acc = 0;
+#pragma unroll
+    for (int p = XP_PLANES - 1; p >= 0; --p) {
+        if (p != XP_PLANES - 1) acc <<= 4;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) acc = __builtin_amdgcn_sdot8((int)s[w], (int)P[p * 4 + w], acc, false);
+    }
+    return acc;
+}
+
+// Transposed butterfly: V values per lane reduced over the 64 lanes; the
+// sum for value index v ends up in lanes whose top log2(V) bits equal v.
+template <int V>
+__device__ __forceinline__ float wave_reduce_v(const float (&acc)[V], int lane) {
+    float cur[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) cur[i] = acc[i];
+    int m = 32;
+#pragma unroll
+    for (int n = V; n > 1; n >>= 1, m >>= 1) {
+        const int h = n / 2;
+        const bool hi = (lane & m) != 0;
+#pragma unroll
+        for (int i = 0; i < V / 2; ++i)
+            if (i < h) {
+                const float send = hi ? cur[i] : cur[i + h];
+                const float keep = hi ? cur[i + h] : cur[i];
+                cur[i] = keep + __shfl_xor(send, m, 64);
+            }
+    }
+    float s = cur[0];
+    for (; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
+    return s;
+}
+
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMaxBlocksPerWave = 128;          // two 64-block passes
+constexpr int kSegWords = kMaxBlocksPerWave * 5; // LDS words per stream
+
+// RPW rows (x NMAT matrices) per wave and row group; WPR waves split K.
+template <int MODE, int RPW, int WPR>
+__global__ __launch_bounds__(256) void k_q4mv(MatvecArgs a) {
+    constexpr int NMAT = (MODE == MV_MLP) ? 2 : 1;
+    constexpr int V = RPW * NMAT;
+    constexpr int G = 4 / WPR;
+    constexpr int LV = (V == 1) ? 0 : (V == 2) ? 1 : (V == 4) ? 2 : 3;
+    static_assert(V == 1 || V == 2 || V == 4 || V == 8, "V must be a power of two <= 8");
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int grp = wave / WPR, part = wave % WPR;
+    const uint32_t nb = a.nb;
+
+    // K range of this wave: blocks [kb0, kb0 + nblk), nblk % 4 == 0 (host
+    // guarantees nb % 4 == 0 and per-wave ranges <= 128 blocks).
+    const uint32_t per = (((nb + WPR - 1) / WPR) + 3) / 4 * 4;
+    const uint32_t kb0 = part * per;
+    const uint32_t kb1 = (kb0 + per < nb) ? kb0 + per : nb;
+    const uint32_t nblk = kb1 > kb0 ? kb1 - kb0 : 0;
+    const uint32_t chunks = nblk * 5 / 4;   // 16-byte chunks per stream segment
+
+    __shared__ uint32_t seg[4][V * kSegWords];
+    __shared__ float red[4][V];
+    uint32_t *L = seg[wave];
+
+    // this lane's two blocks of activation planes
+    uint32_t P[2][XP_WORDS];
+    float xs[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const uint32_t bl = c * 64 + lane;
+        const bool ok = bl < nblk;
+        const uint32_t b = kb0 + bl;
+#pragma unroll
+        for (int i = 0; i < XP_WORDS; ++i) P[c][i] = ok ? a.xp[(size_t)i * nb + b] : 0u;
+        xs[c] = ok ? ((const float *)(a.xp + (size_t)XP_WORDS * nb))[b] : 0.0f;
+    }
+
+    const uint32_t ngroups = (a.M + RPW - 1) / RPW;
+    const uint32_t gstride = gridDim.x * G;
+    u32x4 pf[V][3];
+
+    auto load = [&](uint32_t g) {
+#pragma unroll
+        for (int s = 0; s < V; ++s) {
+            const uint32_t row = g * RPW + s / NMAT;
+            const uint32_t *base = row_base<MODE>(a, row < a.M ? row : 0, s % NMAT) + (size_t)kb0 * 5;
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                const uint32_t c = lane + 64 * j;
+                if (row < a.M && c < chunks)
+                    pf[s][j] = __builtin_nontemporal_load((const u32x4 *)base + c);
+            }
+        }
+    };
+
+    uint32_t g = blockIdx.x * G + grp;
+    if (g < ngroups) load(g);
+    for (uint32_t gb = blockIdx.x * G; gb < ngroups; gb += gstride, g += gstride) {
+        const bool gv = g < ngroups;
+        if (gv) {
+#pragma unroll
+            for (int s = 0; s < V; ++s)
+#pragma unroll
+                for (int j = 0; j < 3; ++j) {
+                    const uint32_t c = lane + 64 * j;
+                    if (c < chunks) *(u32x4 *)(L + s * kSegWords + 4 * c) = pf[s][j];
+                }
+        }
+        wave_lds_fence();
+        if (g + gstride < ngroups) load(g + gstride);
+
+        float acc[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) acc[v] = 0.0f;
+        if (gv) {
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const uint32_t bl = c * 64 + lane;
+                if (bl < nblk) {
+#pragma unroll
+                    for (int s = 0; s < V; ++s) {
+                        const uint32_t *p = L + s * kSegWords + 5 * bl;
+                        const uint32_t w0 = p[0];
+                        const uint32_t q[4] = {p[1], p[2], p[3], p[4]};
+                        const int T = block_idot(q, P[c]);
+                        acc[s] = fmaf((float)T, f16_lo_to_f32(w0) * xs[c], acc[s]);
+                    }
+                }
+            }
+        }
+        wave_lds_fence();
+
+        const float sum = wave_reduce_v<V>(acc, lane);
+        const int vi = lane >> (6 - LV);
+        const bool owner = (lane & ((64 >> LV) - 1)) == 0;
+        if (WPR == 1) {
+            if (gv) {
+                if (NMAT == 1) {
+                    const uint32_t row = g * RPW + vi;
+                    if (owner && row < a.M) store_row<MODE>(a, row, sum);
+                } else {
+                    const float other = __shfl_xor(sum, 64 >> LV, 64);
+                    const uint32_t row = g * RPW + (vi >> 1);
+                    if (owner && (vi & 1) == 0 && row < a.M) a.y0[row] = gelu_tanh(sum) * other;
+                }
+            }
+        } else {
+            if (owner) red[wave][vi] = sum;
+            __syncthreads();
+            if (part == 0 && gv && lane < V) {
+                float t = 0.0f;
+#pragma unroll
+                for (int w = 0; w < WPR; ++w) t += red[grp * WPR + w][lane];
+                if (NMAT == 1) {
+                    const uint32_t row = g * RPW + lane;
+                    if (row < a.M) store_row<MODE>(a, row, t);
+                } else {
+                    const float other = __shfl_xor(t, 1, 64);
+                    const uint32_t row = g * RPW + (lane >> 1);
+                    if ((lane & 1) == 0 && row < a.M) a.y0[row] = gelu_tanh(t) * other;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+struct MvShape {
+    int rpw, wpr;
+    uint32_t grid;
+};
+
+// Launch shape (from a sweep on MI355X over the 12B decode shapes): the
+// fewest waves splitting K such that each wave covers <= 128 blocks; two
+// rows per wave (one gate/up row pair for the fused MLP); at most 1024
+// workgroups (4 per CU), persistent over row groups beyond that.
+static MvShape pick_shape(int mode, uint32_t M, uint32_t nb) {
+    MvShape s;
+    s.wpr = nb <= 128 ? 1 : (nb <= 256 ? 2 : 4);
+    s.rpw = mode == MV_MLP ? 1 : 2;
+    const uint32_t G = 4 / s.wpr;
+    const uint32_t ngroups = (M + s.rpw - 1) / s.rpw;
+    const uint32_t grid = (ngroups + G - 1) / G;
+    s.grid = grid < 1024 ? grid : 1024;
+    return s;
+}
+
+template <int MODE, int WPR>
+static bool launch_wpr(int rpw, const MatvecArgs &a, uint32_t grid, hipStream_t st) {
+    constexpr int NMAT = MODE == MV_MLP ? 2 : 1;
+    switch (rpw) {
+    case 1: k_q4mv<MODE, 1, WPR><<<grid, 256, 0, st>>>(a); return true;
+    case 2: k_q4mv<MODE, 2, WPR><<<grid, 256, 0, st>>>(a); return true;
+    case 4:
+        if constexpr (4 * NMAT <= 8) { k_q4mv<MODE, 4, WPR><<<grid, 256, 0, st>>>(a); return true; }
+        return false;
+    }
+    return false;
+}
+
+template <int MODE>
+static bool launch_mode(const MvShape &s, const MatvecArgs &a, hipStream_t st) {
+    switch (s.wpr) {
+    case 1: return launch_wpr<MODE, 1>(s.rpw, a, s.grid, st);
+    case 2: return launch_wpr<MODE, 2>(s.rpw, a, s.grid, st);
+    case 4: return launch_wpr<MODE, 4>(s.rpw, a, s.grid, st);
+    }
+    return false;
+}
+
+
+// ---------------------------------------------------------------------
+// General-shape fallback (any K % 32 == 0, any 4-byte alignment): one lane
+// per block, fp32 FMAs over v_cvt_f32_ubyteN, activations in registers
+// reused over RPW rows, fixed-order LDS reduction.
+// ---------------------------------------------------------------------
+struct GenericArgs {
+    const uint32_t *W0, *W1, *W2;
+    float *y0, *y1, *y2;
+    const float *x;
+    uint32_t M, seg1, seg2, nb;
+};
+
+template <int MODE>
+__device__ __forceinline__ const uint32_t *gen_row_base(const GenericArgs &a, uint32_t row, int mat) {
     const size_t rw = (size_t)a.nb * 5;
     if (MODE == MV_QKV) {
         if (row < a.seg1) return a.W0 + (size_t)row * rw;
@@ -66,7 +382,7 @@ __device__ __forceinline__ float block_dot(const u32x4_a4 q, const float *xe, co
 }
 
 template <int MODE, int RPW, int WPR>
-__global__ __launch_bounds__(256) void k_matvec_q4(MatvecArgs a) {
+__global__ __launch_bounds__(256) void k_q4mv_generic(GenericArgs a) {
     constexpr int NMAT = (MODE == MV_MLP) ? 2 : 1;
     constexpr int V = RPW * NMAT;     // dot products per lane
     constexpr int G = 4 / WPR;        // row groups per workgroup
@@ -85,7 +401,7 @@ __global__ __launch_bounds__(256) void k_matvec_q4(MatvecArgs a) {
 #pragma unroll
         for (int m = 0; m < NMAT; ++m) {
             const uint32_t row = row0 + r;
-            rp[r * NMAT + m] = row_base<MODE>(a, row < a.M ? row : 0, m);
+            rp[r * NMAT + m] = gen_row_base<MODE>(a, row < a.M ? row : 0, m);
         }
 
     float acc[V];
@@ -169,26 +485,26 @@ __global__ __launch_bounds__(256) void k_matvec_q4(MatvecArgs a) {
 }
 
 template <int MODE, int RPW, int WPR>
-static void launch_one(const MatvecArgs &a, uint32_t grid, hipStream_t s) {
-    k_matvec_q4<MODE, RPW, WPR><<<dim3(grid), dim3(256), 0, s>>>(a);
+static void gen_launch_one(const GenericArgs &a, uint32_t grid, hipStream_t s) {
+    k_q4mv_generic<MODE, RPW, WPR><<<dim3(grid), dim3(256), 0, s>>>(a);
 }
 
 template <int MODE, int WPR>
-static bool launch_rpw(int rpw, const MatvecArgs &a, uint32_t grid, hipStream_t s) {
+static bool gen_launch_rpw(int rpw, const GenericArgs &a, uint32_t grid, hipStream_t s) {
     constexpr int NMAT = (MODE == MV_MLP) ? 2 : 1;
     constexpr int G = 4 / WPR;
     switch (rpw) {
     case 1:
-        if constexpr (G * 1 * NMAT >= 4) { launch_one<MODE, 1, WPR>(a, grid, s); return true; }
+        if constexpr (G * 1 * NMAT >= 4) { gen_launch_one<MODE, 1, WPR>(a, grid, s); return true; }
         return false;
     case 2:
-        if constexpr (G * 2 * NMAT >= 4) { launch_one<MODE, 2, WPR>(a, grid, s); return true; }
+        if constexpr (G * 2 * NMAT >= 4) { gen_launch_one<MODE, 2, WPR>(a, grid, s); return true; }
         return false;
     case 4:
-        launch_one<MODE, 4, WPR>(a, grid, s);
+        gen_launch_one<MODE, 4, WPR>(a, grid, s);
         return true;
     case 8:
-        if constexpr (NMAT == 1) { launch_one<MODE, 8, WPR>(a, grid, s); return true; }
+        if constexpr (NMAT == 1) { gen_launch_one<MODE, 8, WPR>(a, grid, s); return true; }
         return false;
     }
     return false;
@@ -197,7 +513,7 @@ static bool launch_rpw(int rpw, const MatvecArgs &a, uint32_t grid, hipStream_t 
 // Picks the launch shape: WPR waves split the column passes of a row group
 // when a row has several 64-block passes; RPW (rows per wave) is the
 // largest that still puts >= 3072 waves on the 1024 SIMDs.
-int launch_matvec(chn_ctx *ctx, int mode, const MatvecArgs &a) {
+static int launch_generic(chn_ctx *ctx, int mode, const GenericArgs &a) {
     const uint32_t passes = (a.nb + 63) / 64;
     const int wpr = passes >= 4 ? 4 : (passes >= 2 ? 2 : 1);
     const int G = 4 / wpr;
@@ -222,23 +538,48 @@ int launch_matvec(chn_ctx *ctx, int mode, const MatvecArgs &a) {
     hipStream_t s = ctx->stream;
     switch (mode) {
     case MV_GEMV:
-        ok = wpr == 1 ? launch_rpw<MV_GEMV, 1>(rpw, a, grid, s)
-           : wpr == 2 ? launch_rpw<MV_GEMV, 2>(rpw, a, grid, s)
-                      : launch_rpw<MV_GEMV, 4>(rpw, a, grid, s);
+        ok = wpr == 1 ? gen_launch_rpw<MV_GEMV, 1>(rpw, a, grid, s)
+           : wpr == 2 ? gen_launch_rpw<MV_GEMV, 2>(rpw, a, grid, s)
+                      : gen_launch_rpw<MV_GEMV, 4>(rpw, a, grid, s);
         break;
     case MV_QKV:
-        ok = wpr == 1 ? launch_rpw<MV_QKV, 1>(rpw, a, grid, s)
-           : wpr == 2 ? launch_rpw<MV_QKV, 2>(rpw, a, grid, s)
-                      : launch_rpw<MV_QKV, 4>(rpw, a, grid, s);
+        ok = wpr == 1 ? gen_launch_rpw<MV_QKV, 1>(rpw, a, grid, s)
+           : wpr == 2 ? gen_launch_rpw<MV_QKV, 2>(rpw, a, grid, s)
+                      : gen_launch_rpw<MV_QKV, 4>(rpw, a, grid, s);
         break;
     default:
-        ok = wpr == 1 ? launch_rpw<MV_MLP, 1>(rpw, a, grid, s)
-           : wpr == 2 ? launch_rpw<MV_MLP, 2>(rpw, a, grid, s)
-                      : launch_rpw<MV_MLP, 4>(rpw, a, grid, s);
+        ok = wpr == 1 ? gen_launch_rpw<MV_MLP, 1>(rpw, a, grid, s)
+           : wpr == 2 ? gen_launch_rpw<MV_MLP, 2>(rpw, a, grid, s)
+                      : gen_launch_rpw<MV_MLP, 4>(rpw, a, grid, s);
         break;
     }
     if (!ok) return set_err(ctx, CHN_E_UNSUPPORTED, "no matvec tile for M=%u nb=%u", a.M, a.nb);
-    CHN_LAUNCHED(ctx, "k_matvec_q4");
+    CHN_LAUNCHED(ctx, "k_q4mv_generic");
+    return CHN_OK;
+}
+
+
+// x (fp32, K) -> digit planes in the context workspace, then the matvec.
+int launch_matvec(chn_ctx *ctx, int mode, MatvecArgs a, const float *x) {
+    const uint32_t nb = a.nb;
+    const bool fast = nb % 4 == 0 && nb <= 512 && aligned(a.W0, 16) && (!a.W1 || aligned(a.W1, 16)) &&
+                      (!a.W2 || aligned(a.W2, 16));
+    if (!fast) {
+        GenericArgs g{a.W0, a.W1, a.W2, a.y0, a.y1, a.y2, x, a.M, a.seg1, a.seg2, nb};
+        return launch_generic(ctx, mode, g);
+    }
+    int rc = ensure_workspace(ctx, xplanes_bytes(nb));
+    if (rc) return rc;
+    uint32_t *xp = (uint32_t *)ctx->ws;
+    k_xplanes<<<(4 * nb + 255) / 256, 256, 0, ctx->stream>>>(x, xp, nb);
+    CHN_LAUNCHED(ctx, "k_xplanes");
+    a.xp = xp;
+    const MvShape s = pick_shape(mode, a.M, nb);
+    bool ok = mode == MV_GEMV ? launch_mode<MV_GEMV>(s, a, ctx->stream)
+            : mode == MV_QKV  ? launch_mode<MV_QKV>(s, a, ctx->stream)
+                              : launch_mode<MV_MLP>(s, a, ctx->stream);
+    if (!ok) return set_err(ctx, CHN_E_UNSUPPORTED, "no matvec tile for M=%u nb=%u", a.M, nb);
+    CHN_LAUNCHED(ctx, "k_q4mv");
     return CHN_OK;
 }
 
@@ -259,8 +600,8 @@ extern "C" int chn_gemv_q4(chn_ctx *ctx, const uint32_t *W, const float *x, floa
     if (rc) return rc;
     CHN_REQUIRE(ctx, W && y && aligned(W, 4), "W/y must be non-NULL, W 4-byte aligned");
     if (M == 0) return CHN_OK;
-    MatvecArgs a{W, nullptr, nullptr, y, nullptr, nullptr, x, M, M, M, K / 32};
-    return launch_matvec(ctx, MV_GEMV, a);
+    MatvecArgs a{W, nullptr, nullptr, y, nullptr, nullptr, nullptr, M, M, M, K / 32};
+    return launch_matvec(ctx, MV_GEMV, a, x);
 }
 
 extern "C" int chn_fused_qkv_q4(chn_ctx *ctx, const uint32_t *Wq, const uint32_t *Wk,
@@ -274,8 +615,8 @@ extern "C" int chn_fused_qkv_q4(chn_ctx *ctx, const uint32_t *Wq, const uint32_t
     const uint64_t M = (uint64_t)q_dim + 2ull * kv_dim;
     CHN_REQUIRE(ctx, M < (1ull << 31), "q_dim + 2*kv_dim too large");
     if (M == 0) return CHN_OK;
-    MatvecArgs a{Wq, Wk, Wv, q, k, v, x, (uint32_t)M, q_dim, q_dim + kv_dim, K / 32};
-    return launch_matvec(ctx, MV_QKV, a);
+    MatvecArgs a{Wq, Wk, Wv, q, k, v, nullptr, (uint32_t)M, q_dim, q_dim + kv_dim, K / 32};
+    return launch_matvec(ctx, MV_QKV, a, x);
 }
 
 extern "C" int chn_fused_mlp_q4(chn_ctx *ctx, const uint32_t *Wg, const uint32_t *Wu,
@@ -285,6 +626,6 @@ extern "C" int chn_fused_mlp_q4(chn_ctx *ctx, const uint32_t *Wg, const uint32_t
     if (rc) return rc;
     CHN_REQUIRE(ctx, Wg && Wu && act && aligned(Wg, 4) && aligned(Wu, 4), "NULL/misaligned argument");
     if (M == 0) return CHN_OK;
-    MatvecArgs a{Wg, Wu, nullptr, act, nullptr, nullptr, x, M, M, M, K / 32};
-    return launch_matvec(ctx, MV_MLP, a);
+    MatvecArgs a{Wg, Wu, nullptr, act, nullptr, nullptr, nullptr, M, M, M, K / 32};
+    return launch_matvec(ctx, MV_MLP, a, x);
 }

@@ -53,7 +53,11 @@ def test_gemv_q4_parity(ctx, M, K):
 
 
 def test_gemv_q4_zero_codes_and_single_weight(ctx):
-    """All codes 8 -> exactly 0; one code 15 -> s * 7 * x[k] exactly."""
+    """All codes 8 -> 0; one code 15 -> s * 7 * x[k].  The kernel sums
+    q*x - 8*sum(x) per block (one VALU op per weight fewer than (q-8)*x), so
+    these exact answers come back with cancellation rounding of a few ulp of
+    8*sum|x|; the bounds below are 1e-5 of that scale, far below what any
+    wrong nibble position or dropped -8 would produce."""
     M, K = 16, 256
     Wh = oracle.synth_q4(M, K, 5).reshape(M, K // 32, 5).copy()
     Wh[:, :, 1:] = 0x88888888
@@ -65,9 +69,12 @@ def test_gemv_q4_zero_codes_and_single_weight(ctx):
     say("gemv_q4 zero/single")
     ctx.call("chn_gemv_q4", W, x, y, M, K)
     got = f32_host(ctx, y, M)
-    s = np.uint16(Wh[9, 3, 0] & 0xFFFF).view(np.float16).astype(np.float32)
-    assert got[9] == np.float32(s * np.float32(7.0 * xh[3 * 32 + 24 + 6]))
-    assert np.all(np.delete(got, 9) == 0.0)
+    scales = (Wh[:, :, 0] & 0xFFFF).astype(np.uint16).view(np.float16).astype(np.float64)
+    bound = 1e-5 * 8 * scales.max() * np.abs(xh).sum()
+    s = scales[9, 3]
+    assert abs(got[9] - s * 7.0 * xh[3 * 32 + 24 + 6]) <= bound
+    assert abs(got[9]) > 100 * bound
+    assert np.all(np.abs(np.delete(got, 9)) <= bound)
 
 
 @pytest.mark.parametrize("q_dim,kv_dim,K", [(4096, 2048, 3840), (96, 40, 256)])
