@@ -87,4 +87,34 @@ __device__ __forceinline__ float gelu_tanh(float x) {
     return (0.5f * x) * (1.0f + tanhf(inner));
 }
 
+// Transposed butterfly: V values per lane (V a power of two <= 64) summed
+// over the 64 lanes.  The sum for value index v ends up in every lane whose
+// top log2(V) lane-index bits equal v, i.e. v = lane >> (6 - log2 V).
+template <int V>
+__device__ __forceinline__ float wave_reduce_v(const float (&acc)[V], int lane) {
+    static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0, "V must be a power of two <= 64");
+    float cur[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) cur[i] = acc[i];
+    int m = 32;
+#pragma unroll
+    for (int n = V; n > 1; n >>= 1, m >>= 1) {
+        const int h = n / 2;
+        const bool hi = (lane & m) != 0;
+#pragma unroll
+        for (int i = 0; i < V / 2; ++i)
+            if (i < h) {
+                const float send = hi ? cur[i] : cur[i + h];
+                const float keep = hi ? cur[i + h] : cur[i];
+                cur[i] = keep + __shfl_xor(send, m, 64);
+            }
+    }
+    float s = cur[0];
+    for (; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
+    return s;
+}
+
+template <int V>
+constexpr int ilog2_c() { return V <= 1 ? 0 : 1 + ilog2_c<V / 2>(); }
+
 }  // namespace chn

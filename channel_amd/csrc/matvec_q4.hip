@@ -128,31 +128,6 @@ __device__ __forceinline__ int block_idot(const uint32_t *q, const uint32_t (&P)
     return acc;
 }
 
-// Transposed butterfly: V values per lane reduced over the 64 lanes; the
-// sum for value index v ends up in lanes whose top log2(V) bits equal v.
-template <int V>
-__device__ __forceinline__ float wave_reduce_v(const float (&acc)[V], int lane) {
-    float cur[V];
-#pragma unroll
-    for (int i = 0; i < V; ++i) cur[i] = acc[i];
-    int m = 32;
-#pragma unroll
-    for (int n = V; n > 1; n >>= 1, m >>= 1) {
-        const int h = n / 2;
-        const bool hi = (lane & m) != 0;
-#pragma unroll
-        for (int i = 0; i < V / 2; ++i)
-            if (i < h) {
-                const float send = hi ? cur[i] : cur[i + h];
-                const float keep = hi ? cur[i + h] : cur[i];
-                cur[i] = keep + __shfl_xor(send, m, 64);
-            }
-    }
-    float s = cur[0];
-    for (; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
-    return s;
-}
-
 __device__ __forceinline__ void wave_lds_fence() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();

@@ -116,6 +116,49 @@ int chn_fused_mlp_q4(chn_ctx *ctx, const uint32_t *Wg, const uint32_t *Wu,
                      const float *x, float *act, uint32_t M, uint32_t K);
 
 /* ======================================================================
+ * Attention, RoPE and norms (src/gpu/kernels.zig:131-164)
+ * ==================================================================== */
+
+/* Per-head RMSNorm * weight and RoPE for q (into q_out) and k, unit RMSNorm
+ * for v; k and v land in the caches at slot_idx * (num_kv_heads*head_dim).
+ * step_params is DEVICE memory holding {clock, slot_idx} (the reference's
+ * Step_params[0..1]), so a recorded graph can be replayed per token.
+ * recordQkvRope (src/gpu/kernels.zig:159-164) + shaders/qkv_rope.wgsl. */
+int chn_qkv_rope(chn_ctx *ctx, const float *q_in, const float *k_in, const float *v_in,
+                 const float *q_norm_w, const float *k_norm_w, float *q_out,
+                 float *k_cache, float *v_cache, const uint32_t *step_params,
+                 uint32_t num_q_heads, uint32_t num_kv_heads, uint32_t head_dim,
+                 uint32_t rotary_dim, int k_eq_v, float theta, float eps);
+
+/* Softmax attention of each query head over the slot list slots[0..S),
+ * S = *n_slots (DEVICE memory, clamped to max_slots <= 4096): the reference's
+ * Active_slots + Step_params[2] (global) or Active_slots + 4096 +
+ * Step_params[3] (sliding).  Query head h reads KV head h / gqa_ratio at
+ * cache row slot * kv_dim.  scale multiplies q.k (the reference passes 1.0).
+ * head_dim 256 or 512.  recordDecodeAttn (src/gpu/kernels.zig:147-152) +
+ * shaders/decode_attn.wgsl. */
+int chn_decode_attn(chn_ctx *ctx, const float *q, const float *k_cache, const float *v_cache,
+                    const uint32_t *slots, const uint32_t *n_slots, uint32_t max_slots,
+                    uint32_t num_q_heads, uint32_t head_dim, uint32_t kv_dim,
+                    uint32_t gqa_ratio, float scale, float *out);
+
+/* y = x * rsqrt(mean(x^2) + eps) * w over dim (dim % 4 == 0).
+ * recordRmsNorm (src/gpu/kernels.zig:139-142) + shaders/rmsnorm.wgsl. */
+int chn_rmsnorm(chn_ctx *ctx, const float *x, const float *w, float *y, uint32_t dim, float eps);
+
+/* x = (x + r) * scalar (in place), then y = rmsnorm(x) * w.
+ * recordAddRmsNorm (src/gpu/kernels.zig:131-134) + shaders/add_rmsnorm.wgsl. */
+int chn_add_rmsnorm(chn_ctx *ctx, float *x, const float *r, const float *w, float *y,
+                    uint32_t dim, float eps, float scalar);
+
+/* Row-wise versions over n_tok rows of dim (prefill): shaders/batch_rmsnorm.wgsl,
+ * shaders/batch_add_rmsnorm.wgsl (src/gpu/batch_dispatch.zig:64-67,117-119). */
+int chn_batch_rmsnorm(chn_ctx *ctx, const float *X, const float *w, float *Y, uint32_t n_tok,
+                      uint32_t dim, float eps);
+int chn_batch_add_rmsnorm(chn_ctx *ctx, float *X, const float *R, const float *w, float *Y,
+                          uint32_t n_tok, uint32_t dim, float eps, float scalar);
+
+/* ======================================================================
  * Seeded synthetic inputs (no reference counterpart: benchmark and test
  * inputs generated in place on the device; the same counter-based hash is
  * restated on the host, so any block can be regenerated for checking)
