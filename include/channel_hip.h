@@ -116,6 +116,26 @@ int chn_fused_mlp_q4(chn_ctx *ctx, const uint32_t *Wg, const uint32_t *Wu,
                      const float *x, float *act, uint32_t M, uint32_t K);
 
 /* ======================================================================
+ * Prefill contractions (src/gpu/batch_dispatch.zig:70-81,108-130)
+ * ==================================================================== */
+
+/* Y[t][r] = sum_k X[t][k] * W[r][k] for t < n_tok, r < M: X fp32 [n_tok][K]
+ * (16-byte aligned), W Q4 [M][K], Y fp32 [n_tok][M].  Operands are rounded
+ * to bf16 (X) and bf16(scale*(q-8)) (W, dequantized in LDS) for MFMA with
+ * fp32 accumulation; results match the fp32 contraction within 1e-2
+ * relative.  The reference's push constants call n_tok "N" and the output
+ * rows "M".  batch_gemm_q4 (shaders/batch_gemm_q4.wgsl; the unreferenced
+ * batch_gemm_q4_tiled.wgsl computes the same contraction). */
+int chn_batch_gemm_q4(chn_ctx *ctx, const uint32_t *W, const float *X, float *Y,
+                      uint32_t n_tok, uint32_t M, uint32_t K);
+
+/* Y[t][r] = gelu_tanh(G[t][r]) * U[t][r] with G, U as chn_batch_gemm_q4 over
+ * Wg, Wu.  batch_fused_mlp_q4 (shaders/batch_fused_mlp_q4.wgsl,
+ * src/gpu/batch_dispatch.zig:121-123). */
+int chn_batch_fused_mlp_q4(chn_ctx *ctx, const uint32_t *Wg, const uint32_t *Wu,
+                           const float *X, float *Y, uint32_t n_tok, uint32_t M, uint32_t K);
+
+/* ======================================================================
  * Attention, RoPE and norms (src/gpu/kernels.zig:131-164)
  * ==================================================================== */
 
