@@ -27,6 +27,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 METRIC = "decode tok/s + Q4 GEMV achieved HBM GB/s (% of peak), 12B-class, 1 GPU"
 SEED = 0xC4A77E1
 ROTATE_BYTES = 1 << 30  # >= 4x the 256 MB Infinity Cache
@@ -213,7 +214,94 @@ def bench_gemv(ctx, args):
     }
 
 
-WORKLOADS = {"mlp": bench_mlp, "gemv": bench_gemv}
+def bench_prefill(ctx, args):
+    """Batched prefill Q4 GEMM: 512 tokens x K=3840 -> 15360 features."""
+    T, K, N = 512, 3840, 15360
+    w_bytes = q4_bytes(N, K)
+    ncopy = 4
+    Ws = []
+    for c in range(ncopy):
+        b = ctx.alloc(w_bytes)
+        ctx.call("chn_synth_q4", b, N, K, SEED + c, 0.005, 0.02)
+        Ws.append(b)
+    X = ctx.alloc(T * K * 4)
+    ctx.call("chn_synth_normal", X, T * K, SEED + 77, 1.0)
+    Y = ctx.alloc(T * N * 4)
+    ctx.sync()
+    for i in range(args.warmup):
+        ctx.call("chn_batch_gemm_q4", Ws[i % ncopy], X, Y, T, N, K)
+    ctx.sync()
+    t0 = time.perf_counter()
+    ctx.timer_start()
+    for i in range(args.steps):
+        ctx.call("chn_batch_gemm_q4", Ws[i % ncopy], X, Y, T, N, K)
+    gpu_ms = ctx.timer_stop()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    ms = max(gpu_ms, wall_ms) / args.steps
+    flops = 2.0 * T * K * N
+    achieved = flops / (gpu_ms / args.steps * 1e-3) / 1e12
+    return {
+        "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": ms,
+        "config": {"workload": "batched prefill Q4 GEMM 512 tokens x 3840 -> 15360 (bf16 MFMA)",
+                   "tokens": T, "K": K, "N": N, "flop_per_step": flops},
+        "roofline": {"kernel": "k_q4gemm<1> (+ k_to_bf16 pre-pass)", "bound": "mfma",
+                     "achieved": achieved, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / MFMA_BF16_PEAK_TFLOPS, "traffic": None,
+                     "algorithmic_flop_per_launch": flops,
+                     "avg_launch_ms": gpu_ms / args.steps},
+        "cpu_baseline": None,
+        "dtype": "bf16 MFMA operands, fp32 accumulate",
+    }
+
+
+def bench_attn(ctx, args):
+    """Decode attention, 16 query / 8 KV heads, head_dim 256, full 4096-slot
+    ring of fp32 K/V."""
+    import numpy as np
+
+    H, KVH, D, S = 16, 8, 256, 4096
+    kv_dim = KVH * D
+    ncopy = 4     # 4 x 67 MB caches > 256 MB Infinity Cache
+    Kc, Vc = [], []
+    for c in range(ncopy):
+        k = ctx.alloc(S * kv_dim * 4)
+        v = ctx.alloc(S * kv_dim * 4)
+        ctx.call("chn_synth_normal", k, S * kv_dim, SEED + 100 + c, 1.0)
+        ctx.call("chn_synth_normal", v, S * kv_dim, SEED + 200 + c, 1.0)
+        Kc.append(k)
+        Vc.append(v)
+    q = ctx.alloc(H * D * 4)
+    ctx.call("chn_synth_normal", q, H * D, SEED + 300, 0.1)
+    slots = ctx.upload(((np.arange(S) + 1234) % S).astype(np.uint32))
+    ns = ctx.upload(np.array([S], np.uint32))
+    out = ctx.alloc(H * D * 4)
+    ctx.sync()
+    for i in range(args.warmup):
+        ctx.call("chn_decode_attn", q, Kc[i % ncopy], Vc[i % ncopy], slots, ns, S, H, D, kv_dim, 2, 1.0, out)
+    ctx.sync()
+    t0 = time.perf_counter()
+    ctx.timer_start()
+    for i in range(args.steps):
+        ctx.call("chn_decode_attn", q, Kc[i % ncopy], Vc[i % ncopy], slots, ns, S, H, D, kv_dim, 2, 1.0, out)
+    gpu_ms = ctx.timer_stop()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    ms = max(gpu_ms, wall_ms) / args.steps
+    nbytes = 2 * S * kv_dim * 4 + S * 4 + 2 * H * D * 4
+    achieved = nbytes / (gpu_ms / args.steps * 1e-3) / 1e9
+    return {
+        "value": 1e3 / ms, "unit": "attention steps/s", "ms_per_step": ms,
+        "config": {"workload": "decode attention over a full 4096-slot ring (16 q / 8 kv heads, D 256)",
+                   "slots": S, "bytes_per_step": nbytes},
+        "roofline": {"kernel": "k_attn_split + k_attn_combine", "bound": "hbm", "achieved": achieved,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": None, "algorithmic_bytes_per_launch": nbytes,
+                     "avg_launch_ms": gpu_ms / args.steps},
+        "cpu_baseline": None,
+        "dtype": "fp32",
+    }
+
+
+WORKLOADS = {"mlp": bench_mlp, "gemv": bench_gemv, "prefill": bench_prefill, "attn": bench_attn}
 
 
 def main():

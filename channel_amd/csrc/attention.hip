@@ -24,7 +24,42 @@ __host__ __device__ inline size_t attn_ws_bytes(uint32_t num_q_heads, uint32_t h
     return nsplit * num_q_heads * ((size_t)head_dim + 2) * 4;
 }
 
+// Sum over the 16 lanes of each DPP row; every lane of the row gets the sum.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true)); // quad_perm [1,0,3,2]
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true)); // quad_perm [2,3,0,1]
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xF, 0xF, true)); // row_ror:4
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xF, 0xF, true)); // row_ror:8
+    return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xF, 0xF, true)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xF, 0xF, true)));
+    return v;
+}
+// Whole-wave sum / max: row reductions, then the four row results.
+__device__ __forceinline__ float wave_sum64(float v) {
+    v = row16_sum(v);
+    return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16))) +
+           (__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48)));
+}
+__device__ __forceinline__ float wave_max64(float v) {
+    v = row16_max(v);
+    return fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)),
+                       __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16))),
+                 fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32)),
+                       __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48))));
+}
+
 // Partials: acc [nsplit][num_q_heads][D], then m and l [nsplit][num_q_heads].
+// Lane layout: row r = lane / 16 takes slots r, r+4, r+8, r+12 of the
+// wave's 16; column c = lane % 16 takes 16*DV consecutive dims, so one slot's
+// 1 KB (D = 256) row is read by a 16-lane row as 64 contiguous bytes per lane
+// and its score reduces inside the row with DPP.
 template <int DV, int GQA>
 __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ Q, const float *__restrict__ Kc,
                                                     const float *__restrict__ Vc,
@@ -33,7 +68,10 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ Q,
                                                     uint32_t num_q_heads, uint32_t kv_dim, float scale,
                                                     float *__restrict__ ws) {
     constexpr int D = DV * 256;
+    constexpr int NF = 4 * DV;                 // float4 per lane per row
+    constexpr int HC = GQA < 2 ? GQA : 2;      // heads combined per LDS pass
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r = lane >> 4, c = lane & 15;
     const uint32_t split = blockIdx.x, kvh = blockIdx.y;
     uint32_t S = *n_slots;
     if (S > max_slots) S = max_slots;
@@ -43,72 +81,66 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ Q,
     const uint32_t nsplit = (max_slots + kAttnChunk - 1) / kAttnChunk;
 
     __shared__ float sc[GQA][kAttnChunk];
-    __shared__ f4 pacc[4][GQA][DV * 64];
+    __shared__ f4 pacc[16][HC][16 * NF];      // [wave*4 + row][head][column float4]
 
-    // q for this KV head's query heads: lane holds 4 consecutive dims per DV
-    f4 q[GQA][DV];
+    const uint32_t base = s0 + wave * 16;
+    const uint32_t nval = cnt > (uint32_t)(wave * 16) ? cnt - wave * 16 : 0;
+    const uint32_t my_slot = (uint32_t)lane < nval && lane < 16 ? slots[base + lane] : 0u;
+    const size_t dim0 = (size_t)kvh * D + (size_t)c * NF * 4;
+
+    // K rows first, then V rows: 4 slots per lane-row, NF float4 each
+    f4 kr[4][NF], vr[4][NF];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = r + 4 * u;                                   // slot within the wave
+        const uint32_t ps = (uint32_t)__shfl(my_slot, i, 64);
+        const bool ok = (uint32_t)i < nval;
+        const float *kp = Kc + (size_t)ps * kv_dim + dim0;
+#pragma unroll
+        for (int f = 0; f < NF; ++f) kr[u][f] = ok ? *(const f4 *)(kp + 4 * f) : f4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = r + 4 * u;
+        const uint32_t ps = (uint32_t)__shfl(my_slot, i, 64);
+        const bool ok = (uint32_t)i < nval;
+        const float *vp = Vc + (size_t)ps * kv_dim + dim0;
+#pragma unroll
+        for (int f = 0; f < NF; ++f) vr[u][f] = ok ? *(const f4 *)(vp + 4 * f) : f4{0, 0, 0, 0};
+    }
+    f4 q[GQA][NF];
 #pragma unroll
     for (int h = 0; h < GQA; ++h)
 #pragma unroll
-        for (int v = 0; v < DV; ++v)
-            q[h][v] = *(const f4 *)(Q + (size_t)(kvh * GQA + h) * D + 4 * (lane + 64 * v));
+        for (int f = 0; f < NF; ++f) q[h][f] = *(const f4 *)(Q + (size_t)(kvh * GQA + h) * D + c * NF * 4 + 4 * f);
 
-    // ---- scores: wave w takes slots w*16 .. w*16+15 of the chunk
-    const uint32_t base = s0 + wave * 16;
-    float part[16 * GQA];
+    // ---- scores
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        f4 k[DV];
-        const bool ok = (uint32_t)(wave * 16 + i) < cnt;
-        const uint32_t ps = ok ? slots[base + i] : 0u;
-        const float *kr = Kc + (size_t)ps * kv_dim + (size_t)kvh * D;
-#pragma unroll
-        for (int v = 0; v < DV; ++v) k[v] = ok ? *(const f4 *)(kr + 4 * (lane + 64 * v)) : f4{0, 0, 0, 0};
+    for (int u = 0; u < 4; ++u)
 #pragma unroll
         for (int h = 0; h < GQA; ++h) {
             float d = 0.0f;
 #pragma unroll
-            for (int v = 0; v < DV; ++v) {
-                d = fmaf(q[h][v].x, k[v].x, d);
-                d = fmaf(q[h][v].y, k[v].y, d);
-                d = fmaf(q[h][v].z, k[v].z, d);
-                d = fmaf(q[h][v].w, k[v].w, d);
+            for (int f = 0; f < NF; ++f) {
+                d = fmaf(q[h][f].x, kr[u][f].x, d);
+                d = fmaf(q[h][f].y, kr[u][f].y, d);
+                d = fmaf(q[h][f].z, kr[u][f].z, d);
+                d = fmaf(q[h][f].w, kr[u][f].w, d);
             }
-            part[i * GQA + h] = d;
+            d = row16_sum(d);
+            if (c == 0) sc[h][wave * 16 + r + 4 * u] = d * scale;
         }
-    }
-    // reduce the 16*GQA partial dots over the wave, at most 64 values per
-    // butterfly: value v = i*GQA + h lands in lanes with lane >> (6 - LV) == v
-    {
-        constexpr int NG = (16 * GQA <= 64) ? 16 : 64 / GQA;   // slots per round
-        constexpr int NV = NG * GQA;
-        constexpr int LV = ilog2_c<NV>();
-#pragma unroll
-        for (int r = 0; r < 16 / NG; ++r) {
-            float vals[NV];
-#pragma unroll
-            for (int i = 0; i < NV; ++i) vals[i] = part[r * NV + i];
-            const float s = wave_reduce_v<NV>(vals, lane);
-            const int v = lane >> (6 - LV);
-            if ((lane & ((64 >> LV) - 1)) == 0) sc[v % GQA][wave * 16 + r * NG + v / GQA] = s * scale;
-        }
-    }
     __syncthreads();
 
-    // ---- chunk-local softmax statistics; every wave computes them (cheap)
+    // ---- chunk softmax statistics (lane = slot of the 64-slot chunk)
     float m[GQA], l[GQA], p[GQA];
 #pragma unroll
     for (int h = 0; h < GQA; ++h) {
-        const float s = (uint32_t)lane < cnt ? sc[h][lane] : kNegBig;
-        float mm = s;
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) mm = fmaxf(mm, __shfl_xor(mm, off, 64));
-        const float e = (uint32_t)lane < cnt ? expf(s - mm) : 0.0f;
-        float ll = e;
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) ll += __shfl_xor(ll, off, 64);
+        const float sv = (uint32_t)lane < cnt ? sc[h][lane] : kNegBig;
+        const float mm = wave_max64(sv);
+        const float e = (uint32_t)lane < cnt ? expf(sv - mm) : 0.0f;
         m[h] = mm;
-        l[h] = ll;
+        l[h] = wave_sum64(e);
         p[h] = e;
     }
     __syncthreads();
@@ -118,40 +150,45 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ Q,
     }
     __syncthreads();
 
-    // ---- weighted V sum: wave w takes its 16 slots
-    f4 acc[GQA][DV];
+    // ---- p-weighted V rows of this lane
+    f4 acc[GQA][NF];
 #pragma unroll
     for (int h = 0; h < GQA; ++h)
 #pragma unroll
-        for (int v = 0; v < DV; ++v) acc[h][v] = f4{0, 0, 0, 0};
+        for (int f = 0; f < NF; ++f) acc[h][f] = f4{0, 0, 0, 0};
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const uint32_t li = wave * 16 + i;
-        if (li < cnt) {
-            const float *vr = Vc + (size_t)slots[base + i] * kv_dim + (size_t)kvh * D;
+    for (int u = 0; u < 4; ++u) {
+        const int i = r + 4 * u;
+        if ((uint32_t)i < nval) {
 #pragma unroll
-            for (int v = 0; v < DV; ++v) {
-                const f4 vv = *(const f4 *)(vr + 4 * (lane + 64 * v));
+            for (int h = 0; h < GQA; ++h) {
+                const float pw = sc[h][wave * 16 + i];
 #pragma unroll
-                for (int h = 0; h < GQA; ++h) acc[h][v] += sc[h][li] * vv;
+                for (int f = 0; f < NF; ++f) acc[h][f] += pw * vr[u][f];
             }
         }
     }
-#pragma unroll
-    for (int h = 0; h < GQA; ++h)
-#pragma unroll
-        for (int v = 0; v < DV; ++v) pacc[wave][h][lane + 64 * v] = acc[h][v];
-    __syncthreads();
 
-    // ---- combine the four waves (fixed order) and write the partial
+    // ---- combine the 16 (wave, row) partials in a fixed order, HC heads per pass
     float *wacc = ws;
     float *wm = ws + (size_t)nsplit * num_q_heads * D;
     float *wl = wm + (size_t)nsplit * num_q_heads;
-    for (int idx = threadIdx.x; idx < GQA * DV * 64; idx += 256) {
-        const int h = idx / (DV * 64), c = idx % (DV * 64);
-        const f4 t = ((pacc[0][h][c] + pacc[1][h][c]) + pacc[2][h][c]) + pacc[3][h][c];
-        const uint32_t qh = kvh * GQA + h;
-        *(f4 *)(wacc + ((size_t)split * num_q_heads + qh) * D + 4 * c) = t;
+#pragma unroll
+    for (int h0 = 0; h0 < GQA; h0 += HC) {
+#pragma unroll
+        for (int hh = 0; hh < HC; ++hh)
+#pragma unroll
+            for (int f = 0; f < NF; ++f) pacc[wave * 4 + r][hh][c * NF + f] = acc[h0 + hh][f];
+        __syncthreads();
+        for (int idx = threadIdx.x; idx < HC * 16 * NF; idx += 256) {
+            const int hh = idx / (16 * NF), col = idx % (16 * NF);
+            f4 t = pacc[0][hh][col];
+#pragma unroll
+            for (int j = 1; j < 16; ++j) t += pacc[j][hh][col];
+            const uint32_t qh = kvh * GQA + h0 + hh;
+            *(f4 *)(wacc + ((size_t)split * num_q_heads + qh) * D + 4 * col) = t;
+        }
+        __syncthreads();
     }
     if (threadIdx.x < GQA) {
         const uint32_t qh = kvh * GQA + threadIdx.x;
@@ -160,32 +197,58 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ Q,
     }
 }
 
-// One workgroup per query head: merge the chunk partials.
-__global__ __launch_bounds__(128) void k_attn_combine(const float *__restrict__ ws,
+// One 256-thread workgroup per query head merges the chunk partials: chunk
+// weights exp(m_j - M) are computed once, then wave w sums chunks
+// j = w, w + 4, ... for every column with loads batched four at a time, and
+// the four wave sums are added in a fixed order.
+__global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ ws,
                                                       const uint32_t *__restrict__ n_slots, uint32_t max_slots,
                                                       uint32_t num_q_heads, uint32_t head_dim,
                                                       float *__restrict__ out) {
+    __shared__ float ew[64];
+    __shared__ float sinv;
+    __shared__ f4 part[4][128];
     const uint32_t qh = blockIdx.x;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     uint32_t S = *n_slots;
     if (S > max_slots) S = max_slots;
     const uint32_t nsplit_max = (max_slots + kAttnChunk - 1) / kAttnChunk;
-    const uint32_t ns = (S + kAttnChunk - 1) / kAttnChunk;
+    const uint32_t ns = (S + kAttnChunk - 1) / kAttnChunk;     // <= 64
     const float *wacc = ws;
     const float *wm = ws + (size_t)nsplit_max * num_q_heads * head_dim;
     const float *wl = wm + (size_t)nsplit_max * num_q_heads;
-    float M = -1e9f;  // the reference's running-max seed
-    for (uint32_t j = 0; j < ns; ++j) M = fmaxf(M, wm[(size_t)j * num_q_heads + qh]);
-    float L = 0.0f;
-    for (uint32_t j = 0; j < ns; ++j) L += expf(wm[(size_t)j * num_q_heads + qh] - M) * wl[(size_t)j * num_q_heads + qh];
-    const float inv = 1.0f / (L + 1e-9f);
-    for (uint32_t c = threadIdx.x; c < head_dim / 4; c += blockDim.x) {
-        f4 t = f4{0, 0, 0, 0};
-        for (uint32_t j = 0; j < ns; ++j) {
-            const float w = expf(wm[(size_t)j * num_q_heads + qh] - M);
-            t += w * *(const f4 *)(wacc + ((size_t)j * num_q_heads + qh) * head_dim + 4 * c);
-        }
-        *(f4 *)(out + (size_t)qh * head_dim + 4 * c) = t * inv;
+    if (wave == 0) {
+        const float mj = (uint32_t)lane < ns ? wm[(size_t)lane * num_q_heads + qh] : -1e9f;
+        float M = mj;  // seeded at the reference's -1e9 by the padding lanes / the max below
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+        M = fmaxf(M, -1e9f);
+        const float e = (uint32_t)lane < ns ? expf(mj - M) : 0.0f;
+        float L = (uint32_t)lane < ns ? e * wl[(size_t)lane * num_q_heads + qh] : 0.0f;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off, 64);
+        ew[lane] = e;
+        if (lane == 0) sinv = 1.0f / (L + 1e-9f);
     }
+    __syncthreads();
+    const uint32_t ncol = head_dim / 4;          // float4 columns, <= 128
+    for (uint32_t c = lane; c < ncol; c += 64) {
+        f4 t = f4{0, 0, 0, 0};
+        uint32_t j = wave;
+        for (; j + 12 < ns; j += 16) {
+            f4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                v[u] = *(const f4 *)(wacc + ((size_t)(j + 4 * u) * num_q_heads + qh) * head_dim + 4 * c);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) t += ew[j + 4 * u] * v[u];
+        }
+        for (; j < ns; j += 4) t += ew[j] * *(const f4 *)(wacc + ((size_t)j * num_q_heads + qh) * head_dim + 4 * c);
+        part[wave][c] = t;
+    }
+    __syncthreads();
+    for (uint32_t c = threadIdx.x; c < ncol; c += 256)
+        *(f4 *)(out + (size_t)qh * head_dim + 4 * c) = (((part[0][c] + part[1][c]) + part[2][c]) + part[3][c]) * sinv;
 }
 
 int launch_decode_attn(chn_ctx *ctx, const float *q, const float *kc, const float *vc, const uint32_t *slots,
@@ -217,7 +280,7 @@ int launch_decode_attn(chn_ctx *ctx, const float *q, const float *kc, const floa
     }
 #undef CHN_ATTN
     CHN_LAUNCHED(ctx, "k_attn_split");
-    k_attn_combine<<<num_q_heads, 128, 0, s>>>(ws, n_slots, max_slots, num_q_heads, head_dim, out);
+    k_attn_combine<<<num_q_heads, 256, 0, s>>>(ws, n_slots, max_slots, num_q_heads, head_dim, out);
     CHN_LAUNCHED(ctx, "k_attn_combine");
     return CHN_OK;
 }
@@ -321,7 +384,7 @@ extern "C" int chn_decode_attn(chn_ctx *ctx, const float *q, const float *k_cach
                 "kv_dim %u too small for %u kv heads of %u", kv_dim, num_q_heads / gqa_ratio, head_dim);
     CHN_REQUIRE(ctx, aligned(q, 16) && aligned(k_cache, 16) && aligned(v_cache, 16) && aligned(out, 16),
                 "q, caches and out must be 16-byte aligned");
-    CHN_REQUIRE(ctx, max_slots > 0, "max_slots must be > 0");
+    CHN_REQUIRE(ctx, max_slots > 0 && max_slots <= 4096, "max_slots %u must be in 1..4096", max_slots);
     if (!num_q_heads) return CHN_OK;
     int rc = ensure_workspace(ctx, attn_ws_bytes(num_q_heads, head_dim, max_slots));
     if (rc) return rc;
