@@ -55,6 +55,27 @@ PROTOTYPES = {
     "chn_add_rmsnorm": (c_int, [c_void_p] * 5 + [c_u32, c_f32, c_f32]),
     "chn_batch_rmsnorm": (c_int, [c_void_p] * 4 + [c_u32, c_u32, c_f32]),
     "chn_batch_add_rmsnorm": (c_int, [c_void_p] * 5 + [c_u32, c_u32, c_f32, c_f32]),
+    "chn_batch_qkv_rope": (c_int, [c_void_p] + [c_void_p] * 9 + [c_u32] * 7 + [c_int, c_f32, c_f32]),
+    "chn_batch_causal_attn": (c_int, [c_void_p] * 5 + [c_u32] * 6 + [c_f32, c_u32, c_void_p]),
+    "chn_gemv_q8": (c_int, [c_void_p] * 4 + [c_u32, c_u32]),
+    "chn_topk64": (c_int, [c_void_p, c_void_p, c_u32, c_void_p, c_void_p]),
+    "chn_quantize_q4": (c_int, [c_void_p] * 3 + [c_u32, c_u32]),
+    "chn_quantize_q8": (c_int, [c_void_p] * 3 + [c_u32, c_u32]),
+    "chn_to_bf16_bits": (c_int, [c_void_p] * 3 + [c_size]),
+    "chn_model_create": (c_int, [c_void_p] * 5 + [P(c_void_p)]),
+    "chn_model_create_synthetic": (c_int, [c_void_p, c_void_p, c_u64, P(c_void_p)]),
+    "chn_model_destroy": (None, [c_void_p]),
+    "chn_model_get_config": (c_int, [c_void_p, c_void_p]),
+    "chn_model_embedding_bf16": (c_int, [c_void_p, P(c_void_p)]),
+    "chn_decode_step": (c_int, [c_void_p, c_void_p, c_u32, c_u32, c_void_p, c_u32, c_void_p, c_u32,
+                                c_void_p, c_void_p, P(c_u32)]),
+    "chn_decode_token": (c_int, [c_void_p, c_u32, c_u32, c_u32, c_void_p, c_u32, c_void_p, c_u32,
+                                 c_void_p, c_void_p, P(c_u32)]),
+    "chn_prefill": (c_int, [c_void_p, c_void_p, c_u32, c_void_p, c_void_p, c_u32, c_u32, c_u32,
+                            c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "chn_kv_read": (c_int, [c_void_p, c_u32, c_u32, c_u32, c_void_p, c_void_p]),
+    "chn_kv_write": (c_int, [c_void_p, c_u32, c_u32, c_u32, c_void_p, c_void_p]),
+    "chn_model_read_state": (c_int, [c_void_p, c_void_p, c_void_p]),
     "chn_synth_q4": (c_int, [c_void_p, c_void_p, c_u32, c_u32, c_u64, c_f32, c_f32]),
     "chn_synth_q8": (c_int, [c_void_p, c_void_p, c_u32, c_u32, c_u64, c_f32, c_f32]),
     "chn_synth_normal": (c_int, [c_void_p, c_void_p, c_size, c_u64, c_f32]),

@@ -48,6 +48,40 @@ int ensure_workspace(chn_ctx *ctx, size_t bytes);
 
 inline bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
+// ---- internal launchers (explicit workspaces; usable under graph capture)
+size_t mv_ws_bytes(uint32_t K);
+int mv_gemv(chn_ctx *ctx, const uint32_t *W, const float *x, float *y, uint32_t M, uint32_t K, uint32_t *ws);
+int mv_qkv(chn_ctx *ctx, const uint32_t *Wq, const uint32_t *Wk, const uint32_t *Wv, const float *x, float *q,
+           float *k, float *v, uint32_t q_dim, uint32_t kv_dim, uint32_t K, uint32_t *ws);
+int mv_mlp(chn_ctx *ctx, const uint32_t *Wg, const uint32_t *Wu, const float *x, float *act, uint32_t M, uint32_t K,
+           uint32_t *ws);
+int launch_rmsnorm(hipStream_t s, float *x, const float *r, const float *w, float *y, uint32_t dim, uint32_t rows,
+                   float eps, float scalar, bool add);
+int launch_qkv_rope(hipStream_t st, const float *q_in, const float *k_in, const float *v_in, const float *qw,
+                    const float *kw, float *q_out, float *kc, float *vc, const uint32_t *step, uint32_t num_q,
+                    uint32_t num_kv, uint32_t D, uint32_t rot, int k_eq_v, float theta, float eps);
+int launch_batch_qkv_rope(hipStream_t st, const float *q_in, const float *k_in, const float *v_in, const float *qw,
+                          const float *kw, float *q_out, float *kc, float *vc, const uint32_t *slots,
+                          uint32_t slot_offset, uint32_t start_clock, uint32_t n_tok, uint32_t num_q, uint32_t num_kv,
+                          uint32_t D, uint32_t rot, int k_eq_v, float theta, float eps);
+size_t attn_ws_bytes(uint32_t num_q_heads, uint32_t head_dim, uint32_t max_slots);
+int launch_decode_attn(chn_ctx *ctx, const float *q, const float *kc, const float *vc, const uint32_t *slots,
+                       const uint32_t *n_slots, uint32_t max_slots, uint32_t num_q_heads, uint32_t head_dim,
+                       uint32_t kv_dim, uint32_t gqa, float scale, float *out, float *ws);
+int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const float *vc, const uint32_t *slots,
+                        uint32_t n_tok, uint32_t num_prev, uint32_t num_q_heads, uint32_t head_dim, uint32_t kv_dim,
+                        uint32_t gqa, float scale, uint32_t window, float *out);
+size_t xbytes_bytes(uint32_t nb);
+int launch_gemv_q8(hipStream_t st, const uint32_t *W, const float *x, float *y, uint32_t M, uint32_t nb,
+                   uint32_t *xp_ws);
+size_t topk_ws_bytes(uint32_t V);
+int launch_topk64(hipStream_t st, const float *logits, uint32_t V, uint32_t *ids, float *vals, uint64_t *ws);
+int launch_embed(hipStream_t st, const uint16_t *table, const uint32_t *tokens, uint32_t n, uint32_t H, float scale,
+                 float *x);
+int launch_quantize(hipStream_t st, int q8, const uint16_t *src, uint32_t *dst, uint64_t nblk);
+int launch_q4gemm(chn_ctx *ctx, int nmat, const float *X, const uint32_t *W0, const uint32_t *W1, float *Y,
+                  uint32_t n_tok, uint32_t M, uint32_t K, __bf16 *xb);
+
 // ---------------------------------------------------------------------
 // Device helpers
 // ---------------------------------------------------------------------

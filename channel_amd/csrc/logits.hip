@@ -1,0 +1,403 @@
+// Logits and selection on gfx950:
+//  * gemv_q8 (shaders/gemv_q8.wgsl) over the Q8_0 tied embedding,
+//  * softcapped global top-64 (shaders/topk_pass1.wgsl, topk_pass2.wgsl),
+//  * device restatements of the reference quantizers (src/quant.zig:21-98)
+//    for weight ingest, and the embedding gather of forwardToken
+//    (src/model/forward.zig:35-37).
+//
+// The Q8 matvec streams 36-byte blocks the way the Q4 matvec streams
+// 20-byte ones (coalesced non-temporal 16-byte loads of row segments, LDS
+// transpose to one lane per block).  Activations become three balanced
+// base-256 digit planes of a 22-bit fixed-point value per 32-block, so a
+// block is 24 v_dot4c_i32_i8 (signed weights x signed digits, exact), the
+// three plane sums are combined in fp32 and scaled by f32 scale *
+// 2^(e_b - 22).
+#include "chn_internal.h"
+
+namespace chn {
+
+constexpr int XB_PLANES = 3;
+constexpr int XB_FRAC = 22;
+constexpr int XB_WORDS = XB_PLANES * 8;   // 8 int8x4 words per plane per block
+
+size_t xbytes_bytes(uint32_t nb) { return (size_t)nb * (XB_WORDS + 1) * 4; }
+
+// Eight threads per 32-block, one per 4-element weight word.
+__global__ __launch_bounds__(256) void k_xbytes(const float *__restrict__ x, uint32_t *__restrict__ xp, uint32_t nb) {
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t b = t >> 3, w = t & 7;
+    const bool ok = b < nb;
+    float4 v = ok ? *(const float4 *)(x + (size_t)b * 32 + w * 4) : make_float4(0, 0, 0, 0);
+    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    m = fmaxf(m, __shfl_xor(m, 1, 64));
+    m = fmaxf(m, __shfl_xor(m, 2, 64));
+    m = fmaxf(m, __shfl_xor(m, 4, 64));
+    int e = 0;
+    (void)frexpf(m, &e);
+    float scale = 0.0f, inv = 0.0f;
+    if (m > 0.0f && e > -100) {
+        scale = ldexpf(1.0f, XB_FRAC - e);
+        inv = ldexpf(1.0f, e - XB_FRAC);
+    }
+    uint32_t u[4];
+    u[0] = (uint32_t)((int)rintf(v.x * scale) + 0x808080);
+    u[1] = (uint32_t)((int)rintf(v.y * scale) + 0x808080);
+    u[2] = (uint32_t)((int)rintf(v.z * scale) + 0x808080);
+    u[3] = (uint32_t)((int)rintf(v.w * scale) + 0x808080);
+    if (!ok) return;
+#pragma unroll
+    for (int p = 0; p < XB_PLANES; ++p) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) word |= ((u[j] >> (8 * p)) & 0xffu) << (8 * j);
+        xp[(size_t)(p * 8 + w) * nb + b] = word ^ 0x80808080u;
+    }
+    if (w == 0) ((float *)(xp + (size_t)XB_WORDS * nb))[b] = inv;
+}
+
+typedef uint32_t u32x4q __attribute__((ext_vector_type(4)));
+
+constexpr int kQ8Seg = 128 * 9;   // LDS words per stream segment (128 blocks)
+
+__device__ __forceinline__ void q8_lds_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Whole rows per wave (K <= 4096), RPW rows per group, persistent grid.
+template <int RPW>
+__global__ __launch_bounds__(256) void k_q8mv(const uint32_t *__restrict__ W, const uint32_t *__restrict__ xp,
+                                              float *__restrict__ y, uint32_t M, uint32_t nb) {
+    constexpr int LV = RPW == 1 ? 0 : (RPW == 2 ? 1 : 2);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const size_t rw = (size_t)nb * 9;
+    const uint32_t chunks = nb * 9 / 4;          // nb % 4 == 0
+    __shared__ uint32_t seg[4][RPW * kQ8Seg];
+    uint32_t *L = seg[wave];
+
+    uint32_t P[2][XB_WORDS];
+    float xs[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const uint32_t b = c * 64 + lane;
+        const bool ok = b < nb;
+#pragma unroll
+        for (int i = 0; i < XB_WORDS; ++i) P[c][i] = ok ? xp[(size_t)i * nb + b] : 0u;
+        xs[c] = ok ? ((const float *)(xp + (size_t)XB_WORDS * nb))[b] : 0.0f;
+    }
+    const uint32_t ngroups = (M + RPW - 1) / RPW;
+    const uint32_t gstride = gridDim.x * 4;
+    u32x4q pf[RPW][5];
+    auto load = [&](uint32_t g) {
+#pragma unroll
+        for (int s = 0; s < RPW; ++s) {
+            const uint32_t row = g * RPW + s;
+            const u32x4q *base = (const u32x4q *)(W + (size_t)(row < M ? row : 0) * rw);
+#pragma unroll
+            for (int j = 0; j < 5; ++j) {
+                const uint32_t c = lane + 64 * j;
+                if (row < M && c < chunks) pf[s][j] = __builtin_nontemporal_load(base + c);
+            }
+        }
+    };
+    uint32_t g = blockIdx.x * 4 + wave;
+    if (g < ngroups) load(g);
+    for (; g < ngroups; g += gstride) {
+#pragma unroll
+        for (int s = 0; s < RPW; ++s)
+#pragma unroll
+            for (int j = 0; j < 5; ++j) {
+                const uint32_t c = lane + 64 * j;
+                if (c < chunks) *(u32x4q *)(L + s * kQ8Seg + 4 * c) = pf[s][j];
+            }
+        q8_lds_fence();
+        if (g + gstride < ngroups) load(g + gstride);
+        float acc[RPW];
+#pragma unroll
+        for (int s = 0; s < RPW; ++s) acc[s] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const uint32_t b = c * 64 + lane;
+            if (b < nb) {
+#pragma unroll
+                for (int s = 0; s < RPW; ++s) {
+                    const uint32_t *p = L + s * kQ8Seg + 9 * b;
+                    const float sw = __builtin_bit_cast(float, p[0]);
+                    int pl[XB_PLANES];
+#pragma unroll
+                    for (int q = 0; q < XB_PLANES; ++q) {
+                        int t = 0;
+#pragma unroll
+                        for (int w = 0; w < 8; ++w) t = __builtin_amdgcn_sdot4((int)p[1 + w], (int)P[c][q * 8 + w], t, false);
+                        pl[q] = t;
+                    }
+                    const float T = fmaf((float)pl[2], 65536.0f, fmaf((float)pl[1], 256.0f, (float)pl[0]));
+                    acc[s] = fmaf(T, sw * xs[c], acc[s]);
+                }
+            }
+        }
+        q8_lds_fence();
+        const float sum = wave_reduce_v<RPW>(acc, lane);
+        const int vi = lane >> (6 - LV);
+        if ((lane & ((64 >> LV) - 1)) == 0 && g * RPW + vi < M) y[g * RPW + vi] = sum;
+    }
+}
+
+int launch_gemv_q8(hipStream_t st, const uint32_t *W, const float *x, float *y, uint32_t M, uint32_t nb,
+                   uint32_t *xp_ws) {
+    k_xbytes<<<(8 * nb + 255) / 256, 256, 0, st>>>(x, xp_ws, nb);
+    const uint32_t ngroups = (M + 1) / 2;
+    uint32_t grid = (ngroups + 3) / 4;
+    if (grid > 1024) grid = 1024;
+    k_q8mv<2><<<grid, 256, 0, st>>>(W, xp_ws, y, M, nb);
+    return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
+}
+
+// ---------------------------------------------------------------------
+// Softcapped top-64: pass 1 sorts 2048-logit tiles (bitonic, descending on
+// a 64-bit key = orderable(value) << 32 | ~index, so ties keep the lower
+// index first) and keeps 64 per tile; pass 2 sorts the survivors.
+// ---------------------------------------------------------------------
+constexpr int kTopK = 64;
+constexpr int kTile = 2048;
+
+__device__ __forceinline__ uint64_t topk_key(float v, uint32_t idx) {
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)u << 32) | (uint64_t)(0xFFFFFFFFu - idx);
+}
+__device__ __forceinline__ float key_value(uint64_t k) {
+    uint32_t u = (uint32_t)(k >> 32);
+    u = (u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u;
+    return __builtin_bit_cast(float, u);
+}
+
+// descending bitonic sort of n (power of two) keys in LDS by nthreads threads
+__device__ void bitonic_desc(uint64_t *k, int n) {
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int t = threadIdx.x; t < n / 2; t += blockDim.x) {
+                const int i = 2 * t - (t & (stride - 1));
+                const int j = i + stride;
+                const bool desc = ((i & size) == 0);
+                const uint64_t a = k[i], b = k[j];
+                if (desc ? (a < b) : (a > b)) { k[i] = b; k[j] = a; }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void k_topk_pass1(const float *__restrict__ logits, uint32_t V,
+                                                    uint64_t *__restrict__ cand) {
+    __shared__ uint64_t k[kTile];
+    const uint32_t base = blockIdx.x * kTile;
+    for (int i = threadIdx.x; i < kTile; i += 256) {
+        const uint32_t idx = base + i;
+        if (idx < V) {
+            const float v = logits[idx];
+            const float t = tanhf(v * (1.0f / 30.0f));
+            k[i] = topk_key(30.0f * t, idx);
+        } else {
+            k[i] = 0;   // below every real key
+        }
+    }
+    __syncthreads();
+    bitonic_desc(k, kTile);
+    if (threadIdx.x < kTopK) cand[(size_t)blockIdx.x * kTopK + threadIdx.x] = k[threadIdx.x];
+}
+
+__global__ __launch_bounds__(1024) void k_topk_pass2(const uint64_t *__restrict__ cand, uint32_t ncand,
+                                                     uint32_t *__restrict__ ids, float *__restrict__ vals) {
+    extern __shared__ uint64_t k2[];
+    uint32_t n = 1;
+    while (n < ncand) n <<= 1;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) k2[i] = i < ncand ? cand[i] : 0;
+    __syncthreads();
+    bitonic_desc(k2, (int)n);
+    if (threadIdx.x < kTopK) {
+        const uint64_t key = k2[threadIdx.x];
+        if (key) {
+            ids[threadIdx.x] = 0xFFFFFFFFu - (uint32_t)key;
+            vals[threadIdx.x] = key_value(key);
+        } else {
+            ids[threadIdx.x] = 0;
+            vals[threadIdx.x] = -1e30f;
+        }
+    }
+}
+
+size_t topk_ws_bytes(uint32_t V) { return (size_t)((V + kTile - 1) / kTile) * kTopK * 8; }
+
+int launch_topk64(hipStream_t st, const float *logits, uint32_t V, uint32_t *ids, float *vals, uint64_t *ws) {
+    const uint32_t tiles = (V + kTile - 1) / kTile;
+    k_topk_pass1<<<tiles, 256, 0, st>>>(logits, V, ws);
+    const uint32_t ncand = tiles * kTopK;
+    uint32_t n = 1;
+    while (n < ncand) n <<= 1;
+    k_topk_pass2<<<1, 1024, n * 8, st>>>(ws, ncand, ids, vals);
+    return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
+}
+
+// ---------------------------------------------------------------------
+// Quantizers (bit-exact restatements of src/quant.zig:21-98) and the
+// embedding gather x = bf16(embed[tok]) * sqrt(H).
+// ---------------------------------------------------------------------
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+
+__global__ void k_quantize_q4(const uint16_t *__restrict__ src, uint32_t *__restrict__ dst, uint64_t nblk) {
+    // separate roundings of v * id and + 8, as the reference computes them
+    // (HIP contracts a * b + c into one fma by default)
+    #pragma clang fp contract(off)
+    const uint64_t blk = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (blk >= nblk) return;
+    const uint16_t *s = src + blk * 32;
+    float v[32], amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        v[i] = bf16_bits_to_f32(s[i]);
+        amax = fmaxf(amax, fabsf(v[i]));
+    }
+    const float d = amax / 8.0f;
+    const float id = d > 0.0f ? 1.0f / d : 0.0f;
+    // min = f16(-8 d): d >= 0, so it is f16(8 d) with the sign bit set
+    // (written out so that d = 0 gives -0.0 as the reference's f16 cast does)
+    const uint32_t sc = __builtin_bit_cast(unsigned short, (_Float16)d);
+    const uint32_t mn = __builtin_bit_cast(unsigned short, (_Float16)(8.0f * d)) | 0x8000u;
+    uint32_t *o = dst + blk * 5;
+    o[0] = sc | (mn << 16);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int n = 0; n < 8; ++n) {
+            const float t = v[8 * w + n] * id + 8.0f;
+            int q = (int)roundf(t);
+            q = q < 0 ? 0 : (q > 15 ? 15 : q);
+            word |= (uint32_t)q << (4 * n);
+        }
+        o[1 + w] = word;
+    }
+}
+
+__global__ void k_quantize_q8(const uint16_t *__restrict__ src, uint32_t *__restrict__ dst, uint64_t nblk) {
+    #pragma clang fp contract(off)
+    const uint64_t blk = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (blk >= nblk) return;
+    const uint16_t *s = src + blk * 32;
+    float v[32], amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        v[i] = bf16_bits_to_f32(s[i]);
+        amax = fmaxf(amax, fabsf(v[i]));
+    }
+    const float d = amax / 127.0f;
+    const float id = amax > 0.0f ? 127.0f / amax : 0.0f;
+    uint32_t *o = dst + blk * 9;
+    o[0] = __builtin_bit_cast(uint32_t, d);
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            int q = (int)roundf(v[4 * w + j] * id);
+            q = q < -128 ? -128 : (q > 127 ? 127 : q);
+            word |= ((uint32_t)q & 0xffu) << (8 * j);
+        }
+        o[1 + w] = word;
+    }
+}
+
+__global__ void k_embed(const uint16_t *__restrict__ table, const uint32_t *__restrict__ tokens, uint32_t n,
+                        uint32_t H, float scale, float *__restrict__ x) {
+    const uint32_t t = blockIdx.y;
+    if (t >= n) return;
+    const uint16_t *row = table + (size_t)tokens[t] * H;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < H; i += gridDim.x * blockDim.x)
+        x[(size_t)t * H + i] = bf16_bits_to_f32(row[i]) * scale;
+}
+
+__global__ void k_to_bf16_bits(const float *__restrict__ src, uint16_t *__restrict__ dst, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) {
+        const uint32_t u = __builtin_bit_cast(uint32_t, src[i]);
+        dst[i] = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+    }
+}
+
+int launch_embed(hipStream_t st, const uint16_t *table, const uint32_t *tokens, uint32_t n, uint32_t H, float scale,
+                 float *x) {
+    dim3 grid((H + 255) / 256, n);
+    k_embed<<<grid, 256, 0, st>>>(table, tokens, n, H, scale, x);
+    return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
+}
+
+int launch_quantize(hipStream_t st, int q8, const uint16_t *src, uint32_t *dst, uint64_t nblk) {
+    if (!nblk) return CHN_OK;
+    if (q8) k_quantize_q8<<<(unsigned)((nblk + 255) / 256), 256, 0, st>>>(src, dst, nblk);
+    else k_quantize_q4<<<(unsigned)((nblk + 255) / 256), 256, 0, st>>>(src, dst, nblk);
+    return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
+}
+
+}  // namespace chn
+
+using namespace chn;
+
+extern "C" int chn_gemv_q8(chn_ctx *ctx, const uint32_t *W, const float *x, float *y, uint32_t M, uint32_t K) {
+    if (!ctx) return CHN_E_INVALID;
+    CHN_REQUIRE(ctx, W && x && y, "NULL argument");
+    CHN_REQUIRE(ctx, K % 128 == 0 && K > 0 && K <= 4096, "K=%u: the Q8 matvec needs K %% 128 == 0, K <= 4096", K);
+    CHN_REQUIRE(ctx, aligned(W, 16) && aligned(x, 16), "W and x must be 16-byte aligned");
+    if (!M) return CHN_OK;
+    int rc = ensure_workspace(ctx, xbytes_bytes(K / 32));
+    if (rc) return rc;
+    launch_gemv_q8(ctx->stream, W, x, y, M, K / 32, (uint32_t *)ctx->ws);
+    CHN_LAUNCHED(ctx, "k_q8mv");
+    return CHN_OK;
+}
+
+extern "C" int chn_topk64(chn_ctx *ctx, const float *logits, uint32_t V, uint32_t *ids, float *vals) {
+    if (!ctx) return CHN_E_INVALID;
+    CHN_REQUIRE(ctx, logits && ids && vals, "NULL argument");
+    CHN_REQUIRE(ctx, V > 0 && V <= 262144, "V=%u must be in 1..262144", V);
+    int rc = ensure_workspace(ctx, topk_ws_bytes(V));
+    if (rc) return rc;
+    launch_topk64(ctx->stream, logits, V, ids, vals, (uint64_t *)ctx->ws);
+    CHN_LAUNCHED(ctx, "k_topk");
+    return CHN_OK;
+}
+
+extern "C" int chn_quantize_q4(chn_ctx *ctx, const uint16_t *src_bf16, uint32_t *dst, uint32_t rows, uint32_t cols) {
+    if (!ctx) return CHN_E_INVALID;
+    CHN_REQUIRE(ctx, src_bf16 && dst, "NULL argument");
+    CHN_REQUIRE(ctx, cols % 32 == 0, "cols=%u must be a multiple of 32", cols);
+    const uint64_t nblk = (uint64_t)rows * (cols / 32);
+    if (!nblk) return CHN_OK;
+    k_quantize_q4<<<(unsigned)((nblk + 255) / 256), 256, 0, ctx->stream>>>(src_bf16, dst, nblk);
+    CHN_LAUNCHED(ctx, "k_quantize_q4");
+    return CHN_OK;
+}
+
+extern "C" int chn_quantize_q8(chn_ctx *ctx, const uint16_t *src_bf16, uint32_t *dst, uint32_t rows, uint32_t cols) {
+    if (!ctx) return CHN_E_INVALID;
+    CHN_REQUIRE(ctx, src_bf16 && dst, "NULL argument");
+    CHN_REQUIRE(ctx, cols % 32 == 0, "cols=%u must be a multiple of 32", cols);
+    const uint64_t nblk = (uint64_t)rows * (cols / 32);
+    if (!nblk) return CHN_OK;
+    k_quantize_q8<<<(unsigned)((nblk + 255) / 256), 256, 0, ctx->stream>>>(src_bf16, dst, nblk);
+    CHN_LAUNCHED(ctx, "k_quantize_q8");
+    return CHN_OK;
+}
+
+extern "C" int chn_to_bf16_bits(chn_ctx *ctx, const float *src, uint16_t *dst, size_t n) {
+    if (!ctx) return CHN_E_INVALID;
+    CHN_REQUIRE(ctx, (src && dst) || !n, "NULL argument");
+    if (!n) return CHN_OK;
+    size_t g = (n + 255) / 256;
+    if (g > 65536) g = 65536;
+    k_to_bf16_bits<<<(unsigned)g, 256, 0, ctx->stream>>>(src, dst, n);
+    CHN_LAUNCHED(ctx, "k_to_bf16_bits");
+    return CHN_OK;
+}

@@ -534,8 +534,8 @@ static int launch_generic(chn_ctx *ctx, int mode, const GenericArgs &a) {
 }
 
 
-// x (fp32, K) -> digit planes in the context workspace, then the matvec.
-int launch_matvec(chn_ctx *ctx, int mode, MatvecArgs a, const float *x) {
+// x (fp32, K) -> digit planes in xp_ws (xplanes_bytes(K/32)), then the matvec.
+int launch_matvec(chn_ctx *ctx, int mode, MatvecArgs a, const float *x, uint32_t *xp_ws) {
     const uint32_t nb = a.nb;
     const bool fast = nb % 4 == 0 && nb <= 512 && aligned(a.W0, 16) && (!a.W1 || aligned(a.W1, 16)) &&
                       (!a.W2 || aligned(a.W2, 16));
@@ -543,9 +543,7 @@ int launch_matvec(chn_ctx *ctx, int mode, MatvecArgs a, const float *x) {
         GenericArgs g{a.W0, a.W1, a.W2, a.y0, a.y1, a.y2, x, a.M, a.seg1, a.seg2, nb};
         return launch_generic(ctx, mode, g);
     }
-    int rc = ensure_workspace(ctx, xplanes_bytes(nb));
-    if (rc) return rc;
-    uint32_t *xp = (uint32_t *)ctx->ws;
+    uint32_t *xp = xp_ws;
     k_xplanes<<<(4 * nb + 255) / 256, 256, 0, ctx->stream>>>(x, xp, nb);
     CHN_LAUNCHED(ctx, "k_xplanes");
     a.xp = xp;
@@ -556,6 +554,23 @@ int launch_matvec(chn_ctx *ctx, int mode, MatvecArgs a, const float *x) {
     if (!ok) return set_err(ctx, CHN_E_UNSUPPORTED, "no matvec tile for M=%u nb=%u", a.M, nb);
     CHN_LAUNCHED(ctx, "k_q4mv");
     return CHN_OK;
+}
+
+size_t mv_ws_bytes(uint32_t K) { return xplanes_bytes(K / 32); }
+
+int mv_gemv(chn_ctx *ctx, const uint32_t *W, const float *x, float *y, uint32_t M, uint32_t K, uint32_t *ws) {
+    MatvecArgs a{W, nullptr, nullptr, y, nullptr, nullptr, nullptr, M, M, M, K / 32};
+    return launch_matvec(ctx, MV_GEMV, a, x, ws);
+}
+int mv_qkv(chn_ctx *ctx, const uint32_t *Wq, const uint32_t *Wk, const uint32_t *Wv, const float *x, float *q,
+           float *k, float *v, uint32_t q_dim, uint32_t kv_dim, uint32_t K, uint32_t *ws) {
+    MatvecArgs a{Wq, Wk, Wv, q, k, v, nullptr, q_dim + 2 * kv_dim, q_dim, q_dim + kv_dim, K / 32};
+    return launch_matvec(ctx, MV_QKV, a, x, ws);
+}
+int mv_mlp(chn_ctx *ctx, const uint32_t *Wg, const uint32_t *Wu, const float *x, float *act, uint32_t M, uint32_t K,
+           uint32_t *ws) {
+    MatvecArgs a{Wg, Wu, nullptr, act, nullptr, nullptr, nullptr, M, M, M, K / 32};
+    return launch_matvec(ctx, MV_MLP, a, x, ws);
 }
 
 static int check_common(chn_ctx *ctx, const float *x, uint32_t K) {
@@ -576,7 +591,9 @@ extern "C" int chn_gemv_q4(chn_ctx *ctx, const uint32_t *W, const float *x, floa
     CHN_REQUIRE(ctx, W && y && aligned(W, 4), "W/y must be non-NULL, W 4-byte aligned");
     if (M == 0) return CHN_OK;
     MatvecArgs a{W, nullptr, nullptr, y, nullptr, nullptr, nullptr, M, M, M, K / 32};
-    return launch_matvec(ctx, MV_GEMV, a, x);
+    rc = ensure_workspace(ctx, xplanes_bytes(K / 32));
+    if (rc) return rc;
+    return launch_matvec(ctx, MV_GEMV, a, x, (uint32_t *)ctx->ws);
 }
 
 extern "C" int chn_fused_qkv_q4(chn_ctx *ctx, const uint32_t *Wq, const uint32_t *Wk,
@@ -591,7 +608,9 @@ extern "C" int chn_fused_qkv_q4(chn_ctx *ctx, const uint32_t *Wq, const uint32_t
     CHN_REQUIRE(ctx, M < (1ull << 31), "q_dim + 2*kv_dim too large");
     if (M == 0) return CHN_OK;
     MatvecArgs a{Wq, Wk, Wv, q, k, v, nullptr, (uint32_t)M, q_dim, q_dim + kv_dim, K / 32};
-    return launch_matvec(ctx, MV_QKV, a, x);
+    rc = ensure_workspace(ctx, xplanes_bytes(K / 32));
+    if (rc) return rc;
+    return launch_matvec(ctx, MV_QKV, a, x, (uint32_t *)ctx->ws);
 }
 
 extern "C" int chn_fused_mlp_q4(chn_ctx *ctx, const uint32_t *Wg, const uint32_t *Wu,
@@ -602,5 +621,7 @@ extern "C" int chn_fused_mlp_q4(chn_ctx *ctx, const uint32_t *Wg, const uint32_t
     CHN_REQUIRE(ctx, Wg && Wu && act && aligned(Wg, 4) && aligned(Wu, 4), "NULL/misaligned argument");
     if (M == 0) return CHN_OK;
     MatvecArgs a{Wg, Wu, nullptr, act, nullptr, nullptr, nullptr, M, M, M, K / 32};
-    return launch_matvec(ctx, MV_MLP, a, x);
+    rc = ensure_workspace(ctx, xplanes_bytes(K / 32));
+    if (rc) return rc;
+    return launch_matvec(ctx, MV_MLP, a, x, (uint32_t *)ctx->ws);
 }

@@ -1,0 +1,599 @@
+// Model-level host layer: the MI355X counterpart of GpuModelContext
+// (src/gpu/model_gpu.zig:30-216), the decode graph (src/gpu/model_dispatch.zig:
+// 10-153) and the batched prefill (src/gpu/batch_dispatch.zig:27-172).
+//
+// * Weights live in HBM as Q4 (attention and MLP matrices) and Q8 (tied
+//   embedding for the logits); norms as fp32.  They are quantized on the
+//   device from bf16 with bit-exact restatements of quantizeRowQ4_0 /
+//   quantizeRowQ8_0, or generated in place for synthetic models.
+// * One decode token is recorded once as a HIP graph (the counterpart of the
+//   pre-recorded Vulkan command buffers) and replayed per token; the
+//   per-token inputs (x, slot lists, {clock, slot_idx, S_global,
+//   S_sliding}) are copied into fixed device buffers before each replay and
+//   read by the kernels from device memory.
+// * Prefill runs layer by layer on the stream, synchronizing every four
+//   layers and calling the progress callback, as the reference does.
+#include "chn_internal.h"
+
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+struct chn_model {
+    chn_ctx *ctx = nullptr;
+    chn_model_config cfg{};
+    struct Layer {
+        uint32_t *Wq, *Wk, *Wv, *Wo, *Wg, *Wu, *Wd;
+        float *in_norm, *q_norm, *k_norm, *post_attn, *pre_ffn, *post_ffn;
+        float scalar;
+        bool has_post_attn, has_post_ffn, full;
+        float *kc, *vc;
+    };
+    std::vector<Layer> L;
+    uint32_t *embed_q8 = nullptr;
+    uint16_t *embed_bf16 = nullptr;   // device copy (synthetic models; optional otherwise)
+    float *final_norm = nullptr;
+    // decode buffers
+    float *x, *normed, *q, *k, *v, *attn, *mlp_out, *act, *logits;
+    uint32_t *topk_ids;
+    float *topk_vals;
+    uint32_t *slots;   // [8192]: global list at 0, sliding list at 4096
+    uint32_t *step;    // {clock, slot_idx, S_global, S_sliding}
+    uint32_t *tok;     // one token id for chn_decode_token
+    uint32_t *mv_ws;
+    float *attn_ws;
+    uint64_t *topk_ws;
+    // prefill buffers
+    uint32_t max_tok = 0;
+    float *px, *pn, *pq, *pk, *pv, *pattn, *pmlp, *pact;
+    __bf16 *pxb;
+    uint32_t *pslots, *ptok;
+    // pinned staging
+    float *h_x = nullptr;
+    uint32_t *h_slots = nullptr, *h_step = nullptr, *h_ids = nullptr;
+    float *h_vals = nullptr;
+    hipGraphExec_t exec[2] = {nullptr, nullptr};   // [0] without logits, [1] with
+    std::vector<void *> allocs;
+};
+
+namespace chn {
+
+static constexpr uint32_t kSlotsMax = 4096;
+
+static int m_alloc(chn_model *m, size_t bytes, void **p) {
+    hipError_t e = hipMalloc(p, bytes ? bytes : 256);
+    if (e != hipSuccess) return hip_fail(m->ctx, e, "hipMalloc (model)");
+    m->allocs.push_back(*p);
+    return CHN_OK;
+}
+#define M_ALLOC(ptr, bytes)                                     \
+    do {                                                        \
+        void *p_;                                               \
+        int rc_ = m_alloc(m, (bytes), &p_);                     \
+        if (rc_) return rc_;                                    \
+        ptr = (decltype(ptr))p_;                                \
+    } while (0)
+
+static size_t q4b(uint32_t rows, uint32_t K) { return (size_t)rows * (K / 32) * 20; }
+
+static int validate_config(chn_ctx *ctx, const chn_model_config &c) {
+    CHN_REQUIRE(ctx, c.num_layers >= 1 && c.num_layers <= 64, "num_layers %u must be 1..64", c.num_layers);
+    CHN_REQUIRE(ctx, c.hidden_size % 128 == 0 && c.hidden_size <= 16384, "hidden_size %u must be a multiple of 128",
+                c.hidden_size);
+    CHN_REQUIRE(ctx, c.intermediate_size % 128 == 0 && c.intermediate_size <= 16384,
+                "intermediate_size %u must be a multiple of 128", c.intermediate_size);
+    CHN_REQUIRE(ctx, c.head_dim == 256 || c.head_dim == 512, "head_dim %u must be 256 or 512", c.head_dim);
+    CHN_REQUIRE(ctx, c.num_heads > 0 && c.num_kv_heads > 0 && c.num_heads % c.num_kv_heads == 0,
+                "num_heads %u must be a multiple of num_kv_heads %u", c.num_heads, c.num_kv_heads);
+    CHN_REQUIRE(ctx, (c.num_heads * c.head_dim) % 128 == 0, "q_dim must be a multiple of 128");
+    CHN_REQUIRE(ctx, c.rotary_dim <= c.head_dim && c.rotary_dim % 2 == 0, "rotary_dim %u invalid", c.rotary_dim);
+    CHN_REQUIRE(ctx, c.vocab_size >= 64 && c.vocab_size <= 262144, "vocab_size %u must be 64..262144", c.vocab_size);
+    CHN_REQUIRE(ctx, c.hidden_size <= 4096, "hidden_size %u: the Q8 logits matvec needs K <= 4096", c.hidden_size);
+    CHN_REQUIRE(ctx, c.max_prefill_tokens >= 1 && c.max_prefill_tokens <= 4096, "max_prefill_tokens %u invalid",
+                c.max_prefill_tokens);
+    return CHN_OK;
+}
+
+// activation, KV and workspace buffers shared by both constructors
+static int alloc_runtime(chn_model *m) {
+    const chn_model_config &c = m->cfg;
+    const uint32_t H = c.hidden_size, I = c.intermediate_size, V = c.vocab_size;
+    const uint32_t qd = c.num_heads * c.head_dim, kvd = c.num_kv_heads * c.head_dim;
+    for (auto &l : m->L) {
+        M_ALLOC(l.kc, (size_t)kSlotsMax * kvd * 4);
+        M_ALLOC(l.vc, (size_t)kSlotsMax * kvd * 4);
+    }
+    M_ALLOC(m->x, H * 4);
+    M_ALLOC(m->normed, H * 4);
+    M_ALLOC(m->q, qd * 4);
+    M_ALLOC(m->k, kvd * 4);
+    M_ALLOC(m->v, kvd * 4);
+    M_ALLOC(m->attn, qd * 4);
+    M_ALLOC(m->mlp_out, H * 4);
+    M_ALLOC(m->act, I * 4);
+    M_ALLOC(m->logits, (size_t)V * 4);
+    M_ALLOC(m->topk_ids, 64 * 4);
+    M_ALLOC(m->topk_vals, 64 * 4);
+    M_ALLOC(m->slots, 2 * kSlotsMax * 4);
+    M_ALLOC(m->step, 64);
+    M_ALLOC(m->tok, 64);
+    const uint32_t kmax = H > I ? (H > qd ? H : qd) : (I > qd ? I : qd);
+    size_t mvb = mv_ws_bytes(kmax);
+    if (xbytes_bytes(H / 32) > mvb) mvb = xbytes_bytes(H / 32);
+    M_ALLOC(m->mv_ws, mvb);
+    M_ALLOC(m->attn_ws, attn_ws_bytes(c.num_heads, c.head_dim, kSlotsMax));
+    M_ALLOC(m->topk_ws, topk_ws_bytes(V));
+    const uint32_t T = c.max_prefill_tokens;
+    m->max_tok = T;
+    M_ALLOC(m->px, (size_t)T * H * 4);
+    M_ALLOC(m->pn, (size_t)T * H * 4);
+    M_ALLOC(m->pq, (size_t)T * qd * 4);
+    M_ALLOC(m->pk, (size_t)T * kvd * 4);
+    M_ALLOC(m->pv, (size_t)T * kvd * 4);
+    M_ALLOC(m->pattn, (size_t)T * qd * 4);
+    M_ALLOC(m->pmlp, (size_t)T * H * 4);
+    M_ALLOC(m->pact, (size_t)T * I * 4);
+    M_ALLOC(m->pxb, (size_t)T * (I > H ? (I > qd ? I : qd) : (H > qd ? H : qd)) * 2);
+    M_ALLOC(m->pslots, (size_t)(kSlotsMax + T) * 4);
+    M_ALLOC(m->ptok, (size_t)T * 4);
+    hipError_t e = hipHostMalloc((void **)&m->h_x, H * 4);
+    if (e == hipSuccess) e = hipHostMalloc((void **)&m->h_slots, 2 * kSlotsMax * 4);
+    if (e == hipSuccess) e = hipHostMalloc((void **)&m->h_step, 64);
+    if (e == hipSuccess) e = hipHostMalloc((void **)&m->h_ids, 64 * 4);
+    if (e == hipSuccess) e = hipHostMalloc((void **)&m->h_vals, 64 * 4);
+    if (e != hipSuccess) return hip_fail(m->ctx, e, "hipHostMalloc");
+    // zero KV caches and slot buffers with a kernel (no memset nodes anywhere)
+    for (auto &l : m->L) {
+        int rc = chn_fill_u32(m->ctx, l.kc, 0, (size_t)kSlotsMax * kvd);
+        if (!rc) rc = chn_fill_u32(m->ctx, l.vc, 0, (size_t)kSlotsMax * kvd);
+        if (rc) return rc;
+    }
+    int rc = chn_fill_u32(m->ctx, m->slots, 0, 2 * kSlotsMax);
+    if (!rc) rc = chn_fill_u32(m->ctx, m->step, 0, 16);
+    if (!rc) rc = chn_fill_u32(m->ctx, m->topk_ids, 0, 64);
+    return rc;
+}
+
+// ---- the decode sequence (recordLayerDirect / recordForwardGraph,
+// src/gpu/model_dispatch.zig:10-45,103-126)
+static int record_decode(chn_model *m, bool with_logits) {
+    chn_ctx *ctx = m->ctx;
+    hipStream_t s = ctx->stream;
+    const chn_model_config &c = m->cfg;
+    const uint32_t H = c.hidden_size, I = c.intermediate_size;
+    const uint32_t D = c.head_dim, nq = c.num_heads, nkv = c.num_kv_heads;
+    const uint32_t qd = nq * D, kvd = nkv * D, gqa = nq / nkv;
+    const float eps = c.rms_norm_eps;
+    int rc;
+#define R_(call)                 \
+    do {                         \
+        rc = (call);             \
+        if (rc) return rc;       \
+    } while (0)
+    for (uint32_t i = 0; i < c.num_layers; ++i) {
+        const auto &l = m->L[i];
+        const float theta = l.full ? c.rope_theta_full : c.rope_theta;
+        if (i == 0) R_(launch_rmsnorm(s, m->x, nullptr, l.in_norm, m->normed, H, 1, eps, 1.0f, false));
+        R_(mv_qkv(ctx, l.Wq, l.Wk, l.Wv, m->normed, m->q, m->k, m->v, qd, kvd, H, m->mv_ws));
+        R_(launch_qkv_rope(s, m->q, m->k, m->v, l.q_norm, l.k_norm, m->q, l.kc, l.vc, m->step, nq, nkv, D,
+                           c.rotary_dim, (int)c.k_eq_v, theta, eps));
+        R_(launch_decode_attn(ctx, m->q, l.kc, l.vc, m->slots + (l.full ? 0 : kSlotsMax), m->step + (l.full ? 2 : 3),
+                              kSlotsMax, nq, D, kvd, gqa, 1.0f, m->attn, m->attn_ws));
+        R_(mv_gemv(ctx, l.Wo, m->attn, m->mlp_out, H, qd, m->mv_ws));
+        if (l.has_post_attn) R_(launch_rmsnorm(s, m->mlp_out, nullptr, l.post_attn, m->mlp_out, H, 1, eps, 1.0f, false));
+        R_(launch_rmsnorm(s, m->x, m->mlp_out, l.pre_ffn, m->normed, H, 1, eps, 1.0f, true));
+        R_(mv_mlp(ctx, l.Wg, l.Wu, m->normed, m->act, I, H, m->mv_ws));
+        R_(mv_gemv(ctx, l.Wd, m->act, m->mlp_out, H, I, m->mv_ws));
+        if (l.has_post_ffn) R_(launch_rmsnorm(s, m->mlp_out, nullptr, l.post_ffn, m->mlp_out, H, 1, eps, 1.0f, false));
+        const float *next_norm = (i + 1 < c.num_layers) ? m->L[i + 1].in_norm : m->final_norm;
+        R_(launch_rmsnorm(s, m->x, m->mlp_out, next_norm, m->normed, H, 1, eps, l.scalar, true));
+    }
+    if (with_logits) {
+        R_(launch_gemv_q8(s, m->embed_q8, m->normed, m->logits, c.vocab_size, H / 32, m->mv_ws));
+        R_(launch_topk64(s, m->logits, c.vocab_size, m->topk_ids, m->topk_vals, m->topk_ws));
+    }
+#undef R_
+    return CHN_OK;
+}
+
+static int build_graphs(chn_model *m) {
+    hipStream_t s = m->ctx->stream;
+    for (int wl = 0; wl < 2; ++wl) {
+        CHN_HIP(m->ctx, hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+        int rc = record_decode(m, wl == 1);
+        hipGraph_t g = nullptr;
+        hipError_t e = hipStreamEndCapture(s, &g);
+        if (rc) {
+            if (g) (void)hipGraphDestroy(g);
+            return rc;
+        }
+        if (e != hipSuccess) return hip_fail(m->ctx, e, "hipStreamEndCapture");
+        e = hipGraphInstantiate(&m->exec[wl], g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (e != hipSuccess) return hip_fail(m->ctx, e, "hipGraphInstantiate");
+    }
+    return CHN_OK;
+}
+
+static void free_model(chn_model *m) {
+    if (!m) return;
+    if (m->ctx) (void)hipStreamSynchronize(m->ctx->stream);
+    for (int i = 0; i < 2; ++i)
+        if (m->exec[i]) (void)hipGraphExecDestroy(m->exec[i]);
+    for (void *p : m->allocs) (void)hipFree(p);
+    if (m->h_x) (void)hipHostFree(m->h_x);
+    if (m->h_slots) (void)hipHostFree(m->h_slots);
+    if (m->h_step) (void)hipHostFree(m->h_step);
+    if (m->h_ids) (void)hipHostFree(m->h_ids);
+    if (m->h_vals) (void)hipHostFree(m->h_vals);
+    delete m;
+}
+
+// bf16 (host) -> device quantized copy; `tmp` holds at least rows*cols bf16
+static int ingest_q(chn_model *m, const uint16_t *src, uint32_t rows, uint32_t cols, int q8, uint32_t **dst,
+                    uint16_t *tmp) {
+    const size_t nblk = (size_t)rows * (cols / 32);
+    M_ALLOC(*dst, nblk * (q8 ? 36 : 20));
+    CHN_HIP(m->ctx, hipMemcpyAsync(tmp, src, (size_t)rows * cols * 2, hipMemcpyHostToDevice, m->ctx->stream));
+    int rc = launch_quantize(m->ctx->stream, q8, tmp, *dst, nblk);
+    if (rc) return hip_fail(m->ctx, hipGetLastError(), "quantize");
+    CHN_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    return CHN_OK;
+}
+
+// bf16 norm weights -> fp32; missing norms -> 1.0 (createNormBuffer,
+// src/gpu/model_gpu.zig:57-66)
+static int ingest_norm(chn_model *m, const uint16_t *src, uint32_t n, float **dst) {
+    M_ALLOC(*dst, n * 4);
+    std::vector<float> h(n, 1.0f);
+    if (src)
+        for (uint32_t i = 0; i < n; ++i) {
+            uint32_t u = (uint32_t)src[i] << 16;
+            std::memcpy(&h[i], &u, 4);
+        }
+    CHN_HIP(m->ctx, hipMemcpy(*dst, h.data(), n * 4, hipMemcpyHostToDevice));
+    return CHN_OK;
+}
+
+static int fill_ones(chn_model *m, uint32_t n, float **dst) {
+    M_ALLOC(*dst, n * 4);
+    return chn_fill_u32(m->ctx, *dst, 0x3F800000u, n);
+}
+
+}  // namespace chn
+
+using namespace chn;
+
+extern "C" int chn_model_create(chn_ctx *ctx, const chn_model_config *cfg, const chn_layer_weights *layers,
+                                const uint16_t *embed_bf16, const uint16_t *final_norm_bf16, chn_model **out) {
+    if (!ctx || !cfg || !layers || !embed_bf16 || !out) return ctx ? set_err(ctx, CHN_E_INVALID, "NULL argument") : CHN_E_INVALID;
+    *out = nullptr;
+    int rc = validate_config(ctx, *cfg);
+    if (rc) return rc;
+    chn_model *m = new chn_model();
+    m->ctx = ctx;
+    m->cfg = *cfg;
+    const uint32_t H = cfg->hidden_size, I = cfg->intermediate_size;
+    const uint32_t D = cfg->head_dim, qd = cfg->num_heads * D, kvd = cfg->num_kv_heads * D;
+    size_t tmp_elems = (size_t)cfg->vocab_size * H;
+    const size_t big = (size_t)I * H > (size_t)qd * H ? (size_t)I * H : (size_t)qd * H;
+    if (big > tmp_elems) tmp_elems = big;
+    uint16_t *tmp = nullptr;
+    hipError_t e = hipMalloc(&tmp, tmp_elems * 2);
+    if (e != hipSuccess) {
+        free_model(m);
+        return hip_fail(ctx, e, "hipMalloc (ingest staging)");
+    }
+#define C_(call)                 \
+    do {                         \
+        rc = (call);             \
+        if (rc) goto fail;       \
+    } while (0)
+    m->L.resize(cfg->num_layers);
+    for (uint32_t i = 0; i < cfg->num_layers; ++i) {
+        const chn_layer_weights &w = layers[i];
+        auto &l = m->L[i];
+        if (!w.q_proj || !w.k_proj || !w.o_proj || !w.gate_proj || !w.up_proj || !w.down_proj) {
+            rc = set_err(ctx, CHN_E_INVALID, "layer %u: missing projection weights", i);
+            goto fail;
+        }
+        C_(ingest_q(m, w.q_proj, qd, H, 0, &l.Wq, tmp));
+        C_(ingest_q(m, w.k_proj, kvd, H, 0, &l.Wk, tmp));
+        // v_proj absent -> k_proj (src/gpu/model_gpu.zig:123)
+        C_(ingest_q(m, w.v_proj ? w.v_proj : w.k_proj, kvd, H, 0, &l.Wv, tmp));
+        C_(ingest_q(m, w.o_proj, H, qd, 0, &l.Wo, tmp));
+        C_(ingest_q(m, w.gate_proj, I, H, 0, &l.Wg, tmp));
+        C_(ingest_q(m, w.up_proj, I, H, 0, &l.Wu, tmp));
+        C_(ingest_q(m, w.down_proj, H, I, 0, &l.Wd, tmp));
+        C_(ingest_norm(m, w.input_layernorm, H, &l.in_norm));
+        C_(ingest_norm(m, w.q_norm, D, &l.q_norm));
+        C_(ingest_norm(m, w.k_norm, D, &l.k_norm));
+        C_(ingest_norm(m, w.post_attention_layernorm, H, &l.post_attn));
+        C_(ingest_norm(m, w.pre_feedforward_layernorm, H, &l.pre_ffn));
+        C_(ingest_norm(m, w.post_feedforward_layernorm, H, &l.post_ffn));
+        l.has_post_attn = w.post_attention_layernorm != nullptr;
+        l.has_post_ffn = w.post_feedforward_layernorm != nullptr;
+        l.scalar = w.has_layer_scalar ? w.layer_scalar : 1.0f;
+        l.full = cfg->layer_full[i] != 0;
+    }
+    C_(ingest_q(m, embed_bf16, cfg->vocab_size, H, 1, &m->embed_q8, tmp));
+    C_(ingest_norm(m, final_norm_bf16, H, &m->final_norm));
+    C_(alloc_runtime(m));
+    C_(build_graphs(m));
+#undef C_
+    (void)hipFree(tmp);
+    *out = m;
+    return CHN_OK;
+fail:
+    (void)hipFree(tmp);
+    free_model(m);
+    return rc;
+}
+
+extern "C" int chn_model_create_synthetic(chn_ctx *ctx, const chn_model_config *cfg, uint64_t seed,
+                                          chn_model **out) {
+    if (!ctx || !cfg || !out) return ctx ? set_err(ctx, CHN_E_INVALID, "NULL argument") : CHN_E_INVALID;
+    *out = nullptr;
+    int rc = validate_config(ctx, *cfg);
+    if (rc) return rc;
+    chn_model *m = new chn_model();
+    m->ctx = ctx;
+    m->cfg = *cfg;
+    const uint32_t H = cfg->hidden_size, I = cfg->intermediate_size, V = cfg->vocab_size;
+    const uint32_t D = cfg->head_dim, qd = cfg->num_heads * D, kvd = cfg->num_kv_heads * D;
+    const float smin = 0.005f, smax = 0.02f;
+#define C_(call)                 \
+    do {                         \
+        rc = (call);             \
+        if (rc) goto fail;       \
+    } while (0)
+    m->L.resize(cfg->num_layers);
+    for (uint32_t i = 0; i < cfg->num_layers; ++i) {
+        auto &l = m->L[i];
+        const uint64_t ls = seed + 64ull * (i + 1);
+        struct {
+            uint32_t **w;
+            uint32_t rows, cols;
+        } mats[7] = {{&l.Wq, qd, H}, {&l.Wk, kvd, H}, {&l.Wv, kvd, H}, {&l.Wo, H, qd},
+                     {&l.Wg, I, H},  {&l.Wu, I, H},   {&l.Wd, H, I}};
+        for (int j = 0; j < 7; ++j) {
+            M_ALLOC(*mats[j].w, q4b(mats[j].rows, mats[j].cols));
+            C_(chn_synth_q4(ctx, *mats[j].w, mats[j].rows, mats[j].cols, ls + j, smin, smax));
+        }
+        C_(fill_ones(m, H, &l.in_norm));
+        C_(fill_ones(m, D, &l.q_norm));
+        C_(fill_ones(m, D, &l.k_norm));
+        C_(fill_ones(m, H, &l.post_attn));
+        C_(fill_ones(m, H, &l.pre_ffn));
+        C_(fill_ones(m, H, &l.post_ffn));
+        l.has_post_attn = l.has_post_ffn = true;
+        l.scalar = 1.0f;
+        l.full = cfg->layer_full[i] != 0;
+    }
+    // tied embedding: bf16 ~ N(0, 0.02) (kept on device for the input
+    // gather), Q8-quantized for the logits exactly as quantizeRowQ8_0 would
+    {
+        const size_t n = (size_t)V * H;
+        float *tmpf = nullptr;
+        hipError_t e = hipMalloc(&tmpf, n * 4);
+        if (e != hipSuccess) {
+            rc = hip_fail(ctx, e, "hipMalloc (embedding staging)");
+            goto fail;
+        }
+        M_ALLOC(m->embed_bf16, n * 2);
+        rc = chn_synth_normal(ctx, tmpf, n, seed + 7, 0.02f);
+        if (!rc) rc = chn_to_bf16_bits(ctx, tmpf, m->embed_bf16, n);
+        if (!rc) rc = chn_sync(ctx);
+        (void)hipFree(tmpf);
+        if (rc) goto fail;
+        M_ALLOC(m->embed_q8, (size_t)V * (H / 32) * 36);
+        if (launch_quantize(ctx->stream, 1, m->embed_bf16, m->embed_q8, (uint64_t)V * (H / 32))) {
+            rc = hip_fail(ctx, hipGetLastError(), "quantize embedding");
+            goto fail;
+        }
+    }
+    C_(fill_ones(m, H, &m->final_norm));
+    C_(alloc_runtime(m));
+    C_(chn_sync(ctx));
+    C_(build_graphs(m));
+#undef C_
+    *out = m;
+    return CHN_OK;
+fail:
+    free_model(m);
+    return rc;
+}
+
+extern "C" void chn_model_destroy(chn_model *m) { free_model(m); }
+
+extern "C" int chn_model_embedding_bf16(chn_model *m, const uint16_t **table) {
+    if (!m || !table) return CHN_E_INVALID;
+    *table = m->embed_bf16;
+    return CHN_OK;
+}
+
+extern "C" int chn_model_get_config(const chn_model *m, chn_model_config *cfg) {
+    if (!m || !cfg) return CHN_E_INVALID;
+    *cfg = m->cfg;
+    return CHN_OK;
+}
+
+static int decode_run(chn_model *m, uint32_t clock, uint32_t slot_idx, const uint32_t *active, uint32_t n_active,
+                      const uint32_t *sliding, uint32_t n_sliding, uint32_t *topk_ids, float *topk_vals,
+                      uint32_t *token_out, bool x_ready) {
+    chn_ctx *ctx = m->ctx;
+    hipStream_t s = ctx->stream;
+    CHN_REQUIRE(ctx, n_active <= kSlotsMax && n_sliding <= kSlotsMax, "slot lists longer than 4096");
+    CHN_REQUIRE(ctx, slot_idx < kSlotsMax, "slot_idx %u out of range", slot_idx);
+    CHN_REQUIRE(ctx, (active || !n_active) && (sliding || !n_sliding), "NULL slot list");
+    for (uint32_t i = 0; i < n_active; ++i) CHN_REQUIRE(ctx, active[i] < kSlotsMax, "active slot out of range");
+    for (uint32_t i = 0; i < n_sliding; ++i) CHN_REQUIRE(ctx, sliding[i] < kSlotsMax, "sliding slot out of range");
+    std::memcpy(m->h_slots, active, n_active * 4);
+    std::memcpy(m->h_slots + kSlotsMax, sliding, n_sliding * 4);
+    m->h_step[0] = clock;
+    m->h_step[1] = slot_idx;
+    m->h_step[2] = n_active;
+    m->h_step[3] = n_sliding;
+    if (!x_ready) CHN_HIP(ctx, hipMemcpyAsync(m->x, m->h_x, m->cfg.hidden_size * 4, hipMemcpyHostToDevice, s));
+    if (n_active) CHN_HIP(ctx, hipMemcpyAsync(m->slots, m->h_slots, n_active * 4, hipMemcpyHostToDevice, s));
+    if (n_sliding)
+        CHN_HIP(ctx, hipMemcpyAsync(m->slots + kSlotsMax, m->h_slots + kSlotsMax, n_sliding * 4,
+                                    hipMemcpyHostToDevice, s));
+    CHN_HIP(ctx, hipMemcpyAsync(m->step, m->h_step, 16, hipMemcpyHostToDevice, s));
+    const bool wl = topk_ids != nullptr;
+    CHN_HIP(ctx, hipGraphLaunch(m->exec[wl ? 1 : 0], s));
+    CHN_HIP(ctx, hipMemcpyAsync(m->h_ids, m->topk_ids, 64 * 4, hipMemcpyDeviceToHost, s));
+    CHN_HIP(ctx, hipMemcpyAsync(m->h_vals, m->topk_vals, 64 * 4, hipMemcpyDeviceToHost, s));
+    CHN_HIP(ctx, hipStreamSynchronize(s));
+    if (wl) {
+        std::memcpy(topk_ids, m->h_ids, 64 * 4);
+        if (topk_vals) std::memcpy(topk_vals, m->h_vals, 64 * 4);
+    }
+    if (token_out) *token_out = m->h_ids[0];
+    return CHN_OK;
+}
+
+extern "C" int chn_decode_step(chn_model *m, const float *x, uint32_t clock, uint32_t slot_idx,
+                               const uint32_t *active, uint32_t n_active, const uint32_t *sliding,
+                               uint32_t n_sliding, uint32_t *topk_ids, float *topk_vals, uint32_t *token_out) {
+    if (!m || !x) return m ? set_err(m->ctx, CHN_E_INVALID, "x is NULL") : CHN_E_INVALID;
+    std::memcpy(m->h_x, x, m->cfg.hidden_size * 4);
+    return decode_run(m, clock, slot_idx, active, n_active, sliding, n_sliding, topk_ids, topk_vals, token_out, false);
+}
+
+extern "C" int chn_decode_token(chn_model *m, uint32_t token, uint32_t clock, uint32_t slot_idx,
+                                const uint32_t *active, uint32_t n_active, const uint32_t *sliding,
+                                uint32_t n_sliding, uint32_t *topk_ids, float *topk_vals, uint32_t *token_out) {
+    if (!m) return CHN_E_INVALID;
+    chn_ctx *ctx = m->ctx;
+    CHN_REQUIRE(ctx, m->embed_bf16, "model has no device embedding table; use chn_decode_step");
+    CHN_REQUIRE(ctx, token < m->cfg.vocab_size, "token %u out of range", token);
+    m->h_step[8] = token;
+    CHN_HIP(ctx, hipMemcpyAsync(m->tok, m->h_step + 8, 4, hipMemcpyHostToDevice, ctx->stream));
+    const uint32_t H = m->cfg.hidden_size;
+    if (launch_embed(ctx->stream, m->embed_bf16, m->tok, 1, H, sqrtf((float)H), m->x))
+        return hip_fail(ctx, hipGetLastError(), "k_embed");
+    return decode_run(m, clock, slot_idx, active, n_active, sliding, n_sliding, topk_ids, topk_vals, token_out, true);
+}
+
+// gpuDispatchPrefillBatch (src/gpu/batch_dispatch.zig:27-172)
+extern "C" int chn_prefill(chn_model *m, const uint32_t *tokens, uint32_t n, const uint16_t *embed_bf16,
+                           const uint32_t *slots, uint32_t n_slots, uint32_t start_clock, uint32_t num_prev_slots,
+                           float *logits_out, uint32_t *topk_ids, float *topk_vals, chn_progress_fn progress,
+                           void *progress_ctx) {
+    if (!m) return CHN_E_INVALID;
+    chn_ctx *ctx = m->ctx;
+    hipStream_t s = ctx->stream;
+    const chn_model_config &c = m->cfg;
+    if (n == 0 || n > m->max_tok) return set_err(ctx, CHN_E_BATCH_TOO_LARGE, "batch of %u tokens (max %u)", n, m->max_tok);
+    CHN_REQUIRE(ctx, tokens && slots, "NULL tokens or slots");
+    CHN_REQUIRE(ctx, n_slots >= num_prev_slots + n && n_slots <= kSlotsMax + m->max_tok,
+                "slot list of %u entries must cover %u previous + %u new slots", n_slots, num_prev_slots, n);
+    CHN_REQUIRE(ctx, embed_bf16 || m->embed_bf16, "no embedding table");
+    for (uint32_t i = 0; i < n; ++i) CHN_REQUIRE(ctx, tokens[i] < c.vocab_size, "token %u out of range", tokens[i]);
+    for (uint32_t i = 0; i < n_slots; ++i) CHN_REQUIRE(ctx, slots[i] < kSlotsMax, "slot out of range");
+    const uint32_t H = c.hidden_size, I = c.intermediate_size;
+    const uint32_t D = c.head_dim, nq = c.num_heads, nkv = c.num_kv_heads;
+    const uint32_t qd = nq * D, kvd = nkv * D, gqa = nq / nkv;
+    const float eps = c.rms_norm_eps;
+    const float escale = sqrtf((float)H);
+
+    // embeddings: x = bf16(embed[tok]) * sqrt(H) (expandEmbeddings, :14-23)
+    if (embed_bf16) {
+        std::vector<float> hx((size_t)n * H);
+        for (uint32_t t = 0; t < n; ++t)
+            for (uint32_t i = 0; i < H; ++i) {
+                uint32_t u = (uint32_t)embed_bf16[(size_t)tokens[t] * H + i] << 16;
+                float f;
+                std::memcpy(&f, &u, 4);
+                hx[(size_t)t * H + i] = f * escale;
+            }
+        CHN_HIP(ctx, hipMemcpyAsync(m->px, hx.data(), hx.size() * 4, hipMemcpyHostToDevice, s));
+        CHN_HIP(ctx, hipStreamSynchronize(s));
+    } else {
+        CHN_HIP(ctx, hipMemcpyAsync(m->ptok, tokens, n * 4, hipMemcpyHostToDevice, s));
+        if (launch_embed(s, m->embed_bf16, m->ptok, n, H, escale, m->px)) return hip_fail(ctx, hipGetLastError(), "k_embed");
+        CHN_HIP(ctx, hipStreamSynchronize(s));
+    }
+    CHN_HIP(ctx, hipMemcpyAsync(m->pslots, slots, (size_t)n_slots * 4, hipMemcpyHostToDevice, s));
+
+    int rc;
+#define P_(call)                 \
+    do {                         \
+        rc = (call);             \
+        if (rc) return rc;       \
+    } while (0)
+    for (uint32_t i = 0; i < c.num_layers; ++i) {
+        const auto &l = m->L[i];
+        const float theta = l.full ? c.rope_theta_full : c.rope_theta;
+        if (i == 0) P_(launch_rmsnorm(s, m->px, nullptr, l.in_norm, m->pn, H, n, eps, 1.0f, false));
+        P_(launch_q4gemm(ctx, 1, m->pn, l.Wq, nullptr, m->pq, n, qd, H, m->pxb));
+        P_(launch_q4gemm(ctx, 1, m->pn, l.Wk, nullptr, m->pk, n, kvd, H, m->pxb));
+        P_(launch_q4gemm(ctx, 1, m->pn, l.Wv, nullptr, m->pv, n, kvd, H, m->pxb));
+        P_(launch_batch_qkv_rope(s, m->pq, m->pk, m->pv, l.q_norm, l.k_norm, m->pq, l.kc, l.vc, m->pslots,
+                                 num_prev_slots, start_clock, n, nq, nkv, D, c.rotary_dim, (int)c.k_eq_v, theta, eps));
+        // sliding layers see the last 1024 slots (shaders/batch_causal_attn.wgsl:53)
+        P_(launch_prefill_attn(s, m->pq, l.kc, l.vc, m->pslots, n, num_prev_slots, nq, D, kvd, gqa, 1.0f,
+                               l.full ? 0u : 1024u, m->pattn));
+        P_(launch_q4gemm(ctx, 1, m->pattn, l.Wo, nullptr, m->pmlp, n, H, qd, m->pxb));
+        if (l.has_post_attn) P_(launch_rmsnorm(s, m->pmlp, nullptr, l.post_attn, m->pmlp, H, n, eps, 1.0f, false));
+        P_(launch_rmsnorm(s, m->px, m->pmlp, l.pre_ffn, m->pn, H, n, eps, 1.0f, true));
+        P_(launch_q4gemm(ctx, 2, m->pn, l.Wg, l.Wu, m->pact, n, I, H, m->pxb));
+        P_(launch_q4gemm(ctx, 1, m->pact, l.Wd, nullptr, m->pmlp, n, H, I, m->pxb));
+        if (l.has_post_ffn) P_(launch_rmsnorm(s, m->pmlp, nullptr, l.post_ffn, m->pmlp, H, n, eps, 1.0f, false));
+        const float *next_norm = (i + 1 < c.num_layers) ? m->L[i + 1].in_norm : m->final_norm;
+        P_(launch_rmsnorm(s, m->px, m->pmlp, next_norm, m->pn, H, n, eps, l.scalar, true));
+        if ((i + 1) % 4 == 0 || i + 1 == c.num_layers) {
+            if (i + 1 == c.num_layers && (logits_out || topk_ids)) {
+                CHN_HIP(ctx, hipMemcpyAsync(m->normed, m->pn + (size_t)(n - 1) * H, H * 4, hipMemcpyDeviceToDevice, s));
+                P_(launch_gemv_q8(s, m->embed_q8, m->normed, m->logits, c.vocab_size, H / 32, m->mv_ws));
+                P_(launch_topk64(s, m->logits, c.vocab_size, m->topk_ids, m->topk_vals, m->topk_ws));
+            }
+            CHN_HIP(ctx, hipStreamSynchronize(s));
+            if (progress) progress(i + 1, c.num_layers, progress_ctx);
+        }
+    }
+#undef P_
+    if (logits_out) CHN_HIP(ctx, hipMemcpy(logits_out, m->logits, (size_t)c.vocab_size * 4, hipMemcpyDeviceToHost));
+    if (topk_ids) CHN_HIP(ctx, hipMemcpy(topk_ids, m->topk_ids, 64 * 4, hipMemcpyDeviceToHost));
+    if (topk_vals) CHN_HIP(ctx, hipMemcpy(topk_vals, m->topk_vals, 64 * 4, hipMemcpyDeviceToHost));
+    return CHN_OK;
+}
+
+// KV access for the callers that read or write the caches directly under
+// UMA (snapshots, memory, hippocampus, memory_inject): slots
+// [slot_begin, slot_begin + n) of layer `layer`, each row kv_dim floats.
+extern "C" int chn_kv_read(chn_model *m, uint32_t layer, uint32_t slot_begin, uint32_t n, float *k_out,
+                           float *v_out) {
+    if (!m) return CHN_E_INVALID;
+    CHN_REQUIRE(m->ctx, layer < m->cfg.num_layers && slot_begin + n <= kSlotsMax, "layer/slot range out of bounds");
+    const size_t row = (size_t)m->cfg.num_kv_heads * m->cfg.head_dim;
+    const auto &l = m->L[layer];
+    CHN_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    if (k_out) CHN_HIP(m->ctx, hipMemcpy(k_out, l.kc + slot_begin * row, n * row * 4, hipMemcpyDeviceToHost));
+    if (v_out) CHN_HIP(m->ctx, hipMemcpy(v_out, l.vc + slot_begin * row, n * row * 4, hipMemcpyDeviceToHost));
+    return CHN_OK;
+}
+
+extern "C" int chn_kv_write(chn_model *m, uint32_t layer, uint32_t slot_begin, uint32_t n, const float *k_in,
+                            const float *v_in) {
+    if (!m) return CHN_E_INVALID;
+    CHN_REQUIRE(m->ctx, layer < m->cfg.num_layers && slot_begin + n <= kSlotsMax, "layer/slot range out of bounds");
+    const size_t row = (size_t)m->cfg.num_kv_heads * m->cfg.head_dim;
+    const auto &l = m->L[layer];
+    CHN_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    if (k_in) CHN_HIP(m->ctx, hipMemcpy(l.kc + slot_begin * row, k_in, n * row * 4, hipMemcpyHostToDevice));
+    if (v_in) CHN_HIP(m->ctx, hipMemcpy(l.vc + slot_begin * row, v_in, n * row * 4, hipMemcpyHostToDevice));
+    return CHN_OK;
+}
+
+// Device buffers the reference's host code reads through asSlice under UMA
+// (src/server/decode.zig:13, src/server/prefill.zig:92-93): hidden state x
+// and the last normed row.
+extern "C" int chn_model_read_state(chn_model *m, float *x_out, float *normed_out) {
+    if (!m) return CHN_E_INVALID;
+    CHN_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    if (x_out) CHN_HIP(m->ctx, hipMemcpy(x_out, m->x, m->cfg.hidden_size * 4, hipMemcpyDeviceToHost));
+    if (normed_out) CHN_HIP(m->ctx, hipMemcpy(normed_out, m->normed, m->cfg.hidden_size * 4, hipMemcpyDeviceToHost));
+    return CHN_OK;
+}

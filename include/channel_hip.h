@@ -39,6 +39,7 @@ extern "C" {
 #define CHN_E_UNSUPPORTED (-6)      /* shape outside what the kernels support */
 
 typedef struct chn_ctx chn_ctx;
+typedef struct chn_model chn_model;
 
 /* ======================================================================
  * Runtime (replaces the Vulkan runtime, src/gpu/context.zig,
@@ -177,6 +178,138 @@ int chn_batch_rmsnorm(chn_ctx *ctx, const float *X, const float *w, float *Y, ui
                       uint32_t dim, float eps);
 int chn_batch_add_rmsnorm(chn_ctx *ctx, float *X, const float *R, const float *w, float *Y,
                           uint32_t n_tok, uint32_t dim, float eps, float scalar);
+
+/* Prefill RoPE over n_tok tokens: token t uses clock start_clock + t and
+ * writes K/V at slot slots[slot_offset + t]; q/k/v rows are [t][dim].
+ * batch_qkv_rope (shaders/batch_qkv_rope.wgsl, src/gpu/batch_dispatch.zig:84-95). */
+int chn_batch_qkv_rope(chn_ctx *ctx, const float *q_in, const float *k_in, const float *v_in,
+                       const float *q_norm_w, const float *k_norm_w, float *q_out,
+                       float *k_cache, float *v_cache, const uint32_t *slots,
+                       uint32_t slot_offset, uint32_t start_clock, uint32_t n_tok,
+                       uint32_t num_q_heads, uint32_t num_kv_heads, uint32_t head_dim,
+                       uint32_t rotary_dim, int k_eq_v, float theta, float eps);
+
+/* Prefill attention: token t (query rows [t][num_q_heads*head_dim]) attends
+ * over slots[start .. num_prev_slots + t] of the list, start = S - window
+ * when window > 0 and S > window (the reference uses window 1024 on sliding
+ * layers, 0 = whole list on full layers).  batch_causal_attn
+ * (shaders/batch_causal_attn.wgsl, src/gpu/batch_dispatch.zig:97-106). */
+int chn_batch_causal_attn(chn_ctx *ctx, const float *q, const float *k_cache, const float *v_cache,
+                          const uint32_t *slots, uint32_t n_tok, uint32_t num_prev_slots,
+                          uint32_t num_q_heads, uint32_t head_dim, uint32_t kv_dim,
+                          uint32_t gqa_ratio, float scale, uint32_t window, float *out);
+
+/* ======================================================================
+ * Logits, selection, quantization
+ * ==================================================================== */
+
+/* y[M] = W[M x K] (Q8_0: f32 scale + 32 int8 per 36-byte block) . x[K];
+ * K % 128 == 0, K <= 4096.  recordGemvLogits (src/gpu/kernels.zig:119-122) +
+ * shaders/gemv_q8.wgsl. */
+int chn_gemv_q8(chn_ctx *ctx, const uint32_t *W, const float *x, float *y, uint32_t M, uint32_t K);
+
+/* Global top-64 of 30*tanh(logit/30), sorted descending, ties by lower
+ * index; ids/vals are device arrays of 64.  V <= 262144.  recordTopK
+ * (src/gpu/kernels.zig:178-184) + shaders/topk_pass1.wgsl, topk_pass2.wgsl. */
+int chn_topk64(chn_ctx *ctx, const float *logits, uint32_t V, uint32_t *ids, float *vals);
+
+/* bf16 rows (device) -> Q4 / Q8_0 words (device), bit-exact with
+ * quantizeRowQ4_0 / quantizeRowQ8_0 (src/quant.zig:21-98).  cols % 32 == 0. */
+int chn_quantize_q4(chn_ctx *ctx, const uint16_t *src_bf16, uint32_t *dst, uint32_t rows, uint32_t cols);
+int chn_quantize_q8(chn_ctx *ctx, const uint16_t *src_bf16, uint32_t *dst, uint32_t rows, uint32_t cols);
+
+/* fp32 -> bf16 bits with the reference's rounding (bf16.fromF32,
+ * src/tensor.zig:7-13), device to device. */
+int chn_to_bf16_bits(chn_ctx *ctx, const float *src, uint16_t *dst, size_t n);
+
+/* ======================================================================
+ * Model level (GpuModelContext, src/gpu/model_gpu.zig:30-216; decode,
+ * src/gpu/model_dispatch.zig:128-153; prefill, src/gpu/batch_dispatch.zig:27-172)
+ * ==================================================================== */
+
+/* ModelConfig (src/model/types.zig:43-61) fields the GPU path uses. */
+typedef struct chn_model_config {
+    uint32_t hidden_size, intermediate_size, vocab_size, num_layers;
+    uint32_t num_heads, num_kv_heads, head_dim, rotary_dim;
+    float rms_norm_eps, rope_theta, rope_theta_full;
+    uint32_t sliding_window;       /* informational: slot lists come from the caller */
+    uint32_t k_eq_v;               /* attention_k_eq_v */
+    uint32_t max_prefill_tokens;   /* BatchPrefillContext max_tokens (model_gpu.zig:178) */
+    uint8_t layer_full[64];        /* 1 = full_attention, 0 = sliding_attention */
+} chn_model_config;
+
+/* LayerWeights (src/model/types.zig:13-41): host bf16 tensors, row-major
+ * [out][in]; NULL v_proj uses k_proj; NULL norms read as 1.0; NULL post
+ * norms are skipped. */
+typedef struct chn_layer_weights {
+    const uint16_t *input_layernorm, *q_proj, *k_proj, *v_proj, *o_proj, *q_norm, *k_norm;
+    const uint16_t *post_attention_layernorm, *pre_feedforward_layernorm;
+    const uint16_t *gate_proj, *up_proj, *down_proj, *post_feedforward_layernorm;
+    float layer_scalar;
+    int has_layer_scalar;
+} chn_layer_weights;
+
+/* ProgressFn (src/gpu/batch_dispatch.zig:25). */
+typedef void (*chn_progress_fn)(size_t layer_idx, size_t total_layers, void *ctx);
+
+/* GpuModelContext.init: quantize bf16 weights on the device (Q4 for the
+ * layers, Q8 for the tied embedding), allocate KV caches (4096 slots per
+ * layer), record the decode graphs.  The caller may drop its bf16 pages
+ * afterwards. */
+int chn_model_create(chn_ctx *ctx, const chn_model_config *cfg, const chn_layer_weights *layers,
+                     const uint16_t *embed_bf16, const uint16_t *final_norm_bf16, chn_model **out);
+
+/* Same, with seeded synthetic weights generated in HBM (codes uniform,
+ * f16 scales U(0.005, 0.02), norms 1.0, bf16 embedding ~ N(0, 0.02) kept on
+ * the device for the input gather).  No reference counterpart. */
+int chn_model_create_synthetic(chn_ctx *ctx, const chn_model_config *cfg, uint64_t seed, chn_model **out);
+
+/* GpuModelContext.deinit (src/gpu/model_gpu.zig:203-215). */
+void chn_model_destroy(chn_model *m);
+
+int chn_model_get_config(const chn_model *m, chn_model_config *cfg);
+
+/* Device pointer to the synthetic model's bf16 embedding (NULL otherwise). */
+int chn_model_embedding_bf16(chn_model *m, const uint16_t **table);
+
+/* gpuDispatchForwardToken (src/gpu/model_dispatch.zig:128-153): x[hidden]
+ * (host), the global and sliding slot lists (host, <= 4096 each), clock and
+ * the slot receiving this token's K/V.  With topk_ids != NULL the logits
+ * graph runs and 64 candidates are returned; *token_out = ids[0] (the
+ * reference's return value).  Returns a status; the reference's "return 0
+ * on submit failure" is the caller's choice. */
+int chn_decode_step(chn_model *m, const float *x, uint32_t clock, uint32_t slot_idx,
+                    const uint32_t *active, uint32_t n_active, const uint32_t *sliding,
+                    uint32_t n_sliding, uint32_t *topk_ids, float *topk_vals, uint32_t *token_out);
+
+/* forwardToken's embedding step (src/model/forward.zig:35-37) on the
+ * device, then chn_decode_step.  Needs a model with a device embedding. */
+int chn_decode_token(chn_model *m, uint32_t token, uint32_t clock, uint32_t slot_idx,
+                     const uint32_t *active, uint32_t n_active, const uint32_t *sliding,
+                     uint32_t n_sliding, uint32_t *topk_ids, float *topk_vals, uint32_t *token_out);
+
+/* gpuDispatchPrefillBatch: n <= max_prefill_tokens tokens (else
+ * CHN_E_BATCH_TOO_LARGE); slots[0..n_slots) lists num_prev_slots earlier
+ * slots then one slot per new token; embed_bf16 is the host table
+ * (vocab x hidden) or NULL to use the model's device table.  Synchronizes
+ * every 4 layers and calls progress.  logits_out (host, vocab floats) and
+ * topk_ids/topk_vals (host, 64) may be NULL. */
+int chn_prefill(chn_model *m, const uint32_t *tokens, uint32_t n, const uint16_t *embed_bf16,
+                const uint32_t *slots, uint32_t n_slots, uint32_t start_clock, uint32_t num_prev_slots,
+                float *logits_out, uint32_t *topk_ids, float *topk_vals, chn_progress_fn progress,
+                void *progress_ctx);
+
+/* KV cache access replacing the UMA reads/writes of buf_k_cache/buf_v_cache
+ * (src/snapshot.zig:95-98,171-174, src/memory.zig:104-107,
+ * src/hippocampus.zig:166-169, src/model/memory_inject.zig:14-30): n slots
+ * from slot_begin of one layer, each num_kv_heads*head_dim floats. */
+int chn_kv_read(chn_model *m, uint32_t layer, uint32_t slot_begin, uint32_t n, float *k_out, float *v_out);
+int chn_kv_write(chn_model *m, uint32_t layer, uint32_t slot_begin, uint32_t n, const float *k_in,
+                 const float *v_in);
+
+/* Reads of buf_x / buf_normed_x (src/server/decode.zig:13,
+ * src/model/memory_inject.zig:56): hidden state and last normed row. */
+int chn_model_read_state(chn_model *m, float *x_out, float *normed_out);
 
 /* ======================================================================
  * Seeded synthetic inputs (no reference counterpart: benchmark and test

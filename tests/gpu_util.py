@@ -37,3 +37,18 @@ def q4_host(ctx, buf, rows, K):
 
 def f32_host(ctx, buf, n, byte_offset=0):
     return ctx.download(buf, np.float32, n, byte_offset)
+
+
+def assert_topk_valid(ids, vals, logits_want, tol):
+    """ids/vals are a valid top-64 of softcap(logits_want) under tolerance:
+    values match the exact top-64 within tol * max|value|, ids are distinct,
+    and each id's exact capped value is within 2 * that of the value at its
+    position (so only near-ties may be ordered differently)."""
+    import oracle
+    capped = oracle.softcap(logits_want)
+    want_ids, want_vals = oracle.topk64(logits_want)
+    atol = tol * float(np.max(np.abs(want_vals)))
+    assert len(set(int(i) for i in ids)) == 64
+    assert np.all(np.abs(np.asarray(vals, np.float64) - want_vals) <= atol)
+    assert np.all(np.abs(capped[np.asarray(ids, np.int64)].astype(np.float64) - want_vals) <= 2 * atol)
+    return int(np.sum(np.asarray(ids) == want_ids))

@@ -1,0 +1,188 @@
+"""GPU parity of the model level: a small random model ingested from bf16
+through chn_model_create (device Q4/Q8 quantization), batched prefill, then
+graph-replayed decode steps, all against the model oracle (oracle/model.py,
+following src/gpu/model_dispatch.zig and src/gpu/batch_dispatch.zig).
+
+Bars: prefill runs on bf16 MFMA operands (normwise 1e-2 on logits and KV
+rows); decode is fp32 (1e-3), with its caches taken from the GPU after the
+prefill so that the bf16 prefill error does not enter the decode check.
+Top-64 lists must be a valid top-64 of the oracle's logits (identical up to
+the order of near-ties).
+"""
+import numpy as np
+import pytest
+
+import channel_amd as ca
+from channel_amd.model import Model
+from gpu_util import assert_topk_valid, rel_err, say
+from oracle import model as OM
+
+pytestmark = pytest.mark.gpu
+
+CFG = OM.default_config(hidden_size=256, intermediate_size=512, vocab_size=4096, num_layers=3,
+                        num_heads=4, num_kv_heads=2, head_dim=256, rotary_dim=128,
+                        layer_full=[0, 1, 0], max_prefill_tokens=64, sliding_window=16)
+WINDOW = 16
+
+
+@pytest.fixture(scope="module")
+def pair(ctx):
+    layers, embed, final = OM.random_model(CFG, 21)
+    W = OM.Weights(CFG, layers, embed, final)
+    say("model_create small random model")
+    m = Model.create(ctx, CFG, layers, embed, final)
+    yield W, m
+    m.close()
+
+
+def _kv_all(m, n):
+    return [m.kv_read(i, 0, n) for i in range(CFG["num_layers"])]
+
+
+def test_prefill_then_decode(pair):
+    W, m = pair
+    kvd = CFG["num_kv_heads"] * CFG["head_dim"]
+    toks = [int(t) for t in np.random.default_rng(3).integers(0, CFG["vocab_size"], 40)]
+    n = len(toks)
+    calls = []
+    say("prefill 40 tokens")
+    lg, ids, vals = m.prefill_batch(toks, np.arange(n), 0, 0, embed_bf16=W.embed_bf16,
+                                    progress=lambda i, t: calls.append((i, t)))
+    assert calls == [(3, 3)]
+    kc, vc = OM.new_caches(CFG, 4096)
+    _, Xn, lg_o, ids_o, vals_o = OM.prefill(W, kc, vc, toks, np.arange(n), 0, 0, bf16_gemm=True,
+                                            window=1024)
+    assert rel_err(lg, lg_o) < 1e-2
+    assert_topk_valid(ids, vals, lg_o, 1e-2)
+    kv = _kv_all(m, n)
+    for i in range(CFG["num_layers"]):
+        assert rel_err(kv[i][0], kc[i][: n * kvd].reshape(n, kvd)) < 1e-2
+        assert rel_err(kv[i][1], vc[i][: n * kvd].reshape(n, kvd)) < 1e-2
+    # the decode state holds the last normed row
+    _, normed = m.read_state()
+    assert rel_err(normed, Xn[n - 1]) < 1e-2
+
+    # continue with greedy decode from the GPU's caches
+    for i in range(CFG["num_layers"]):
+        kc[i][: n * kvd] = kv[i][0].ravel()
+        vc[i][: n * kvd] = kv[i][1].ravel()
+    tok = int(ids[0])
+    for clock in range(n, n + 4):
+        active, sliding = OM.slot_lists(clock, WINDOW)
+        x_in = W.embed([tok])[0]
+        say(f"decode clock={clock} tok={tok}")
+        t_gpu, ids_g, vals_g = m.forward_token(x_in, clock, clock, active, sliding)
+        x_o, nx_o, lg_o, ids_o, vals_o = OM.decode_step(W, kc, vc, x_in, clock, clock, active, sliding)
+        assert t_gpu == ids_g[0]
+        assert_topk_valid(ids_g, vals_g, lg_o, 1e-3)
+        x_g, nx_g = m.read_state()
+        assert rel_err(x_g, x_o) < 1e-3
+        assert rel_err(nx_g, nx_o) < 1e-3
+        for i in range(CFG["num_layers"]):
+            k_g, v_g = m.kv_read(i, clock, 1)
+            assert rel_err(k_g[0], kc[i][clock * kvd:(clock + 1) * kvd]) < 1e-3
+            assert rel_err(v_g[0], vc[i][clock * kvd:(clock + 1) * kvd]) < 1e-3
+        tok = int(ids_g[0])
+
+
+def test_decode_without_logits_and_ring_slots(pair):
+    """The no-logits graph updates state and caches only; slot lists in ring
+    order (the write head mid-ring) and a slot index different from clock."""
+    W, m = pair
+    kvd = CFG["num_kv_heads"] * CFG["head_dim"]
+    rng = np.random.default_rng(9)
+    # fill 200 ring slots with random K/V, identical on both sides
+    kc, vc = OM.new_caches(CFG, 4096)
+    for i in range(CFG["num_layers"]):
+        k = rng.standard_normal((200, kvd)).astype(np.float32)
+        v = rng.standard_normal((200, kvd)).astype(np.float32)
+        m.kv_write(i, 3000, k, v)
+        kc[i][3000 * kvd:3200 * kvd] = k.ravel()
+        vc[i][3000 * kvd:3200 * kvd] = v.ravel()
+        k_back, v_back = m.kv_read(i, 3000, 200)
+        assert np.array_equal(k_back, k) and np.array_equal(v_back, v)
+    clock, slot = 5000, 3199
+    active = np.arange(3000, 3200, dtype=np.uint32)
+    sliding = active[-WINDOW:]
+    x_in = W.embed([77])[0]
+    say("decode without logits")
+    m.forward_token(x_in, clock, slot, active, sliding, topk=False)
+    x_o, nx_o, *_ = OM.decode_step(W, kc, vc, x_in, clock, slot, active, sliding, with_logits=False)
+    x_g, nx_g = m.read_state()
+    assert rel_err(x_g, x_o) < 1e-3
+    assert rel_err(nx_g, nx_o) < 1e-3
+    for i in range(CFG["num_layers"]):
+        k_g, _ = m.kv_read(i, slot, 1)
+        assert rel_err(k_g[0], kc[i][slot * kvd:(slot + 1) * kvd]) < 1e-3
+
+
+def test_prefill_after_previous_slots(pair):
+    """A second prefill chunk attends over num_prev_slots earlier slots."""
+    W, m = pair
+    kvd = CFG["num_kv_heads"] * CFG["head_dim"]
+    rng = np.random.default_rng(5)
+    kc, vc = OM.new_caches(CFG, 4096)
+    prev = np.arange(100, 130, dtype=np.uint32)
+    for i in range(CFG["num_layers"]):
+        k = (rng.standard_normal((30, kvd)) * 0.5).astype(np.float32)
+        v = rng.standard_normal((30, kvd)).astype(np.float32)
+        m.kv_write(i, 100, k, v)
+        kc[i][100 * kvd:130 * kvd] = k.ravel()
+        vc[i][100 * kvd:130 * kvd] = v.ravel()
+    toks = [5, 900, 31, 4000, 2, 2, 17, 64]
+    new = np.arange(130, 138, dtype=np.uint32)
+    slots = np.concatenate([prev, new])
+    say("prefill with 30 previous slots")
+    lg, ids, vals = m.prefill_batch(toks, slots, 30, 30, embed_bf16=W.embed_bf16)
+    _, _, lg_o, _, _ = OM.prefill(W, kc, vc, toks, slots, 30, 30, bf16_gemm=True)
+    assert rel_err(lg, lg_o) < 1e-2
+    assert_topk_valid(ids, vals, lg_o, 1e-2)
+
+
+def test_model_errors(pair):
+    W, m = pair
+    with pytest.raises(ca.ChannelError) as e:
+        m.prefill_batch(list(range(65)), np.arange(65), 0, 0, embed_bf16=W.embed_bf16)
+    assert e.value.status == "BatchTooLarge"
+    with pytest.raises(ca.ChannelError) as e:
+        m.prefill_batch([], [], 0, 0, embed_bf16=W.embed_bf16)
+    assert e.value.status == "BatchTooLarge"
+    with pytest.raises(ca.ChannelError):
+        m.prefill_batch([1, 2], [0, 4096], 0, 0, embed_bf16=W.embed_bf16)
+    with pytest.raises(ca.ChannelError):
+        m.prefill_batch([1, 5000], [0, 1], 0, 0, embed_bf16=W.embed_bf16)
+    with pytest.raises(ca.ChannelError):
+        m.forward_token(np.zeros(256, np.float32), 0, 4096, [0], [0])
+    with pytest.raises(ca.ChannelError):
+        m.forward_token(np.zeros(256, np.float32), 0, 0, np.arange(4097), [0])
+    with pytest.raises(ca.ChannelError):
+        # this model has no device embedding table
+        m.forward_token_id(3, 0, 0, [0], [0])
+    with pytest.raises(ca.ChannelError):
+        m.kv_read(3, 0, 1)
+    with pytest.raises(ca.ChannelError):
+        m.kv_read(0, 4090, 7)
+
+
+def test_synthetic_model_token_path(ctx):
+    """chn_decode_token gathers bf16(embed[tok]) * sqrt(H) on the device; it
+    must match chn_decode_step fed with the same row from the host."""
+    cfg = dict(CFG, num_layers=2, layer_full=[1, 0])
+    say("model_create_synthetic")
+    with Model.synthetic(ctx, cfg, 1234) as m1, Model.synthetic(ctx, cfg, 1234) as m2:
+        import ctypes
+        p = ctypes.c_void_p()
+        assert ca.lib.chn_model_embedding_bf16(m1.handle, ctypes.byref(p)) == 0 and p.value
+        H = cfg["hidden_size"]
+        tok = 1001
+        row = ctx.download(p.value + tok * H * 2, np.uint16, H)
+        x_in = OM.bf16_to_f32(row) * np.float32(np.sqrt(np.float32(H)))
+        for clock in range(3):
+            active, sliding = OM.slot_lists(clock, WINDOW)
+            t1, ids1, vals1 = m1.forward_token_id(tok, clock, clock, active, sliding)
+            t2, ids2, vals2 = m2.forward_token(x_in, clock, clock, active, sliding)
+            assert np.array_equal(ids1, ids2) and np.array_equal(vals1, vals2)
+            assert np.all(np.diff(vals1) <= 0) and np.all(ids1 < cfg["vocab_size"])
+            tok = int(t1)
+            row = ctx.download(p.value + tok * H * 2, np.uint16, H)
+            x_in = OM.bf16_to_f32(row) * np.float32(np.sqrt(np.float32(H)))

@@ -1,0 +1,111 @@
+"""CPU checks of the model-level oracle (oracle/model.py).
+
+The decode sequence (src/gpu/model_dispatch.zig:10-45) and the batched
+prefill (src/gpu/batch_dispatch.zig:27-172) are two separately written
+compositions of the same layer; run over the same prompt token by token and
+as one batch they must agree (fp32 GEMMs, so only summation order differs).
+The sliding window is exercised by giving the decode steps a short sliding
+list and the prefill the same window.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from oracle import model as OM
+
+
+def _cfg():
+    return OM.default_config(hidden_size=128, intermediate_size=256, vocab_size=512, num_layers=3,
+                             num_heads=2, num_kv_heads=1, head_dim=256, rotary_dim=128,
+                             layer_full=[0, 1, 0], max_prefill_tokens=16)
+
+
+@pytest.fixture(scope="module")
+def weights():
+    cfg = _cfg()
+    layers, embed, final = OM.random_model(cfg, 11)
+    return OM.Weights(cfg, layers, embed, final)
+
+
+def _rel(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
+
+
+@pytest.mark.parametrize("window", [1024, 5])
+def test_prefill_equals_token_by_token_decode(weights, window):
+    cfg = weights.cfg
+    toks = [3, 17, 255, 4, 99, 100, 7, 300, 42, 1]
+    kc1, vc1 = OM.new_caches(cfg, 64)
+    kc2, vc2 = OM.new_caches(cfg, 64)
+    X, Xn, logits_p, ids_p, _ = OM.prefill(weights, kc1, vc1, toks, np.arange(len(toks)), 0, 0,
+                                           bf16_gemm=False, window=window)
+    for t, tok in enumerate(toks):
+        active, sliding = OM.slot_lists(t, window)
+        x, normed, logits_d, ids_d, _ = OM.decode_step(weights, kc2, vc2, weights.embed([tok])[0], t, t,
+                                                       active, sliding)
+        assert _rel(X[t], x) < 1e-4
+        assert _rel(Xn[t], normed) < 1e-4
+    for i in range(cfg["num_layers"]):
+        assert _rel(kc1[i][: len(toks) * 256], kc2[i][: len(toks) * 256]) < 1e-4
+        assert _rel(vc1[i][: len(toks) * 256], vc2[i][: len(toks) * 256]) < 1e-4
+    assert _rel(logits_p, logits_d) < 1e-4
+    assert ids_p[0] == ids_d[0]
+
+
+def test_window_changes_sliding_layers_only(weights):
+    """A window shorter than the prompt changes the output (the sliding
+    layers see fewer slots); the full layer's K/V rows, computed before any
+    attention of that layer, depend only on earlier layers."""
+    cfg = weights.cfg
+    toks = [5, 6, 7, 8, 9, 10, 11, 12]
+    out = []
+    for w in (1024, 3):
+        kc, vc = OM.new_caches(cfg, 64)
+        X, *_ = OM.prefill(weights, kc, vc, toks, np.arange(8), 0, 0, bf16_gemm=False, window=w)
+        out.append((X, kc, vc))
+    # layer 0 K/V are written before its attention: identical
+    assert np.array_equal(out[0][1][0], out[1][1][0])
+    # the last rows differ once the window cuts slots
+    assert _rel(out[0][0][7], out[1][0][7]) > 1e-3
+    # the first 3 tokens see at most 3 slots either way
+    assert _rel(out[0][0][:3], out[1][0][:3]) < 1e-6
+
+
+def test_bf16_prefill_close_to_fp32(weights):
+    """The bf16-operand GEMM model stays within the bf16 bar of the fp32 path."""
+    cfg = weights.cfg
+    toks = [1, 2, 3, 4, 5, 6]
+    r = []
+    for bf in (False, True):
+        kc, vc = OM.new_caches(cfg, 64)
+        r.append(OM.prefill(weights, kc, vc, toks, np.arange(6), 0, 0, bf16_gemm=bf))
+    assert _rel(r[1][2], r[0][2]) < 1e-2
+
+
+def test_embed_scale_and_missing_norms():
+    """x = bf16(embed) * sqrt(H) (src/model/forward.zig:35-37); absent norms
+    read as 1.0 and absent post norms are skipped."""
+    cfg = _cfg()
+    layers, embed, _ = OM.random_model(cfg, 5)
+    for l in layers:
+        l["post_attention_layernorm"] = None
+        l["q_norm"] = None
+    W = OM.Weights(cfg, layers, embed, None)
+    assert np.all(W.final_norm == 1.0) and np.all(W.layers[0]["q_norm"] == 1.0)
+    assert W.layers[0]["post_attn"] is None
+    e = W.embed([7])[0]
+    want = OM.bf16_to_f32(embed[7]) * np.float32(np.sqrt(np.float32(128)))
+    assert np.array_equal(e, want.astype(np.float32))
+    assert abs(float(e[0]) - float(OM.bf16_to_f32(embed[7][0])) * 128 ** 0.5) < 1e-4
+
+
+def test_topk_of_decode_matches_logits(weights):
+    cfg = weights.cfg
+    kc, vc = OM.new_caches(cfg, 16)
+    a, s = OM.slot_lists(0, 1024)
+    _, _, logits, ids, vals = OM.decode_step(weights, kc, vc, weights.embed([9])[0], 0, 0, a, s)
+    capped = O.softcap(logits)
+    order = np.argsort(-capped.astype(np.float64), kind="stable")[:64]
+    assert np.array_equal(ids, order.astype(np.uint32))
+    assert np.array_equal(vals, capped[order])
