@@ -7,15 +7,22 @@ Prints ONE JSON line.  Workloads (inputs synthetic, seeded, generated in HBM
 before the timed region; weights rotate over enough distinct copies that the
 working set exceeds the 256 MB Infinity Cache, so every step streams HBM):
 
-  mlp   (default) fused Q4 gated MLP decode step at 12B dims: hidden 3840,
-        FFN 15360: fused gate/up + GELU-tanh (chn_fused_mlp_q4), then down
-        (chn_gemv_q4).  One step = one token's MLP.
-  gemv  single Q4 matvec, W 8192 x 2048, x fp32 [2048].
+  decode  (default) the full 48-layer 12B-class Q4 model (hidden 3840, FFN
+          15360, 16 query / 8 KV heads, head_dim 256, vocab 262144, every
+          fifth layer global, sliding window 512): a 512-token prompt of
+          uniform random ids is prefilled, then greedy decode steps run
+          through the recorded decode graph.  One step = one token
+          (embedding gather, 48 layers, Q8 logits, top-64, argmax).
+  mlp     fused Q4 gated MLP decode step at 12B dims: fused gate/up +
+          GELU-tanh (chn_fused_mlp_q4), then down (chn_gemv_q4).
+  gemv    single Q4 matvec, W 8192 x 2048, x fp32 [2048].
+  prefill batched prefill Q4 GEMM 512 x 3840 -> 15360 on bf16 MFMA.
+  attn    decode attention over a full 4096-slot ring.
 
-`roofline` is for the dominant kernel (the fused gate/up matvec for `mlp`),
-timed with HIP events on the library's stream over back-to-back launches;
-`cpu_baseline` times the oracle's threaded restatement of the same step on
-this host's cores (rank 0, N=1 only) on a bounded sample.
+`roofline` is for the dominant kernel (the fused gate/up matvec for decode
+and mlp), timed with HIP events on the library's stream over back-to-back
+launches; `cpu_baseline` times the oracle's threaded restatement of the same
+work on this host's cores (rank 0, N=1 only) on a bounded sample.
 """
 import argparse
 import json
@@ -155,6 +162,219 @@ def bench_mlp(ctx, args):
                      "avg_launch_ms": k_ms},
         "cpu_baseline": cpu,
         "dtype": "fp32 accumulate over Q4 weights",
+    }
+
+
+def alloc_gateup_copies(ctx, H, I, min_bytes=ROTATE_BYTES):
+    """Distinct 12B-dims gate/up pairs, enough to exceed the Infinity Cache."""
+    w_bytes = q4_bytes(I, H)
+    ncopy = max(4, -(-min_bytes // (2 * w_bytes)))
+    pairs = []
+    for c in range(ncopy):
+        g = ctx.alloc(w_bytes)
+        u = ctx.alloc(w_bytes)
+        ctx.call("chn_synth_q4", g, I, H, SEED + 16 * c, 0.005, 0.02)
+        ctx.call("chn_synth_q4", u, I, H, SEED + 16 * c + 1, 0.005, 0.02)
+        pairs.append((g, u))
+    return pairs
+
+
+def time_gateup(ctx, pairs, x, act, H, I, reps):
+    """Average duration (ms) of chn_fused_mlp_q4 (k_xplanes + k_q4mv<MLP>)
+    over back-to-back launches on the library stream, HIP events."""
+    for i in range(4):
+        ctx.call("chn_fused_mlp_q4", pairs[i % len(pairs)][0], pairs[i % len(pairs)][1], x, act, I, H)
+    ctx.timer_start()
+    for i in range(reps):
+        g, u = pairs[i % len(pairs)]
+        ctx.call("chn_fused_mlp_q4", g, u, x, act, I, H)
+    return ctx.timer_stop() / reps
+
+
+def gateup_bytes(H, I):
+    return 2 * q4_bytes(I, H) + H * 4 + I * 4
+
+
+CFG_12B = dict(hidden_size=3840, intermediate_size=15360, vocab_size=262144, num_layers=48,
+               num_heads=16, num_kv_heads=8, head_dim=256, rotary_dim=256, rms_norm_eps=1e-6,
+               rope_theta=1e4, rope_theta_full=1e6, sliding_window=512, k_eq_v=0,
+               max_prefill_tokens=512, layer_full=[1 if (l + 1) % 5 == 0 else 0 for l in range(48)])
+PROMPT = 512
+
+
+def token_bytes(cfg, ctx_len):
+    """Algorithmic HBM bytes of one decode token: every Q4 layer matrix and
+    the Q8 tied embedding once, plus the K/V rows each layer's attention
+    reads (fp32) and the new K/V row it writes."""
+    H, I, D = cfg["hidden_size"], cfg["intermediate_size"], cfg["head_dim"]
+    qd, kvd = cfg["num_heads"] * D, cfg["num_kv_heads"] * D
+    layer_w = q4_bytes(qd + 2 * kvd, H) + q4_bytes(H, qd) + 2 * q4_bytes(I, H) + q4_bytes(H, I)
+    w = cfg["num_layers"] * layer_w + cfg["vocab_size"] * (H // 32) * 36
+    kv = 0
+    for full in cfg["layer_full"]:
+        n = ctx_len if full else min(ctx_len, cfg["sliding_window"])
+        kv += 2 * n * kvd * 4 + 2 * kvd * 4
+    return w, kv
+
+
+def cpu_decode_sample(cfg, seed, ctx_len, seconds):
+    """The oracle's threaded restatement of one decode token, timed on a
+    bounded sample: two layers (one sliding, one global) with the synthetic
+    model's own seeded weights, stepped alternately for about `seconds`, and
+    the Q8 logits over a 16384-row slice of the vocabulary plus one top-64
+    over 262144 logits; scaled to a 48-layer, 262144-vocab token."""
+    import numpy as np
+
+    import oracle
+    nthr, model = cpu_info()
+    nthr = min(nthr, 16)
+    H, I, D = cfg["hidden_size"], cfg["intermediate_size"], cfg["head_dim"]
+    nq, nkv = cfg["num_heads"], cfg["num_kv_heads"]
+    qd, kvd = nq * D, nkv * D
+    eps = cfg["rms_norm_eps"]
+    layers = []
+    for li in (0, 4):
+        ls = seed + 64 * (li + 1)
+        shapes = [(qd, H), (kvd, H), (kvd, H), (H, qd), (I, H), (I, H), (H, I)]
+        W = [oracle.synth_q4(r, k, ls + j) for j, (r, k) in enumerate(shapes)]
+        layers.append((li, W))
+    kc = oracle.synth_normal(4096 * kvd, seed + 11)
+    vc = oracle.synth_normal(4096 * kvd, seed + 12)
+    ones_h = np.ones(H, np.float32)
+    ones_d = np.ones(D, np.float32)
+    x = oracle.synth_normal(H, seed + 13)
+    slots_full = np.arange(ctx_len, dtype=np.uint32)
+    slots_sl = slots_full[-cfg["sliding_window"]:]
+
+    def layer_step(li, W, x):
+        full = cfg["layer_full"][li]
+        normed = oracle.rmsnorm(x, ones_h, eps)
+        q = oracle.gemv_q4_mt(W[0], normed, qd, H, nthr - 1)
+        k = oracle.gemv_q4_mt(W[1], normed, kvd, H, nthr - 1)
+        v = oracle.gemv_q4_mt(W[2], normed, kvd, H, nthr - 1)
+        q = oracle.qkv_rope(q, k, v, ones_d, ones_d, kc, vc, nq, nkv, D, D, 0,
+                            cfg["rope_theta_full"] if full else cfg["rope_theta"], eps,
+                            ctx_len - 1, ctx_len - 1)
+        a = oracle.decode_attn(q, kc, vc, slots_full if full else slots_sl, nq, D, kvd, nq // nkv)
+        o = oracle.gemv_q4_mt(W[3], a, H, qd, nthr - 1)
+        x, normed = oracle.add_rmsnorm(x, oracle.rmsnorm(o, ones_h, eps), ones_h, eps, 1.0)
+        _, d = oracle.fused_mlp_step_mt(W[4], W[5], W[6], normed, H, I, nthr - 1)
+        x, _ = oracle.add_rmsnorm(x, oracle.rmsnorm(d, ones_h, eps), ones_h, eps, 1.0)
+        return x
+
+    n, t0 = 0, time.perf_counter()
+    while True:
+        for li, W in layers:
+            x = layer_step(li, W, x)
+            n += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    t_layer = (time.perf_counter() - t0) / n
+    rows = 16384
+    E = oracle.synth_q8(rows, H, seed + 7, 0.0001, 0.0005)
+    t1 = time.perf_counter()
+    lg = oracle.gemv_q8_mt(E, x, rows, H, nthr - 1)
+    t_logits = (time.perf_counter() - t1) * (cfg["vocab_size"] / rows)
+    full_lg = np.resize(lg, cfg["vocab_size"])
+    t2 = time.perf_counter()
+    oracle.topk64(full_lg)
+    t_topk = time.perf_counter() - t2
+    t_tok = cfg["num_layers"] * t_layer + t_logits + t_topk
+    return {"value": 1.0 / t_tok, "unit": "tok/s", "cores": nthr, "kind": "port",
+            "sample": f"{n} decoder-layer steps (layers 0 and 4 of the 12B model, context {ctx_len}) "
+                      f"at {t_layer * 1e3:.1f} ms each x 48, plus Q8 logits over 16384 of 262144 rows "
+                      f"scaled ({t_logits * 1e3:.0f} ms) and one top-64 ({t_topk * 1e3:.0f} ms); "
+                      f"{nthr} threads ({nthr - 1} pool workers + caller), {model}"}
+
+
+def bench_decode(ctx, args):
+    """Greedy decode through the recorded graph of the synthetic 12B model."""
+    import numpy as np
+
+    from channel_amd.model import Model
+
+    cfg = CFG_12B
+    H, I = cfg["hidden_size"], cfg["intermediate_size"]
+    t_create = time.perf_counter()
+    m = Model.synthetic(ctx, cfg, SEED)
+    t_create = time.perf_counter() - t_create
+    if args.eager:
+        m.set_graph(False)
+    rng = np.random.default_rng(SEED)
+    prompt = rng.integers(0, cfg["vocab_size"], PROMPT).astype(np.uint32)
+    slots = np.arange(PROMPT, dtype=np.uint32)
+    # prefill twice: the first run warms code objects, the second is timed
+    m.prefill_batch(prompt, slots, 0, 0, logits=False, topk=True)
+    t0 = time.perf_counter()
+    _, ids, _ = m.prefill_batch(prompt, slots, 0, 0, logits=False, topk=True)
+    prefill_s = time.perf_counter() - t0
+
+    tok = int(ids[0])
+    clock = PROMPT
+    window = cfg["sliding_window"]
+
+    def step():
+        # ring of 4096 slots, no anchors: slot = clock mod 4096, the global
+        # list holds the last min(clock + 1, 4096) slots in time order and
+        # the sliding list the last `window` of them
+        nonlocal tok, clock
+        n = min(clock + 1, 4096)
+        active = ((np.arange(n, dtype=np.int64) + clock + 1 - n) % 4096).astype(np.uint32)
+        sliding = active[max(0, n - window):]
+        tok, _, _ = m.forward_token_id(tok, clock, clock % 4096, active, sliding, topk=True)
+        clock += 1
+
+    for _ in range(args.warmup):
+        step()
+    ctx.sync()
+    ctx_start = clock
+    t0 = time.perf_counter()
+    ctx.timer_start()
+    for _ in range(args.steps):
+        step()
+    gpu_ms = ctx.timer_stop()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    ms_per_tok = max(gpu_ms, wall_ms) / args.steps
+    mid_ctx = (ctx_start + clock) // 2
+    w_bytes, kv_bytes = token_bytes(cfg, mid_ctx)
+    m.close()
+
+    # dominant kernel: fused gate/up matvec at the model's shape, rotating
+    # distinct weight pairs, back to back on the library stream
+    pairs = alloc_gateup_copies(ctx, H, I)
+    x = ctx.alloc(H * 4)
+    ctx.call("chn_synth_normal", x, H, SEED + 7, 1.0)
+    act = ctx.alloc(I * 4)
+    k_ms = time_gateup(ctx, pairs, x, act, H, I, max(192, 4 * len(pairs)))
+    achieved = gateup_bytes(H, I) / (k_ms * 1e-3) / 1e9
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_decode_sample(cfg, SEED, mid_ctx, args.cpu_seconds)
+
+    return {
+        "value": 1e3 / ms_per_tok,
+        "unit": "tok/s",
+        "ms_per_step": ms_per_tok,
+        "config": {"workload": "12B-class Q4 decode: 48 layers, hidden 3840, FFN 15360, 16 q / 8 kv heads, "
+                               "head_dim 256, vocab 262144; 512-token prompt prefill, then greedy decode",
+                   "prompt_tokens": PROMPT, "decode_context": [ctx_start, clock],
+                   "prefill_tok_s": PROMPT / prefill_s, "prefill_ms": prefill_s * 1e3,
+                   "token_weight_bytes": w_bytes, "token_kv_bytes_mid": kv_bytes,
+                   "token_hbm_gbps": (w_bytes + kv_bytes) / (ms_per_tok * 1e-3) / 1e9,
+                   "token_roofline_frac": (w_bytes + kv_bytes) / (ms_per_tok * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                   "model_create_s": t_create,
+                   "decode_launch": "eager kernel launches" if args.eager else "HIP graph replay"},
+        "roofline": {"kernel": "chn_fused_mlp_q4 = k_xplanes + k_q4mv<MLP> (gate/up + GELU-tanh, 15360x3840 x2)",
+                     "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": load_traffic("k_q4mv<MLP>", "decode"),
+                     "algorithmic_bytes_per_launch": gateup_bytes(H, I), "avg_launch_ms": k_ms},
+        "cpu_baseline": cpu,
+        "dtype": "fp32 accumulate over Q4 weights (Q8 logits)",
+        "data": "synthetic (seeded random-init 12B Q4 weights: codes uniform 0..15, f16 scales "
+                "U(0.005, 0.02), norms 1, bf16 embedding ~ N(0, 0.02) tied to Q8 logits; prompt of "
+                "uniform random token ids)",
     }
 
 
@@ -301,24 +521,32 @@ def bench_attn(ctx, args):
     }
 
 
-WORKLOADS = {"mlp": bench_mlp, "gemv": bench_gemv, "prefill": bench_prefill, "attn": bench_attn}
+WORKLOADS = {"decode": bench_decode, "mlp": bench_mlp, "gemv": bench_gemv, "prefill": bench_prefill,
+             "attn": bench_attn}
+DEFAULT_STEPS = {"decode": (256, 8)}
 
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="mlp", choices=sorted(WORKLOADS))
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--workload", default="decode", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--eager", action="store_true",
+                    help="decode: launch the kernels one by one instead of replaying the graph")
     args = ap.parse_args()
+    d_steps, d_warm = DEFAULT_STEPS.get(args.workload, (200, 20))
+    args.steps = d_steps if args.steps is None else args.steps
+    args.warmup = d_warm if args.warmup is None else args.warmup
+    if args.steps < 1 or args.warmup < 0:
+        ap.error("--steps must be >= 1 and --warmup >= 0")
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures the single-GPU hot path only: run it with --gpus 1 "
-              "(this build has no multi-GPU path; see DESIGN.md for how it would shard).",
-              file=sys.stderr)
+        print("bench.py measures the single-GPU hot path only; run it with --gpus 1 "
+              "(there is no multi-GPU path to measure).", file=sys.stderr)
         sys.exit(2)
 
     import __graft_entry__
@@ -339,8 +567,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": r["dtype"],
-        "data": "synthetic (seeded; Q4 codes uniform 0..15, f16 scales U(0.005, 0.02), "
-                "x ~ N(0,1))",
+        "data": r.get("data", "synthetic (seeded; Q4 codes uniform 0..15, f16 scales U(0.005, 0.02), "
+                              "x ~ N(0,1))"),
         "config": r["config"],
         "roofline": r["roofline"],
         "cpu_baseline": r["cpu_baseline"],

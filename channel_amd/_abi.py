@@ -67,6 +67,7 @@ PROTOTYPES = {
     "chn_model_destroy": (None, [c_void_p]),
     "chn_model_get_config": (c_int, [c_void_p, c_void_p]),
     "chn_model_embedding_bf16": (c_int, [c_void_p, P(c_void_p)]),
+    "chn_model_set_graph": (c_int, [c_void_p, c_int]),
     "chn_decode_step": (c_int, [c_void_p, c_void_p, c_u32, c_u32, c_void_p, c_u32, c_void_p, c_u32,
                                 c_void_p, c_void_p, P(c_u32)]),
     "chn_decode_token": (c_int, [c_void_p, c_u32, c_u32, c_u32, c_void_p, c_u32, c_void_p, c_u32,

@@ -53,6 +53,7 @@ struct chn_model {
     uint32_t *h_slots = nullptr, *h_step = nullptr, *h_ids = nullptr;
     float *h_vals = nullptr;
     hipGraphExec_t exec[2] = {nullptr, nullptr};   // [0] without logits, [1] with
+    bool use_graph = true;                          // false: launch the kernels one by one
     std::vector<void *> allocs;
 };
 
@@ -406,6 +407,13 @@ fail:
 
 extern "C" void chn_model_destroy(chn_model *m) { free_model(m); }
 
+extern "C" int chn_model_set_graph(chn_model *m, int enabled) {
+    if (!m) return CHN_E_INVALID;
+    CHN_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    m->use_graph = enabled != 0;
+    return CHN_OK;
+}
+
 extern "C" int chn_model_embedding_bf16(chn_model *m, const uint16_t **table) {
     if (!m || !table) return CHN_E_INVALID;
     *table = m->embed_bf16;
@@ -441,7 +449,12 @@ static int decode_run(chn_model *m, uint32_t clock, uint32_t slot_idx, const uin
                                     hipMemcpyHostToDevice, s));
     CHN_HIP(ctx, hipMemcpyAsync(m->step, m->h_step, 16, hipMemcpyHostToDevice, s));
     const bool wl = topk_ids != nullptr;
-    CHN_HIP(ctx, hipGraphLaunch(m->exec[wl ? 1 : 0], s));
+    if (m->use_graph) {
+        CHN_HIP(ctx, hipGraphLaunch(m->exec[wl ? 1 : 0], s));
+    } else {
+        int rc = record_decode(m, wl);
+        if (rc) return rc;
+    }
     CHN_HIP(ctx, hipMemcpyAsync(m->h_ids, m->topk_ids, 64 * 4, hipMemcpyDeviceToHost, s));
     CHN_HIP(ctx, hipMemcpyAsync(m->h_vals, m->topk_vals, 64 * 4, hipMemcpyDeviceToHost, s));
     CHN_HIP(ctx, hipStreamSynchronize(s));

@@ -116,6 +116,11 @@ class Model:
             raise ChannelError("chn_model_create_synthetic", rc, lib.chn_last_error(ctx.handle).decode())
         return cls(ctx, h.value)
 
+    def set_graph(self, enabled):
+        """Replay the recorded decode graph (default) or launch its kernels
+        one by one."""
+        self._check("chn_model_set_graph", lib.chn_model_set_graph(self.handle, 1 if enabled else 0))
+
     @staticmethod
     def _slots(s):
         a = np.ascontiguousarray(s if s is not None else [], dtype=np.uint32)

@@ -269,6 +269,11 @@ void chn_model_destroy(chn_model *m);
 
 int chn_model_get_config(const chn_model *m, chn_model_config *cfg);
 
+/* Decode launch mode: enabled != 0 (default) replays the recorded graph;
+ * 0 launches the same kernels one by one on the stream (for tools that do
+ * not follow graph launches).  No reference counterpart. */
+int chn_model_set_graph(chn_model *m, int enabled);
+
 /* Device pointer to the synthetic model's bf16 embedding (NULL otherwise). */
 int chn_model_embedding_bf16(chn_model *m, const uint16_t **table);
 

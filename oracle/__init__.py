@@ -53,6 +53,7 @@ _PROTOS = {
     "orc_synth_normal": (None, [_f32p, _size, _u64, _f32]),
     "orc_gemv_q4_mt": (None, [_u32p, _f32p, _f32p, _u32, _u32, _int]),
     "orc_fused_mlp_step_mt": (None, [_u32p, _u32p, _u32p, _f32p, _f32p, _f32p, _u32, _u32, _int]),
+    "orc_gemv_q8_mt": (None, [_u32p, _f32p, _f32p, _u32, _u32, _int]),
 }
 
 
@@ -152,6 +153,12 @@ def fused_mlp_step_mt(Wg, Wu, Wd, x, H, I, nthreads):
     lib.orc_fused_mlp_step_mt(_c(Wg, np.uint32), _c(Wu, np.uint32), _c(Wd, np.uint32),
                               _c(x, np.float32), act, y, H, I, int(nthreads))
     return act, y
+
+
+def gemv_q8_mt(W, x, M, K, nthreads):
+    y = np.zeros(M, dtype=np.float32)
+    lib.orc_gemv_q8_mt(_c(W, np.uint32), _c(x, np.float32), y, M, K, int(nthreads))
+    return y
 
 
 def gemv_q8(W, x, M, K):

@@ -287,37 +287,38 @@ void orc_fused_mlp_q4(const uint32_t *Wg, const uint32_t *Wu, const float *x,
  * word-pair); acc += s * sum of 8 int8*x; 16..1 tree.  The shader reads
  * blocks base+0..7 without a bound; here blocks >= K/32 are skipped (all
  * live calls have K/32 % 8 == 0, where the two agree). */
+static float gemv_q8_row(const uint32_t *Wrow, const float *x, uint32_t nb) {
+    float lanes[32];
+    for (uint32_t lane = 0; lane < 32; ++lane) {
+        uint32_t bi = lane >> 2, sub = lane & 3u;
+        float acc = 0.0f;
+        for (uint32_t base = 0; base < nb; base += 8) {
+            uint32_t b = base + bi;
+            if (b >= nb) continue;
+            const uint32_t *blk = Wrow + b * 9;
+            float s;
+            memcpy(&s, &blk[0], 4);
+            uint32_t wa = blk[1 + sub * 2], wb = blk[2 + sub * 2];
+            const float *xv = x + b * 32 + sub * 8;
+            float sum = 0.0f;
+            for (int i = 0; i < 8; ++i) {
+                uint32_t w = i < 4 ? wa : wb;
+                float q = (float)(int8_t)((w >> (8 * (i & 3))) & 0xffu);
+                float p = q * xv[i];
+                sum = (i == 0) ? p : sum + p;
+            }
+            acc = acc + s * sum;
+        }
+        lanes[lane] = acc;
+    }
+    for (uint32_t off = 16; off >= 1; off >>= 1)
+        for (uint32_t l = 0; l < off; ++l) lanes[l] = lanes[l] + lanes[l + off];
+    return lanes[0];
+}
+
 void orc_gemv_q8(const uint32_t *W, const float *x, float *y, uint32_t M, uint32_t K) {
     uint32_t nb = K / 32;
-    for (uint32_t r = 0; r < M; ++r) {
-        const uint32_t *Wrow = W + (size_t)r * nb * 9;
-        float lanes[32];
-        for (uint32_t lane = 0; lane < 32; ++lane) {
-            uint32_t bi = lane >> 2, sub = lane & 3u;
-            float acc = 0.0f;
-            for (uint32_t base = 0; base < nb; base += 8) {
-                uint32_t b = base + bi;
-                if (b >= nb) continue;
-                const uint32_t *blk = Wrow + b * 9;
-                float s;
-                memcpy(&s, &blk[0], 4);
-                uint32_t wa = blk[1 + sub * 2], wb = blk[2 + sub * 2];
-                const float *xv = x + b * 32 + sub * 8;
-                float sum = 0.0f;
-                for (int i = 0; i < 8; ++i) {
-                    uint32_t w = i < 4 ? wa : wb;
-                    float q = (float)(int8_t)((w >> (8 * (i & 3))) & 0xffu);
-                    float p = q * xv[i];
-                    sum = (i == 0) ? p : sum + p;
-                }
-                acc = acc + s * sum;
-            }
-            lanes[lane] = acc;
-        }
-        for (uint32_t off = 16; off >= 1; off >>= 1)
-            for (uint32_t l = 0; l < off; ++l) lanes[l] = lanes[l] + lanes[l + off];
-        y[r] = lanes[0];
-    }
+    for (uint32_t r = 0; r < M; ++r) y[r] = gemv_q8_row(W + (size_t)r * nb * 9, x, nb);
 }
 
 /* ======================================================================
@@ -728,7 +729,7 @@ typedef struct {
     const float *x;
     float *y;
     uint32_t rows, nb, chunk;
-    int mlp;
+    int mode;   /* 0 Q4 matvec, 1 fused gate/up, 2 Q8 matvec */
     atomic_uint next;
 } pool_job_t;
 
@@ -739,8 +740,12 @@ static void run_chunks(pool_job_t *j) {
         if (s >= j->rows) return;
         uint32_t e = (uint32_t)(s + j->chunk < j->rows ? s + j->chunk : j->rows);
         for (uint32_t r = (uint32_t)s; r < e; ++r) {
+            if (j->mode == 2) {
+                j->y[r] = gemv_q8_row(j->W + (size_t)r * j->nb * 9, j->x, j->nb);
+                continue;
+            }
             float g = gemv_q4_row(j->W + (size_t)r * j->nb * 5, j->x, j->nb);
-            if (j->mlp) {
+            if (j->mode == 1) {
                 float u = gemv_q4_row(j->W2 + (size_t)r * j->nb * 5, j->x, j->nb);
                 j->y[r] = orc_gelu_tanh(g) * u;
             } else {
@@ -773,7 +778,7 @@ void orc_gemv_q4_mt(const uint32_t *W, const float *x, float *y, uint32_t M,
                     uint32_t K, int nthreads) {
     pool_job_t j;
     memset(&j, 0, sizeof(j));
-    j.W = W; j.x = x; j.y = y; j.rows = M; j.nb = K / 32; j.mlp = 0;
+    j.W = W; j.x = x; j.y = y; j.rows = M; j.nb = K / 32; j.mode = 0;
     run_pool(&j, nthreads);
 }
 
@@ -782,7 +787,15 @@ void orc_fused_mlp_step_mt(const uint32_t *Wg, const uint32_t *Wu,
                            float *y, uint32_t H, uint32_t I, int nthreads) {
     pool_job_t j;
     memset(&j, 0, sizeof(j));
-    j.W = Wg; j.W2 = Wu; j.x = x; j.y = act; j.rows = I; j.nb = H / 32; j.mlp = 1;
+    j.W = Wg; j.W2 = Wu; j.x = x; j.y = act; j.rows = I; j.nb = H / 32; j.mode = 1;
     run_pool(&j, nthreads);
     orc_gemv_q4_mt(Wd, act, y, H, I, nthreads);
+}
+
+void orc_gemv_q8_mt(const uint32_t *W, const float *x, float *y, uint32_t M,
+                    uint32_t K, int nthreads) {
+    pool_job_t j;
+    memset(&j, 0, sizeof(j));
+    j.W = W; j.x = x; j.y = y; j.rows = M; j.nb = K / 32; j.mode = 2;
+    run_pool(&j, nthreads);
 }

@@ -105,6 +105,8 @@ void orc_gemv_q4_mt(const uint32_t *W, const float *x, float *y, uint32_t M,
 void orc_fused_mlp_step_mt(const uint32_t *Wg, const uint32_t *Wu,
                            const uint32_t *Wd, const float *x, float *act,
                            float *y, uint32_t H, uint32_t I, int nthreads);
+void orc_gemv_q8_mt(const uint32_t *W, const float *x, float *y, uint32_t M,
+                    uint32_t K, int nthreads);
 
 #ifdef __cplusplus
 }

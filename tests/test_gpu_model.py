@@ -186,3 +186,21 @@ def test_synthetic_model_token_path(ctx):
             tok = int(t1)
             row = ctx.download(p.value + tok * H * 2, np.uint16, H)
             x_in = OM.bf16_to_f32(row) * np.float32(np.sqrt(np.float32(H)))
+
+
+def test_eager_launches_match_graph(ctx):
+    """chn_model_set_graph(0) launches the decode kernels one by one; the
+    results are bit-identical to the graph replay."""
+    cfg = dict(CFG, num_layers=2, layer_full=[0, 1])
+    say("eager vs graph decode")
+    with Model.synthetic(ctx, cfg, 77) as mg, Model.synthetic(ctx, cfg, 77) as me:
+        me.set_graph(False)
+        tok_g = tok_e = 5
+        for clock in range(4):
+            active, sliding = OM.slot_lists(clock, WINDOW)
+            tok_g, ids_g, vals_g = mg.forward_token_id(tok_g, clock, clock, active, sliding)
+            tok_e, ids_e, vals_e = me.forward_token_id(tok_e, clock, clock, active, sliding)
+            assert np.array_equal(ids_g, ids_e) and np.array_equal(vals_g, vals_e)
+            xg, ng = mg.read_state()
+            xe, ne = me.read_state()
+            assert np.array_equal(xg, xe) and np.array_equal(ng, ne)
