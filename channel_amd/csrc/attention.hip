@@ -1,27 +1,37 @@
-// Decode attention over the ring-buffer slot list (shaders/decode_attn.wgsl)
-// and the per-head RMSNorm + RoPE + KV-cache write (shaders/qkv_rope.wgsl).
+// Decode attention over the ring-buffer slot list (shaders/decode_attn.wgsl),
+// prefill causal attention (shaders/batch_causal_attn.wgsl) and the
+// per-head RMSNorm + RoPE + KV-cache write (shaders/qkv_rope.wgsl).
 //
-// Decode attention is split over the slot list ("flash-decoding"): a
-// workgroup takes one KV head and a chunk of 64 slots, serves all of that
-// head's GQA query heads from one pass over K and V (1 KB contiguous rows,
-// one coalesced 16-byte load per lane per row), and leaves a partial
-// (max m, sum l, sum p*V) per query head; a second kernel merges the
-// chunks.  The merged result equals the reference's two-pass softmax
-// p_i = exp(s_i - max) / (sum exp(s_j - max) + 1e-9) up to rounding.  The
-// slot count is read from device memory, so a captured graph can be
-// replayed with a new count.
+// Decode attention is split over the slot list ("flash-decoding").  The
+// slot count S is read from device memory (so a captured graph replays with
+// a new count) and the list is cut into at most 64 chunks of
+// max(16, ceil(S / 64)) slots, so short contexts still spread over many
+// workgroups.  A workgroup takes one KV head and one chunk and serves all of
+// that head's GQA query heads from one pass over K and V: each 16-lane row
+// of a wave owns one slot at a time (a 1 KB row, 64 contiguous bytes per
+// lane), scores reduce inside the row with DPP, and each wave keeps its own
+// online softmax state, so the loop has no barriers.  The four waves merge
+// in LDS into one partial (m, l, sum p*V) per query head; the last
+// workgroup of a KV head to finish (an agent-scope counter) merges the
+// partials in a fixed order, writes the output and, optionally, its
+// activation digit planes for the o_proj matvec.  The result equals the
+// reference's two-pass softmax p_i = exp(s_i - max) / (sum exp(s_j - max) +
+// 1e-9) up to rounding.
 #include "chn_internal.h"
 
 namespace chn {
 
-constexpr int kAttnChunk = 64;   // slots per workgroup
+constexpr int kAttnChunk = 64;     // prefill: slots per online-softmax step
+constexpr int kDecSplits = 64;     // decode: most chunks per KV head
 constexpr float kNegBig = -1e30f;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
+// Decode workspace: partial sums [64][num_q_heads][head_dim], then maxima
+// and sums [64][num_q_heads].
 size_t attn_ws_bytes(uint32_t num_q_heads, uint32_t head_dim, uint32_t max_slots) {
-    const size_t nsplit = (max_slots + kAttnChunk - 1) / kAttnChunk;
-    return nsplit * num_q_heads * ((size_t)head_dim + 2) * 4;
+    (void)max_slots;
+    return (size_t)kDecSplits * num_q_heads * ((size_t)head_dim + 2) * 4;
 }
 
 // Sum over the 16 lanes of each DPP row; every lane of the row gets the sum.
@@ -188,47 +198,319 @@ __device__ __forceinline__ void load_q(f4 (&q)[GQA][4 * DV], const float *__rest
         for (int f = 0; f < 4 * DV; ++f) q[h][f] = *(const f4 *)(Q + (size_t)(qh0 + h) * D + c * 16 * DV + 4 * f);
 }
 
-// Decode: one workgroup per (64-slot chunk, KV head) writes a partial
-// (m, l, sum p*V) per query head: acc [nsplit][num_q_heads][D], then m and l.
-template <int DV, int GQA>
-__global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ Q, const float *__restrict__ Kc,
-                                                    const float *__restrict__ Vc,
-                                                    const uint32_t *__restrict__ slots,
-                                                    const uint32_t *__restrict__ n_slots, uint32_t max_slots,
-                                                    uint32_t num_q_heads, uint32_t kv_dim, float scale,
-                                                    float *__restrict__ ws) {
+// Inputs of the fused per-head RMSNorm + RoPE of the decode step
+// (shaders/qkv_rope.wgsl): raw q/k/v from the QKV matvec, norm weights,
+// device {clock, slot_idx}.
+struct RopeArgs {
+    const float *k_in, *v_in, *qw, *kw;
+    const uint32_t *step;
+    uint32_t rot;
+    float theta, eps;
+    int k_eq_v;
+};
+
+// One wave: RMSNorm (times w, or unit with w == NULL) of the D values at
+// `in` into LDS row `dst` (lane holds d = lane + 64 j).
+template <int D>
+__device__ __forceinline__ void wave_norm_to_lds(const float *__restrict__ in, const float *__restrict__ w,
+                                                 float *dst, float eps, int lane) {
+    float v[D / 64];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < D / 64; ++j) {
+        v[j] = in[lane + 64 * j];
+        ss += v[j] * v[j];
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+#pragma unroll
+    for (int j = 0; j < D / 64; ++j) {
+        const float n = v[j] * inv;
+        dst[lane + 64 * j] = w ? n * w[lane + 64 * j] : n;
+    }
+}
+
+// One wave: RoPE over pairs (d, d + rot/2) of an LDS row in place,
+// freq = 1 / theta^(2d / rot), angle = clock * freq.
+__device__ __forceinline__ void wave_rope_lds(float *row, uint32_t rot, float theta, uint32_t clock, int lane) {
+    const uint32_t half = rot / 2;
+    for (uint32_t d = lane; d < half; d += 64) {
+        const float v0 = row[d], v1 = row[d + half];
+        const float fe = (2.0f * (float)d) / (float)rot;
+        const float freq = 1.0f / powf(theta, fe);
+        const float ang = (float)clock * freq;
+        float sn, cs;
+        sincosf(ang, &sn, &cs);
+        row[d] = v0 * cs - v1 * sn;
+        row[d + half] = v0 * sn + v1 * cs;
+    }
+}
+
+// Decode: workgroup (split, KV head).  IT slots per row are loaded at once
+// (all K rows, then all V rows, before any arithmetic).  With ROPE, Q holds
+// the raw q of the QKV matvec: every workgroup normalises and rotates its
+// GQA query heads and the new token's K (and normalises its V) in LDS,
+// uses them in place of the cache row of slot_idx, and split 0 writes them
+// to the caches.
+template <int DV, int GQA, bool ROPE>
+__global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q, float *Kc, float *Vc,
+                                                     const uint32_t *__restrict__ slots,
+                                                     const uint32_t *__restrict__ n_slots, uint32_t max_slots,
+                                                     uint32_t num_q_heads, uint32_t kv_dim, float scale,
+                                                     float *__restrict__ ws, RopeArgs ra) {
     constexpr int D = DV * 256;
+    constexpr int NF = 4 * DV;          // float4 per lane per row
+    constexpr int IT = (GQA >= 4 ? 2 : 4) / DV;   // slots per row per batch (register budget)
     const uint32_t split = blockIdx.x, kvh = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r = lane >> 4, c = lane & 15;
+    const uint32_t qh0 = kvh * GQA;
+
+    __shared__ f4 sh_acc[4][GQA][D / 4];
+    __shared__ float sh_m[4][GQA], sh_l[4][GQA];
+    __shared__ float sh_q[ROPE ? GQA : 1][ROPE ? D : 4];
+    __shared__ float sh_k[ROPE ? D : 4], sh_v[ROPE ? D : 4];
+
     uint32_t S = *n_slots;
     if (S > max_slots) S = max_slots;
-    const uint32_t s0 = split * kAttnChunk;
-    if (s0 >= S) return;
-    const uint32_t cnt = (S - s0 < (uint32_t)kAttnChunk) ? S - s0 : kAttnChunk;
-    const uint32_t nsplit = (max_slots + kAttnChunk - 1) / kAttnChunk;
-    __shared__ float sc[GQA][kAttnChunk];
-    __shared__ f4 pacc[16][GQA < 2 ? GQA : 2][64 * DV];
+    uint32_t chunk = (S + kDecSplits - 1) / kDecSplits;
+    chunk = (chunk + 15) & ~15u;
+    const uint32_t nsp = S ? (S + chunk - 1) / chunk : 0;
+    // split 0 always runs when it has to write the new token's K/V
+    if (split >= nsp && !(ROPE && split == 0)) return;
+    const uint32_t c0 = split * chunk;
+    const uint32_t c1 = (c0 + chunk < S) ? c0 + chunk : S;
+    const uint32_t nit = split < nsp ? (c1 - c0 + 15) / 16 : 0;   // 16-slot steps; row r of wave w: slot 4w + r
+    const uint32_t clock = ROPE ? ra.step[0] : 0u, new_slot = ROPE ? ra.step[1] : 0xFFFFFFFFu;
+    const size_t dim0 = (size_t)kvh * D + (size_t)c * 4 * NF;
 
-    f4 q[GQA][4 * DV];
-    load_q<DV, GQA>(q, Q, kvh * GQA);
-    AttnState<DV, GQA> st;
+    f4 kr[IT][NF], vr[IT][NF];
+    bool ok[IT], fresh[IT];
+    auto load_batch = [&](uint32_t jb) {
+        uint32_t ps[IT];
+#pragma unroll
+        for (int u = 0; u < IT; ++u) {
+            const uint32_t i = c0 + 16 * (jb + u) + 4 * wave + r;
+            ok[u] = (jb + u < nit) && i < c1;
+            ps[u] = ok[u] ? slots[i] : 0u;
+            fresh[u] = ROPE && ok[u] && ps[u] == new_slot;
+        }
+#pragma unroll
+        for (int u = 0; u < IT; ++u) {
+            const float *kp = Kc + (size_t)ps[u] * kv_dim + dim0;
+#pragma unroll
+            for (int f = 0; f < NF; ++f) kr[u][f] = (ok[u] && !fresh[u]) ? *(const f4 *)(kp + 4 * f) : f4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < IT; ++u) {
+            const float *vp = Vc + (size_t)ps[u] * kv_dim + dim0;
+#pragma unroll
+            for (int f = 0; f < NF; ++f) vr[u][f] = (ok[u] && !fresh[u]) ? *(const f4 *)(vp + 4 * f) : f4{0, 0, 0, 0};
+        }
+    };
+    auto take_fresh = [&]() {
+        if (ROPE) {
+#pragma unroll
+            for (int u = 0; u < IT; ++u)
+                if (fresh[u]) {
+#pragma unroll
+                    for (int f = 0; f < NF; ++f) {
+                        kr[u][f] = *(const f4 *)&sh_k[c * 4 * NF + 4 * f];
+                        vr[u][f] = *(const f4 *)&sh_v[c * 4 * NF + 4 * f];
+                    }
+                }
+        }
+    };
+    load_batch(0);
+
+    f4 q[GQA][NF];
+    if (ROPE) {
+        // items: GQA query heads, the new K head, the new V head
+        const float *vsrc = ra.k_eq_v ? ra.k_in : ra.v_in;
+        for (int it = wave; it < GQA + 2; it += 4) {
+            if (it < GQA) wave_norm_to_lds<D>(Q + (size_t)(qh0 + it) * D, ra.qw, sh_q[it], ra.eps, lane);
+            else if (it == GQA) wave_norm_to_lds<D>(ra.k_in + (size_t)kvh * D, ra.kw, sh_k, ra.eps, lane);
+            else wave_norm_to_lds<D>(vsrc + (size_t)kvh * D, nullptr, sh_v, ra.eps, lane);
+        }
+        __syncthreads();
+        for (int it = wave; it < GQA + 1; it += 4)
+            wave_rope_lds(it < GQA ? sh_q[it] : sh_k, ra.rot, ra.theta, clock, lane);
+        __syncthreads();
+        if (split == 0) {
+            float *kd = Kc + (size_t)new_slot * kv_dim + (size_t)kvh * D;
+            float *vd = Vc + (size_t)new_slot * kv_dim + (size_t)kvh * D;
+            for (int d = threadIdx.x; d < D; d += 256) {
+                kd[d] = sh_k[d];
+                vd[d] = sh_v[d];
+            }
+        }
+        if (split >= nsp) return;
+#pragma unroll
+        for (int h = 0; h < GQA; ++h)
+#pragma unroll
+            for (int f = 0; f < NF; ++f) q[h][f] = *(const f4 *)&sh_q[h][c * 4 * NF + 4 * f];
+    } else {
+#pragma unroll
+        for (int h = 0; h < GQA; ++h)
+#pragma unroll
+            for (int f = 0; f < NF; ++f) q[h][f] = *(const f4 *)(Q + (size_t)(qh0 + h) * D + c * 4 * NF + 4 * f);
+    }
+
+    float M[GQA], L[GQA];
+    f4 acc[GQA][NF];
 #pragma unroll
     for (int h = 0; h < GQA; ++h) {
-        st.M[h] = -1e9f;
-        st.l[h] = 0.0f;
+        M[h] = kNegBig;
+        L[h] = 0.0f;
 #pragma unroll
-        for (int f = 0; f < 4 * DV; ++f) st.acc[h][f] = f4{0, 0, 0, 0};
+        for (int f = 0; f < NF; ++f) acc[h][f] = f4{0, 0, 0, 0};
     }
-    attn_chunk<DV, GQA>(st, q, Kc, Vc, slots, s0, cnt, kv_dim, kvh, scale, sc);
+    for (uint32_t jb = 0; jb < nit; jb += IT) {
+        if (jb > 0) load_batch(jb);
+        take_fresh();
+#pragma unroll
+        for (int h = 0; h < GQA; ++h) {
+            float sc[IT];
+            float mx = kNegBig;
+#pragma unroll
+            for (int u = 0; u < IT; ++u) {
+                float d = 0.0f;
+#pragma unroll
+                for (int f = 0; f < NF; ++f) {
+                    d = fmaf(q[h][f].x, kr[u][f].x, d);
+                    d = fmaf(q[h][f].y, kr[u][f].y, d);
+                    d = fmaf(q[h][f].z, kr[u][f].z, d);
+                    d = fmaf(q[h][f].w, kr[u][f].w, d);
+                }
+                sc[u] = ok[u] ? row16_sum(d) * scale : kNegBig;
+                mx = fmaxf(mx, sc[u]);
+            }
+            // the wave's four rows
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float Mn = fmaxf(M[h], mx);
+            const float rs = expf(M[h] - Mn);
+            float ps_sum = 0.0f;
+#pragma unroll
+            for (int f = 0; f < NF; ++f) acc[h][f] *= rs;
+#pragma unroll
+            for (int u = 0; u < IT; ++u) {
+                const float p = ok[u] ? expf(sc[u] - Mn) : 0.0f;
+                ps_sum += p;
+#pragma unroll
+                for (int f = 0; f < NF; ++f) acc[h][f] += p * vr[u][f];
+            }
+            ps_sum += __shfl_xor(ps_sum, 16, 64);
+            ps_sum += __shfl_xor(ps_sum, 32, 64);
+            L[h] = L[h] * rs + ps_sum;
+            M[h] = Mn;
+        }
+    }
+    // rows of the wave hold different slots of the same columns
+#pragma unroll
+    for (int h = 0; h < GQA; ++h)
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            f4 t = acc[h][f];
+            t.x += __shfl_xor(t.x, 16, 64); t.y += __shfl_xor(t.y, 16, 64);
+            t.z += __shfl_xor(t.z, 16, 64); t.w += __shfl_xor(t.w, 16, 64);
+            t.x += __shfl_xor(t.x, 32, 64); t.y += __shfl_xor(t.y, 32, 64);
+            t.z += __shfl_xor(t.z, 32, 64); t.w += __shfl_xor(t.w, 32, 64);
+            if (r == 0) sh_acc[wave][h][c * NF + f] = t;
+        }
+    if (lane < GQA) {
+        sh_m[wave][lane] = M[lane];
+        sh_l[wave][lane] = L[lane];
+    }
+    __syncthreads();
+
+    // workgroup partial for this chunk
     float *wacc = ws;
-    float *wm = ws + (size_t)nsplit * num_q_heads * D;
-    float *wl = wm + (size_t)nsplit * num_q_heads;
-    attn_reduce<DV, GQA>(st, pacc, [&](int h, int col, f4 t) {
-        *(f4 *)(wacc + ((size_t)split * num_q_heads + kvh * GQA + h) * D + 4 * col) = t;
-    });
-    if (threadIdx.x < GQA) {
-        const uint32_t qh = kvh * GQA + threadIdx.x;
-        wm[(size_t)split * num_q_heads + qh] = st.M[threadIdx.x];
-        wl[(size_t)split * num_q_heads + qh] = st.l[threadIdx.x];
+    float *wm = ws + (size_t)kDecSplits * num_q_heads * D;
+    float *wl = wm + (size_t)kDecSplits * num_q_heads;
+    for (int idx = threadIdx.x; idx < GQA * (D / 4); idx += 256) {
+        const int h = idx / (D / 4), col = idx % (D / 4);
+        float Mw = -1e9f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) Mw = fmaxf(Mw, sh_m[w][h]);
+        f4 t = f4{0, 0, 0, 0};
+        float lw = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float e = expf(sh_m[w][h] - Mw);
+            t += e * sh_acc[w][h][col];
+            lw += e * sh_l[w][h];
+        }
+        *(f4 *)(wacc + ((size_t)split * num_q_heads + qh0 + h) * D + 4 * col) = t;
+        if (col == 0) {
+            wm[(size_t)split * num_q_heads + qh0 + h] = Mw;
+            wl[(size_t)split * num_q_heads + qh0 + h] = lw;
+        }
+    }
+}
+
+// Merge of the chunk partials, one 256-thread workgroup per query head:
+// weights exp(m_j - M) once (wave 0), then the weighted sum of the partial
+// rows in chunk order (four chunks per batch of loads), the output row and,
+// for the o_proj matvec, its digit planes.  S = 0 gives a zero row.
+template <int DV>
+__global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ ws,
+                                                    const uint32_t *__restrict__ n_slots, uint32_t max_slots,
+                                                    uint32_t num_q_heads, float *__restrict__ out,
+                                                    uint32_t *__restrict__ xp, uint32_t xp_nb) {
+    constexpr int D = DV * 256;
+    __shared__ float ew[kDecSplits];
+    __shared__ float sinv;
+    __shared__ f4 part[4][D / 4];
+    const uint32_t qh = blockIdx.x;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    uint32_t S = *n_slots;
+    if (S > max_slots) S = max_slots;
+    uint32_t chunk = (S + kDecSplits - 1) / kDecSplits;
+    chunk = (chunk + 15) & ~15u;
+    const uint32_t ns = S ? (S + chunk - 1) / chunk : 0;
+    const float *wacc = ws;
+    const float *wm = ws + (size_t)kDecSplits * num_q_heads * D;
+    const float *wl = wm + (size_t)kDecSplits * num_q_heads;
+    if (wave == 0) {
+        const bool v = (uint32_t)lane < ns;
+        const float mj = v ? wm[(size_t)lane * num_q_heads + qh] : kNegBig;
+        const float M = fmaxf(wave_max64(mj), -1e9f);
+        const float e = v ? expf(mj - M) : 0.0f;
+        const float L = wave_sum64(v ? e * wl[(size_t)lane * num_q_heads + qh] : 0.0f);
+        ew[lane] = e;
+        if (lane == 0) sinv = 1.0f / (L + 1e-9f);
+    }
+    __syncthreads();
+    // wave w sums chunks w, w + 4, ... for columns lane, lane + 64
+    for (uint32_t col = lane; col < (uint32_t)D / 4; col += 64) {
+        f4 t = f4{0, 0, 0, 0};
+        const float *src = wacc + (size_t)qh * D + 4 * col;
+        const size_t stride = (size_t)num_q_heads * D;
+        uint32_t j = wave;
+        for (; j + 12 < ns; j += 16) {
+            f4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = *(const f4 *)(src + (j + 4 * u) * stride);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) t += ew[j + 4 * u] * v[u];
+        }
+        for (; j < ns; j += 4) t += ew[j] * *(const f4 *)(src + j * stride);
+        part[wave][col] = t;
+    }
+    __syncthreads();
+    const uint32_t k = threadIdx.x;        // eight values per thread: D / 8 threads
+    if (k < (uint32_t)D / 8) {
+        float o[8];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const uint32_t col = 2 * k + hf;
+            const f4 t = (((part[0][col] + part[1][col]) + part[2][col]) + part[3][col]) * sinv;
+            o[4 * hf + 0] = t.x; o[4 * hf + 1] = t.y; o[4 * hf + 2] = t.z; o[4 * hf + 3] = t.w;
+            *(f4 *)(out + (size_t)qh * D + 4 * col) = t;
+        }
+        if (xp) emit_planes8(o, xp, xp_nb, qh * (D / 32) + (k >> 2), k & 3, true);
     }
 }
 
@@ -270,69 +552,24 @@ __global__ __launch_bounds__(256) void k_prefill_attn(const float *__restrict__ 
     });
 }
 
-// One 256-thread workgroup per query head merges the chunk partials: chunk
-// weights exp(m_j - M) are computed once, then wave w sums chunks
-// j = w, w + 4, ... for every column with loads batched four at a time, and
-// the four wave sums are added in a fixed order.
-__global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ ws,
-                                                      const uint32_t *__restrict__ n_slots, uint32_t max_slots,
-                                                      uint32_t num_q_heads, uint32_t head_dim,
-                                                      float *__restrict__ out) {
-    __shared__ float ew[64];
-    __shared__ float sinv;
-    __shared__ f4 part[4][128];
-    const uint32_t qh = blockIdx.x;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    uint32_t S = *n_slots;
-    if (S > max_slots) S = max_slots;
-    const uint32_t nsplit_max = (max_slots + kAttnChunk - 1) / kAttnChunk;
-    const uint32_t ns = (S + kAttnChunk - 1) / kAttnChunk;     // <= 64
-    const float *wacc = ws;
-    const float *wm = ws + (size_t)nsplit_max * num_q_heads * head_dim;
-    const float *wl = wm + (size_t)nsplit_max * num_q_heads;
-    if (wave == 0) {
-        const float mj = (uint32_t)lane < ns ? wm[(size_t)lane * num_q_heads + qh] : -1e9f;
-        float M = mj;  // seeded at the reference's -1e9 by the padding lanes / the max below
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-        M = fmaxf(M, -1e9f);
-        const float e = (uint32_t)lane < ns ? expf(mj - M) : 0.0f;
-        float L = (uint32_t)lane < ns ? e * wl[(size_t)lane * num_q_heads + qh] : 0.0f;
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off, 64);
-        ew[lane] = e;
-        if (lane == 0) sinv = 1.0f / (L + 1e-9f);
-    }
-    __syncthreads();
-    const uint32_t ncol = head_dim / 4;          // float4 columns, <= 128
-    for (uint32_t c = lane; c < ncol; c += 64) {
-        f4 t = f4{0, 0, 0, 0};
-        uint32_t j = wave;
-        for (; j + 12 < ns; j += 16) {
-            f4 v[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                v[u] = *(const f4 *)(wacc + ((size_t)(j + 4 * u) * num_q_heads + qh) * head_dim + 4 * c);
-#pragma unroll
-            for (int u = 0; u < 4; ++u) t += ew[j + 4 * u] * v[u];
-        }
-        for (; j < ns; j += 4) t += ew[j] * *(const f4 *)(wacc + ((size_t)j * num_q_heads + qh) * head_dim + 4 * c);
-        part[wave][c] = t;
-    }
-    __syncthreads();
-    for (uint32_t c = threadIdx.x; c < ncol; c += 256)
-        *(f4 *)(out + (size_t)qh * head_dim + 4 * c) = (((part[0][c] + part[1][c]) + part[2][c]) + part[3][c]) * sinv;
-}
-
-int launch_decode_attn(chn_ctx *ctx, const float *q, const float *kc, const float *vc, const uint32_t *slots,
-                       const uint32_t *n_slots, uint32_t max_slots, uint32_t num_q_heads, uint32_t head_dim,
-                       uint32_t kv_dim, uint32_t gqa, float scale, float *out, float *ws) {
-    const uint32_t nsplit = (max_slots + kAttnChunk - 1) / kAttnChunk;
+static int launch_decode_impl(chn_ctx *ctx, const float *q, float *kc, float *vc, const uint32_t *slots,
+                              const uint32_t *n_slots, uint32_t max_slots, uint32_t num_q_heads, uint32_t head_dim,
+                              uint32_t kv_dim, uint32_t gqa, float scale, float *out, float *ws, uint32_t *xp,
+                              const RopeArgs *ra) {
     const uint32_t num_kv = num_q_heads / gqa;
-    dim3 grid(nsplit, num_kv);
+    const uint32_t xp_nb = num_q_heads * head_dim / 32;
+    dim3 grid(kDecSplits, num_kv);
     hipStream_t s = ctx->stream;
-#define CHN_ATTN(DV, G) \
-    k_attn_split<DV, G><<<grid, 256, 0, s>>>(q, kc, vc, slots, n_slots, max_slots, num_q_heads, kv_dim, scale, ws)
+    const RopeArgs rz = ra ? *ra : RopeArgs{nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0.0f, 0.0f, 0};
+#define CHN_ATTN(DV, G)                                                                                           \
+    do {                                                                                                          \
+        if (ra)                                                                                                   \
+            k_attn_decode<DV, G, true><<<grid, 256, 0, s>>>(q, kc, vc, slots, n_slots, max_slots, num_q_heads,    \
+                                                            kv_dim, scale, ws, rz);                               \
+        else                                                                                                      \
+            k_attn_decode<DV, G, false><<<grid, 256, 0, s>>>(q, kc, vc, slots, n_slots, max_slots, num_q_heads,   \
+                                                             kv_dim, scale, ws, rz);                              \
+    } while (0)
     if (head_dim == 256) {
         switch (gqa) {
         case 1: CHN_ATTN(1, 1); break;
@@ -352,10 +589,28 @@ int launch_decode_attn(chn_ctx *ctx, const float *q, const float *kc, const floa
         return set_err(ctx, CHN_E_UNSUPPORTED, "head_dim %u unsupported (256 or 512)", head_dim);
     }
 #undef CHN_ATTN
-    CHN_LAUNCHED(ctx, "k_attn_split");
-    k_attn_combine<<<num_q_heads, 256, 0, s>>>(ws, n_slots, max_slots, num_q_heads, head_dim, out);
-    CHN_LAUNCHED(ctx, "k_attn_combine");
+    CHN_LAUNCHED(ctx, "k_attn_decode");
+    if (head_dim == 256) k_attn_merge<1><<<num_q_heads, 256, 0, s>>>(ws, n_slots, max_slots, num_q_heads, out, xp, xp_nb);
+    else k_attn_merge<2><<<num_q_heads, 256, 0, s>>>(ws, n_slots, max_slots, num_q_heads, out, xp, xp_nb);
+    CHN_LAUNCHED(ctx, "k_attn_merge");
     return CHN_OK;
+}
+
+int launch_decode_attn(chn_ctx *ctx, const float *q, const float *kc, const float *vc, const uint32_t *slots,
+                       const uint32_t *n_slots, uint32_t max_slots, uint32_t num_q_heads, uint32_t head_dim,
+                       uint32_t kv_dim, uint32_t gqa, float scale, float *out, float *ws, uint32_t *xp) {
+    return launch_decode_impl(ctx, q, (float *)kc, (float *)vc, slots, n_slots, max_slots, num_q_heads, head_dim,
+                              kv_dim, gqa, scale, out, ws, xp, nullptr);
+}
+
+int launch_rope_decode_attn(chn_ctx *ctx, const float *q_in, const float *k_in, const float *v_in, const float *qw,
+                            const float *kw, float *kc, float *vc, const uint32_t *step, const uint32_t *slots,
+                            const uint32_t *n_slots, uint32_t max_slots, uint32_t num_q_heads, uint32_t head_dim,
+                            uint32_t kv_dim, uint32_t gqa, uint32_t rot, int k_eq_v, float theta, float eps,
+                            float scale, float *out, float *ws, uint32_t *xp) {
+    const RopeArgs ra{k_in, v_in, qw, kw, step, rot, theta, eps, k_eq_v};
+    return launch_decode_impl(ctx, q_in, kc, vc, slots, n_slots, max_slots, num_q_heads, head_dim, kv_dim, gqa, scale,
+                              out, ws, xp, &ra);
 }
 
 int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const float *vc, const uint32_t *slots,
@@ -539,7 +794,7 @@ extern "C" int chn_decode_attn(chn_ctx *ctx, const float *q, const float *k_cach
     int rc = ensure_workspace(ctx, attn_ws_bytes(num_q_heads, head_dim, max_slots));
     if (rc) return rc;
     return launch_decode_attn(ctx, q, k_cache, v_cache, slots, n_slots, max_slots, num_q_heads, head_dim,
-                              kv_dim, gqa_ratio, scale, out, (float *)ctx->ws);
+                              kv_dim, gqa_ratio, scale, out, (float *)ctx->ws, nullptr);
 }
 
 extern "C" int chn_batch_qkv_rope(chn_ctx *ctx, const float *q_in, const float *k_in, const float *v_in,

@@ -48,15 +48,35 @@ int ensure_workspace(chn_ctx *ctx, size_t bytes);
 
 inline bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
+// ---- activation digit planes (the matvec's input format)
+// Per 32-block b of an activation vector: X_i = rint(x_i * 2^(22 - e_b))
+// with |x_i| < 2^e_b, six balanced base-16 digits per X_i, each digit plane
+// packed as signed 4-bit lanes in the weights' nibble order.  Stored SoA:
+// u32 plane words at [(p * 4 + w) * nb + b] (p = plane, w = 8-element
+// word), then nb float scales 2^(e_b - 22).
+constexpr int XP_PLANES = 6;
+constexpr int XP_FRAC = 22;
+constexpr int XP_WORDS = XP_PLANES * 4;
+inline size_t xplanes_bytes(uint32_t nb) { return (size_t)nb * (XP_WORDS + 1) * 4; }
+
 // ---- internal launchers (explicit workspaces; usable under graph capture)
+// With planes_ready, `ws` already holds the digit planes of x (written by
+// the producing kernel) and the fast matvec path reads them directly; x is
+// still read by the general-shape path.
 size_t mv_ws_bytes(uint32_t K);
-int mv_gemv(chn_ctx *ctx, const uint32_t *W, const float *x, float *y, uint32_t M, uint32_t K, uint32_t *ws);
+int mv_gemv(chn_ctx *ctx, const uint32_t *W, const float *x, float *y, uint32_t M, uint32_t K, uint32_t *ws,
+            bool planes_ready = false);
 int mv_qkv(chn_ctx *ctx, const uint32_t *Wq, const uint32_t *Wk, const uint32_t *Wv, const float *x, float *q,
-           float *k, float *v, uint32_t q_dim, uint32_t kv_dim, uint32_t K, uint32_t *ws);
+           float *k, float *v, uint32_t q_dim, uint32_t kv_dim, uint32_t K, uint32_t *ws, bool planes_ready = false);
 int mv_mlp(chn_ctx *ctx, const uint32_t *Wg, const uint32_t *Wu, const float *x, float *act, uint32_t M, uint32_t K,
-           uint32_t *ws);
+           uint32_t *ws, bool planes_ready = false);
 int launch_rmsnorm(hipStream_t s, float *x, const float *r, const float *w, float *y, uint32_t dim, uint32_t rows,
                    float eps, float scalar, bool add);
+// Decode-step norm with planes: r' = post ? rmsnorm(r) * post_w : r;
+// x = add ? (x + r') * scalar : x; y = rmsnorm(x) * w; planes of y into xp
+// (if non-NULL).  One row, dim % 8 == 0, dim <= 8192.
+int launch_norm_planes(hipStream_t s, float *x, const float *r, const float *post_w, const float *w, float *y,
+                       uint32_t *xp, uint32_t dim, float eps, float scalar, bool add);
 int launch_qkv_rope(hipStream_t st, const float *q_in, const float *k_in, const float *v_in, const float *qw,
                     const float *kw, float *q_out, float *kc, float *vc, const uint32_t *step, uint32_t num_q,
                     uint32_t num_kv, uint32_t D, uint32_t rot, int k_eq_v, float theta, float eps);
@@ -65,9 +85,19 @@ int launch_batch_qkv_rope(hipStream_t st, const float *q_in, const float *k_in, 
                           uint32_t slot_offset, uint32_t start_clock, uint32_t n_tok, uint32_t num_q, uint32_t num_kv,
                           uint32_t D, uint32_t rot, int k_eq_v, float theta, float eps);
 size_t attn_ws_bytes(uint32_t num_q_heads, uint32_t head_dim, uint32_t max_slots);
+// ws holds attn_ws_bytes(); xp (nullable) receives the digit planes of out
+// (num_q_heads * head_dim / 32 blocks).
 int launch_decode_attn(chn_ctx *ctx, const float *q, const float *kc, const float *vc, const uint32_t *slots,
                        const uint32_t *n_slots, uint32_t max_slots, uint32_t num_q_heads, uint32_t head_dim,
-                       uint32_t kv_dim, uint32_t gqa, float scale, float *out, float *ws);
+                       uint32_t kv_dim, uint32_t gqa, float scale, float *out, float *ws, uint32_t *xp);
+// The decode step's qkv_rope fused into decode attention: q_in/k_in/v_in
+// are the raw QKV matvec outputs, step = {clock, slot_idx, ...} on the
+// device; the new token's K/V are written to the caches at slot_idx.
+int launch_rope_decode_attn(chn_ctx *ctx, const float *q_in, const float *k_in, const float *v_in, const float *qw,
+                            const float *kw, float *kc, float *vc, const uint32_t *step, const uint32_t *slots,
+                            const uint32_t *n_slots, uint32_t max_slots, uint32_t num_q_heads, uint32_t head_dim,
+                            uint32_t kv_dim, uint32_t gqa, uint32_t rot, int k_eq_v, float theta, float eps,
+                            float scale, float *out, float *ws, uint32_t *xp);
 int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const float *vc, const uint32_t *slots,
                         uint32_t n_tok, uint32_t num_prev, uint32_t num_q_heads, uint32_t head_dim, uint32_t kv_dim,
                         uint32_t gqa, float scale, uint32_t window, float *out);
@@ -150,5 +180,36 @@ __device__ __forceinline__ float wave_reduce_v(const float (&acc)[V], int lane) 
 
 template <int V>
 constexpr int ilog2_c() { return V <= 1 ? 0 : 1 + ilog2_c<V / 2>(); }
+
+// Digit planes of one 32-block from the four lanes 4k..4k+3 of a wave that
+// hold its words w = lane & 3 (eight consecutive values each).  All four
+// lanes must call (with zeros where ok is false); only ok lanes store.
+__device__ __forceinline__ void emit_planes8(const float (&v)[8], uint32_t *__restrict__ xp, uint32_t nb,
+                                             uint32_t b, uint32_t w, bool ok) {
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
+    m = fmaxf(m, __shfl_xor(m, 1, 64));
+    m = fmaxf(m, __shfl_xor(m, 2, 64));
+    int e = 0;
+    (void)frexpf(m, &e);           // m = f * 2^e, f in [0.5, 1): |x_i| < 2^e
+    float scale = 0.0f, inv = 0.0f;
+    if (m > 0.0f && e > -100) {
+        scale = ldexpf(1.0f, XP_FRAC - e);
+        inv = ldexpf(1.0f, e - XP_FRAC);
+    }
+    uint32_t u[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) u[i] = (uint32_t)((int)rintf(v[i] * scale) + 0x888888);
+    if (!ok) return;
+#pragma unroll
+    for (int p = 0; p < XP_PLANES; ++p) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int n = 0; n < 8; ++n) word |= ((u[n] >> (4 * p)) & 15u) << (4 * n);
+        xp[(size_t)(p * 4 + w) * nb + b] = word ^ 0x88888888u;
+    }
+    if (w == 0) ((float *)(xp + (size_t)XP_WORDS * nb))[b] = inv;
+}
 
 }  // namespace chn

@@ -26,17 +26,7 @@
 
 namespace chn {
 
-constexpr int XP_PLANES = 6;      // digit planes per activation block
-constexpr int XP_FRAC = 22;       // fixed-point bits below the block exponent
-constexpr int XP_WORDS = XP_PLANES * 4;
-
-// Planes for K/32 blocks: u32 plane words in SoA order [(p*4 + w) * nb + b],
-// followed by nb float scales 2^(e_b - 22).
-__host__ __device__ inline size_t xplanes_bytes(uint32_t nb) { return (size_t)nb * (XP_WORDS + 1) * 4; }
-
-// Four threads per 32-block, one per 8-element weight word: block maximum
-// over the four (two xor-shuffles), quantise, split into balanced hex digits
-// and pack this word's six plane words.
+// Four threads per 32-block, one per 8-element weight word.
 __global__ __launch_bounds__(256) void k_xplanes(const float *__restrict__ x, uint32_t *__restrict__ xp,
                                                  uint32_t nb) {
     const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
@@ -52,30 +42,7 @@ __global__ __launch_bounds__(256) void k_xplanes(const float *__restrict__ x, ui
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = 0.0f;
     }
-    float m = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
-    m = fmaxf(m, __shfl_xor(m, 1, 64));
-    m = fmaxf(m, __shfl_xor(m, 2, 64));
-    int e = 0;
-    (void)frexpf(m, &e);           // m = f * 2^e, f in [0.5, 1): |x_i| < 2^e
-    float scale = 0.0f, inv = 0.0f;
-    if (m > 0.0f && e > -100) {
-        scale = ldexpf(1.0f, XP_FRAC - e);
-        inv = ldexpf(1.0f, e - XP_FRAC);
-    }
-    uint32_t u[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) u[i] = (uint32_t)((int)rintf(v[i] * scale) + 0x888888);
-    if (!ok) return;
-#pragma unroll
-    for (int p = 0; p < XP_PLANES; ++p) {
-        uint32_t word = 0;
-#pragma unroll
-        for (int n = 0; n < 8; ++n) word |= ((u[n] >> (4 * p)) & 15u) << (4 * n);
-        xp[(size_t)(p * 4 + w) * nb + b] = word ^ 0x88888888u;
-    }
-    if (w == 0) ((float *)(xp + (size_t)XP_WORDS * nb))[b] = inv;
+    emit_planes8(v, xp, nb, b, w, ok);
 }
 
 enum MatvecMode { MV_GEMV = 0, MV_QKV = 1, MV_MLP = 2 };
@@ -535,7 +502,7 @@ static int launch_generic(chn_ctx *ctx, int mode, const GenericArgs &a) {
 
 
 // x (fp32, K) -> digit planes in xp_ws (xplanes_bytes(K/32)), then the matvec.
-int launch_matvec(chn_ctx *ctx, int mode, MatvecArgs a, const float *x, uint32_t *xp_ws) {
+int launch_matvec(chn_ctx *ctx, int mode, MatvecArgs a, const float *x, uint32_t *xp_ws, bool planes_ready) {
     const uint32_t nb = a.nb;
     const bool fast = nb % 4 == 0 && nb <= 512 && aligned(a.W0, 16) && (!a.W1 || aligned(a.W1, 16)) &&
                       (!a.W2 || aligned(a.W2, 16));
@@ -544,8 +511,10 @@ int launch_matvec(chn_ctx *ctx, int mode, MatvecArgs a, const float *x, uint32_t
         return launch_generic(ctx, mode, g);
     }
     uint32_t *xp = xp_ws;
-    k_xplanes<<<(4 * nb + 255) / 256, 256, 0, ctx->stream>>>(x, xp, nb);
-    CHN_LAUNCHED(ctx, "k_xplanes");
+    if (!planes_ready) {
+        k_xplanes<<<(4 * nb + 255) / 256, 256, 0, ctx->stream>>>(x, xp, nb);
+        CHN_LAUNCHED(ctx, "k_xplanes");
+    }
     a.xp = xp;
     const MvShape s = pick_shape(mode, a.M, nb);
     bool ok = mode == MV_GEMV ? launch_mode<MV_GEMV>(s, a, ctx->stream)
@@ -558,19 +527,20 @@ int launch_matvec(chn_ctx *ctx, int mode, MatvecArgs a, const float *x, uint32_t
 
 size_t mv_ws_bytes(uint32_t K) { return xplanes_bytes(K / 32); }
 
-int mv_gemv(chn_ctx *ctx, const uint32_t *W, const float *x, float *y, uint32_t M, uint32_t K, uint32_t *ws) {
+int mv_gemv(chn_ctx *ctx, const uint32_t *W, const float *x, float *y, uint32_t M, uint32_t K, uint32_t *ws,
+            bool planes_ready) {
     MatvecArgs a{W, nullptr, nullptr, y, nullptr, nullptr, nullptr, M, M, M, K / 32};
-    return launch_matvec(ctx, MV_GEMV, a, x, ws);
+    return launch_matvec(ctx, MV_GEMV, a, x, ws, planes_ready);
 }
 int mv_qkv(chn_ctx *ctx, const uint32_t *Wq, const uint32_t *Wk, const uint32_t *Wv, const float *x, float *q,
-           float *k, float *v, uint32_t q_dim, uint32_t kv_dim, uint32_t K, uint32_t *ws) {
+           float *k, float *v, uint32_t q_dim, uint32_t kv_dim, uint32_t K, uint32_t *ws, bool planes_ready) {
     MatvecArgs a{Wq, Wk, Wv, q, k, v, nullptr, q_dim + 2 * kv_dim, q_dim, q_dim + kv_dim, K / 32};
-    return launch_matvec(ctx, MV_QKV, a, x, ws);
+    return launch_matvec(ctx, MV_QKV, a, x, ws, planes_ready);
 }
 int mv_mlp(chn_ctx *ctx, const uint32_t *Wg, const uint32_t *Wu, const float *x, float *act, uint32_t M, uint32_t K,
-           uint32_t *ws) {
+           uint32_t *ws, bool planes_ready) {
     MatvecArgs a{Wg, Wu, nullptr, act, nullptr, nullptr, nullptr, M, M, M, K / 32};
-    return launch_matvec(ctx, MV_MLP, a, x, ws);
+    return launch_matvec(ctx, MV_MLP, a, x, ws, planes_ready);
 }
 
 static int check_common(chn_ctx *ctx, const float *x, uint32_t K) {
@@ -593,7 +563,7 @@ extern "C" int chn_gemv_q4(chn_ctx *ctx, const uint32_t *W, const float *x, floa
     MatvecArgs a{W, nullptr, nullptr, y, nullptr, nullptr, nullptr, M, M, M, K / 32};
     rc = ensure_workspace(ctx, xplanes_bytes(K / 32));
     if (rc) return rc;
-    return launch_matvec(ctx, MV_GEMV, a, x, (uint32_t *)ctx->ws);
+    return launch_matvec(ctx, MV_GEMV, a, x, (uint32_t *)ctx->ws, false);
 }
 
 extern "C" int chn_fused_qkv_q4(chn_ctx *ctx, const uint32_t *Wq, const uint32_t *Wk,
@@ -610,7 +580,7 @@ extern "C" int chn_fused_qkv_q4(chn_ctx *ctx, const uint32_t *Wq, const uint32_t
     MatvecArgs a{Wq, Wk, Wv, q, k, v, nullptr, (uint32_t)M, q_dim, q_dim + kv_dim, K / 32};
     rc = ensure_workspace(ctx, xplanes_bytes(K / 32));
     if (rc) return rc;
-    return launch_matvec(ctx, MV_QKV, a, x, (uint32_t *)ctx->ws);
+    return launch_matvec(ctx, MV_QKV, a, x, (uint32_t *)ctx->ws, false);
 }
 
 extern "C" int chn_fused_mlp_q4(chn_ctx *ctx, const uint32_t *Wg, const uint32_t *Wu,
@@ -623,5 +593,5 @@ extern "C" int chn_fused_mlp_q4(chn_ctx *ctx, const uint32_t *Wg, const uint32_t
     MatvecArgs a{Wg, Wu, nullptr, act, nullptr, nullptr, nullptr, M, M, M, K / 32};
     rc = ensure_workspace(ctx, xplanes_bytes(K / 32));
     if (rc) return rc;
-    return launch_matvec(ctx, MV_MLP, a, x, (uint32_t *)ctx->ws);
+    return launch_matvec(ctx, MV_MLP, a, x, (uint32_t *)ctx->ws, false);
 }

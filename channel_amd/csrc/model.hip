@@ -171,23 +171,27 @@ static int record_decode(chn_model *m, bool with_logits) {
         rc = (call);             \
         if (rc) return rc;       \
     } while (0)
+    // Each norm kernel also writes the digit planes of its output into
+    // mv_ws, and attention writes those of its output, so the matvec that
+    // follows reads them directly; only the down projection's input (the
+    // gate/up activations) is converted by a separate pass.
+    uint32_t *xp = m->mv_ws;
     for (uint32_t i = 0; i < c.num_layers; ++i) {
         const auto &l = m->L[i];
         const float theta = l.full ? c.rope_theta_full : c.rope_theta;
-        if (i == 0) R_(launch_rmsnorm(s, m->x, nullptr, l.in_norm, m->normed, H, 1, eps, 1.0f, false));
-        R_(mv_qkv(ctx, l.Wq, l.Wk, l.Wv, m->normed, m->q, m->k, m->v, qd, kvd, H, m->mv_ws));
-        R_(launch_qkv_rope(s, m->q, m->k, m->v, l.q_norm, l.k_norm, m->q, l.kc, l.vc, m->step, nq, nkv, D,
-                           c.rotary_dim, (int)c.k_eq_v, theta, eps));
-        R_(launch_decode_attn(ctx, m->q, l.kc, l.vc, m->slots + (l.full ? 0 : kSlotsMax), m->step + (l.full ? 2 : 3),
-                              kSlotsMax, nq, D, kvd, gqa, 1.0f, m->attn, m->attn_ws));
-        R_(mv_gemv(ctx, l.Wo, m->attn, m->mlp_out, H, qd, m->mv_ws));
-        if (l.has_post_attn) R_(launch_rmsnorm(s, m->mlp_out, nullptr, l.post_attn, m->mlp_out, H, 1, eps, 1.0f, false));
-        R_(launch_rmsnorm(s, m->x, m->mlp_out, l.pre_ffn, m->normed, H, 1, eps, 1.0f, true));
-        R_(mv_mlp(ctx, l.Wg, l.Wu, m->normed, m->act, I, H, m->mv_ws));
-        R_(mv_gemv(ctx, l.Wd, m->act, m->mlp_out, H, I, m->mv_ws));
-        if (l.has_post_ffn) R_(launch_rmsnorm(s, m->mlp_out, nullptr, l.post_ffn, m->mlp_out, H, 1, eps, 1.0f, false));
+        if (i == 0) R_(launch_norm_planes(s, m->x, nullptr, nullptr, l.in_norm, m->normed, xp, H, eps, 1.0f, false));
+        R_(mv_qkv(ctx, l.Wq, l.Wk, l.Wv, m->normed, m->q, m->k, m->v, qd, kvd, H, xp, true));
+        R_(launch_rope_decode_attn(ctx, m->q, m->k, m->v, l.q_norm, l.k_norm, l.kc, l.vc, m->step,
+                                   m->slots + (l.full ? 0 : kSlotsMax), m->step + (l.full ? 2 : 3), kSlotsMax, nq, D,
+                                   kvd, gqa, c.rotary_dim, (int)c.k_eq_v, theta, eps, 1.0f, m->attn, m->attn_ws, xp));
+        R_(mv_gemv(ctx, l.Wo, m->attn, m->mlp_out, H, qd, xp, true));
+        R_(launch_norm_planes(s, m->x, m->mlp_out, l.has_post_attn ? l.post_attn : nullptr, l.pre_ffn, m->normed, xp,
+                              H, eps, 1.0f, true));
+        R_(mv_mlp(ctx, l.Wg, l.Wu, m->normed, m->act, I, H, xp, true));
+        R_(mv_gemv(ctx, l.Wd, m->act, m->mlp_out, H, I, xp, false));
         const float *next_norm = (i + 1 < c.num_layers) ? m->L[i + 1].in_norm : m->final_norm;
-        R_(launch_rmsnorm(s, m->x, m->mlp_out, next_norm, m->normed, H, 1, eps, l.scalar, true));
+        R_(launch_norm_planes(s, m->x, m->mlp_out, l.has_post_ffn ? l.post_ffn : nullptr, next_norm, m->normed, xp, H,
+                              eps, l.scalar, true));
     }
     if (with_logits) {
         R_(launch_gemv_q8(s, m->embed_q8, m->normed, m->logits, c.vocab_size, H / 32, m->mv_ws));

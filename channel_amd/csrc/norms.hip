@@ -53,6 +53,91 @@ int launch_rmsnorm(hipStream_t s, float *x, const float *r, const float *w, floa
     return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
 }
 
+// Sum over the whole workgroup (blockDim.x a multiple of 64, <= 1024):
+// wave sums, then the wave partials in index order.
+__device__ __forceinline__ float block_sum_n(float v, float *sh) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    if ((threadIdx.x & 63) == 0) sh[wave] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (int i = 0; i < nw; ++i) t += sh[i];
+    __syncthreads();
+    return t;
+}
+
+__device__ __forceinline__ void load8(const float *p, uint32_t t, bool ok, float (&v)[8]) {
+    if (ok) {
+        const f4n a = *(const f4n *)(p + 8 * (size_t)t), b = *(const f4n *)(p + 8 * (size_t)t + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    }
+}
+__device__ __forceinline__ void store8(float *p, uint32_t t, const float (&v)[8]) {
+    *(f4n *)(p + 8 * (size_t)t) = f4n{v[0], v[1], v[2], v[3]};
+    *(f4n *)(p + 8 * (size_t)t + 4) = f4n{v[4], v[5], v[6], v[7]};
+}
+
+// The decode step's norms fused with the matvec input: with POST the
+// residual branch is normalised first (post_attention / post_feedforward
+// norm), with ADD it is added to x and scaled (add_rmsnorm), then
+// y = rmsnorm(x) * w and the digit planes of y.  One workgroup of
+// ceil(dim / 8) threads rounded up to whole waves, eight values per thread
+// (four threads per 32-block, as the planes want them).
+template <bool POST, bool ADD>
+__global__ __launch_bounds__(1024) void k_norm_planes(float *__restrict__ x, const float *__restrict__ r,
+                                                      const float *__restrict__ pw, const float *__restrict__ w,
+                                                      float *__restrict__ y, uint32_t *__restrict__ xp, uint32_t dim,
+                                                      float eps, float scalar) {
+    __shared__ float sh[16];
+    const uint32_t t = threadIdx.x;
+    const bool ok = 8 * t < dim;
+    // every load is issued before the first reduction
+    float xv[8], rv[8], pv[8], wv[8];
+    load8(x, t, ok, xv);
+    if (ADD) load8(r, t, ok, rv);
+    if (POST) load8(pw, t, ok, pv);
+    load8(w, t, ok, wv);
+    if (ADD) {
+        if (POST) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ss += rv[i] * rv[i];
+            ss = block_sum_n(ss, sh);
+            const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) rv[i] = (rv[i] * inv) * pv[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xv[i] = (xv[i] + rv[i]) * scalar;
+        if (ok) store8(x, t, xv);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += xv[i] * xv[i];
+    ss = block_sum_n(ss, sh);
+    const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+    float yv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) yv[i] = (xv[i] * inv) * wv[i];
+    if (ok) store8(y, t, yv);
+    if (xp) emit_planes8(yv, xp, dim / 32, t >> 2, t & 3, ok);
+}
+
+int launch_norm_planes(hipStream_t s, float *x, const float *r, const float *post_w, const float *w, float *y,
+                       uint32_t *xp, uint32_t dim, float eps, float scalar, bool add) {
+    if (dim % 32 != 0 || dim > 8192) return CHN_E_UNSUPPORTED;
+    const uint32_t nt = ((dim / 8 + 63) / 64) * 64;
+    if (!add) k_norm_planes<false, false><<<1, nt, 0, s>>>(x, r, post_w, w, y, xp, dim, eps, scalar);
+    else if (post_w) k_norm_planes<true, true><<<1, nt, 0, s>>>(x, r, post_w, w, y, xp, dim, eps, scalar);
+    else k_norm_planes<false, true><<<1, nt, 0, s>>>(x, r, post_w, w, y, xp, dim, eps, scalar);
+    return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
+}
+
 static int check_norm(chn_ctx *ctx, const void *x, const void *w, const void *y, uint32_t dim) {
     CHN_REQUIRE(ctx, x && w && y, "NULL argument");
     CHN_REQUIRE(ctx, dim > 0 && dim % 4 == 0, "dim %u must be a positive multiple of 4", dim);
