@@ -46,7 +46,8 @@ def q4_bytes(rows, K):
 
 def load_traffic(kernel, workload):
     """HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE /
-    WRITE_SIZE, from profiles/traffic.md (None if not measured)."""
+    WRITE_SIZE and calibrated on a plain copy, read from the table in
+    profiles/traffic.md (None if that kernel and workload were not measured)."""
     path = os.path.join(ROOT, "profiles", "traffic.md")
     if not os.path.exists(path):
         return None
@@ -124,7 +125,7 @@ def bench_mlp(ctx, args):
     gateup_bytes = 2 * w_bytes + H * 4 + I * 4
     down_bytes = w_bytes + I * 4 + H * 4
     achieved = gateup_bytes / (k_ms * 1e-3) / 1e9
-    traffic = load_traffic("k_matvec_q4<MLP>", "mlp")
+    traffic = load_traffic("k_q4mv<MLP>", "gate/up 15360x3840")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -155,7 +156,7 @@ def bench_mlp(ctx, args):
                    "step_bytes": step_bytes,
                    "down_gemv_ms": d_ms,
                    "down_gemv_gbps": down_bytes / (d_ms * 1e-3) / 1e9},
-        "roofline": {"kernel": "k_matvec_q4<MLP> (fused gate/up + GELU-tanh)",
+        "roofline": {"kernel": "chn_fused_mlp_q4 = k_xplanes + k_q4mv<MLP> (fused gate/up + GELU-tanh)",
                      "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "algorithmic_bytes_per_launch": gateup_bytes,
@@ -309,33 +310,46 @@ def bench_decode(ctx, args):
     _, ids, _ = m.prefill_batch(prompt, slots, 0, 0, logits=False, topk=True)
     prefill_s = time.perf_counter() - t0
 
+    # greedy decode on the device: the step parameters and the slot lists of
+    # the 4096-slot ring are generated on the GPU, the argmax feeds the next
+    # step's embedding gather; the timed region holds K decode tokens
+    def greedy(tok, clock, n):
+        out = []
+        while n > 0:
+            k = min(n, 4096)
+            g = m.decode_greedy(tok, clock, k)
+            out.append(g)
+            tok, clock, n = int(g[-1]), clock + k, n - k
+        return np.concatenate(out) if out else np.zeros(0, np.uint32)
+
     tok = int(ids[0])
     clock = PROMPT
-    window = cfg["sliding_window"]
-
-    def step():
-        # ring of 4096 slots, no anchors: slot = clock mod 4096, the global
-        # list holds the last min(clock + 1, 4096) slots in time order and
-        # the sliding list the last `window` of them
-        nonlocal tok, clock
-        n = min(clock + 1, 4096)
-        active = ((np.arange(n, dtype=np.int64) + clock + 1 - n) % 4096).astype(np.uint32)
-        sliding = active[max(0, n - window):]
-        tok, _, _ = m.forward_token_id(tok, clock, clock % 4096, active, sliding, topk=True)
-        clock += 1
-
-    for _ in range(args.warmup):
-        step()
+    if args.warmup:
+        tok = int(greedy(tok, clock, args.warmup)[-1])
+        clock += args.warmup
     ctx.sync()
     ctx_start = clock
     t0 = time.perf_counter()
     ctx.timer_start()
-    for _ in range(args.steps):
-        step()
+    gen = greedy(tok, clock, args.steps)
     gpu_ms = ctx.timer_stop()
     wall_ms = (time.perf_counter() - t0) * 1e3
+    clock += args.steps
     ms_per_tok = max(gpu_ms, wall_ms) / args.steps
-    mid_ctx = (ctx_start + clock) // 2
+
+    # the same steps driven token by token through the reference-shaped
+    # interface (host slot lists uploaded per token, ids copied back)
+    window = cfg["sliding_window"]
+    tok = int(gen[-1])
+    n_api = 32
+    t0 = time.perf_counter()
+    for _ in range(n_api):
+        n = min(clock + 1, 4096)
+        active = ((np.arange(n, dtype=np.int64) + clock + 1 - n) % 4096).astype(np.uint32)
+        tok, _, _ = m.forward_token_id(tok, clock, clock % 4096, active, active[max(0, n - window):])
+        clock += 1
+    api_ms = (time.perf_counter() - t0) * 1e3 / n_api
+    mid_ctx = ctx_start + args.steps // 2
     w_bytes, kv_bytes = token_bytes(cfg, mid_ctx)
     m.close()
 
@@ -358,7 +372,9 @@ def bench_decode(ctx, args):
         "ms_per_step": ms_per_tok,
         "config": {"workload": "12B-class Q4 decode: 48 layers, hidden 3840, FFN 15360, 16 q / 8 kv heads, "
                                "head_dim 256, vocab 262144; 512-token prompt prefill, then greedy decode",
-                   "prompt_tokens": PROMPT, "decode_context": [ctx_start, clock],
+                   "prompt_tokens": PROMPT, "decode_context": [ctx_start, ctx_start + args.steps],
+                   "decode_mode": "device-resident greedy steps (chn_decode_greedy)",
+                   "api_tok_s": 1e3 / api_ms,
                    "prefill_tok_s": PROMPT / prefill_s, "prefill_ms": prefill_s * 1e3,
                    "token_weight_bytes": w_bytes, "token_kv_bytes_mid": kv_bytes,
                    "token_hbm_gbps": (w_bytes + kv_bytes) / (ms_per_tok * 1e-3) / 1e9,
@@ -368,7 +384,7 @@ def bench_decode(ctx, args):
         "roofline": {"kernel": "chn_fused_mlp_q4 = k_xplanes + k_q4mv<MLP> (gate/up + GELU-tanh, 15360x3840 x2)",
                      "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": load_traffic("k_q4mv<MLP>", "decode"),
+                     "traffic": load_traffic("k_q4mv<MLP>", "gate/up 15360x3840"),
                      "algorithmic_bytes_per_launch": gateup_bytes(H, I), "avg_launch_ms": k_ms},
         "cpu_baseline": cpu,
         "dtype": "fp32 accumulate over Q4 weights (Q8 logits)",
@@ -427,7 +443,7 @@ def bench_gemv(ctx, args):
                    "weight_copies_rotated": ncopy},
         "roofline": {"kernel": "k_matvec_q4<GEMV>", "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": load_traffic("k_matvec_q4<GEMV>", "gemv"),
+                     "traffic": load_traffic("k_q4mv<GEMV>", "8192x2048"),
                      "algorithmic_bytes_per_launch": nbytes, "avg_launch_ms": k_ms},
         "cpu_baseline": cpu,
         "dtype": "fp32 accumulate over Q4 weights",
@@ -521,9 +537,41 @@ def bench_attn(ctx, args):
     }
 
 
+def bench_copy(ctx, args):
+    """Device-to-device copy of 1 GiB (chn_copy): the HBM copy rate and the
+    known-size kernel against which rocprofv3 FETCH_SIZE / WRITE_SIZE are
+    calibrated."""
+    n = 1 << 30
+    src = ctx.alloc(n)
+    dst = ctx.alloc(n)
+    ctx.fill_u32(src, 0x3F800000, n // 4)
+    ctx.sync()
+    for _ in range(args.warmup):
+        ctx.call("chn_copy", dst, src, n)
+    ctx.sync()
+    t0 = time.perf_counter()
+    ctx.timer_start()
+    for _ in range(args.steps):
+        ctx.call("chn_copy", dst, src, n)
+    gpu_ms = ctx.timer_stop()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    ms = max(gpu_ms, wall_ms) / args.steps
+    achieved = 2 * n / (gpu_ms / args.steps * 1e-3) / 1e9
+    return {
+        "value": 2 * n / (ms * 1e-3) / 1e9, "unit": "GB/s (read + write)", "ms_per_step": ms,
+        "config": {"workload": "device copy of 1 GiB (chn_copy)", "bytes_copied": n},
+        "roofline": {"kernel": "device copy", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "algorithmic_bytes_per_launch": 2 * n, "avg_launch_ms": gpu_ms / args.steps},
+        "cpu_baseline": None,
+        "dtype": "bytes",
+        "data": "constant fill",
+    }
+
+
 WORKLOADS = {"decode": bench_decode, "mlp": bench_mlp, "gemv": bench_gemv, "prefill": bench_prefill,
-             "attn": bench_attn}
-DEFAULT_STEPS = {"decode": (256, 8)}
+             "attn": bench_attn, "copy": bench_copy}
+DEFAULT_STEPS = {"decode": (256, 8), "copy": (20, 2)}
 
 
 def main():

@@ -72,6 +72,7 @@ PROTOTYPES = {
                                 c_void_p, c_void_p, P(c_u32)]),
     "chn_decode_token": (c_int, [c_void_p, c_u32, c_u32, c_u32, c_void_p, c_u32, c_void_p, c_u32,
                                  c_void_p, c_void_p, P(c_u32)]),
+    "chn_decode_greedy": (c_int, [c_void_p, c_u32, c_u32, c_u32, c_void_p]),
     "chn_prefill": (c_int, [c_void_p, c_void_p, c_u32, c_void_p, c_void_p, c_u32, c_u32, c_u32,
                             c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "chn_kv_read": (c_int, [c_void_p, c_u32, c_u32, c_u32, c_void_p, c_void_p]),

@@ -31,7 +31,7 @@ struct chn_model {
     };
     std::vector<Layer> L;
     uint32_t *embed_q8 = nullptr;
-    uint16_t *embed_bf16 = nullptr;   // device copy (synthetic models; optional otherwise)
+    uint16_t *embed_bf16 = nullptr;   // device copy of the tied embedding (input gather)
     float *final_norm = nullptr;
     // decode buffers
     float *x, *normed, *q, *k, *v, *attn, *mlp_out, *act, *logits;
@@ -52,14 +52,18 @@ struct chn_model {
     float *h_x = nullptr;
     uint32_t *h_slots = nullptr, *h_step = nullptr, *h_ids = nullptr;
     float *h_vals = nullptr;
-    hipGraphExec_t exec[2] = {nullptr, nullptr};   // [0] without logits, [1] with
-    bool use_graph = true;                          // false: launch the kernels one by one
+    hipGraphExec_t exec[3] = {nullptr, nullptr, nullptr};   // without logits, with, greedy step
+    bool use_graph = true;                                   // false: launch the kernels one by one
+    // device-resident greedy decoding: {clock, count, start token}, tokens out
+    uint32_t *gen = nullptr, *gen_tokens = nullptr;
+    uint32_t *h_gen = nullptr;
     std::vector<void *> allocs;
 };
 
 namespace chn {
 
 static constexpr uint32_t kSlotsMax = 4096;
+static constexpr uint32_t kGreedyCap = 4096;   // most steps per chn_decode_greedy call
 
 static int m_alloc(chn_model *m, size_t bytes, void **p) {
     hipError_t e = hipMalloc(p, bytes ? bytes : 256);
@@ -118,6 +122,8 @@ static int alloc_runtime(chn_model *m) {
     M_ALLOC(m->slots, 2 * kSlotsMax * 4);
     M_ALLOC(m->step, 64);
     M_ALLOC(m->tok, 64);
+    M_ALLOC(m->gen, 64);
+    M_ALLOC(m->gen_tokens, (size_t)kGreedyCap * 4);
     const uint32_t kmax = H > I ? (H > qd ? H : qd) : (I > qd ? I : qd);
     size_t mvb = mv_ws_bytes(kmax);
     if (xbytes_bytes(H / 32) > mvb) mvb = xbytes_bytes(H / 32);
@@ -142,6 +148,7 @@ static int alloc_runtime(chn_model *m) {
     if (e == hipSuccess) e = hipHostMalloc((void **)&m->h_step, 64);
     if (e == hipSuccess) e = hipHostMalloc((void **)&m->h_ids, 64 * 4);
     if (e == hipSuccess) e = hipHostMalloc((void **)&m->h_vals, 64 * 4);
+    if (e == hipSuccess) e = hipHostMalloc((void **)&m->h_gen, (size_t)kGreedyCap * 4);
     if (e != hipSuccess) return hip_fail(m->ctx, e, "hipHostMalloc");
     // zero KV caches and slot buffers with a kernel (no memset nodes anywhere)
     for (auto &l : m->L) {
@@ -152,7 +159,45 @@ static int alloc_runtime(chn_model *m) {
     int rc = chn_fill_u32(m->ctx, m->slots, 0, 2 * kSlotsMax);
     if (!rc) rc = chn_fill_u32(m->ctx, m->step, 0, 16);
     if (!rc) rc = chn_fill_u32(m->ctx, m->topk_ids, 0, 64);
+    if (!rc) rc = chn_fill_u32(m->ctx, m->gen, 0, 16);
     return rc;
+}
+
+// ---- device-resident greedy steps
+// Head: the step parameters and the chronological slot lists of a 4096-slot
+// ring without anchors (slot = clock mod 4096; the global list holds the
+// last min(clock + 1, 4096) slots, the sliding list the last `window` of
+// them: getSlotIndexLayer / getActiveSlotsLayer, src/ring_buffer.zig:
+// 118-121,287-333, for num_anchors = 0), and the input token: the start
+// token on the first step, the previous step's argmax after that.
+__global__ __launch_bounds__(256) void k_greedy_head(const uint32_t *__restrict__ gen,
+                                                     const uint32_t *__restrict__ topk_ids,
+                                                     uint32_t *__restrict__ step, uint32_t *__restrict__ slots,
+                                                     uint32_t *__restrict__ tok, uint32_t window) {
+    const uint32_t clock = gen[0], count = gen[1];
+    const uint32_t n = clock + 1 < kSlotsMax ? clock + 1 : kSlotsMax;
+    const uint32_t ns = n < window ? n : window;
+    if (threadIdx.x == 0) {
+        step[0] = clock;
+        step[1] = clock % kSlotsMax;
+        step[2] = n;
+        step[3] = ns;
+        tok[0] = count == 0 ? gen[2] : topk_ids[0];
+    }
+    const uint32_t first = clock + 1 - n;
+    for (uint32_t i = threadIdx.x; i < n; i += 256) slots[i] = (first + i) % kSlotsMax;
+    for (uint32_t i = threadIdx.x; i < ns; i += 256) slots[kSlotsMax + i] = (clock + 1 - ns + i) % kSlotsMax;
+}
+
+// Tail: append this step's argmax (top-64 ids[0]) and advance the clock.
+__global__ void k_greedy_tail(uint32_t *__restrict__ gen, const uint32_t *__restrict__ topk_ids,
+                              uint32_t *__restrict__ out, uint32_t cap) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) {
+        const uint32_t count = gen[1];
+        if (count < cap) out[count] = topk_ids[0];
+        gen[1] = count + 1;
+        gen[0] = gen[0] + 1;
+    }
 }
 
 // ---- the decode sequence (recordLayerDirect / recordForwardGraph,
@@ -201,11 +246,25 @@ static int record_decode(chn_model *m, bool with_logits) {
     return CHN_OK;
 }
 
+static int record_greedy(chn_model *m) {
+    hipStream_t s = m->ctx->stream;
+    const uint32_t H = m->cfg.hidden_size;
+    k_greedy_head<<<1, 256, 0, s>>>(m->gen, m->topk_ids, m->step, m->slots, m->tok, m->cfg.sliding_window);
+    if (hipGetLastError() != hipSuccess) return hip_fail(m->ctx, hipGetLastError(), "k_greedy_head");
+    if (launch_embed(s, m->embed_bf16, m->tok, 1, H, sqrtf((float)H), m->x))
+        return hip_fail(m->ctx, hipGetLastError(), "k_embed");
+    int rc = record_decode(m, true);
+    if (rc) return rc;
+    k_greedy_tail<<<1, 64, 0, s>>>(m->gen, m->topk_ids, m->gen_tokens, kGreedyCap);
+    if (hipGetLastError() != hipSuccess) return hip_fail(m->ctx, hipGetLastError(), "k_greedy_tail");
+    return CHN_OK;
+}
+
 static int build_graphs(chn_model *m) {
     hipStream_t s = m->ctx->stream;
-    for (int wl = 0; wl < 2; ++wl) {
+    for (int wl = 0; wl < 3; ++wl) {
         CHN_HIP(m->ctx, hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-        int rc = record_decode(m, wl == 1);
+        int rc = wl == 2 ? record_greedy(m) : record_decode(m, wl == 1);
         hipGraph_t g = nullptr;
         hipError_t e = hipStreamEndCapture(s, &g);
         if (rc) {
@@ -223,7 +282,7 @@ static int build_graphs(chn_model *m) {
 static void free_model(chn_model *m) {
     if (!m) return;
     if (m->ctx) (void)hipStreamSynchronize(m->ctx->stream);
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 3; ++i)
         if (m->exec[i]) (void)hipGraphExecDestroy(m->exec[i]);
     for (void *p : m->allocs) (void)hipFree(p);
     if (m->h_x) (void)hipHostFree(m->h_x);
@@ -231,6 +290,7 @@ static void free_model(chn_model *m) {
     if (m->h_step) (void)hipHostFree(m->h_step);
     if (m->h_ids) (void)hipHostFree(m->h_ids);
     if (m->h_vals) (void)hipHostFree(m->h_vals);
+    if (m->h_gen) (void)hipHostFree(m->h_gen);
     delete m;
 }
 
@@ -280,9 +340,7 @@ extern "C" int chn_model_create(chn_ctx *ctx, const chn_model_config *cfg, const
     m->cfg = *cfg;
     const uint32_t H = cfg->hidden_size, I = cfg->intermediate_size;
     const uint32_t D = cfg->head_dim, qd = cfg->num_heads * D, kvd = cfg->num_kv_heads * D;
-    size_t tmp_elems = (size_t)cfg->vocab_size * H;
-    const size_t big = (size_t)I * H > (size_t)qd * H ? (size_t)I * H : (size_t)qd * H;
-    if (big > tmp_elems) tmp_elems = big;
+    const size_t tmp_elems = (size_t)I * H > (size_t)qd * H ? (size_t)I * H : (size_t)qd * H;
     uint16_t *tmp = nullptr;
     hipError_t e = hipMalloc(&tmp, tmp_elems * 2);
     if (e != hipSuccess) {
@@ -321,7 +379,14 @@ extern "C" int chn_model_create(chn_ctx *ctx, const chn_model_config *cfg, const
         l.scalar = w.has_layer_scalar ? w.layer_scalar : 1.0f;
         l.full = cfg->layer_full[i] != 0;
     }
-    C_(ingest_q(m, embed_bf16, cfg->vocab_size, H, 1, &m->embed_q8, tmp));
+    // tied embedding: a device bf16 copy for the input gather, Q8 for the logits
+    C_(m_alloc(m, (size_t)cfg->vocab_size * H * 2, (void **)&m->embed_bf16));
+    C_(chn_upload(ctx, m->embed_bf16, embed_bf16, (size_t)cfg->vocab_size * H * 2));
+    C_(m_alloc(m, (size_t)cfg->vocab_size * (H / 32) * 36, (void **)&m->embed_q8));
+    if (launch_quantize(ctx->stream, 1, m->embed_bf16, m->embed_q8, (uint64_t)cfg->vocab_size * (H / 32))) {
+        rc = hip_fail(ctx, hipGetLastError(), "quantize embedding");
+        goto fail;
+    }
     C_(ingest_norm(m, final_norm_bf16, H, &m->final_norm));
     C_(alloc_runtime(m));
     C_(build_graphs(m));
@@ -362,7 +427,7 @@ extern "C" int chn_model_create_synthetic(chn_ctx *ctx, const chn_model_config *
         } mats[7] = {{&l.Wq, qd, H}, {&l.Wk, kvd, H}, {&l.Wv, kvd, H}, {&l.Wo, H, qd},
                      {&l.Wg, I, H},  {&l.Wu, I, H},   {&l.Wd, H, I}};
         for (int j = 0; j < 7; ++j) {
-            M_ALLOC(*mats[j].w, q4b(mats[j].rows, mats[j].cols));
+            C_(m_alloc(m, q4b(mats[j].rows, mats[j].cols), (void **)mats[j].w));
             C_(chn_synth_q4(ctx, *mats[j].w, mats[j].rows, mats[j].cols, ls + j, smin, smax));
         }
         C_(fill_ones(m, H, &l.in_norm));
@@ -385,13 +450,17 @@ extern "C" int chn_model_create_synthetic(chn_ctx *ctx, const chn_model_config *
             rc = hip_fail(ctx, e, "hipMalloc (embedding staging)");
             goto fail;
         }
-        M_ALLOC(m->embed_bf16, n * 2);
+        rc = m_alloc(m, n * 2, (void **)&m->embed_bf16);
+        if (rc) {
+            (void)hipFree(tmpf);
+            goto fail;
+        }
         rc = chn_synth_normal(ctx, tmpf, n, seed + 7, 0.02f);
         if (!rc) rc = chn_to_bf16_bits(ctx, tmpf, m->embed_bf16, n);
         if (!rc) rc = chn_sync(ctx);
         (void)hipFree(tmpf);
         if (rc) goto fail;
-        M_ALLOC(m->embed_q8, (size_t)V * (H / 32) * 36);
+        C_(m_alloc(m, (size_t)V * (H / 32) * 36, (void **)&m->embed_q8));
         if (launch_quantize(ctx->stream, 1, m->embed_bf16, m->embed_q8, (uint64_t)V * (H / 32))) {
             rc = hip_fail(ctx, hipGetLastError(), "quantize embedding");
             goto fail;
@@ -483,7 +552,6 @@ extern "C" int chn_decode_token(chn_model *m, uint32_t token, uint32_t clock, ui
                                 uint32_t n_sliding, uint32_t *topk_ids, float *topk_vals, uint32_t *token_out) {
     if (!m) return CHN_E_INVALID;
     chn_ctx *ctx = m->ctx;
-    CHN_REQUIRE(ctx, m->embed_bf16, "model has no device embedding table; use chn_decode_step");
     CHN_REQUIRE(ctx, token < m->cfg.vocab_size, "token %u out of range", token);
     m->h_step[8] = token;
     CHN_HIP(ctx, hipMemcpyAsync(m->tok, m->h_step + 8, 4, hipMemcpyHostToDevice, ctx->stream));
@@ -491,6 +559,36 @@ extern "C" int chn_decode_token(chn_model *m, uint32_t token, uint32_t clock, ui
     if (launch_embed(ctx->stream, m->embed_bf16, m->tok, 1, H, sqrtf((float)H), m->x))
         return hip_fail(ctx, hipGetLastError(), "k_embed");
     return decode_run(m, clock, slot_idx, active, n_active, sliding, n_sliding, topk_ids, topk_vals, token_out, true);
+}
+
+// n greedy steps on the device (see k_greedy_head): one host round trip
+// for the whole run.
+extern "C" int chn_decode_greedy(chn_model *m, uint32_t token, uint32_t clock, uint32_t n_steps,
+                                 uint32_t *tokens_out) {
+    if (!m) return CHN_E_INVALID;
+    chn_ctx *ctx = m->ctx;
+    hipStream_t s = ctx->stream;
+    CHN_REQUIRE(ctx, token < m->cfg.vocab_size, "token %u out of range", token);
+    CHN_REQUIRE(ctx, n_steps <= kGreedyCap, "n_steps %u exceeds %u", n_steps, kGreedyCap);
+    CHN_REQUIRE(ctx, tokens_out || !n_steps, "NULL tokens_out");
+    if (!n_steps) return CHN_OK;
+    CHN_HIP(ctx, hipStreamSynchronize(s));
+    m->h_gen[0] = clock;
+    m->h_gen[1] = 0;
+    m->h_gen[2] = token;
+    CHN_HIP(ctx, hipMemcpyAsync(m->gen, m->h_gen, 12, hipMemcpyHostToDevice, s));
+    for (uint32_t i = 0; i < n_steps; ++i) {
+        if (m->use_graph) {
+            CHN_HIP(ctx, hipGraphLaunch(m->exec[2], s));
+        } else {
+            int rc = record_greedy(m);
+            if (rc) return rc;
+        }
+    }
+    CHN_HIP(ctx, hipMemcpyAsync(m->h_gen, m->gen_tokens, (size_t)n_steps * 4, hipMemcpyDeviceToHost, s));
+    CHN_HIP(ctx, hipStreamSynchronize(s));
+    std::memcpy(tokens_out, m->h_gen, (size_t)n_steps * 4);
+    return CHN_OK;
 }
 
 // gpuDispatchPrefillBatch (src/gpu/batch_dispatch.zig:27-172)

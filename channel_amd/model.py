@@ -145,7 +145,7 @@ class Model:
         return tok.value, ids, vals
 
     def forward_token_id(self, token, clock, slot_idx, active_slots, sliding_slots, topk=True):
-        """Embedding gather on the device (synthetic models), then forward_token."""
+        """Embedding gather on the device, then forward_token."""
         a, ap = self._slots(active_slots)
         s, sp = self._slots(sliding_slots)
         ids = np.zeros(64, np.uint32) if topk else None
@@ -156,6 +156,14 @@ class Model:
             None if ids is None else ids.ctypes.data_as(c_void_p),
             None if vals is None else vals.ctypes.data_as(c_void_p), ctypes.byref(tok)))
         return tok.value, ids, vals
+
+    def decode_greedy(self, token, clock, n_steps):
+        """n_steps greedy steps on the device over an anchor-free 4096-slot
+        ring; returns the generated token ids."""
+        out = np.zeros(max(int(n_steps), 1), np.uint32)
+        self._check("chn_decode_greedy", lib.chn_decode_greedy(self.handle, int(token), int(clock), int(n_steps),
+                                                               out.ctypes.data_as(c_void_p)))
+        return out[: int(n_steps)]
 
     def prefill_batch(self, tokens, slots, start_clock, num_prev_slots, embed_bf16=None,
                       logits=True, topk=True, progress=None):

@@ -274,7 +274,7 @@ int chn_model_get_config(const chn_model *m, chn_model_config *cfg);
  * not follow graph launches).  No reference counterpart. */
 int chn_model_set_graph(chn_model *m, int enabled);
 
-/* Device pointer to the synthetic model's bf16 embedding (NULL otherwise). */
+/* Device pointer to the model's bf16 embedding table (vocab x hidden). */
 int chn_model_embedding_bf16(chn_model *m, const uint16_t **table);
 
 /* gpuDispatchForwardToken (src/gpu/model_dispatch.zig:128-153): x[hidden]
@@ -288,10 +288,20 @@ int chn_decode_step(chn_model *m, const float *x, uint32_t clock, uint32_t slot_
                     uint32_t n_sliding, uint32_t *topk_ids, float *topk_vals, uint32_t *token_out);
 
 /* forwardToken's embedding step (src/model/forward.zig:35-37) on the
- * device, then chn_decode_step.  Needs a model with a device embedding. */
+ * device (gather from the model's bf16 embedding), then chn_decode_step. */
 int chn_decode_token(chn_model *m, uint32_t token, uint32_t clock, uint32_t slot_idx,
                      const uint32_t *active, uint32_t n_active, const uint32_t *sliding,
                      uint32_t n_sliding, uint32_t *topk_ids, float *topk_vals, uint32_t *token_out);
+
+/* n_steps (<= 4096) greedy decode steps without host round trips: the
+ * server's decode loop (src/server/decode.zig) over gpuDispatchForwardToken
+ * with the slot lists of a 4096-slot ring without anchors (slot = clock mod
+ * 4096; global list = the last min(clock + 1, 4096) slots, sliding list =
+ * the last cfg.sliding_window of them; src/ring_buffer.zig:118-121,287-333)
+ * generated on the device.  Step i feeds token (i = 0) or step i-1's argmax
+ * at clock + i; tokens_out[i] = step i's argmax.  Equivalent to n calls of
+ * chn_decode_token with those lists.  No direct reference counterpart. */
+int chn_decode_greedy(chn_model *m, uint32_t token, uint32_t clock, uint32_t n_steps, uint32_t *tokens_out);
 
 /* gpuDispatchPrefillBatch: n <= max_prefill_tokens tokens (else
  * CHN_E_BATCH_TOO_LARGE); slots[0..n_slots) lists num_prev_slots earlier

@@ -156,8 +156,11 @@ def test_model_errors(pair):
     with pytest.raises(ca.ChannelError):
         m.forward_token(np.zeros(256, np.float32), 0, 0, np.arange(4097), [0])
     with pytest.raises(ca.ChannelError):
-        # this model has no device embedding table
-        m.forward_token_id(3, 0, 0, [0], [0])
+        m.forward_token_id(CFG["vocab_size"], 0, 0, [0], [0])
+    with pytest.raises(ca.ChannelError):
+        m.decode_greedy(1, 0, 4097)
+    with pytest.raises(ca.ChannelError):
+        m.decode_greedy(CFG["vocab_size"], 0, 1)
     with pytest.raises(ca.ChannelError):
         m.kv_read(3, 0, 1)
     with pytest.raises(ca.ChannelError):
@@ -204,3 +207,51 @@ def test_eager_launches_match_graph(ctx):
             xg, ng = mg.read_state()
             xe, ne = me.read_state()
             assert np.array_equal(xg, xe) and np.array_equal(ng, ne)
+
+
+def ring_lists(clock, window, nslot=4096):
+    """Slot lists of an anchor-free ring: slot = clock mod nslot."""
+    n = min(clock + 1, nslot)
+    active = ((np.arange(n, dtype=np.int64) + clock + 1 - n) % nslot).astype(np.uint32)
+    return active, active[max(0, n - window):]
+
+
+@pytest.mark.parametrize("clock0", [0, 4093])
+def test_decode_greedy_matches_token_loop(ctx, clock0):
+    """chn_decode_greedy (device-resident steps, ring slot lists generated on
+    the device) equals the same steps driven from the host, bit for bit; the
+    second case wraps the ring (slots 4093, 4094, 4095, 0, 1)."""
+    cfg = dict(CFG, num_layers=2, layer_full=[0, 1])
+    say(f"decode_greedy clock0={clock0}")
+    with Model.synthetic(ctx, cfg, 99) as mg, Model.synthetic(ctx, cfg, 99) as mh:
+        toks = mg.decode_greedy(17, clock0, 5)
+        tok = 17
+        want = []
+        for i in range(5):
+            clock = clock0 + i
+            active, sliding = ring_lists(clock, WINDOW)
+            tok, _, _ = mh.forward_token_id(tok, clock, clock % 4096, active, sliding)
+            want.append(tok)
+        assert list(toks) == want
+        xg, ng = mg.read_state()
+        xh, nh = mh.read_state()
+        assert np.array_equal(xg, xh) and np.array_equal(ng, nh)
+        for layer in range(2):
+            for clock in range(clock0, clock0 + 5):
+                kg, vg = mg.kv_read(layer, clock % 4096, 1)
+                kh, vh = mh.kv_read(layer, clock % 4096, 1)
+                assert np.array_equal(kg, kh) and np.array_equal(vg, vh)
+
+
+def test_created_model_token_path_matches_step(pair):
+    """Models ingested from bf16 keep a device copy of the embedding: the
+    device gather equals bf16(embed[tok]) * sqrt(H) fed from the host."""
+    W, m = pair
+    x_in = W.embed([123])[0]
+    active, sliding = ring_lists(900, WINDOW)
+    t1, ids1, vals1 = m.forward_token_id(123, 900, 900, active, sliding)
+    x1, n1 = m.read_state()
+    t2, ids2, vals2 = m.forward_token(x_in, 900, 900, active, sliding)
+    x2, n2 = m.read_state()
+    assert np.array_equal(ids1, ids2) and np.array_equal(vals1, vals2)
+    assert np.array_equal(x1, x2) and np.array_equal(n1, n2)
