@@ -28,6 +28,9 @@ struct chn_model {
         float scalar;
         bool has_post_attn, has_post_ffn, full;
         float *kc, *vc;
+        // head shape of this layer (full-attention layers may use the
+        // global head_dim / KV head count, src/model/loader.zig:37-41)
+        uint32_t D, nkv, qd, kvd, rot, gqa;
     };
     std::vector<Layer> L;
     uint32_t *embed_q8 = nullptr;
@@ -81,17 +84,61 @@ static int m_alloc(chn_model *m, size_t bytes, void **p) {
 
 static size_t q4b(uint32_t rows, uint32_t K) { return (size_t)rows * (K / 32) * 20; }
 
+// Head shape of a layer kind: full-attention layers take global_head_dim and
+// num_global_kv_heads when those are set (0 = same as the sliding layers),
+// and rotate their whole head (loader.zig:37-41).
+struct HeadShape {
+    uint32_t D, nkv, rot;
+};
+static HeadShape head_shape(const chn_model_config &c, bool full) {
+    HeadShape h{c.head_dim, c.num_kv_heads, c.rotary_dim};
+    if (full && c.global_head_dim) {
+        h.D = c.global_head_dim;
+        h.rot = c.global_head_dim;
+    }
+    if (full && c.num_global_kv_heads) h.nkv = c.num_global_kv_heads;
+    return h;
+}
+static void set_layer_shape(const chn_model_config &c, uint32_t i, chn_model::Layer &l) {
+    l.full = c.layer_full[i] != 0;
+    const HeadShape h = head_shape(c, l.full);
+    l.D = h.D;
+    l.nkv = h.nkv;
+    l.rot = h.rot;
+    l.qd = c.num_heads * h.D;
+    l.kvd = h.nkv * h.D;
+    l.gqa = c.num_heads / h.nkv;
+}
+struct MaxDims {
+    uint32_t D, qd, kvd;
+};
+static MaxDims max_dims(const chn_model &m) {
+    MaxDims d{0, 0, 0};
+    for (const auto &l : m.L) {
+        d.D = l.D > d.D ? l.D : d.D;
+        d.qd = l.qd > d.qd ? l.qd : d.qd;
+        d.kvd = l.kvd > d.kvd ? l.kvd : d.kvd;
+    }
+    return d;
+}
+
 static int validate_config(chn_ctx *ctx, const chn_model_config &c) {
     CHN_REQUIRE(ctx, c.num_layers >= 1 && c.num_layers <= 64, "num_layers %u must be 1..64", c.num_layers);
     CHN_REQUIRE(ctx, c.hidden_size % 128 == 0 && c.hidden_size <= 16384, "hidden_size %u must be a multiple of 128",
                 c.hidden_size);
     CHN_REQUIRE(ctx, c.intermediate_size % 128 == 0 && c.intermediate_size <= 16384,
                 "intermediate_size %u must be a multiple of 128", c.intermediate_size);
-    CHN_REQUIRE(ctx, c.head_dim == 256 || c.head_dim == 512, "head_dim %u must be 256 or 512", c.head_dim);
-    CHN_REQUIRE(ctx, c.num_heads > 0 && c.num_kv_heads > 0 && c.num_heads % c.num_kv_heads == 0,
-                "num_heads %u must be a multiple of num_kv_heads %u", c.num_heads, c.num_kv_heads);
-    CHN_REQUIRE(ctx, (c.num_heads * c.head_dim) % 128 == 0, "q_dim must be a multiple of 128");
-    CHN_REQUIRE(ctx, c.rotary_dim <= c.head_dim && c.rotary_dim % 2 == 0, "rotary_dim %u invalid", c.rotary_dim);
+    for (int full = 0; full < 2; ++full) {
+        const HeadShape h = head_shape(c, full != 0);
+        CHN_REQUIRE(ctx, h.D == 256 || h.D == 512, "head_dim %u must be 256 or 512", h.D);
+        CHN_REQUIRE(ctx, c.num_heads > 0 && h.nkv > 0 && c.num_heads % h.nkv == 0,
+                    "num_heads %u must be a multiple of the KV head count %u", c.num_heads, h.nkv);
+        const uint32_t gqa = c.num_heads / h.nkv;
+        CHN_REQUIRE(ctx, gqa == 1 || gqa == 2 || gqa == 4 || (gqa == 8 && h.D == 256),
+                    "GQA ratio %u unsupported at head_dim %u", gqa, h.D);
+        CHN_REQUIRE(ctx, (c.num_heads * h.D) % 128 == 0, "q_dim must be a multiple of 128");
+        CHN_REQUIRE(ctx, h.rot <= h.D && h.rot % 2 == 0, "rotary_dim %u invalid", h.rot);
+    }
     CHN_REQUIRE(ctx, c.vocab_size >= 64 && c.vocab_size <= 262144, "vocab_size %u must be 64..262144", c.vocab_size);
     CHN_REQUIRE(ctx, c.hidden_size <= 4096, "hidden_size %u: the Q8 logits matvec needs K <= 4096", c.hidden_size);
     CHN_REQUIRE(ctx, c.max_prefill_tokens >= 1 && c.max_prefill_tokens <= 4096, "max_prefill_tokens %u invalid",
@@ -103,10 +150,11 @@ static int validate_config(chn_ctx *ctx, const chn_model_config &c) {
 static int alloc_runtime(chn_model *m) {
     const chn_model_config &c = m->cfg;
     const uint32_t H = c.hidden_size, I = c.intermediate_size, V = c.vocab_size;
-    const uint32_t qd = c.num_heads * c.head_dim, kvd = c.num_kv_heads * c.head_dim;
+    const MaxDims md = max_dims(*m);
+    const uint32_t qd = md.qd, kvd = md.kvd;
     for (auto &l : m->L) {
-        M_ALLOC(l.kc, (size_t)kSlotsMax * kvd * 4);
-        M_ALLOC(l.vc, (size_t)kSlotsMax * kvd * 4);
+        M_ALLOC(l.kc, (size_t)kSlotsMax * l.kvd * 4);
+        M_ALLOC(l.vc, (size_t)kSlotsMax * l.kvd * 4);
     }
     M_ALLOC(m->x, H * 4);
     M_ALLOC(m->normed, H * 4);
@@ -128,7 +176,7 @@ static int alloc_runtime(chn_model *m) {
     size_t mvb = mv_ws_bytes(kmax);
     if (xbytes_bytes(H / 32) > mvb) mvb = xbytes_bytes(H / 32);
     M_ALLOC(m->mv_ws, mvb);
-    M_ALLOC(m->attn_ws, attn_ws_bytes(c.num_heads, c.head_dim, kSlotsMax));
+    M_ALLOC(m->attn_ws, attn_ws_bytes(c.num_heads, md.D, kSlotsMax));
     M_ALLOC(m->topk_ws, topk_ws_bytes(V));
     const uint32_t T = c.max_prefill_tokens;
     m->max_tok = T;
@@ -152,8 +200,8 @@ static int alloc_runtime(chn_model *m) {
     if (e != hipSuccess) return hip_fail(m->ctx, e, "hipHostMalloc");
     // zero KV caches and slot buffers with a kernel (no memset nodes anywhere)
     for (auto &l : m->L) {
-        int rc = chn_fill_u32(m->ctx, l.kc, 0, (size_t)kSlotsMax * kvd);
-        if (!rc) rc = chn_fill_u32(m->ctx, l.vc, 0, (size_t)kSlotsMax * kvd);
+        int rc = chn_fill_u32(m->ctx, l.kc, 0, (size_t)kSlotsMax * l.kvd);
+        if (!rc) rc = chn_fill_u32(m->ctx, l.vc, 0, (size_t)kSlotsMax * l.kvd);
         if (rc) return rc;
     }
     int rc = chn_fill_u32(m->ctx, m->slots, 0, 2 * kSlotsMax);
@@ -206,9 +254,7 @@ static int record_decode(chn_model *m, bool with_logits) {
     chn_ctx *ctx = m->ctx;
     hipStream_t s = ctx->stream;
     const chn_model_config &c = m->cfg;
-    const uint32_t H = c.hidden_size, I = c.intermediate_size;
-    const uint32_t D = c.head_dim, nq = c.num_heads, nkv = c.num_kv_heads;
-    const uint32_t qd = nq * D, kvd = nkv * D, gqa = nq / nkv;
+    const uint32_t H = c.hidden_size, I = c.intermediate_size, nq = c.num_heads;
     const float eps = c.rms_norm_eps;
     int rc;
 #define R_(call)                 \
@@ -225,11 +271,11 @@ static int record_decode(chn_model *m, bool with_logits) {
         const auto &l = m->L[i];
         const float theta = l.full ? c.rope_theta_full : c.rope_theta;
         if (i == 0) R_(launch_norm_planes(s, m->x, nullptr, nullptr, l.in_norm, m->normed, xp, H, eps, 1.0f, false));
-        R_(mv_qkv(ctx, l.Wq, l.Wk, l.Wv, m->normed, m->q, m->k, m->v, qd, kvd, H, xp, true));
+        R_(mv_qkv(ctx, l.Wq, l.Wk, l.Wv, m->normed, m->q, m->k, m->v, l.qd, l.kvd, H, xp, true));
         R_(launch_rope_decode_attn(ctx, m->q, m->k, m->v, l.q_norm, l.k_norm, l.kc, l.vc, m->step,
-                                   m->slots + (l.full ? 0 : kSlotsMax), m->step + (l.full ? 2 : 3), kSlotsMax, nq, D,
-                                   kvd, gqa, c.rotary_dim, (int)c.k_eq_v, theta, eps, 1.0f, m->attn, m->attn_ws, xp));
-        R_(mv_gemv(ctx, l.Wo, m->attn, m->mlp_out, H, qd, xp, true));
+                                   m->slots + (l.full ? 0 : kSlotsMax), m->step + (l.full ? 2 : 3), kSlotsMax, nq, l.D,
+                                   l.kvd, l.gqa, l.rot, (int)c.k_eq_v, theta, eps, 1.0f, m->attn, m->attn_ws, xp));
+        R_(mv_gemv(ctx, l.Wo, m->attn, m->mlp_out, H, l.qd, xp, true));
         R_(launch_norm_planes(s, m->x, m->mlp_out, l.has_post_attn ? l.post_attn : nullptr, l.pre_ffn, m->normed, xp,
                               H, eps, 1.0f, true));
         R_(mv_mlp(ctx, l.Wg, l.Wu, m->normed, m->act, I, H, xp, true));
@@ -339,8 +385,10 @@ extern "C" int chn_model_create(chn_ctx *ctx, const chn_model_config *cfg, const
     m->ctx = ctx;
     m->cfg = *cfg;
     const uint32_t H = cfg->hidden_size, I = cfg->intermediate_size;
-    const uint32_t D = cfg->head_dim, qd = cfg->num_heads * D, kvd = cfg->num_kv_heads * D;
-    const size_t tmp_elems = (size_t)I * H > (size_t)qd * H ? (size_t)I * H : (size_t)qd * H;
+    m->L.resize(cfg->num_layers);
+    for (uint32_t i = 0; i < cfg->num_layers; ++i) set_layer_shape(*cfg, i, m->L[i]);
+    const MaxDims md = max_dims(*m);
+    const size_t tmp_elems = (size_t)I * H > (size_t)md.qd * H ? (size_t)I * H : (size_t)md.qd * H;
     uint16_t *tmp = nullptr;
     hipError_t e = hipMalloc(&tmp, tmp_elems * 2);
     if (e != hipSuccess) {
@@ -352,10 +400,10 @@ extern "C" int chn_model_create(chn_ctx *ctx, const chn_model_config *cfg, const
         rc = (call);             \
         if (rc) goto fail;       \
     } while (0)
-    m->L.resize(cfg->num_layers);
     for (uint32_t i = 0; i < cfg->num_layers; ++i) {
         const chn_layer_weights &w = layers[i];
         auto &l = m->L[i];
+        const uint32_t D = l.D, qd = l.qd, kvd = l.kvd;
         if (!w.q_proj || !w.k_proj || !w.o_proj || !w.gate_proj || !w.up_proj || !w.down_proj) {
             rc = set_err(ctx, CHN_E_INVALID, "layer %u: missing projection weights", i);
             goto fail;
@@ -377,7 +425,6 @@ extern "C" int chn_model_create(chn_ctx *ctx, const chn_model_config *cfg, const
         l.has_post_attn = w.post_attention_layernorm != nullptr;
         l.has_post_ffn = w.post_feedforward_layernorm != nullptr;
         l.scalar = w.has_layer_scalar ? w.layer_scalar : 1.0f;
-        l.full = cfg->layer_full[i] != 0;
     }
     // tied embedding: a device bf16 copy for the input gather, Q8 for the logits
     C_(m_alloc(m, (size_t)cfg->vocab_size * H * 2, (void **)&m->embed_bf16));
@@ -410,7 +457,6 @@ extern "C" int chn_model_create_synthetic(chn_ctx *ctx, const chn_model_config *
     m->ctx = ctx;
     m->cfg = *cfg;
     const uint32_t H = cfg->hidden_size, I = cfg->intermediate_size, V = cfg->vocab_size;
-    const uint32_t D = cfg->head_dim, qd = cfg->num_heads * D, kvd = cfg->num_kv_heads * D;
     const float smin = 0.005f, smax = 0.02f;
 #define C_(call)                 \
     do {                         \
@@ -420,6 +466,8 @@ extern "C" int chn_model_create_synthetic(chn_ctx *ctx, const chn_model_config *
     m->L.resize(cfg->num_layers);
     for (uint32_t i = 0; i < cfg->num_layers; ++i) {
         auto &l = m->L[i];
+        set_layer_shape(*cfg, i, l);
+        const uint32_t D = l.D, qd = l.qd, kvd = l.kvd;
         const uint64_t ls = seed + 64ull * (i + 1);
         struct {
             uint32_t **w;
@@ -438,7 +486,6 @@ extern "C" int chn_model_create_synthetic(chn_ctx *ctx, const chn_model_config *
         C_(fill_ones(m, H, &l.post_ffn));
         l.has_post_attn = l.has_post_ffn = true;
         l.scalar = 1.0f;
-        l.full = cfg->layer_full[i] != 0;
     }
     // tied embedding: bf16 ~ N(0, 0.02) (kept on device for the input
     // gather), Q8-quantized for the logits exactly as quantizeRowQ8_0 would
@@ -607,9 +654,7 @@ extern "C" int chn_prefill(chn_model *m, const uint32_t *tokens, uint32_t n, con
     CHN_REQUIRE(ctx, embed_bf16 || m->embed_bf16, "no embedding table");
     for (uint32_t i = 0; i < n; ++i) CHN_REQUIRE(ctx, tokens[i] < c.vocab_size, "token %u out of range", tokens[i]);
     for (uint32_t i = 0; i < n_slots; ++i) CHN_REQUIRE(ctx, slots[i] < kSlotsMax, "slot out of range");
-    const uint32_t H = c.hidden_size, I = c.intermediate_size;
-    const uint32_t D = c.head_dim, nq = c.num_heads, nkv = c.num_kv_heads;
-    const uint32_t qd = nq * D, kvd = nkv * D, gqa = nq / nkv;
+    const uint32_t H = c.hidden_size, I = c.intermediate_size, nq = c.num_heads;
     const float eps = c.rms_norm_eps;
     const float escale = sqrtf((float)H);
 
@@ -642,11 +687,12 @@ extern "C" int chn_prefill(chn_model *m, const uint32_t *tokens, uint32_t n, con
         const auto &l = m->L[i];
         const float theta = l.full ? c.rope_theta_full : c.rope_theta;
         if (i == 0) P_(launch_rmsnorm(s, m->px, nullptr, l.in_norm, m->pn, H, n, eps, 1.0f, false));
+        const uint32_t D = l.D, nkv = l.nkv, qd = l.qd, kvd = l.kvd, gqa = l.gqa;
         P_(launch_q4gemm(ctx, 1, m->pn, l.Wq, nullptr, m->pq, n, qd, H, m->pxb));
         P_(launch_q4gemm(ctx, 1, m->pn, l.Wk, nullptr, m->pk, n, kvd, H, m->pxb));
         P_(launch_q4gemm(ctx, 1, m->pn, l.Wv, nullptr, m->pv, n, kvd, H, m->pxb));
         P_(launch_batch_qkv_rope(s, m->pq, m->pk, m->pv, l.q_norm, l.k_norm, m->pq, l.kc, l.vc, m->pslots,
-                                 num_prev_slots, start_clock, n, nq, nkv, D, c.rotary_dim, (int)c.k_eq_v, theta, eps));
+                                 num_prev_slots, start_clock, n, nq, nkv, D, l.rot, (int)c.k_eq_v, theta, eps));
         // sliding layers see the last 1024 slots (shaders/batch_causal_attn.wgsl:53)
         P_(launch_prefill_attn(s, m->pq, l.kc, l.vc, m->pslots, n, num_prev_slots, nq, D, kvd, gqa, 1.0f,
                                l.full ? 0u : 1024u, m->pattn));
@@ -682,8 +728,8 @@ extern "C" int chn_kv_read(chn_model *m, uint32_t layer, uint32_t slot_begin, ui
                            float *v_out) {
     if (!m) return CHN_E_INVALID;
     CHN_REQUIRE(m->ctx, layer < m->cfg.num_layers && slot_begin + n <= kSlotsMax, "layer/slot range out of bounds");
-    const size_t row = (size_t)m->cfg.num_kv_heads * m->cfg.head_dim;
     const auto &l = m->L[layer];
+    const size_t row = l.kvd;
     CHN_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
     if (k_out) CHN_HIP(m->ctx, hipMemcpy(k_out, l.kc + slot_begin * row, n * row * 4, hipMemcpyDeviceToHost));
     if (v_out) CHN_HIP(m->ctx, hipMemcpy(v_out, l.vc + slot_begin * row, n * row * 4, hipMemcpyDeviceToHost));
@@ -694,8 +740,8 @@ extern "C" int chn_kv_write(chn_model *m, uint32_t layer, uint32_t slot_begin, u
                             const float *v_in) {
     if (!m) return CHN_E_INVALID;
     CHN_REQUIRE(m->ctx, layer < m->cfg.num_layers && slot_begin + n <= kSlotsMax, "layer/slot range out of bounds");
-    const size_t row = (size_t)m->cfg.num_kv_heads * m->cfg.head_dim;
     const auto &l = m->L[layer];
+    const size_t row = l.kvd;
     CHN_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
     if (k_in) CHN_HIP(m->ctx, hipMemcpy(l.kc + slot_begin * row, k_in, n * row * 4, hipMemcpyHostToDevice));
     if (v_in) CHN_HIP(m->ctx, hipMemcpy(l.vc + slot_begin * row, v_in, n * row * 4, hipMemcpyHostToDevice));

@@ -22,6 +22,7 @@ class ModelConfig(ctypes.Structure):
         ("hidden_size", c_u32), ("intermediate_size", c_u32), ("vocab_size", c_u32),
         ("num_layers", c_u32), ("num_heads", c_u32), ("num_kv_heads", c_u32),
         ("head_dim", c_u32), ("rotary_dim", c_u32),
+        ("global_head_dim", c_u32), ("num_global_kv_heads", c_u32),
         ("rms_norm_eps", c_f32), ("rope_theta", c_f32), ("rope_theta_full", c_f32),
         ("sliding_window", c_u32), ("k_eq_v", c_u32), ("max_prefill_tokens", c_u32),
         ("layer_full", ctypes.c_uint8 * 64),
@@ -35,7 +36,7 @@ class ModelConfig(ctypes.Structure):
                 for i, v in enumerate(d["layer_full"]):
                     c.layer_full[i] = 1 if v else 0
             else:
-                setattr(c, name, d[name])
+                setattr(c, name, d.get(name, 0) if name in ("global_head_dim", "num_global_kv_heads") else d[name])
         return c
 
     def to_dict(self):
@@ -77,7 +78,6 @@ class Model:
         self._check("chn_model_get_config", lib.chn_model_get_config(handle, ctypes.byref(cfg)))
         self.config = cfg
         self.H = cfg.hidden_size
-        self.kv_dim = cfg.num_kv_heads * cfg.head_dim
 
     def _check(self, fn, rc):
         if rc != 0:
@@ -181,16 +181,25 @@ class Model:
             p(lg), p(ids), p(vals), cb, None))
         return lg, ids, vals
 
+    def layer_kv_dim(self, layer):
+        c = self.config
+        full = bool(c.layer_full[layer])
+        D = c.global_head_dim if full and c.global_head_dim else c.head_dim
+        nkv = c.num_global_kv_heads if full and c.num_global_kv_heads else c.num_kv_heads
+        return D * nkv
+
     def kv_read(self, layer, slot_begin, n):
-        k = np.zeros((n, self.kv_dim), np.float32)
-        v = np.zeros((n, self.kv_dim), np.float32)
+        kvd = self.layer_kv_dim(layer)
+        k = np.zeros((n, kvd), np.float32)
+        v = np.zeros((n, kvd), np.float32)
         self._check("chn_kv_read", lib.chn_kv_read(self.handle, layer, slot_begin, n,
                                                    k.ctypes.data_as(c_void_p), v.ctypes.data_as(c_void_p)))
         return k, v
 
     def kv_write(self, layer, slot_begin, k, v):
-        kk = np.ascontiguousarray(k, dtype=np.float32).reshape(-1, self.kv_dim)
-        vv = np.ascontiguousarray(v, dtype=np.float32).reshape(-1, self.kv_dim)
+        kvd = self.layer_kv_dim(layer)
+        kk = np.ascontiguousarray(k, dtype=np.float32).reshape(-1, kvd)
+        vv = np.ascontiguousarray(v, dtype=np.float32).reshape(-1, kvd)
         if kk.shape != vv.shape:
             raise ValueError("k and v differ in shape")
         self._check("chn_kv_write", lib.chn_kv_write(self.handle, layer, slot_begin, kk.shape[0],

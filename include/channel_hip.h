@@ -231,6 +231,10 @@ int chn_to_bf16_bits(chn_ctx *ctx, const float *src, uint16_t *dst, size_t n);
 typedef struct chn_model_config {
     uint32_t hidden_size, intermediate_size, vocab_size, num_layers;
     uint32_t num_heads, num_kv_heads, head_dim, rotary_dim;
+    /* full-attention layers: global_head_dim / num_global_key_value_heads
+     * (0 = same as head_dim / num_kv_heads); such layers rotate their whole
+     * head (src/model/loader.zig:37-41) */
+    uint32_t global_head_dim, num_global_kv_heads;
     float rms_norm_eps, rope_theta, rope_theta_full;
     uint32_t sliding_window;       /* informational: slot lists come from the caller */
     uint32_t k_eq_v;               /* attention_k_eq_v */
@@ -317,7 +321,7 @@ int chn_prefill(chn_model *m, const uint32_t *tokens, uint32_t n, const uint16_t
 /* KV cache access replacing the UMA reads/writes of buf_k_cache/buf_v_cache
  * (src/snapshot.zig:95-98,171-174, src/memory.zig:104-107,
  * src/hippocampus.zig:166-169, src/model/memory_inject.zig:14-30): n slots
- * from slot_begin of one layer, each num_kv_heads*head_dim floats. */
+ * from slot_begin of one layer, each that layer's kv_dim floats. */
 int chn_kv_read(chn_model *m, uint32_t layer, uint32_t slot_begin, uint32_t n, float *k_out, float *v_out);
 int chn_kv_write(chn_model *m, uint32_t layer, uint32_t slot_begin, uint32_t n, const float *k_in,
                  const float *v_in);

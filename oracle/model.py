@@ -16,6 +16,19 @@ def bf16_to_f32(b):
     return (np.asarray(b, np.uint32) << 16).view(np.float32)
 
 
+def layer_shape(cfg, i):
+    """(D, num_kv_heads, rotary_dim) of layer i: full-attention layers take
+    global_head_dim / num_global_kv_heads when set and rotate the whole head
+    (src/model/loader.zig:37-41)."""
+    full = bool(cfg["layer_full"][i])
+    D, nkv, rot = cfg["head_dim"], cfg["num_kv_heads"], cfg["rotary_dim"]
+    if full and cfg.get("global_head_dim"):
+        D = rot = cfg["global_head_dim"]
+    if full and cfg.get("num_global_kv_heads"):
+        nkv = cfg["num_global_kv_heads"]
+    return D, nkv, rot
+
+
 class Weights:
     """Quantized / fp32 copies of a model given as bf16 arrays (dict per layer
     with keys q_proj, k_proj, v_proj, o_proj, gate_proj, up_proj, down_proj,
@@ -24,9 +37,11 @@ class Weights:
 
     def __init__(self, cfg, layers, embed_bf16, final_norm_bf16):
         self.cfg = cfg
-        H, D = cfg["hidden_size"], cfg["head_dim"]
+        H = cfg["hidden_size"]
         self.layers = []
-        for l in layers:
+        for i, l in enumerate(layers):
+            D, nkv, rot = layer_shape(cfg, i)
+
             def norm(key, n):
                 v = l.get(key)
                 return np.ones(n, np.float32) if v is None else bf16_to_f32(v).astype(np.float32)
@@ -42,6 +57,7 @@ class Weights:
                 "post_ffn": None if l.get("post_feedforward_layernorm") is None
                 else norm("post_feedforward_layernorm", H),
                 "scalar": np.float32(l.get("layer_scalar", 1.0)),
+                "D": D, "nkv": nkv, "rot": rot,
             }
             self.layers.append(d)
         self.embed_bf16 = embed_bf16
@@ -58,26 +74,26 @@ class Weights:
 
 
 def new_caches(cfg, nslot=4096):
-    kvd = cfg["num_kv_heads"] * cfg["head_dim"]
-    L = cfg["num_layers"]
-    return ([np.zeros(nslot * kvd, np.float32) for _ in range(L)],
-            [np.zeros(nslot * kvd, np.float32) for _ in range(L)])
+    kvds = [layer_shape(cfg, i)[0] * layer_shape(cfg, i)[1] for i in range(cfg["num_layers"])]
+    return ([np.zeros(nslot * k, np.float32) for k in kvds],
+            [np.zeros(nslot * k, np.float32) for k in kvds])
 
 
 def decode_step(W, kc, vc, x, clock, slot_idx, active, sliding, with_logits=True):
     """One token through every layer; kc / vc (per-layer flat arrays) are
     updated in place.  Returns (x, normed, logits, ids, vals)."""
     c = W.cfg
-    H, I, D = c["hidden_size"], c["intermediate_size"], c["head_dim"]
-    nq, nkv = c["num_heads"], c["num_kv_heads"]
-    qd, kvd, eps = nq * D, nkv * D, c["rms_norm_eps"]
+    H, I = c["hidden_size"], c["intermediate_size"]
+    nq, eps = c["num_heads"], c["rms_norm_eps"]
     x = np.array(x, np.float32)
     normed = O.rmsnorm(x, W.layers[0]["in_norm"], eps)
     for i, l in enumerate(W.layers):
         full = bool(c["layer_full"][i])
         theta = c["rope_theta_full"] if full else c["rope_theta"]
+        D, nkv = l["D"], l["nkv"]
+        qd, kvd = nq * D, nkv * D
         q, k, v = O.fused_qkv_q4(l["Wq"], l["Wk"], l["Wv"], normed, qd, kvd, H)
-        q = O.qkv_rope(q, k, v, l["q_norm"], l["k_norm"], kc[i], vc[i], nq, nkv, D, c["rotary_dim"],
+        q = O.qkv_rope(q, k, v, l["q_norm"], l["k_norm"], kc[i], vc[i], nq, nkv, D, l["rot"],
                        c["k_eq_v"], theta, eps, clock, slot_idx)
         slots = np.asarray(active if full else sliding, np.uint32)
         attn = O.decode_attn(q, kc[i], vc[i], slots, nq, D, kvd, nq // nkv, 1.0)
@@ -106,9 +122,8 @@ def prefill(W, kc, vc, tokens, slots, start_clock, num_prev, bf16_gemm=True, win
     """gpuDispatchPrefillBatch; GEMMs use the bf16-operand model of the MFMA
     path when bf16_gemm (else fp32).  Returns (X, Xn, logits, ids, vals)."""
     c = W.cfg
-    H, I, D = c["hidden_size"], c["intermediate_size"], c["head_dim"]
-    nq, nkv = c["num_heads"], c["num_kv_heads"]
-    qd, kvd, eps = nq * D, nkv * D, c["rms_norm_eps"]
+    H, I = c["hidden_size"], c["intermediate_size"]
+    nq, eps = c["num_heads"], c["rms_norm_eps"]
     n = len(tokens)
     gemm = O.batch_gemm_q4_bf16 if bf16_gemm else O.batch_gemm_q4
     slots = np.asarray(slots, np.uint32)
@@ -117,13 +132,15 @@ def prefill(W, kc, vc, tokens, slots, start_clock, num_prev, bf16_gemm=True, win
     for i, l in enumerate(W.layers):
         full = bool(c["layer_full"][i])
         theta = c["rope_theta_full"] if full else c["rope_theta"]
+        D, nkv = l["D"], l["nkv"]
+        qd, kvd = nq * D, nkv * D
         Q = gemm(l["Wq"], Xn, n, qd, H)
         K = gemm(l["Wk"], Xn, n, kvd, H)
         V = gemm(l["Wv"], Xn, n, kvd, H)
         Qr = np.zeros_like(Q)
         for t in range(n):
             Qr[t] = O.qkv_rope(Q[t], K[t], V[t], l["q_norm"], l["k_norm"], kc[i], vc[i], nq, nkv, D,
-                               c["rotary_dim"], c["k_eq_v"], theta, eps, start_clock + t,
+                               l["rot"], c["k_eq_v"], theta, eps, start_clock + t,
                                int(slots[num_prev + t]))
         A = O.batch_causal_attn(Qr, kc[i], vc[i], slots, n, num_prev, nq, D, kvd, nq // nkv, 1.0,
                                 0 if full else window).reshape(n, qd)
@@ -165,8 +182,7 @@ def random_model(cfg, seed):
     (q/k norms a quarter of that, so that unit-scale q.k scores stay O(1)
     as trained q/k norms keep them), embedding ~ N(0, 0.02^2); even layers
     carry a post-FFN norm, odd layers a layer scalar of 0.75."""
-    H, I, D = cfg["hidden_size"], cfg["intermediate_size"], cfg["head_dim"]
-    qd, kvd = cfg["num_heads"] * D, cfg["num_kv_heads"] * D
+    H, I = cfg["hidden_size"], cfg["intermediate_size"]
 
     def nrm(n, s, base=1.0):
         return _bf16_round((bf16_to_f32(random_bf16((n,), s, 0.1)) + np.float32(1.0)) * np.float32(base))
@@ -174,6 +190,8 @@ def random_model(cfg, seed):
     layers = []
     for i in range(cfg["num_layers"]):
         s = seed + 100 * i
+        D, nkv, _ = layer_shape(cfg, i)
+        qd, kvd = cfg["num_heads"] * D, nkv * D
         layers.append({
             "q_proj": random_bf16((qd, H), s + 1, 0.05), "k_proj": random_bf16((kvd, H), s + 2, 0.05),
             "v_proj": random_bf16((kvd, H), s + 3, 0.05), "o_proj": random_bf16((H, qd), s + 4, 0.05),
@@ -190,7 +208,8 @@ def random_model(cfg, seed):
 
 def default_config(**kw):
     c = dict(hidden_size=3840, intermediate_size=15360, vocab_size=262144, num_layers=48,
-             num_heads=16, num_kv_heads=8, head_dim=256, rotary_dim=256, rms_norm_eps=1e-6,
+             num_heads=16, num_kv_heads=8, head_dim=256, rotary_dim=256, global_head_dim=0,
+             num_global_kv_heads=0, rms_norm_eps=1e-6,
              rope_theta=1e4, rope_theta_full=1e6, sliding_window=512, k_eq_v=0,
              max_prefill_tokens=1024)
     c.update(kw)

@@ -255,3 +255,43 @@ def test_created_model_token_path_matches_step(pair):
     x2, n2 = m.read_state()
     assert np.array_equal(ids1, ids2) and np.array_equal(vals1, vals2)
     assert np.array_equal(x1, x2) and np.array_equal(n1, n2)
+
+
+CFG_G = OM.default_config(hidden_size=256, intermediate_size=512, vocab_size=4096, num_layers=3,
+                          num_heads=4, num_kv_heads=2, head_dim=256, rotary_dim=128, global_head_dim=512,
+                          num_global_kv_heads=1, layer_full=[0, 1, 0], max_prefill_tokens=64,
+                          sliding_window=16)
+
+
+def test_global_head_shape_model(ctx):
+    """Full-attention layers with global_head_dim 512 and one KV head (GQA 4)
+    next to sliding layers with head_dim 256 (GQA 2): prefill and decode
+    against the oracle."""
+    layers, embed, final = OM.random_model(CFG_G, 31)
+    W = OM.Weights(CFG_G, layers, embed, final)
+    say("model_create global head shapes")
+    with Model.create(ctx, CFG_G, layers, embed, final) as m:
+        toks = [int(t) for t in np.random.default_rng(8).integers(0, 4096, 20)]
+        n = len(toks)
+        lg, ids, vals = m.prefill_batch(toks, np.arange(n), 0, 0, embed_bf16=W.embed_bf16)
+        kc, vc = OM.new_caches(CFG_G, 4096)
+        _, _, lg_o, _, _ = OM.prefill(W, kc, vc, toks, np.arange(n), 0, 0, bf16_gemm=True)
+        assert rel_err(lg, lg_o) < 1e-2
+        for i in range(3):
+            k, v = m.kv_read(i, 0, n)
+            kvd = k.shape[1]
+            assert kvd == 512   # one 512-wide global KV head, or two 256-wide sliding ones
+            assert rel_err(k, kc[i][: n * kvd].reshape(n, kvd)) < 1e-2
+            kc[i][: n * kvd] = k.ravel()
+            vc[i][: n * kvd] = v.ravel()
+        tok = int(ids[0])
+        for clock in range(n, n + 3):
+            active, sliding = OM.slot_lists(clock, WINDOW)
+            x_in = W.embed([tok])[0]
+            say(f"global-shape decode clock={clock}")
+            t_gpu, ids_g, vals_g = m.forward_token(x_in, clock, clock, active, sliding)
+            x_o, nx_o, lg_o, _, _ = OM.decode_step(W, kc, vc, x_in, clock, clock, active, sliding)
+            assert_topk_valid(ids_g, vals_g, lg_o, 1e-3)
+            x_g, _ = m.read_state()
+            assert rel_err(x_g, x_o) < 1e-3
+            tok = int(ids_g[0])

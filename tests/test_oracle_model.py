@@ -109,3 +109,24 @@ def test_topk_of_decode_matches_logits(weights):
     order = np.argsort(-capped.astype(np.float64), kind="stable")[:64]
     assert np.array_equal(ids, order.astype(np.uint32))
     assert np.array_equal(vals, capped[order])
+
+
+def test_global_head_shape_layers():
+    """Full-attention layers with their own head_dim / KV head count
+    (global_head_dim 512, one global KV head, whole-head rotation) run
+    through both compositions consistently."""
+    cfg = OM.default_config(hidden_size=128, intermediate_size=256, vocab_size=512, num_layers=3,
+                            num_heads=2, num_kv_heads=1, head_dim=256, rotary_dim=128, global_head_dim=512,
+                            num_global_kv_heads=1, layer_full=[0, 1, 0], max_prefill_tokens=16)
+    layers, embed, final = OM.random_model(cfg, 3)
+    assert layers[1]["q_proj"].shape == (2 * 512, 128) and layers[0]["q_proj"].shape == (2 * 256, 128)
+    W = OM.Weights(cfg, layers, embed, final)
+    toks = [1, 5, 9, 13, 17, 21]
+    kc1, vc1 = OM.new_caches(cfg, 32)
+    kc2, vc2 = OM.new_caches(cfg, 32)
+    assert kc1[1].size == 32 * 512 and kc1[0].size == 32 * 256
+    X, *_ = OM.prefill(W, kc1, vc1, toks, np.arange(6), 0, 0, bf16_gemm=False)
+    for t, tok in enumerate(toks):
+        a, s = OM.slot_lists(t, 1024)
+        x, *_ = OM.decode_step(W, kc2, vc2, W.embed([tok])[0], t, t, a, s)
+        assert _rel(X[t], x) < 1e-4
