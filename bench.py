@@ -44,6 +44,10 @@ def q4_bytes(rows, K):
     return rows * (K // 32) * 20
 
 
+def q4r_bytes(rows, K):
+    return rows * (K // 32) * 18
+
+
 def load_traffic(kernel, workload):
     """HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE /
     WRITE_SIZE and calibrated on a plain copy, read from the table in
@@ -166,34 +170,46 @@ def bench_mlp(ctx, args):
     }
 
 
-def alloc_gateup_copies(ctx, H, I, min_bytes=ROTATE_BYTES):
-    """Distinct 12B-dims gate/up pairs, enough to exceed the Infinity Cache."""
+def alloc_gateup_copies(ctx, H, I, min_bytes=ROTATE_BYTES, repacked=False):
+    """Distinct 12B-dims gate/up pairs, enough to exceed the Infinity Cache,
+    in the reference Q4 layout or repacked (Q4R, the model's layout)."""
     w_bytes = q4_bytes(I, H)
     ncopy = max(4, -(-min_bytes // (2 * w_bytes)))
     pairs = []
     for c in range(ncopy):
-        g = ctx.alloc(w_bytes)
-        u = ctx.alloc(w_bytes)
-        ctx.call("chn_synth_q4", g, I, H, SEED + 16 * c, 0.005, 0.02)
-        ctx.call("chn_synth_q4", u, I, H, SEED + 16 * c + 1, 0.005, 0.02)
-        pairs.append((g, u))
+        pair = []
+        for k in range(2):
+            w = ctx.alloc(w_bytes)
+            ctx.call("chn_synth_q4", w, I, H, SEED + 16 * c + k, 0.005, 0.02)
+            if repacked:
+                r = ctx.alloc(q4r_bytes(I, H))
+                ctx.call("chn_q4_repack", w, I, H, r)
+                ctx.sync()
+                w.free()
+                w = r
+            pair.append(w)
+        pairs.append(tuple(pair))
     return pairs
 
 
-def time_gateup(ctx, pairs, x, act, H, I, reps):
-    """Average duration (ms) of chn_fused_mlp_q4 (k_xplanes + k_q4mv<MLP>)
-    over back-to-back launches on the library stream, HIP events."""
+def time_gateup(ctx, pairs, x, act, H, I, reps, repacked=False):
+    """Average duration (ms) of the fused gate/up matvec (planes pass +
+    matvec) over back-to-back launches on the library stream, HIP events."""
+    fn = "chn_fused_mlp_q4r" if repacked else "chn_fused_mlp_q4"
     for i in range(4):
-        ctx.call("chn_fused_mlp_q4", pairs[i % len(pairs)][0], pairs[i % len(pairs)][1], x, act, I, H)
+        ctx.call(fn, pairs[i % len(pairs)][0], pairs[i % len(pairs)][1], x, act, I, H)
     ctx.timer_start()
     for i in range(reps):
         g, u = pairs[i % len(pairs)]
-        ctx.call("chn_fused_mlp_q4", g, u, x, act, I, H)
+        ctx.call(fn, g, u, x, act, I, H)
     return ctx.timer_stop() / reps
 
 
-def gateup_bytes(H, I):
-    return 2 * q4_bytes(I, H) + H * 4 + I * 4
+def gateup_bytes(H, I, repacked=False):
+    """Bytes of one gate/up launch: the reference layout's algorithmic count
+    (20 B per 32 weights), or what the repacked layout reads (18 B)."""
+    w = q4r_bytes(I, H) if repacked else q4_bytes(I, H)
+    return 2 * w + H * 4 + I * 4
 
 
 CFG_12B = dict(hidden_size=3840, intermediate_size=15360, vocab_size=262144, num_layers=48,
@@ -355,11 +371,11 @@ def bench_decode(ctx, args):
 
     # dominant kernel: fused gate/up matvec at the model's shape, rotating
     # distinct weight pairs, back to back on the library stream
-    pairs = alloc_gateup_copies(ctx, H, I)
+    pairs = alloc_gateup_copies(ctx, H, I, repacked=True)
     x = ctx.alloc(H * 4)
     ctx.call("chn_synth_normal", x, H, SEED + 7, 1.0)
     act = ctx.alloc(I * 4)
-    k_ms = time_gateup(ctx, pairs, x, act, H, I, max(192, 4 * len(pairs)))
+    k_ms = time_gateup(ctx, pairs, x, act, H, I, max(192, 4 * len(pairs)), repacked=True)
     achieved = gateup_bytes(H, I) / (k_ms * 1e-3) / 1e9
 
     cpu = None
@@ -381,11 +397,14 @@ def bench_decode(ctx, args):
                    "token_roofline_frac": (w_bytes + kv_bytes) / (ms_per_tok * 1e-3) / 1e9 / HBM_PEAK_GBS,
                    "model_create_s": t_create,
                    "decode_launch": "eager kernel launches" if args.eager else "HIP graph replay"},
-        "roofline": {"kernel": "chn_fused_mlp_q4 = k_xplanes + k_q4mv<MLP> (gate/up + GELU-tanh, 15360x3840 x2)",
+        "roofline": {"kernel": "chn_fused_mlp_q4r = k_xplanes + k_q4rmv<MLP> (gate/up + GELU-tanh, "
+                               "15360x3840 x2, repacked weights as the model holds them)",
                      "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": load_traffic("k_q4mv<MLP>", "gate/up 15360x3840"),
-                     "algorithmic_bytes_per_launch": gateup_bytes(H, I), "avg_launch_ms": k_ms},
+                     "traffic": load_traffic("k_q4rmv<MLP>", "gate/up 15360x3840"),
+                     "algorithmic_bytes_per_launch": gateup_bytes(H, I),
+                     "bytes_per_launch_repacked_layout": gateup_bytes(H, I, repacked=True),
+                     "avg_launch_ms": k_ms},
         "cpu_baseline": cpu,
         "dtype": "fp32 accumulate over Q4 weights (Q8 logits)",
         "data": "synthetic (seeded random-init 12B Q4 weights: codes uniform 0..15, f16 scales "

@@ -16,10 +16,16 @@ def q4_bytes(rows, K):
     return rows * ((K + 31) // 32) * Q4_BLOCK_BYTES
 
 
+def q4r_bytes(rows, K):
+    """Bytes of a repacked (Q4R) matrix: 16 B of nibbles + 2 B of f16 scale
+    per 32 weights."""
+    return rows * (K // 32) * 18
+
+
 def q8_bytes(rows, K):
     """getQuantizedSizeBytes(rows, K, .q8) (src/quant.zig:181-183)."""
     return rows * ((K + 31) // 32) * Q8_BLOCK_BYTES
 
 
 __all__ = ["Buffer", "ChannelError", "Context", "HEADER_PATH", "LIB_PATH", "PROTOTYPES",
-           "device_count", "lib", "q4_bytes", "q8_bytes"]
+           "device_count", "lib", "q4_bytes", "q4r_bytes", "q8_bytes"]

@@ -72,6 +72,23 @@ int mv_mlp(chn_ctx *ctx, const uint32_t *Wg, const uint32_t *Wu, const float *x,
            uint32_t *ws, bool planes_ready = false);
 int launch_rmsnorm(hipStream_t s, float *x, const float *r, const float *w, float *y, uint32_t dim, uint32_t rows,
                    float eps, float scalar, bool add);
+// Digit planes of x (nb 32-blocks) into xp (xplanes_bytes(nb)).
+int launch_xplanes(hipStream_t s, const float *x, uint32_t *xp, uint32_t nb);
+
+// ---- repacked Q4 ("Q4R"): per matrix [rows][nb] 16-byte nibble words
+// (each nibble XOR 8, i.e. two's-complement q - 8), then [rows][nb] f16
+// scales.  18 bytes per 32 weights; the reference layout's unused f16 min
+// is dropped.
+inline size_t q4r_bytes(uint32_t rows, uint32_t K) { return (size_t)rows * (K / 32) * 18; }
+int launch_q4_repack(hipStream_t s, const uint32_t *W, uint32_t rows, uint32_t K, void *dst);
+// Matvecs over Q4R weights with activation planes already in xp (or, if
+// !planes_ready, computed from x into xp first).  K % 32 == 0, K <= 16384.
+int mvr_gemv(chn_ctx *ctx, const void *W, const float *x, float *y, uint32_t M, uint32_t K, uint32_t *xp,
+             bool planes_ready);
+int mvr_qkv(chn_ctx *ctx, const void *Wq, const void *Wk, const void *Wv, const float *x, float *q, float *k,
+            float *v, uint32_t q_dim, uint32_t kv_dim, uint32_t K, uint32_t *xp, bool planes_ready);
+int mvr_mlp(chn_ctx *ctx, const void *Wg, const void *Wu, const float *x, float *act, uint32_t M, uint32_t K,
+            uint32_t *xp, bool planes_ready);
 // Decode-step norm with planes: r' = post ? rmsnorm(r) * post_w : r;
 // x = add ? (x + r') * scalar : x; y = rmsnorm(x) * w; planes of y into xp
 // (if non-NULL).  One row, dim % 8 == 0, dim <= 8192.
@@ -109,8 +126,9 @@ int launch_topk64(hipStream_t st, const float *logits, uint32_t V, uint32_t *ids
 int launch_embed(hipStream_t st, const uint16_t *table, const uint32_t *tokens, uint32_t n, uint32_t H, float scale,
                  float *x);
 int launch_quantize(hipStream_t st, int q8, const uint16_t *src, uint32_t *dst, uint64_t nblk);
+// W0/W1 in the reference Q4 layout, or in Q4R with repacked.
 int launch_q4gemm(chn_ctx *ctx, int nmat, const float *X, const uint32_t *W0, const uint32_t *W1, float *Y,
-                  uint32_t n_tok, uint32_t M, uint32_t K, __bf16 *xb);
+                  uint32_t n_tok, uint32_t M, uint32_t K, __bf16 *xb, bool repacked);
 
 // ---------------------------------------------------------------------
 // Device helpers
@@ -180,6 +198,37 @@ __device__ __forceinline__ float wave_reduce_v(const float (&acc)[V], int lane) 
 
 template <int V>
 constexpr int ilog2_c() { return V <= 1 ? 0 : 1 + ilog2_c<V / 2>(); }
+
+// Sum over the 16 lanes of each DPP row; every lane of the row gets the sum.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true)); // quad_perm [1,0,3,2]
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true)); // quad_perm [2,3,0,1]
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xF, 0xF, true)); // row_ror:4
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xF, 0xF, true)); // row_ror:8
+    return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xF, 0xF, true)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xF, 0xF, true)));
+    return v;
+}
+// Whole-wave sum / max: row reductions, then the four row results.
+__device__ __forceinline__ float wave_sum64(float v) {
+    v = row16_sum(v);
+    return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16))) +
+           (__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48)));
+}
+__device__ __forceinline__ float wave_max64(float v) {
+    v = row16_max(v);
+    return fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)),
+                       __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16))),
+                 fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32)),
+                       __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48))));
+}
 
 // Digit planes of one 32-block from the four lanes 4k..4k+3 of a wave that
 // hold its words w = lane & 3 (eight consecutive values each).  All four

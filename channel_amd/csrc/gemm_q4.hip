@@ -48,10 +48,12 @@ __global__ __launch_bounds__(256) void k_to_bf16(const float *__restrict__ x, __
 
 struct GemmArgs {
     const __bf16 *X;       // [n_tok][K] bf16
-    const uint32_t *W0, *W1; // Q4 [M][K/32][5] (W1: up matrix for the fused MLP)
+    const uint32_t *W0, *W1; // Q4 [M][K/32][5], or Q4R (W1: up matrix for the fused MLP)
     float *Y;              // [n_tok][M]
     uint32_t n_tok, M, K;
 };
+
+typedef uint32_t u32x4g __attribute__((ext_vector_type(4)));
 
 // Dequantize one Q4 block (5 words) to 32 bf16 = 4 x 16 bytes.
 __device__ __forceinline__ void dequant_block_bf16(const uint32_t w0, const u32x4v q, u32x4v (&out)[4]) {
@@ -78,7 +80,9 @@ __device__ __forceinline__ void dequant_block_bf16(const uint32_t w0, const u32x
     }
 }
 
-template <int NMAT>
+// REP: weights in the repacked layout (16-byte nibble words, each nibble
+// XOR 8, then f16 scales), un-XORed here so the dequantization is shared.
+template <int NMAT, bool REP>
 __global__ __launch_bounds__(256, 2) void k_q4gemm(GemmArgs a) {
     __shared__ __attribute__((aligned(16))) unsigned char lx[GT * LROW];
     __shared__ __attribute__((aligned(16))) unsigned char lw[NMAT][GN * LROW];
@@ -110,9 +114,17 @@ __global__ __launch_bounds__(256, 2) void k_q4gemm(GemmArgs a) {
         for (int m = 0; m < NMAT; ++m) {
             const uint32_t *W = m == 0 ? a.W0 : a.W1;
             if (n < a.M && b < nb) {
-                const uint32_t *p = W + ((size_t)n * nb + b) * 5;
-                ww0[m] = p[0];
-                wq[m] = *(const u32x4_a4 *)(p + 1);
+                if (REP) {
+                    const size_t i = (size_t)n * nb + b;
+                    const u32x4g qv = ((const u32x4g *)W)[i];
+                    wq[m] = u32x4v{qv[0] ^ 0x88888888u, qv[1] ^ 0x88888888u, qv[2] ^ 0x88888888u,
+                                   qv[3] ^ 0x88888888u};
+                    ww0[m] = ((const uint16_t *)((const unsigned char *)W + (size_t)a.M * nb * 16))[i];
+                } else {
+                    const uint32_t *p = W + ((size_t)n * nb + b) * 5;
+                    ww0[m] = p[0];
+                    wq[m] = *(const u32x4_a4 *)(p + 1);
+                }
             } else {
                 ww0[m] = 0;
                 wq[m] = u32x4v{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
@@ -189,7 +201,7 @@ __global__ __launch_bounds__(256, 2) void k_q4gemm(GemmArgs a) {
 }
 
 int launch_q4gemm(chn_ctx *ctx, int nmat, const float *X, const uint32_t *W0, const uint32_t *W1, float *Y,
-                  uint32_t n_tok, uint32_t M, uint32_t K, __bf16 *xb) {
+                  uint32_t n_tok, uint32_t M, uint32_t K, __bf16 *xb, bool repacked) {
     const size_t n = (size_t)n_tok * K;
     unsigned g = (unsigned)((n / 4 + 255) / 256);
     if (g > 8192) g = 8192;
@@ -198,8 +210,13 @@ int launch_q4gemm(chn_ctx *ctx, int nmat, const float *X, const uint32_t *W0, co
     CHN_LAUNCHED(ctx, "k_to_bf16");
     GemmArgs a{xb, W0, W1, Y, n_tok, M, K};
     dim3 grid((M + GN - 1) / GN, (n_tok + GT - 1) / GT);
-    if (nmat == 1) k_q4gemm<1><<<grid, 256, 0, ctx->stream>>>(a);
-    else k_q4gemm<2><<<grid, 256, 0, ctx->stream>>>(a);
+    if (repacked) {
+        if (nmat == 1) k_q4gemm<1, true><<<grid, 256, 0, ctx->stream>>>(a);
+        else k_q4gemm<2, true><<<grid, 256, 0, ctx->stream>>>(a);
+    } else {
+        if (nmat == 1) k_q4gemm<1, false><<<grid, 256, 0, ctx->stream>>>(a);
+        else k_q4gemm<2, false><<<grid, 256, 0, ctx->stream>>>(a);
+    }
     CHN_LAUNCHED(ctx, "k_q4gemm");
     return CHN_OK;
 }
@@ -213,7 +230,7 @@ static int gemm_common(chn_ctx *ctx, int nmat, const uint32_t *W0, const uint32_
     if (!n_tok || !M) return CHN_OK;
     int rc = ensure_workspace(ctx, (size_t)n_tok * K * 2);
     if (rc) return rc;
-    return launch_q4gemm(ctx, nmat, X, W0, W1, Y, n_tok, M, K, (__bf16 *)ctx->ws);
+    return launch_q4gemm(ctx, nmat, X, W0, W1, Y, n_tok, M, K, (__bf16 *)ctx->ws, false);
 }
 
 }  // namespace chn

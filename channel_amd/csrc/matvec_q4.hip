@@ -45,6 +45,11 @@ __global__ __launch_bounds__(256) void k_xplanes(const float *__restrict__ x, ui
     emit_planes8(v, xp, nb, b, w, ok);
 }
 
+int launch_xplanes(hipStream_t s, const float *x, uint32_t *xp, uint32_t nb) {
+    k_xplanes<<<(4 * nb + 255) / 256, 256, 0, s>>>(x, xp, nb);
+    return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
+}
+
 enum MatvecMode { MV_GEMV = 0, MV_QKV = 1, MV_MLP = 2 };
 
 struct MatvecArgs {

@@ -1,0 +1,348 @@
+// Batch-1 decode matvecs over repacked Q4 weights ("Q4R"), the layout the
+// model keeps in HBM.  Same contractions as gemv_q4 / fused_qkv_q4 /
+// fused_mlp_q4 (shaders/gemv_q4.wgsl, fused_qkv_q4.wgsl, fused_mlp_q4.wgsl):
+//
+//   y[r] = sum_b f16(s_rb) * sum_i (q_rbi - 8) * x[32 b + i]
+//
+// Q4R stores, per matrix, the 16 nibble bytes of every 32-block as one
+// aligned 16-byte word ([rows][nb]) with each nibble XOR 8 -- exactly the
+// signed value q - 8 in two's-complement 4-bit -- followed by the f16 scales
+// ([rows][nb]).  The reference layout's f16 "min" half-word is never read
+// by the dequantization (scale * (q - 8)) and is dropped: 18 bytes per 32
+// weights instead of 20.  The repack is a pure bit permutation, so every
+// product is the same as on the reference layout.
+//
+// Lane l of a wave owns blocks l and l + 64 of its K range: one aligned,
+// fully coalesced 16-byte load (nibbles) and one 2-byte load (scale) per
+// block, no LDS staging.  Activations arrive as digit planes (see
+// chn_internal.h) held in registers; a block is 24 v_dot8c_i32_i4 in plane
+// order, the exact integer sum is scaled once.  Waves are persistent over
+// row groups; the next group's weights are in flight while the current one
+// is reduced (DPP row sums + readlane).  Waves that split K (WPR > 1) meet
+// in LDS in a fixed order.
+#include "chn_internal.h"
+
+namespace chn {
+
+typedef uint32_t u32x4r __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void k_repack_q4(const uint32_t *__restrict__ src, u32x4r *__restrict__ N,
+                                                   uint16_t *__restrict__ S, size_t nblk) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblk) return;
+    const uint32_t *p = src + i * 5;
+    N[i] = u32x4r{p[1] ^ 0x88888888u, p[2] ^ 0x88888888u, p[3] ^ 0x88888888u, p[4] ^ 0x88888888u};
+    S[i] = (uint16_t)(p[0] & 0xffffu);
+}
+
+int launch_q4_repack(hipStream_t s, const uint32_t *W, uint32_t rows, uint32_t K, void *dst) {
+    const size_t nblk = (size_t)rows * (K / 32);
+    if (!nblk) return CHN_OK;
+    u32x4r *N = (u32x4r *)dst;
+    uint16_t *S = (uint16_t *)((unsigned char *)dst + nblk * 16);
+    k_repack_q4<<<(unsigned)((nblk + 255) / 256), 256, 0, s>>>(W, N, S, nblk);
+    return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
+}
+
+enum RMode { RV_GEMV = 0, RV_QKV = 1, RV_MLP = 2 };
+
+struct RMat {
+    const u32x4r *N;
+    const uint16_t *S;
+};
+
+struct RArgs {
+    RMat m0, m1, m2;            // GEMV: m0. QKV: q, k, v. MLP: gate, up.
+    float *y0, *y1, *y2;
+    const uint32_t *xp;
+    uint32_t M, seg1, seg2, nb;
+};
+
+// sum_i (q_i - 8) X_i of one block: the signed nibbles times each plane.
+__device__ __forceinline__ int block_idot_r(const u32x4r s, const uint32_t (&P)[XP_WORDS]) {
+    int t[XP_PLANES];
+#pragma unroll
+    for (int p = 0; p < XP_PLANES; ++p) {
+        int a = 0;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) a = __builtin_amdgcn_sdot8((int)s[w], (int)P[p * 4 + w], a, false);
+        t[p] = a;
+    }
+    int T = t[XP_PLANES - 1];
+#pragma unroll
+    for (int p = XP_PLANES - 2; p >= 0; --p) T = (T << 4) + t[p];
+    return T;
+}
+
+template <int MODE>
+__device__ __forceinline__ void row_ptrs(const RArgs &a, uint32_t row, int mat, const u32x4r *&N,
+                                         const uint16_t *&S) {
+    const size_t nb = a.nb;
+    if (MODE == RV_QKV) {
+        if (row < a.seg1) {
+            N = a.m0.N + row * nb;
+            S = a.m0.S + row * nb;
+        } else if (row < a.seg2) {
+            N = a.m1.N + (row - a.seg1) * nb;
+            S = a.m1.S + (row - a.seg1) * nb;
+        } else {
+            N = a.m2.N + (row - a.seg2) * nb;
+            S = a.m2.S + (row - a.seg2) * nb;
+        }
+        return;
+    }
+    const RMat &m = (MODE == RV_MLP && mat == 1) ? a.m1 : a.m0;
+    N = m.N + row * nb;
+    S = m.S + row * nb;
+}
+
+template <int MODE>
+__device__ __forceinline__ void store_r(const RArgs &a, uint32_t row, float v) {
+    if (MODE == RV_QKV) {
+        if (row < a.seg1) a.y0[row] = v;
+        else if (row < a.seg2) a.y1[row - a.seg1] = v;
+        else a.y2[row - a.seg2] = v;
+    } else {
+        a.y0[row] = v;
+    }
+}
+
+template <int MODE, int RPW, int WPR>
+__global__ __launch_bounds__(256) void k_q4rmv(RArgs a) {
+    constexpr int NMAT = (MODE == RV_MLP) ? 2 : 1;
+    constexpr int V = RPW * NMAT;
+    constexpr int G = 4 / WPR;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int grp = wave / WPR, part = wave % WPR;
+    const uint32_t nb = a.nb;
+    // K range of this wave: blocks [kb0, kb0 + nblk), nblk <= 128
+    const uint32_t per = (nb + WPR - 1) / WPR;
+    const uint32_t kb0 = part * per;
+    const uint32_t kb1 = (kb0 + per < nb) ? kb0 + per : nb;
+    const uint32_t nblk = kb1 > kb0 ? kb1 - kb0 : 0;
+    const bool ok0 = (uint32_t)lane < nblk, ok1 = (uint32_t)(64 + lane) < nblk;
+    // blocks without data read block 0 of the row (always valid) and are
+    // zeroed through their planes
+    const uint32_t b0 = ok0 ? kb0 + lane : 0u, b1 = ok1 ? kb0 + 64 + lane : 0u;
+    __shared__ float red[4][V];
+
+    const uint32_t ngroups = (a.M + RPW - 1) / RPW;
+    const uint32_t gstride = gridDim.x * G;
+    u32x4r nq[V][2];
+    uint16_t sq[V][2];
+    auto load = [&](uint32_t g) {
+#pragma unroll
+        for (int s = 0; s < V; ++s) {
+            uint32_t row = g * RPW + s / NMAT;
+            row = row < a.M ? row : a.M - 1;
+            const u32x4r *N;
+            const uint16_t *S;
+            row_ptrs<MODE>(a, row, s % NMAT, N, S);
+            nq[s][0] = __builtin_nontemporal_load(N + b0);
+            nq[s][1] = __builtin_nontemporal_load(N + b1);
+            sq[s][0] = __builtin_nontemporal_load(S + b0);
+            sq[s][1] = __builtin_nontemporal_load(S + b1);
+        }
+    };
+    uint32_t g = blockIdx.x * G + grp;
+    if (g < ngroups) load(g);
+
+    // this lane's two blocks of activation planes (read from a valid block,
+    // then masked, so no branches surround the loads)
+    uint32_t P[2][XP_WORDS];
+    float xs[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const bool ok = c ? ok1 : ok0;
+        const uint32_t b = c ? b1 : b0;
+#pragma unroll
+        for (int i = 0; i < XP_WORDS; ++i) P[c][i] = a.xp[(size_t)i * nb + b];
+        xs[c] = ((const float *)(a.xp + (size_t)XP_WORDS * nb))[b];
+#pragma unroll
+        for (int i = 0; i < XP_WORDS; ++i) P[c][i] = ok ? P[c][i] : 0u;
+        xs[c] = ok ? xs[c] : 0.0f;
+    }
+
+    for (uint32_t gb = blockIdx.x * G; gb < ngroups; gb += gstride, g += gstride) {
+        const bool gv = g < ngroups;
+        u32x4r cq[V][2];
+        uint16_t cs[V][2];
+#pragma unroll
+        for (int s = 0; s < V; ++s)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                cq[s][c] = nq[s][c];
+                cs[s][c] = sq[s][c];
+            }
+        if (g + gstride < ngroups) load(g + gstride);
+        float tot[V];
+#pragma unroll
+        for (int s = 0; s < V; ++s) {
+            float r = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const int T = block_idot_r(cq[s][c], P[c]);
+                const float sf = (float)__builtin_bit_cast(_Float16, cs[s][c]);
+                r = fmaf((float)T, sf * xs[c], r);
+            }
+            tot[s] = wave_sum64(r);
+        }
+        if (WPR == 1) {
+            if (gv && lane == 0) {
+#pragma unroll
+                for (int r = 0; r < RPW; ++r) {
+                    const uint32_t row = g * RPW + r;
+                    if (row < a.M) {
+                        if (NMAT == 1) store_r<MODE>(a, row, tot[r]);
+                        else a.y0[row] = gelu_tanh(tot[2 * r]) * tot[2 * r + 1];
+                    }
+                }
+            }
+        } else {
+            if (lane == 0) {
+#pragma unroll
+                for (int s = 0; s < V; ++s) red[wave][s] = tot[s];
+            }
+            __syncthreads();
+            if (part == 0 && gv && lane < RPW) {
+                float t0 = 0.0f, t1 = 0.0f;
+#pragma unroll
+                for (int w = 0; w < WPR; ++w) {
+                    t0 += red[grp * WPR + w][lane * NMAT];
+                    if (NMAT == 2) t1 += red[grp * WPR + w][lane * 2 + 1];
+                }
+                const uint32_t row = g * RPW + lane;
+                if (row < a.M) {
+                    if (NMAT == 1) store_r<MODE>(a, row, t0);
+                    else a.y0[row] = gelu_tanh(t0) * t1;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// Launch shape (from a sweep on MI355X at the 12B decode shapes): the
+// fewest waves splitting K such that each covers <= 128 blocks; one
+// gate/up row pair or two rows per wave; about three row groups per wave,
+// 256..1024 workgroups.
+template <int MODE, int WPR>
+static void launch_rw(const RArgs &a, int rpw, uint32_t grid, hipStream_t s) {
+    if (rpw == 1) k_q4rmv<MODE, 1, WPR><<<grid, 256, 0, s>>>(a);
+    else k_q4rmv<MODE, 2, WPR><<<grid, 256, 0, s>>>(a);
+}
+
+static int launch_q4rmv(chn_ctx *ctx, int mode, RArgs a, const float *x, uint32_t *xp, bool planes_ready) {
+    const uint32_t nb = a.nb;
+    if (!planes_ready) {
+        if (launch_xplanes(ctx->stream, x, xp, nb)) return hip_fail(ctx, hipGetLastError(), "k_xplanes");
+    }
+    a.xp = xp;
+    const int wpr = nb <= 128 ? 1 : (nb <= 256 ? 2 : 4);
+    const int rpw = mode == RV_MLP ? 1 : 2;
+    const uint32_t G = 4 / wpr;
+    const uint32_t ngroups = (a.M + rpw - 1) / rpw;
+    uint32_t grid = ngroups / (G * 3);
+    grid = grid < 256 ? 256 : (grid > 1024 ? 1024 : grid);
+    const uint32_t need = (ngroups + G - 1) / G;
+    if (grid > need) grid = need;
+    hipStream_t s = ctx->stream;
+    switch (mode) {
+    case RV_GEMV:
+        wpr == 1 ? launch_rw<RV_GEMV, 1>(a, rpw, grid, s)
+                 : (wpr == 2 ? launch_rw<RV_GEMV, 2>(a, rpw, grid, s) : launch_rw<RV_GEMV, 4>(a, rpw, grid, s));
+        break;
+    case RV_QKV:
+        wpr == 1 ? launch_rw<RV_QKV, 1>(a, rpw, grid, s)
+                 : (wpr == 2 ? launch_rw<RV_QKV, 2>(a, rpw, grid, s) : launch_rw<RV_QKV, 4>(a, rpw, grid, s));
+        break;
+    default:
+        wpr == 1 ? launch_rw<RV_MLP, 1>(a, rpw, grid, s)
+                 : (wpr == 2 ? launch_rw<RV_MLP, 2>(a, rpw, grid, s) : launch_rw<RV_MLP, 4>(a, rpw, grid, s));
+        break;
+    }
+    CHN_LAUNCHED(ctx, "k_q4rmv");
+    return CHN_OK;
+}
+
+static RMat host_rmat(const void *W, uint32_t rows, uint32_t nb) {
+    RMat m;
+    m.N = (const u32x4r *)W;
+    m.S = (const uint16_t *)((const unsigned char *)W + (size_t)rows * nb * 16);
+    return m;
+}
+
+int mvr_gemv(chn_ctx *ctx, const void *W, const float *x, float *y, uint32_t M, uint32_t K, uint32_t *xp,
+             bool planes_ready) {
+    const uint32_t nb = K / 32;
+    RArgs a{host_rmat(W, M, nb), {}, {}, y, nullptr, nullptr, nullptr, M, M, M, nb};
+    return launch_q4rmv(ctx, RV_GEMV, a, x, xp, planes_ready);
+}
+int mvr_qkv(chn_ctx *ctx, const void *Wq, const void *Wk, const void *Wv, const float *x, float *q, float *k,
+            float *v, uint32_t q_dim, uint32_t kv_dim, uint32_t K, uint32_t *xp, bool planes_ready) {
+    const uint32_t nb = K / 32;
+    RArgs a{host_rmat(Wq, q_dim, nb), host_rmat(Wk, kv_dim, nb), host_rmat(Wv, kv_dim, nb), q, k, v, nullptr,
+            q_dim + 2 * kv_dim, q_dim, q_dim + kv_dim, nb};
+    return launch_q4rmv(ctx, RV_QKV, a, x, xp, planes_ready);
+}
+int mvr_mlp(chn_ctx *ctx, const void *Wg, const void *Wu, const float *x, float *act, uint32_t M, uint32_t K,
+            uint32_t *xp, bool planes_ready) {
+    const uint32_t nb = K / 32;
+    RArgs a{host_rmat(Wg, M, nb), host_rmat(Wu, M, nb), {}, act, nullptr, nullptr, nullptr, M, M, M, nb};
+    return launch_q4rmv(ctx, RV_MLP, a, x, xp, planes_ready);
+}
+
+static int check_r(chn_ctx *ctx, const float *x, uint32_t K) {
+    CHN_REQUIRE(ctx, K > 0 && K % 32 == 0 && K <= 16384, "K=%u must be a positive multiple of 32, <= 16384", K);
+    CHN_REQUIRE(ctx, x && aligned(x, 16), "x must be non-NULL and 16-byte aligned");
+    return CHN_OK;
+}
+
+}  // namespace chn
+
+using namespace chn;
+
+extern "C" int chn_q4_repack(chn_ctx *ctx, const uint32_t *W, uint32_t rows, uint32_t K, void *dst) {
+    if (!ctx) return CHN_E_INVALID;
+    CHN_REQUIRE(ctx, W && dst, "NULL argument");
+    CHN_REQUIRE(ctx, K % 32 == 0, "K=%u must be a multiple of 32", K);
+    CHN_REQUIRE(ctx, aligned(dst, 16), "dst must be 16-byte aligned");
+    if (launch_q4_repack(ctx->stream, W, rows, K, dst)) return hip_fail(ctx, hipGetLastError(), "k_repack_q4");
+    return CHN_OK;
+}
+
+extern "C" int chn_gemv_q4r(chn_ctx *ctx, const void *W, const float *x, float *y, uint32_t M, uint32_t K) {
+    if (!ctx) return CHN_E_INVALID;
+    int rc = check_r(ctx, x, K);
+    if (rc) return rc;
+    CHN_REQUIRE(ctx, W && y && aligned(W, 16), "W/y must be non-NULL, W 16-byte aligned");
+    if (!M) return CHN_OK;
+    rc = ensure_workspace(ctx, xplanes_bytes(K / 32));
+    if (rc) return rc;
+    return mvr_gemv(ctx, W, x, y, M, K, (uint32_t *)ctx->ws, false);
+}
+
+extern "C" int chn_fused_qkv_q4r(chn_ctx *ctx, const void *Wq, const void *Wk, const void *Wv, const float *x,
+                                 float *q, float *k, float *v, uint32_t q_dim, uint32_t kv_dim, uint32_t K) {
+    if (!ctx) return CHN_E_INVALID;
+    int rc = check_r(ctx, x, K);
+    if (rc) return rc;
+    CHN_REQUIRE(ctx, Wq && Wk && Wv && q && k && v, "NULL argument");
+    CHN_REQUIRE(ctx, aligned(Wq, 16) && aligned(Wk, 16) && aligned(Wv, 16), "weights must be 16-byte aligned");
+    if (!(q_dim + 2 * kv_dim)) return CHN_OK;
+    rc = ensure_workspace(ctx, xplanes_bytes(K / 32));
+    if (rc) return rc;
+    return mvr_qkv(ctx, Wq, Wk, Wv, x, q, k, v, q_dim, kv_dim, K, (uint32_t *)ctx->ws, false);
+}
+
+extern "C" int chn_fused_mlp_q4r(chn_ctx *ctx, const void *Wg, const void *Wu, const float *x, float *act,
+                                 uint32_t M, uint32_t K) {
+    if (!ctx) return CHN_E_INVALID;
+    int rc = check_r(ctx, x, K);
+    if (rc) return rc;
+    CHN_REQUIRE(ctx, Wg && Wu && act && aligned(Wg, 16) && aligned(Wu, 16), "NULL or misaligned argument");
+    if (!M) return CHN_OK;
+    rc = ensure_workspace(ctx, xplanes_bytes(K / 32));
+    if (rc) return rc;
+    return mvr_mlp(ctx, Wg, Wu, x, act, M, K, (uint32_t *)ctx->ws, false);
+}

@@ -82,8 +82,6 @@ static int m_alloc(chn_model *m, size_t bytes, void **p) {
         ptr = (decltype(ptr))p_;                                \
     } while (0)
 
-static size_t q4b(uint32_t rows, uint32_t K) { return (size_t)rows * (K / 32) * 20; }
-
 // Head shape of a layer kind: full-attention layers take global_head_dim and
 // num_global_kv_heads when those are set (0 = same as the sliding layers),
 // and rotate their whole head (loader.zig:37-41).
@@ -271,15 +269,15 @@ static int record_decode(chn_model *m, bool with_logits) {
         const auto &l = m->L[i];
         const float theta = l.full ? c.rope_theta_full : c.rope_theta;
         if (i == 0) R_(launch_norm_planes(s, m->x, nullptr, nullptr, l.in_norm, m->normed, xp, H, eps, 1.0f, false));
-        R_(mv_qkv(ctx, l.Wq, l.Wk, l.Wv, m->normed, m->q, m->k, m->v, l.qd, l.kvd, H, xp, true));
+        R_(mvr_qkv(ctx, l.Wq, l.Wk, l.Wv, m->normed, m->q, m->k, m->v, l.qd, l.kvd, H, xp, true));
         R_(launch_rope_decode_attn(ctx, m->q, m->k, m->v, l.q_norm, l.k_norm, l.kc, l.vc, m->step,
                                    m->slots + (l.full ? 0 : kSlotsMax), m->step + (l.full ? 2 : 3), kSlotsMax, nq, l.D,
                                    l.kvd, l.gqa, l.rot, (int)c.k_eq_v, theta, eps, 1.0f, m->attn, m->attn_ws, xp));
-        R_(mv_gemv(ctx, l.Wo, m->attn, m->mlp_out, H, l.qd, xp, true));
+        R_(mvr_gemv(ctx, l.Wo, m->attn, m->mlp_out, H, l.qd, xp, true));
         R_(launch_norm_planes(s, m->x, m->mlp_out, l.has_post_attn ? l.post_attn : nullptr, l.pre_ffn, m->normed, xp,
                               H, eps, 1.0f, true));
-        R_(mv_mlp(ctx, l.Wg, l.Wu, m->normed, m->act, I, H, xp, true));
-        R_(mv_gemv(ctx, l.Wd, m->act, m->mlp_out, H, I, xp, false));
+        R_(mvr_mlp(ctx, l.Wg, l.Wu, m->normed, m->act, I, H, xp, true));
+        R_(mvr_gemv(ctx, l.Wd, m->act, m->mlp_out, H, I, xp, false));
         const float *next_norm = (i + 1 < c.num_layers) ? m->L[i + 1].in_norm : m->final_norm;
         R_(launch_norm_planes(s, m->x, m->mlp_out, l.has_post_ffn ? l.post_ffn : nullptr, next_norm, m->normed, xp, H,
                               eps, l.scalar, true));
@@ -341,13 +339,16 @@ static void free_model(chn_model *m) {
 }
 
 // bf16 (host) -> device quantized copy; `tmp` holds at least rows*cols bf16
-static int ingest_q(chn_model *m, const uint16_t *src, uint32_t rows, uint32_t cols, int q8, uint32_t **dst,
-                    uint16_t *tmp) {
+// bf16 (host) -> quantizeRowQ4_0 on the device into the reference layout
+// (staging `tq`), then repacked into the model's Q4R matrix.  `tmp` holds
+// at least rows*cols bf16, `tq` rows*cols/32 Q4 blocks.
+static int ingest_q4r(chn_model *m, const uint16_t *src, uint32_t rows, uint32_t cols, uint32_t **dst,
+                      uint16_t *tmp, uint32_t *tq) {
     const size_t nblk = (size_t)rows * (cols / 32);
-    M_ALLOC(*dst, nblk * (q8 ? 36 : 20));
+    M_ALLOC(*dst, q4r_bytes(rows, cols));
     CHN_HIP(m->ctx, hipMemcpyAsync(tmp, src, (size_t)rows * cols * 2, hipMemcpyHostToDevice, m->ctx->stream));
-    int rc = launch_quantize(m->ctx->stream, q8, tmp, *dst, nblk);
-    if (rc) return hip_fail(m->ctx, hipGetLastError(), "quantize");
+    if (launch_quantize(m->ctx->stream, 0, tmp, tq, nblk)) return hip_fail(m->ctx, hipGetLastError(), "quantize");
+    if (launch_q4_repack(m->ctx->stream, tq, rows, cols, *dst)) return hip_fail(m->ctx, hipGetLastError(), "repack");
     CHN_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
     return CHN_OK;
 }
@@ -390,8 +391,11 @@ extern "C" int chn_model_create(chn_ctx *ctx, const chn_model_config *cfg, const
     const MaxDims md = max_dims(*m);
     const size_t tmp_elems = (size_t)I * H > (size_t)md.qd * H ? (size_t)I * H : (size_t)md.qd * H;
     uint16_t *tmp = nullptr;
+    uint32_t *tq = nullptr;
     hipError_t e = hipMalloc(&tmp, tmp_elems * 2);
+    if (e == hipSuccess) e = hipMalloc(&tq, tmp_elems / 32 * 20);
     if (e != hipSuccess) {
+        (void)hipFree(tmp);
         free_model(m);
         return hip_fail(ctx, e, "hipMalloc (ingest staging)");
     }
@@ -408,14 +412,14 @@ extern "C" int chn_model_create(chn_ctx *ctx, const chn_model_config *cfg, const
             rc = set_err(ctx, CHN_E_INVALID, "layer %u: missing projection weights", i);
             goto fail;
         }
-        C_(ingest_q(m, w.q_proj, qd, H, 0, &l.Wq, tmp));
-        C_(ingest_q(m, w.k_proj, kvd, H, 0, &l.Wk, tmp));
+        C_(ingest_q4r(m, w.q_proj, qd, H, &l.Wq, tmp, tq));
+        C_(ingest_q4r(m, w.k_proj, kvd, H, &l.Wk, tmp, tq));
         // v_proj absent -> k_proj (src/gpu/model_gpu.zig:123)
-        C_(ingest_q(m, w.v_proj ? w.v_proj : w.k_proj, kvd, H, 0, &l.Wv, tmp));
-        C_(ingest_q(m, w.o_proj, H, qd, 0, &l.Wo, tmp));
-        C_(ingest_q(m, w.gate_proj, I, H, 0, &l.Wg, tmp));
-        C_(ingest_q(m, w.up_proj, I, H, 0, &l.Wu, tmp));
-        C_(ingest_q(m, w.down_proj, H, I, 0, &l.Wd, tmp));
+        C_(ingest_q4r(m, w.v_proj ? w.v_proj : w.k_proj, kvd, H, &l.Wv, tmp, tq));
+        C_(ingest_q4r(m, w.o_proj, H, qd, &l.Wo, tmp, tq));
+        C_(ingest_q4r(m, w.gate_proj, I, H, &l.Wg, tmp, tq));
+        C_(ingest_q4r(m, w.up_proj, I, H, &l.Wu, tmp, tq));
+        C_(ingest_q4r(m, w.down_proj, H, I, &l.Wd, tmp, tq));
         C_(ingest_norm(m, w.input_layernorm, H, &l.in_norm));
         C_(ingest_norm(m, w.q_norm, D, &l.q_norm));
         C_(ingest_norm(m, w.k_norm, D, &l.k_norm));
@@ -439,10 +443,12 @@ extern "C" int chn_model_create(chn_ctx *ctx, const chn_model_config *cfg, const
     C_(build_graphs(m));
 #undef C_
     (void)hipFree(tmp);
+    (void)hipFree(tq);
     *out = m;
     return CHN_OK;
 fail:
     (void)hipFree(tmp);
+    (void)hipFree(tq);
     free_model(m);
     return rc;
 }
@@ -458,6 +464,21 @@ extern "C" int chn_model_create_synthetic(chn_ctx *ctx, const chn_model_config *
     m->cfg = *cfg;
     const uint32_t H = cfg->hidden_size, I = cfg->intermediate_size, V = cfg->vocab_size;
     const float smin = 0.005f, smax = 0.02f;
+    // staging for one matrix in the reference Q4 layout
+    uint32_t *tq = nullptr;
+    {
+        size_t big = (size_t)I * H;
+        for (uint32_t i = 0; i < cfg->num_layers; ++i) {
+            const HeadShape h = head_shape(*cfg, cfg->layer_full[i] != 0);
+            const size_t qh = (size_t)cfg->num_heads * h.D * H;
+            if (qh > big) big = qh;
+        }
+        hipError_t e = hipMalloc(&tq, big / 32 * 20);
+        if (e != hipSuccess) {
+            delete m;
+            return hip_fail(ctx, e, "hipMalloc (synthetic staging)");
+        }
+    }
 #define C_(call)                 \
     do {                         \
         rc = (call);             \
@@ -475,8 +496,13 @@ extern "C" int chn_model_create_synthetic(chn_ctx *ctx, const chn_model_config *
         } mats[7] = {{&l.Wq, qd, H}, {&l.Wk, kvd, H}, {&l.Wv, kvd, H}, {&l.Wo, H, qd},
                      {&l.Wg, I, H},  {&l.Wu, I, H},   {&l.Wd, H, I}};
         for (int j = 0; j < 7; ++j) {
-            C_(m_alloc(m, q4b(mats[j].rows, mats[j].cols), (void **)mats[j].w));
-            C_(chn_synth_q4(ctx, *mats[j].w, mats[j].rows, mats[j].cols, ls + j, smin, smax));
+            // generated in the reference layout, kept repacked (Q4R)
+            C_(m_alloc(m, q4r_bytes(mats[j].rows, mats[j].cols), (void **)mats[j].w));
+            C_(chn_synth_q4(ctx, tq, mats[j].rows, mats[j].cols, ls + j, smin, smax));
+            if (launch_q4_repack(ctx->stream, tq, mats[j].rows, mats[j].cols, *mats[j].w)) {
+                rc = hip_fail(ctx, hipGetLastError(), "repack");
+                goto fail;
+            }
         }
         C_(fill_ones(m, H, &l.in_norm));
         C_(fill_ones(m, D, &l.q_norm));
@@ -518,9 +544,11 @@ extern "C" int chn_model_create_synthetic(chn_ctx *ctx, const chn_model_config *
     C_(chn_sync(ctx));
     C_(build_graphs(m));
 #undef C_
+    (void)hipFree(tq);
     *out = m;
     return CHN_OK;
 fail:
+    (void)hipFree(tq);
     free_model(m);
     return rc;
 }
@@ -688,19 +716,19 @@ extern "C" int chn_prefill(chn_model *m, const uint32_t *tokens, uint32_t n, con
         const float theta = l.full ? c.rope_theta_full : c.rope_theta;
         if (i == 0) P_(launch_rmsnorm(s, m->px, nullptr, l.in_norm, m->pn, H, n, eps, 1.0f, false));
         const uint32_t D = l.D, nkv = l.nkv, qd = l.qd, kvd = l.kvd, gqa = l.gqa;
-        P_(launch_q4gemm(ctx, 1, m->pn, l.Wq, nullptr, m->pq, n, qd, H, m->pxb));
-        P_(launch_q4gemm(ctx, 1, m->pn, l.Wk, nullptr, m->pk, n, kvd, H, m->pxb));
-        P_(launch_q4gemm(ctx, 1, m->pn, l.Wv, nullptr, m->pv, n, kvd, H, m->pxb));
+        P_(launch_q4gemm(ctx, 1, m->pn, l.Wq, nullptr, m->pq, n, qd, H, m->pxb, true));
+        P_(launch_q4gemm(ctx, 1, m->pn, l.Wk, nullptr, m->pk, n, kvd, H, m->pxb, true));
+        P_(launch_q4gemm(ctx, 1, m->pn, l.Wv, nullptr, m->pv, n, kvd, H, m->pxb, true));
         P_(launch_batch_qkv_rope(s, m->pq, m->pk, m->pv, l.q_norm, l.k_norm, m->pq, l.kc, l.vc, m->pslots,
                                  num_prev_slots, start_clock, n, nq, nkv, D, l.rot, (int)c.k_eq_v, theta, eps));
         // sliding layers see the last 1024 slots (shaders/batch_causal_attn.wgsl:53)
         P_(launch_prefill_attn(s, m->pq, l.kc, l.vc, m->pslots, n, num_prev_slots, nq, D, kvd, gqa, 1.0f,
                                l.full ? 0u : 1024u, m->pattn));
-        P_(launch_q4gemm(ctx, 1, m->pattn, l.Wo, nullptr, m->pmlp, n, H, qd, m->pxb));
+        P_(launch_q4gemm(ctx, 1, m->pattn, l.Wo, nullptr, m->pmlp, n, H, qd, m->pxb, true));
         if (l.has_post_attn) P_(launch_rmsnorm(s, m->pmlp, nullptr, l.post_attn, m->pmlp, H, n, eps, 1.0f, false));
         P_(launch_rmsnorm(s, m->px, m->pmlp, l.pre_ffn, m->pn, H, n, eps, 1.0f, true));
-        P_(launch_q4gemm(ctx, 2, m->pn, l.Wg, l.Wu, m->pact, n, I, H, m->pxb));
-        P_(launch_q4gemm(ctx, 1, m->pact, l.Wd, nullptr, m->pmlp, n, H, I, m->pxb));
+        P_(launch_q4gemm(ctx, 2, m->pn, l.Wg, l.Wu, m->pact, n, I, H, m->pxb, true));
+        P_(launch_q4gemm(ctx, 1, m->pact, l.Wd, nullptr, m->pmlp, n, H, I, m->pxb, true));
         if (l.has_post_ffn) P_(launch_rmsnorm(s, m->pmlp, nullptr, l.post_ffn, m->pmlp, H, n, eps, 1.0f, false));
         const float *next_norm = (i + 1 < c.num_layers) ? m->L[i + 1].in_norm : m->final_norm;
         P_(launch_rmsnorm(s, m->px, m->pmlp, next_norm, m->pn, H, n, eps, l.scalar, true));

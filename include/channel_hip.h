@@ -120,6 +120,30 @@ int chn_fused_mlp_q4(chn_ctx *ctx, const uint32_t *Wg, const uint32_t *Wu,
  * Prefill contractions (src/gpu/batch_dispatch.zig:70-81,108-130)
  * ==================================================================== */
 
+/* ======================================================================
+ * Repacked Q4 ("Q4R"): the layout the model keeps in HBM.  Per matrix of
+ * rows x K: [rows][K/32] 16-byte words of nibbles, each nibble XOR 8 (the
+ * two's-complement value q - 8), then [rows][K/32] f16 scales; 18 bytes per
+ * 32 weights (the reference's unused f16 min half-word is dropped).  A pure
+ * bit permutation of the reference layout, so products are unchanged.  No
+ * reference counterpart: these replace the same recorders as the entries
+ * above (src/gpu/kernels.zig:89-126) over weights that model ingest
+ * (GpuModelContext.init, src/gpu/model_gpu.zig:68) repacks once.
+ * ==================================================================== */
+
+#define CHN_Q4R_BYTES(rows, K) ((size_t)(rows) * ((K) / 32) * 18)
+
+/* Reference-layout Q4 (device) -> Q4R (device, 16-byte aligned, CHN_Q4R_BYTES). */
+int chn_q4_repack(chn_ctx *ctx, const uint32_t *W, uint32_t rows, uint32_t K, void *dst);
+
+/* As chn_gemv_q4 / chn_fused_qkv_q4 / chn_fused_mlp_q4 over Q4R weights;
+ * K % 32 == 0, K <= 16384. */
+int chn_gemv_q4r(chn_ctx *ctx, const void *W, const float *x, float *y, uint32_t M, uint32_t K);
+int chn_fused_qkv_q4r(chn_ctx *ctx, const void *Wq, const void *Wk, const void *Wv, const float *x,
+                      float *q, float *k, float *v, uint32_t q_dim, uint32_t kv_dim, uint32_t K);
+int chn_fused_mlp_q4r(chn_ctx *ctx, const void *Wg, const void *Wu, const float *x, float *act,
+                      uint32_t M, uint32_t K);
+
 /* Y[t][r] = sum_k X[t][k] * W[r][k] for t < n_tok, r < M: X fp32 [n_tok][K]
  * (16-byte aligned), W Q4 [M][K], Y fp32 [n_tok][M].  Operands are rounded
  * to bf16 (X) and bf16(scale*(q-8)) (W, dequantized in LDS) for MFMA with

@@ -62,3 +62,54 @@ def test_init_without_device_reports_no_device():
     with pytest.raises(ca.ChannelError) as e:
         ca.Context(0)
     assert e.value.status == "NoDevice"
+
+
+def declared_prototypes():
+    """name -> list of parameter classes ('ptr', 'u32', 'u64', 'int', 'f32',
+    'size') parsed from the header declarations."""
+    protos = {}
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        for name, params in re.findall(r"\b(chn_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+            params = params.strip()
+            classes = []
+            if params and params != "void":
+                for p in params.split(","):
+                    p = " ".join(p.split())
+                    if "*" in p or "chn_progress_fn" in p:
+                        classes.append("ptr")
+                    elif p.startswith(("uint32_t", "const uint32_t")):
+                        classes.append("u32")
+                    elif p.startswith("uint64_t"):
+                        classes.append("u64")
+                    elif p.startswith("size_t"):
+                        classes.append("size")
+                    elif p.startswith("float"):
+                        classes.append("f32")
+                    elif p.startswith("int"):
+                        classes.append("int")
+                    else:
+                        classes.append("?" + p)
+            protos[name] = classes
+    return protos
+
+
+def _ctype_class(t):
+    if t in (ctypes.c_void_p, ctypes.c_char_p) or (isinstance(t, type) and issubclass(t, ctypes._Pointer)):
+        return "ptr"
+    return {ctypes.c_uint32: "u32", ctypes.c_uint64: "u64", ctypes.c_size_t: "size", ctypes.c_float: "f32",
+            ctypes.c_int: "int"}.get(t, "?" + repr(t))
+
+
+def test_python_prototypes_match_header_parameters():
+    """Every ctypes prototype has the header's parameter count and classes."""
+    protos = declared_prototypes()
+    assert len(protos) == len(declared_functions())
+    bad = []
+    same = {"u64": "size"}   # c_uint64 is c_size_t on LP64
+    for name, (_, args) in ca.PROTOTYPES.items():
+        got = [same.get(c, c) for c in (_ctype_class(a) for a in args)]
+        want = [same.get(c, c) for c in protos[name]]
+        if got != want:
+            bad.append((name, got, want))
+    assert not bad, bad

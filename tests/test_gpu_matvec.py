@@ -5,6 +5,7 @@ Tolerance: normwise relative error <= 1e-3 (fp32 accumulation)."""
 import numpy as np
 import pytest
 
+import channel_amd as ca
 import oracle
 from gpu_util import f32_host, q4_host, rel_err, say, synth_normal_dev, synth_q4_dev
 
@@ -119,3 +120,69 @@ def test_rejects_bad_shapes(ctx):
     assert e.value.status == "Invalid"
     with pytest.raises(ca.ChannelError):
         ctx.call("chn_gemv_q4", W, x.ptr + 4, y, 4, 32)  # x not 16-byte aligned
+
+
+# ---- repacked (Q4R) weights: the layout the model keeps in HBM ------------
+
+def q4r_host(Wref, rows, K):
+    """Host restatement of the repack: nibble words XOR 0x88888888, f16 scales."""
+    W = Wref.reshape(rows, K // 32, 5)
+    N = (W[:, :, 1:5] ^ np.uint32(0x88888888)).reshape(-1)
+    S = (W[:, :, 0] & np.uint32(0xFFFF)).astype(np.uint16).reshape(-1)
+    return np.concatenate([N.view(np.uint8), S.view(np.uint8)])
+
+
+def repack_dev(ctx, W, rows, K):
+    R = ctx.alloc(ca.q4r_bytes(rows, K))
+    ctx.call("chn_q4_repack", W, rows, K, R)
+    return R
+
+
+@pytest.mark.parametrize("M,K", [(15360, 3840), (3840, 15360), (8192, 3840), (3840, 4096), (7, 32), (33, 2080),
+                                 (100, 640), (1, 8192), (15, 16384)])
+def test_q4r_gemv_parity(ctx, M, K):
+    W = synth_q4_dev(ctx, M, K, 900 + M + K)
+    x = synth_normal_dev(ctx, K, 901 + K)
+    say(f"q4r gemv M={M} K={K}")
+    R = repack_dev(ctx, W, M, K)
+    Wh = q4_host(ctx, W, M, K)
+    assert np.array_equal(ctx.download(R, np.uint8, ca.q4r_bytes(M, K)), q4r_host(Wh, M, K))
+    y = ctx.alloc(M * 4)
+    ctx.call("chn_gemv_q4r", R, x, y, M, K)
+    got = f32_host(ctx, y, M)
+    want = oracle.gemv_q4(Wh, f32_host(ctx, x, K), M, K)
+    assert rel_err(got, want) < 1e-3
+    y2 = ctx.alloc(M * 4)
+    ctx.call("chn_gemv_q4", W, x, y2, M, K)
+    assert rel_err(got, f32_host(ctx, y2, M)) < 1e-5
+
+
+def test_q4r_fused_qkv_and_mlp(ctx):
+    H, qd, kvd, I = 3840, 4096, 2048, 15360
+    Wq, Wk, Wv = (synth_q4_dev(ctx, r, H, 950 + i) for i, r in enumerate((qd, kvd, kvd)))
+    Rq, Rk, Rv = repack_dev(ctx, Wq, qd, H), repack_dev(ctx, Wk, kvd, H), repack_dev(ctx, Wv, kvd, H)
+    x = synth_normal_dev(ctx, H, 960)
+    q, k, v = ctx.alloc(qd * 4), ctx.alloc(kvd * 4), ctx.alloc(kvd * 4)
+    say("q4r fused qkv 12B")
+    ctx.call("chn_fused_qkv_q4r", Rq, Rk, Rv, x, q, k, v, qd, kvd, H)
+    xh = f32_host(ctx, x, H)
+    wq, wk, wv = oracle.fused_qkv_q4(q4_host(ctx, Wq, qd, H), q4_host(ctx, Wk, kvd, H), q4_host(ctx, Wv, kvd, H),
+                                     xh, qd, kvd, H)
+    assert rel_err(f32_host(ctx, q, qd), wq) < 1e-3
+    assert rel_err(f32_host(ctx, k, kvd), wk) < 1e-3
+    assert rel_err(f32_host(ctx, v, kvd), wv) < 1e-3
+    Wg, Wu = synth_q4_dev(ctx, I, H, 970), synth_q4_dev(ctx, I, H, 971)
+    Rg, Ru = repack_dev(ctx, Wg, I, H), repack_dev(ctx, Wu, I, H)
+    act = ctx.alloc(I * 4)
+    say("q4r fused mlp 12B")
+    ctx.call("chn_fused_mlp_q4r", Rg, Ru, x, act, I, H)
+    want = oracle.fused_mlp_q4(q4_host(ctx, Wg, I, H), q4_host(ctx, Wu, I, H), xh, I, H)
+    assert rel_err(f32_host(ctx, act, I), want) < 1e-3
+
+
+def test_q4r_bad_shapes(ctx):
+    W = ctx.alloc(1 << 20)
+    x = ctx.alloc(1 << 16)
+    for K in (0, 48, 16416):
+        with pytest.raises(ca.ChannelError):
+            ctx.call("chn_gemv_q4r", W, x, x, 4, K)
