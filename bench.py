@@ -510,13 +510,18 @@ def bench_prefill(ctx, args):
 
 
 def bench_attn(ctx, args):
-    """Decode attention, 16 query / 8 KV heads, head_dim 256, full 4096-slot
-    ring of fp32 K/V."""
+    """Decode attention, 16 query / 8 KV heads, head_dim 256, over --slots
+    entries (default the full 4096-slot ring) of fp32 K/V."""
     import numpy as np
 
-    H, KVH, D, S = 16, 8, 256, 4096
+    H, KVH, D, NSLOT = 16, 8, 256, 4096
+    S = args.slots
+    if not 1 <= S <= NSLOT:
+        raise SystemExit(f"--slots must be in 1..{NSLOT}")
     kv_dim = KVH * D
-    ncopy = 4     # 4 x 67 MB caches > 256 MB Infinity Cache
+    # caches of S rows, rotated over enough copies (> 512 MB) that no call
+    # finds its K/V in the 256 MB Infinity Cache
+    ncopy = max(4, -(-(512 << 20) // (2 * S * kv_dim * 4)))
     Kc, Vc = [], []
     for c in range(ncopy):
         k = ctx.alloc(S * kv_dim * 4)
@@ -527,17 +532,18 @@ def bench_attn(ctx, args):
         Vc.append(v)
     q = ctx.alloc(H * D * 4)
     ctx.call("chn_synth_normal", q, H * D, SEED + 300, 0.1)
-    slots = ctx.upload(((np.arange(S) + 1234) % S).astype(np.uint32))
+    # a ring list of NSLOT entries whose slot values index the S cache rows
+    slots = ctx.upload(((np.arange(NSLOT) + 1234) % S).astype(np.uint32))
     ns = ctx.upload(np.array([S], np.uint32))
     out = ctx.alloc(H * D * 4)
     ctx.sync()
     for i in range(args.warmup):
-        ctx.call("chn_decode_attn", q, Kc[i % ncopy], Vc[i % ncopy], slots, ns, S, H, D, kv_dim, 2, 1.0, out)
+        ctx.call("chn_decode_attn", q, Kc[i % ncopy], Vc[i % ncopy], slots, ns, NSLOT, H, D, kv_dim, 2, 1.0, out)
     ctx.sync()
     t0 = time.perf_counter()
     ctx.timer_start()
     for i in range(args.steps):
-        ctx.call("chn_decode_attn", q, Kc[i % ncopy], Vc[i % ncopy], slots, ns, S, H, D, kv_dim, 2, 1.0, out)
+        ctx.call("chn_decode_attn", q, Kc[i % ncopy], Vc[i % ncopy], slots, ns, NSLOT, H, D, kv_dim, 2, 1.0, out)
     gpu_ms = ctx.timer_stop()
     wall_ms = (time.perf_counter() - t0) * 1e3
     ms = max(gpu_ms, wall_ms) / args.steps
@@ -545,9 +551,9 @@ def bench_attn(ctx, args):
     achieved = nbytes / (gpu_ms / args.steps * 1e-3) / 1e9
     return {
         "value": 1e3 / ms, "unit": "attention steps/s", "ms_per_step": ms,
-        "config": {"workload": "decode attention over a full 4096-slot ring (16 q / 8 kv heads, D 256)",
+        "config": {"workload": f"decode attention over {S} of 4096 ring slots (16 q / 8 kv heads, D 256)",
                    "slots": S, "bytes_per_step": nbytes},
-        "roofline": {"kernel": "k_attn_split + k_attn_combine", "bound": "hbm", "achieved": achieved,
+        "roofline": {"kernel": "k_attn_decode + k_attn_merge", "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": None, "algorithmic_bytes_per_launch": nbytes,
                      "avg_launch_ms": gpu_ms / args.steps},
@@ -601,6 +607,7 @@ def main():
     ap.add_argument("--workload", default="decode", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--slots", type=int, default=4096, help="attn workload: slot count (<= 4096)")
     ap.add_argument("--eager", action="store_true",
                     help="decode: launch the kernels one by one instead of replaying the graph")
     args = ap.parse_args()

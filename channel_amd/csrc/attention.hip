@@ -4,34 +4,40 @@
 //
 // Decode attention is split over the slot list ("flash-decoding").  The
 // slot count S is read from device memory (so a captured graph replays with
-// a new count) and the list is cut into at most 64 chunks of
-// max(16, ceil(S / 64)) slots, so short contexts still spread over many
-// workgroups.  A workgroup takes one KV head and one chunk and serves all of
-// that head's GQA query heads from one pass over K and V: each 16-lane row
-// of a wave owns one slot at a time (a 1 KB row, 64 contiguous bytes per
-// lane), scores reduce inside the row with DPP, and each wave keeps its own
-// online softmax state, so the loop has no barriers.  The four waves merge
-// in LDS into one partial (m, l, sum p*V) per query head; the last
-// workgroup of a KV head to finish (an agent-scope counter) merges the
-// partials in a fixed order, writes the output and, optionally, its
-// activation digit planes for the o_proj matvec.  The result equals the
-// reference's two-pass softmax p_i = exp(s_i - max) / (sum exp(s_j - max) +
-// 1e-9) up to rounding.
+// a new count).  The list is cut into 16-entry chunks dealt round-robin to
+// at most 32 workgroups per KV head, so a 512-entry sliding window spreads
+// over 256 workgroups and a full 4096-entry ring gives each eight chunks.
+// A workgroup serves all of its KV head's GQA query heads from one pass over
+// K and V: each 16-lane row of a wave owns one list entry per chunk (a 1 KB
+// row, 64 contiguous bytes per lane), scores reduce inside the row with
+// DPP, and each wave keeps its own online softmax state.  The four waves
+// merge in LDS into one partial (m, l, sum p*V) per query head; a second
+// kernel merges the partials (online, in a fixed order), writes the output
+// and, optionally, its activation digit planes for the o_proj matvec.  The
+// result equals the reference's two-pass softmax p_i = exp(s_i - max) /
+// (sum exp(s_j - max) + 1e-9) up to rounding.
 #include "chn_internal.h"
 
 namespace chn {
 
 constexpr int kAttnChunk = 64;     // prefill: slots per online-softmax step
-constexpr int kDecSplits = 64;     // decode: most chunks per KV head
+constexpr int kDecIters = 8;       // decode: most 16-entry chunks per workgroup
+constexpr uint32_t kDecGrid = 32;  // decode: workgroups per KV head (at most)
 constexpr float kNegBig = -1e30f;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-// Decode workspace: partial sums [64][num_q_heads][head_dim], then maxima
-// and sums [64][num_q_heads].
+// Decode splits per KV head: one per 16-entry chunk of max_slots, at most
+// kDecGrid (then a split takes up to kDecIters chunks: 32 * 8 * 16 = 4096).
+static uint32_t dec_splits(uint32_t max_slots) {
+    const uint32_t n = (max_slots + 15) / 16;
+    return n < kDecGrid ? n : kDecGrid;
+}
+
+// Decode workspace: partial sums [splits][num_q_heads][head_dim], then
+// maxima and denominators [splits][num_q_heads].
 size_t attn_ws_bytes(uint32_t num_q_heads, uint32_t head_dim, uint32_t max_slots) {
-    (void)max_slots;
-    return (size_t)kDecSplits * num_q_heads * ((size_t)head_dim + 2) * 4;
+    return (size_t)dec_splits(max_slots) * num_q_heads * ((size_t)head_dim + 2) * 4;
 }
 
 // Running softmax state of one lane: lane row r = lane / 16 holds slots
@@ -216,12 +222,18 @@ __device__ __forceinline__ void wave_rope_lds(float *row, uint32_t rot, float th
     }
 }
 
-// Decode: workgroup (split, KV head).  IT slots per row are loaded at once
-// (all K rows, then all V rows, before any arithmetic).  With ROPE, Q holds
-// the raw q of the QKV matvec: every workgroup normalises and rotates its
-// GQA query heads and the new token's K (and normalises its V) in LDS,
-// uses them in place of the cache row of slot_idx, and split 0 writes them
-// to the caches.
+// Decode: grid (G, KV heads).  The slot list is taken in 16-entry chunks;
+// workgroup `split` takes chunks split, split + G, split + 2 G, ... (at most
+// kDecIters of them), two at a time, and row r of wave w holds entry
+// 16 c + 4 w + r of chunk c.  The list entries of its first two chunks are
+// read together with the slot count (the list holds max_slots entries; an
+// entry is used only below the count), so the first K/V loads wait on one
+// memory round trip; the next pair's entries are read while a pair is
+// reduced, and each wave keeps a running softmax (max, sum, p-weighted V)
+// over its chunks.  With ROPE, Q holds the raw q of the QKV matvec: every
+// workgroup normalises and rotates its GQA query heads and the new token's
+// K (and normalises its V) in LDS, uses them in place of the cache row of
+// slot_idx, and split 0 writes them to the caches.
 template <int DV, int GQA, bool ROPE>
 __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q, float *Kc, float *Vc,
                                                      const uint32_t *__restrict__ slots,
@@ -230,8 +242,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
                                                      float *__restrict__ ws, RopeArgs ra) {
     constexpr int D = DV * 256;
     constexpr int NF = 4 * DV;          // float4 per lane per row
-    constexpr int IT = (GQA >= 4 ? 2 : 4) / DV;   // slots per row per batch (register budget)
-    const uint32_t split = blockIdx.x, kvh = blockIdx.y;
+    const uint32_t split = blockIdx.x, kvh = blockIdx.y, G = gridDim.x;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r = lane >> 4, c = lane & 15;
     const uint32_t qh0 = kvh * GQA;
@@ -241,60 +252,45 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
     __shared__ float sh_q[ROPE ? GQA : 1][ROPE ? D : 4];
     __shared__ float sh_k[ROPE ? D : 4], sh_v[ROPE ? D : 4];
 
+    const uint32_t row_ent = 4 * wave + r;
+    const uint32_t ntmax = ((max_slots + 15) / 16 + G - 1 - split) / G;   // chunks this split could own
+    auto entry = [&](uint32_t t) { return (split + G * t) * 16 + row_ent; };
+    auto slot_at = [&](uint32_t t) {
+        const uint32_t e = entry(t);
+        return t < ntmax ? slots[e < max_slots ? e : max_slots - 1] : 0u;
+    };
+    uint32_t pa = slot_at(0), pb = slot_at(1);
     uint32_t S = *n_slots;
     if (S > max_slots) S = max_slots;
-    uint32_t chunk = (S + kDecSplits - 1) / kDecSplits;
-    chunk = (chunk + 15) & ~15u;
-    const uint32_t nsp = S ? (S + chunk - 1) / chunk : 0;
+    const uint32_t nch = (S + 15) / 16;
+    const uint32_t iters = split < nch ? (nch - split + G - 1) / G : 0;
     // split 0 always runs when it has to write the new token's K/V
-    if (split >= nsp && !(ROPE && split == 0)) return;
-    const uint32_t c0 = split * chunk;
-    const uint32_t c1 = (c0 + chunk < S) ? c0 + chunk : S;
-    const uint32_t nit = split < nsp ? (c1 - c0 + 15) / 16 : 0;   // 16-slot steps; row r of wave w: slot 4w + r
-    const uint32_t clock = ROPE ? ra.step[0] : 0u, new_slot = ROPE ? ra.step[1] : 0xFFFFFFFFu;
+    if (!iters && !(ROPE && split == 0)) return;
     const size_t dim0 = (size_t)kvh * D + (size_t)c * 4 * NF;
 
-    f4 kr[IT][NF], vr[IT][NF];
-    bool ok[IT], fresh[IT];
-    auto load_batch = [&](uint32_t jb) {
-        uint32_t ps[IT];
+    bool ok[2];
+    f4 kr[2][NF], vr[2][NF];
+    auto issue = [&](uint32_t t) {       // chunks t, t + 1
+        ok[0] = entry(t) < S;
+        ok[1] = t + 1 < iters && entry(t + 1) < S;
+        const float *ka = Kc + (size_t)pa * kv_dim + dim0, *va = Vc + (size_t)pa * kv_dim + dim0;
+        const float *kb = Kc + (size_t)pb * kv_dim + dim0, *vb = Vc + (size_t)pb * kv_dim + dim0;
 #pragma unroll
-        for (int u = 0; u < IT; ++u) {
-            const uint32_t i = c0 + 16 * (jb + u) + 4 * wave + r;
-            ok[u] = (jb + u < nit) && i < c1;
-            ps[u] = ok[u] ? slots[i] : 0u;
-            fresh[u] = ROPE && ok[u] && ps[u] == new_slot;
-        }
+        for (int f = 0; f < NF; ++f) kr[0][f] = ok[0] ? *(const f4 *)(ka + 4 * f) : f4{0, 0, 0, 0};
 #pragma unroll
-        for (int u = 0; u < IT; ++u) {
-            const float *kp = Kc + (size_t)ps[u] * kv_dim + dim0;
+        for (int f = 0; f < NF; ++f) kr[1][f] = ok[1] ? *(const f4 *)(kb + 4 * f) : f4{0, 0, 0, 0};
 #pragma unroll
-            for (int f = 0; f < NF; ++f) kr[u][f] = (ok[u] && !fresh[u]) ? *(const f4 *)(kp + 4 * f) : f4{0, 0, 0, 0};
-        }
+        for (int f = 0; f < NF; ++f) vr[0][f] = ok[0] ? *(const f4 *)(va + 4 * f) : f4{0, 0, 0, 0};
 #pragma unroll
-        for (int u = 0; u < IT; ++u) {
-            const float *vp = Vc + (size_t)ps[u] * kv_dim + dim0;
-#pragma unroll
-            for (int f = 0; f < NF; ++f) vr[u][f] = (ok[u] && !fresh[u]) ? *(const f4 *)(vp + 4 * f) : f4{0, 0, 0, 0};
-        }
+        for (int f = 0; f < NF; ++f) vr[1][f] = ok[1] ? *(const f4 *)(vb + 4 * f) : f4{0, 0, 0, 0};
     };
-    auto take_fresh = [&]() {
-        if (ROPE) {
-#pragma unroll
-            for (int u = 0; u < IT; ++u)
-                if (fresh[u]) {
-#pragma unroll
-                    for (int f = 0; f < NF; ++f) {
-                        kr[u][f] = *(const f4 *)&sh_k[c * 4 * NF + 4 * f];
-                        vr[u][f] = *(const f4 *)&sh_v[c * 4 * NF + 4 * f];
-                    }
-                }
-        }
-    };
-    load_batch(0);
+    if (iters) issue(0);
 
     f4 q[GQA][NF];
+    uint32_t new_slot = 0xFFFFFFFFu;
     if (ROPE) {
+        const uint32_t clock = ra.step[0];
+        new_slot = ra.step[1];
         // items: GQA query heads, the new K head, the new V head
         const float *vsrc = ra.k_eq_v ? ra.k_in : ra.v_in;
         for (int it = wave; it < GQA + 2; it += 4) {
@@ -314,7 +310,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
                 vd[d] = sh_v[d];
             }
         }
-        if (split >= nsp) return;
+        if (!iters) return;
 #pragma unroll
         for (int h = 0; h < GQA; ++h)
 #pragma unroll
@@ -335,48 +331,51 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
 #pragma unroll
         for (int f = 0; f < NF; ++f) acc[h][f] = f4{0, 0, 0, 0};
     }
-    for (uint32_t jb = 0; jb < nit; jb += IT) {
-        if (jb > 0) load_batch(jb);
-        take_fresh();
+    // one chunk of buffer b into the running state
+    auto reduce = [&](int b, uint32_t ps) {
+        // the new token's row comes from LDS (the cache row just loaded may
+        // predate split 0's write)
+        if (ROPE && ok[b] && ps == new_slot) {
+#pragma unroll
+            for (int f = 0; f < NF; ++f) {
+                kr[b][f] = *(const f4 *)&sh_k[c * 4 * NF + 4 * f];
+                vr[b][f] = *(const f4 *)&sh_v[c * 4 * NF + 4 * f];
+            }
+        }
 #pragma unroll
         for (int h = 0; h < GQA; ++h) {
-            float sc[IT];
-            float mx = kNegBig;
+            float d = 0.0f;
 #pragma unroll
-            for (int u = 0; u < IT; ++u) {
-                float d = 0.0f;
-#pragma unroll
-                for (int f = 0; f < NF; ++f) {
-                    d = fmaf(q[h][f].x, kr[u][f].x, d);
-                    d = fmaf(q[h][f].y, kr[u][f].y, d);
-                    d = fmaf(q[h][f].z, kr[u][f].z, d);
-                    d = fmaf(q[h][f].w, kr[u][f].w, d);
-                }
-                sc[u] = ok[u] ? row16_sum(d) * scale : kNegBig;
-                mx = fmaxf(mx, sc[u]);
+            for (int f = 0; f < NF; ++f) {
+                d = fmaf(q[h][f].x, kr[b][f].x, d);
+                d = fmaf(q[h][f].y, kr[b][f].y, d);
+                d = fmaf(q[h][f].z, kr[b][f].z, d);
+                d = fmaf(q[h][f].w, kr[b][f].w, d);
             }
-            // the wave's four rows
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            const float sc = ok[b] ? row16_sum(d) * scale : kNegBig;
+            float mx = fmaxf(sc, __shfl_xor(sc, 16, 64));
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
             const float Mn = fmaxf(M[h], mx);
             const float rs = expf(M[h] - Mn);
-            float ps_sum = 0.0f;
+            const float p = ok[b] ? expf(sc - Mn) : 0.0f;
+            float psum = p + __shfl_xor(p, 16, 64);
+            psum += __shfl_xor(psum, 32, 64);
 #pragma unroll
-            for (int f = 0; f < NF; ++f) acc[h][f] *= rs;
-#pragma unroll
-            for (int u = 0; u < IT; ++u) {
-                const float p = ok[u] ? expf(sc[u] - Mn) : 0.0f;
-                ps_sum += p;
-#pragma unroll
-                for (int f = 0; f < NF; ++f) acc[h][f] += p * vr[u][f];
-            }
-            ps_sum += __shfl_xor(ps_sum, 16, 64);
-            ps_sum += __shfl_xor(ps_sum, 32, 64);
-            L[h] = L[h] * rs + ps_sum;
+            for (int f = 0; f < NF; ++f) acc[h][f] = acc[h][f] * rs + p * vr[b][f];
+            L[h] = L[h] * rs + psum;
             M[h] = Mn;
         }
+    };
+#pragma unroll 1
+    for (uint32_t t = 0; t < iters; t += 2) {
+        if (t > 0) issue(t);
+        const uint32_t na = slot_at(t + 2), nb = slot_at(t + 3);
+        reduce(0, pa);
+        if (t + 1 < iters) reduce(1, pb);
+        pa = na;
+        pb = nb;
     }
-    // rows of the wave hold different slots of the same columns
+    // rows of the wave hold different entries of the same columns
 #pragma unroll
     for (int h = 0; h < GQA; ++h)
 #pragma unroll
@@ -394,10 +393,11 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
     }
     __syncthreads();
 
-    // workgroup partial for this chunk
+    // workgroup partial for this split: [G][nq][D] sums, then [G][nq] maxima
+    // and [G][nq] denominators
     float *wacc = ws;
-    float *wm = ws + (size_t)kDecSplits * num_q_heads * D;
-    float *wl = wm + (size_t)kDecSplits * num_q_heads;
+    float *wm = ws + (size_t)G * num_q_heads * D;
+    float *wl = wm + (size_t)G * num_q_heads;
     for (int idx = threadIdx.x; idx < GQA * (D / 4); idx += 256) {
         const int h = idx / (D / 4), col = idx % (D / 4);
         float Mw = -1e9f;
@@ -419,67 +419,84 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
     }
 }
 
-// Merge of the chunk partials, one 256-thread workgroup per query head:
-// weights exp(m_j - M) once (wave 0), then the weighted sum of the partial
-// rows in chunk order (four chunks per batch of loads), the output row and,
-// for the o_proj matvec, its digit planes.  S = 0 gives a zero row.
+// Merge of the split partials.  Workgroup (column block, query head) owns 64
+// output values (16 float4 columns); thread (j, col), j = tid / 16, merges
+// splits j, j + 16, ... online (running max, rescaled sums) with all of its
+// loads issued at once, then the 16 running states meet in LDS in a fixed
+// order.  Writes the output and, for the o_proj matvec, its digit planes.
+// S = 0 gives a zero row.
 template <int DV>
 __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ ws,
                                                     const uint32_t *__restrict__ n_slots, uint32_t max_slots,
-                                                    uint32_t num_q_heads, float *__restrict__ out,
-                                                    uint32_t *__restrict__ xp, uint32_t xp_nb) {
+                                                    uint32_t nsplit, uint32_t num_q_heads,
+                                                    float *__restrict__ out, uint32_t *__restrict__ xp,
+                                                    uint32_t xp_nb) {
     constexpr int D = DV * 256;
-    __shared__ float ew[kDecSplits];
-    __shared__ float sinv;
-    __shared__ f4 part[4][D / 4];
-    const uint32_t qh = blockIdx.x;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    constexpr int U = 8;                 // splits per thread per batch of loads
+    __shared__ f4 st_t[16][16];
+    __shared__ float st_m[16][16], st_l[16][16];
+    __shared__ float res[64];
+    const uint32_t cb = blockIdx.x, qh = blockIdx.y;
+    const int j0 = threadIdx.x >> 4, col = threadIdx.x & 15;
     uint32_t S = *n_slots;
     if (S > max_slots) S = max_slots;
-    uint32_t chunk = (S + kDecSplits - 1) / kDecSplits;
-    chunk = (chunk + 15) & ~15u;
-    const uint32_t ns = S ? (S + chunk - 1) / chunk : 0;
-    const float *wacc = ws;
-    const float *wm = ws + (size_t)kDecSplits * num_q_heads * D;
-    const float *wl = wm + (size_t)kDecSplits * num_q_heads;
-    if (wave == 0) {
-        const bool v = (uint32_t)lane < ns;
-        const float mj = v ? wm[(size_t)lane * num_q_heads + qh] : kNegBig;
-        const float M = fmaxf(wave_max64(mj), -1e9f);
-        const float e = v ? expf(mj - M) : 0.0f;
-        const float L = wave_sum64(v ? e * wl[(size_t)lane * num_q_heads + qh] : 0.0f);
-        ew[lane] = e;
-        if (lane == 0) sinv = 1.0f / (L + 1e-9f);
-    }
-    __syncthreads();
-    // wave w sums chunks w, w + 4, ... for columns lane, lane + 64
-    for (uint32_t col = lane; col < (uint32_t)D / 4; col += 64) {
-        f4 t = f4{0, 0, 0, 0};
-        const float *src = wacc + (size_t)qh * D + 4 * col;
-        const size_t stride = (size_t)num_q_heads * D;
-        uint32_t j = wave;
-        for (; j + 12 < ns; j += 16) {
-            f4 v[4];
+    const uint32_t nch = (S + 15) / 16;
+    const uint32_t ns = nch < nsplit ? nch : nsplit;    // splits that hold a partial
+    const float *wacc = ws + (size_t)qh * D + cb * 64 + 4 * col;
+    const float *wm = ws + (size_t)nsplit * num_q_heads * D + qh;
+    const float *wl = wm + (size_t)nsplit * num_q_heads;
+    const size_t stride = (size_t)num_q_heads * D;
+
+    float m = kNegBig, l = 0.0f;
+    f4 t = f4{0, 0, 0, 0};
+    for (uint32_t jb = j0; jb < ns; jb += 16 * U) {
+        float mj[U], lj[U];
+        f4 aj[U];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) v[u] = *(const f4 *)(src + (j + 4 * u) * stride);
-#pragma unroll
-            for (int u = 0; u < 4; ++u) t += ew[j + 4 * u] * v[u];
+        for (int u = 0; u < U; ++u) {
+            const uint32_t j = jb + 16 * u;
+            const bool v = j < ns;
+            mj[u] = v ? wm[(size_t)j * num_q_heads] : kNegBig;
+            lj[u] = v ? wl[(size_t)j * num_q_heads] : 0.0f;
+            aj[u] = v ? *(const f4 *)(wacc + j * stride) : f4{0, 0, 0, 0};
         }
-        for (; j < ns; j += 4) t += ew[j] * *(const f4 *)(src + j * stride);
-        part[wave][col] = t;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const float mn = fmaxf(m, mj[u]);
+            const float a = expf(m - mn), b = expf(mj[u] - mn);
+            t = t * a + aj[u] * b;
+            l = l * a + lj[u] * b;
+            m = mn;
+        }
     }
+    st_t[j0][col] = t;
+    st_m[j0][col] = m;
+    st_l[j0][col] = l;
     __syncthreads();
-    const uint32_t k = threadIdx.x;        // eight values per thread: D / 8 threads
-    if (k < (uint32_t)D / 8) {
+    if (threadIdx.x < 16) {
+        const int cc = threadIdx.x;
+        float M = kNegBig;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) M = fmaxf(M, st_m[j][cc]);
+        f4 T = f4{0, 0, 0, 0};
+        float Lt = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const float e = expf(st_m[j][cc] - M);
+            T += e * st_t[j][cc];
+            Lt += e * st_l[j][cc];
+        }
+        T *= 1.0f / (Lt + 1e-9f);
+        *(f4 *)(out + (size_t)qh * D + cb * 64 + 4 * cc) = T;
+        res[4 * cc + 0] = T.x; res[4 * cc + 1] = T.y; res[4 * cc + 2] = T.z; res[4 * cc + 3] = T.w;
+    }
+    if (!xp) return;
+    __syncthreads();
+    if (threadIdx.x < 8) {            // two 32-value blocks, four lanes each
         float o[8];
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            const uint32_t col = 2 * k + hf;
-            const f4 t = (((part[0][col] + part[1][col]) + part[2][col]) + part[3][col]) * sinv;
-            o[4 * hf + 0] = t.x; o[4 * hf + 1] = t.y; o[4 * hf + 2] = t.z; o[4 * hf + 3] = t.w;
-            *(f4 *)(out + (size_t)qh * D + 4 * col) = t;
-        }
-        if (xp) emit_planes8(o, xp, xp_nb, qh * (D / 32) + (k >> 2), k & 3, true);
+        for (int i = 0; i < 8; ++i) o[i] = res[8 * threadIdx.x + i];
+        emit_planes8(o, xp, xp_nb, qh * (D / 32) + cb * 2 + (threadIdx.x >> 2), threadIdx.x & 3, true);
     }
 }
 
@@ -527,17 +544,18 @@ static int launch_decode_impl(chn_ctx *ctx, const float *q, float *kc, float *vc
                               const RopeArgs *ra) {
     const uint32_t num_kv = num_q_heads / gqa;
     const uint32_t xp_nb = num_q_heads * head_dim / 32;
-    dim3 grid(kDecSplits, num_kv);
+    const uint32_t nsplit = dec_splits(max_slots);
+    dim3 grid(nsplit, num_kv);
     hipStream_t s = ctx->stream;
     const RopeArgs rz = ra ? *ra : RopeArgs{nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0.0f, 0.0f, 0};
 #define CHN_ATTN(DV, G)                                                                                           \
     do {                                                                                                          \
         if (ra)                                                                                                   \
-            k_attn_decode<DV, G, true><<<grid, 256, 0, s>>>(q, kc, vc, slots, n_slots, max_slots, num_q_heads,    \
-                                                            kv_dim, scale, ws, rz);                               \
+            k_attn_decode<DV, G, true><<<grid, 256, 0, s>>>(q, kc, vc, slots, n_slots, max_slots,        \
+                                                                     num_q_heads, kv_dim, scale, ws, rz);         \
         else                                                                                                      \
-            k_attn_decode<DV, G, false><<<grid, 256, 0, s>>>(q, kc, vc, slots, n_slots, max_slots, num_q_heads,   \
-                                                             kv_dim, scale, ws, rz);                              \
+            k_attn_decode<DV, G, false><<<grid, 256, 0, s>>>(q, kc, vc, slots, n_slots, max_slots,       \
+                                                                      num_q_heads, kv_dim, scale, ws, rz);        \
     } while (0)
     if (head_dim == 256) {
         switch (gqa) {
@@ -559,8 +577,11 @@ static int launch_decode_impl(chn_ctx *ctx, const float *q, float *kc, float *vc
     }
 #undef CHN_ATTN
     CHN_LAUNCHED(ctx, "k_attn_decode");
-    if (head_dim == 256) k_attn_merge<1><<<num_q_heads, 256, 0, s>>>(ws, n_slots, max_slots, num_q_heads, out, xp, xp_nb);
-    else k_attn_merge<2><<<num_q_heads, 256, 0, s>>>(ws, n_slots, max_slots, num_q_heads, out, xp, xp_nb);
+    const dim3 mgrid(head_dim / 64, num_q_heads);
+    if (head_dim == 256)
+        k_attn_merge<1><<<mgrid, 256, 0, s>>>(ws, n_slots, max_slots, nsplit, num_q_heads, out, xp, xp_nb);
+    else
+        k_attn_merge<2><<<mgrid, 256, 0, s>>>(ws, n_slots, max_slots, nsplit, num_q_heads, out, xp, xp_nb);
     CHN_LAUNCHED(ctx, "k_attn_merge");
     return CHN_OK;
 }

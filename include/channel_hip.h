@@ -176,9 +176,11 @@ int chn_qkv_rope(chn_ctx *ctx, const float *q_in, const float *k_in, const float
                  uint32_t rotary_dim, int k_eq_v, float theta, float eps);
 
 /* Softmax attention of each query head over the slot list slots[0..S),
- * S = *n_slots (DEVICE memory, clamped to max_slots <= 4096): the reference's
- * Active_slots + Step_params[2] (global) or Active_slots + 4096 +
- * Step_params[3] (sliding).  Query head h reads KV head h / gqa_ratio at
+ * S = *n_slots (DEVICE memory, clamped to max_slots <= 4096).  The list
+ * buffer holds max_slots entries: entries at S and beyond are read (with
+ * the count, in one round trip) but never used.  List and count are the
+ * reference's Active_slots + Step_params[2] (global) or Active_slots +
+ * 4096 + Step_params[3] (sliding).  Query head h reads KV head h / gqa_ratio at
  * cache row slot * kv_dim.  scale multiplies q.k (the reference passes 1.0).
  * head_dim 256 or 512.  recordDecodeAttn (src/gpu/kernels.zig:147-152) +
  * shaders/decode_attn.wgsl. */

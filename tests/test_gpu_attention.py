@@ -44,8 +44,9 @@ def test_decode_attn_parity(ctx, H, gqa, D, S, q_scale):
     Vc = synth_normal_dev(ctx, nslot * kv_dim, seed + 1)
     Q = synth_normal_dev(ctx, H * D, seed + 2, q_scale)
     rng = np.random.default_rng(seed)
-    slots_h = rng.permutation(nslot).astype(np.uint32)[:S]
-    slots = u32_dev(ctx, slots_h)
+    perm = rng.permutation(nslot).astype(np.uint32)
+    slots_h = perm[:S]
+    slots = u32_dev(ctx, perm)      # the list has room for max_slots entries
     ns = u32_dev(ctx, [S])
     out = ctx.alloc(H * D * 4)
     say(f"decode_attn H={H} gqa={gqa} D={D} S={S}")

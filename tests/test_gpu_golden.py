@@ -47,7 +47,7 @@ def test_golden_matvecs(ctx):
 
 def test_golden_attention(ctx):
     q, K, V = ctx.upload(G["attn_q"]), ctx.upload(G["attn_K"]), ctx.upload(G["attn_V"])
-    slots = ctx.upload(G["attn_slots"])
+    slots = ctx.upload(np.concatenate([G["attn_slots"], np.zeros(16, np.uint32)]))   # room for max_slots = 80
     ns = ctx.upload(np.array([64], np.uint32))
     out = ctx.alloc(4 * 256 * 4)
     say("golden decode_attn")
