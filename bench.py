@@ -44,6 +44,10 @@ def q4_bytes(rows, K):
     return rows * (K // 32) * 20
 
 
+def xplanes_bytes(K):
+    return (K // 32) * 25 * 4
+
+
 def q4r_bytes(rows, K):
     return rows * (K // 32) * 18
 
@@ -82,24 +86,51 @@ def bench_mlp(ctx, args):
     import numpy as np
 
     H, I = 3840, 15360
-    w_bytes = q4_bytes(I, H)
+    rep = args.layout == "q4r"
+    w_bytes = q4_bytes(I, H)               # algorithmic bytes (the reference layout)
     ncopy = max(4, -(-ROTATE_BYTES // (3 * w_bytes)))
+    mlp_fn, gemv_fn = "chn_fused_mlp_q4", "chn_gemv_q4"     # repacked: replaced below
     Wg, Wu, Wd = [], [], []
+    ref0 = []                              # copy 0 in the reference layout, for the CPU baseline
     for c in range(ncopy):
         for lst, rows, K, k in ((Wg, I, H, 0), (Wu, I, H, 1), (Wd, H, I, 2)):
             b = ctx.alloc(q4_bytes(rows, K))
             ctx.call("chn_synth_q4", b, rows, K, SEED + 16 * c + k, 0.005, 0.02)
+            if rep:
+                r = ctx.alloc(q4r_bytes(rows, K))
+                ctx.call("chn_q4_repack", b, rows, K, r)
+                ctx.sync()
+                if c == 0:
+                    ref0.append(b)
+                else:
+                    b.free()
+                b = r
+            elif c == 0:
+                ref0.append(b)
             lst.append(b)
     x = ctx.alloc(H * 4)
     ctx.call("chn_synth_normal", x, H, SEED + 7, 1.0)
     act = ctx.alloc(I * 4)
     y = ctx.alloc(H * 4)
+    if rep:
+        # as the model runs it: planes of x once (the norm kernel writes them
+        # there), gate/up writing act and its planes, down reading those
+        xpl, apl = ctx.alloc(xplanes_bytes(H)), ctx.alloc(xplanes_bytes(I))
+        ctx.call("chn_xplanes", x, H, xpl)
+        mlp_fn, gemv_fn = "chn_fused_mlp_q4r_xp", "chn_gemv_q4r_xp"
+        mlp_args = lambda c: (Wg[c], Wu[c], xpl, act, apl, I, H)
+        gemv_args = lambda c: (Wd[c], apl, y, H, I)
+    else:
+        mlp_args = lambda c: (Wg[c], Wu[c], x, act, I, H)
+        gemv_args = lambda c: (Wd[c], act, y, H, I)
     ctx.sync()
 
+    mlp_calls = [ctx.bind(mlp_fn, *mlp_args(c)) for c in range(ncopy)]
+    gemv_calls = [ctx.bind(gemv_fn, *gemv_args(c)) for c in range(ncopy)]
+
     def step(i):
-        c = i % ncopy
-        ctx.call("chn_fused_mlp_q4", Wg[c], Wu[c], x, act, I, H)
-        ctx.call("chn_gemv_q4", Wd[c], act, y, H, I)
+        mlp_calls[i % ncopy]()
+        gemv_calls[i % ncopy]()
 
     for i in range(args.warmup):
         step(i)
@@ -116,28 +147,24 @@ def bench_mlp(ctx, args):
     reps = max(args.steps, 64)
     ctx.timer_start()
     for i in range(reps):
-        c = i % ncopy
-        ctx.call("chn_fused_mlp_q4", Wg[c], Wu[c], x, act, I, H)
+        mlp_calls[i % ncopy]()
     k_ms = ctx.timer_stop() / reps
     ctx.timer_start()
     for i in range(reps):
-        c = i % ncopy
-        ctx.call("chn_gemv_q4", Wd[c], act, y, H, I)
+        gemv_calls[i % ncopy]()
     d_ms = ctx.timer_stop() / reps
 
     step_bytes = 3 * w_bytes + H * 4 + H * 4 + 2 * I * 4
     gateup_bytes = 2 * w_bytes + H * 4 + I * 4
     down_bytes = w_bytes + I * 4 + H * 4
     achieved = gateup_bytes / (k_ms * 1e-3) / 1e9
-    traffic = load_traffic("k_q4mv<MLP>", "gate/up 15360x3840")
+    traffic = load_traffic("k_q4rmv_mlp_xp" if rep else "k_q4mv<MLP>", "gate/up 15360x3840")
 
     cpu = None
     if not args.no_cpu_baseline:
         import oracle
         nthr, model = cpu_info()
-        hg = ctx.download(Wg[0], np.uint32, w_bytes // 4)
-        hu = ctx.download(Wu[0], np.uint32, w_bytes // 4)
-        hd = ctx.download(Wd[0], np.uint32, w_bytes // 4)
+        hg, hu, hd = (ctx.download(b, np.uint32, w_bytes // 4) for b in ref0)
         hx = ctx.download(x, np.float32, H)
         n, t_start = 0, time.perf_counter()
         while True:
@@ -156,11 +183,13 @@ def bench_mlp(ctx, args):
         "ms_per_step": ms_per_step,
         "config": {"workload": "fused Q4 gated MLP decode step (gate/up/down Q4, GELU-tanh)",
                    "hidden": H, "ffn": I, "batch": 1, "weight_copies_rotated": ncopy,
+                   "weight_layout": "repacked Q4R (18 B per 32 weights)" if rep else "reference Q4 (20 B)",
                    "step_hbm_gbps": step_bytes / (ms_per_step * 1e-3) / 1e9,
                    "step_bytes": step_bytes,
                    "down_gemv_ms": d_ms,
                    "down_gemv_gbps": down_bytes / (d_ms * 1e-3) / 1e9},
-        "roofline": {"kernel": "chn_fused_mlp_q4 = k_xplanes + k_q4mv<MLP> (fused gate/up + GELU-tanh)",
+        "roofline": {"kernel": ("k_q4rmv_mlp_xp (chn_fused_mlp_q4r_xp: gate/up + GELU-tanh + planes of act)" if rep
+                                else "chn_fused_mlp_q4 = k_xplanes + k_q4mv<MLP> (fused gate/up + GELU-tanh)"),
                      "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "algorithmic_bytes_per_launch": gateup_bytes,
@@ -193,15 +222,23 @@ def alloc_gateup_copies(ctx, H, I, min_bytes=ROTATE_BYTES, repacked=False):
 
 
 def time_gateup(ctx, pairs, x, act, H, I, reps, repacked=False):
-    """Average duration (ms) of the fused gate/up matvec (planes pass +
-    matvec) over back-to-back launches on the library stream, HIP events."""
-    fn = "chn_fused_mlp_q4r" if repacked else "chn_fused_mlp_q4"
+    """Average duration (ms) of the fused gate/up matvec over back-to-back
+    launches on the library stream, HIP events.  Repacked: the model's
+    kernel alone (k_q4rmv_mlp_xp: planes of x in, act and its planes out),
+    x's planes made once beforehand; reference layout: chn_fused_mlp_q4
+    (its planes pass + matvec)."""
+    if repacked:
+        planes = ctx.alloc(xplanes_bytes(H))
+        act_planes = ctx.alloc(xplanes_bytes(I))
+        ctx.call("chn_xplanes", x, H, planes)
+        calls = [ctx.bind("chn_fused_mlp_q4r_xp", g, u, planes, act, act_planes, I, H) for g, u in pairs]
+    else:
+        calls = [ctx.bind("chn_fused_mlp_q4", g, u, x, act, I, H) for g, u in pairs]
     for i in range(4):
-        ctx.call(fn, pairs[i % len(pairs)][0], pairs[i % len(pairs)][1], x, act, I, H)
+        calls[i % len(calls)]()
     ctx.timer_start()
     for i in range(reps):
-        g, u = pairs[i % len(pairs)]
-        ctx.call(fn, g, u, x, act, I, H)
+        calls[i % len(calls)]()
     return ctx.timer_stop() / reps
 
 
@@ -397,11 +434,11 @@ def bench_decode(ctx, args):
                    "token_roofline_frac": (w_bytes + kv_bytes) / (ms_per_tok * 1e-3) / 1e9 / HBM_PEAK_GBS,
                    "model_create_s": t_create,
                    "decode_launch": "eager kernel launches" if args.eager else "HIP graph replay"},
-        "roofline": {"kernel": "chn_fused_mlp_q4r = k_xplanes + k_q4rmv<MLP> (gate/up + GELU-tanh, "
+        "roofline": {"kernel": "k_q4rmv_mlp_xp (chn_fused_mlp_q4r_xp: gate/up + GELU-tanh + planes of act, "
                                "15360x3840 x2, repacked weights as the model holds them)",
                      "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": load_traffic("k_q4rmv<MLP>", "gate/up 15360x3840"),
+                     "traffic": load_traffic("k_q4rmv_mlp_xp", "gate/up 15360x3840"),
                      "algorithmic_bytes_per_launch": gateup_bytes(H, I),
                      "bytes_per_launch_repacked_layout": gateup_bytes(H, I, repacked=True),
                      "avg_launch_ms": k_ms},
@@ -608,6 +645,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--slots", type=int, default=4096, help="attn workload: slot count (<= 4096)")
+    ap.add_argument("--layout", default="q4r", choices=["q4r", "q4"],
+                    help="mlp workload: repacked weights as the model holds them, or the reference layout")
     ap.add_argument("--eager", action="store_true",
                     help="decode: launch the kernels one by one instead of replaying the graph")
     args = ap.parse_args()

@@ -22,6 +22,12 @@ def q4r_bytes(rows, K):
     return rows * (K // 32) * 18
 
 
+def xplanes_bytes(K):
+    """Bytes of the activation digit planes of K values (chn_xplanes): 24
+    plane words and one float scale per 32 values."""
+    return (K // 32) * 25 * 4
+
+
 def q8_bytes(rows, K):
     """getQuantizedSizeBytes(rows, K, .q8) (src/quant.zig:181-183)."""
     return rows * ((K + 31) // 32) * Q8_BLOCK_BYTES

@@ -51,6 +51,9 @@ PROTOTYPES = {
     "chn_gemv_q4r": (c_int, [c_void_p] * 4 + [c_u32, c_u32]),
     "chn_fused_qkv_q4r": (c_int, [c_void_p] * 8 + [c_u32, c_u32, c_u32]),
     "chn_fused_mlp_q4r": (c_int, [c_void_p] * 5 + [c_u32, c_u32]),
+    "chn_xplanes": (c_int, [c_void_p, c_void_p, c_u32, c_void_p]),
+    "chn_gemv_q4r_xp": (c_int, [c_void_p] * 4 + [c_u32, c_u32]),
+    "chn_fused_mlp_q4r_xp": (c_int, [c_void_p] * 6 + [c_u32, c_u32]),
     "chn_batch_gemm_q4": (c_int, [c_void_p] * 4 + [c_u32] * 3),
     "chn_batch_fused_mlp_q4": (c_int, [c_void_p] * 5 + [c_u32] * 3),
     "chn_qkv_rope": (c_int, [c_void_p] + [c_void_p] * 9 + [c_u32] * 4 + [c_int, c_f32, c_f32]),

@@ -21,14 +21,13 @@
 namespace chn {
 
 constexpr int kAttnChunk = 64;     // prefill: slots per online-softmax step
-constexpr int kDecIters = 8;       // decode: most 16-entry chunks per workgroup
 constexpr uint32_t kDecGrid = 32;  // decode: workgroups per KV head (at most)
 constexpr float kNegBig = -1e30f;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 // Decode splits per KV head: one per 16-entry chunk of max_slots, at most
-// kDecGrid (then a split takes up to kDecIters chunks: 32 * 8 * 16 = 4096).
+// kDecGrid (a split then takes every kDecGrid-th chunk: 8 of 256 at 4096).
 static uint32_t dec_splits(uint32_t max_slots) {
     const uint32_t n = (max_slots + 15) / 16;
     return n < kDecGrid ? n : kDecGrid;
@@ -223,8 +222,8 @@ __device__ __forceinline__ void wave_rope_lds(float *row, uint32_t rot, float th
 }
 
 // Decode: grid (G, KV heads).  The slot list is taken in 16-entry chunks;
-// workgroup `split` takes chunks split, split + G, split + 2 G, ... (at most
-// kDecIters of them), two at a time, and row r of wave w holds entry
+// workgroup `split` takes chunks split, split + G, split + 2 G, ..., two
+// at a time, and row r of wave w holds entry
 // 16 c + 4 w + r of chunk c.  The list entries of its first two chunks are
 // read together with the slot count (the list holds max_slots entries; an
 // entry is used only below the count), so the first K/V loads wait on one

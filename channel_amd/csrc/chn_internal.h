@@ -89,6 +89,10 @@ int mvr_qkv(chn_ctx *ctx, const void *Wq, const void *Wk, const void *Wv, const 
             float *v, uint32_t q_dim, uint32_t kv_dim, uint32_t K, uint32_t *xp, bool planes_ready);
 int mvr_mlp(chn_ctx *ctx, const void *Wg, const void *Wu, const float *x, float *act, uint32_t M, uint32_t K,
             uint32_t *xp, bool planes_ready);
+// gate/up that also writes the digit planes of act into xp_out (the down
+// projection's input); xp_out must not alias xp_in
+int mvr_mlp_xp(chn_ctx *ctx, const void *Wg, const void *Wu, const uint32_t *xp_in, float *act,
+               uint32_t *xp_out, uint32_t M, uint32_t K);
 // Decode-step norm with planes: r' = post ? rmsnorm(r) * post_w : r;
 // x = add ? (x + r') * scalar : x; y = rmsnorm(x) * w; planes of y into xp
 // (if non-NULL).  One row, dim % 8 == 0, dim <= 8192.

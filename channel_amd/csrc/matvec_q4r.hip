@@ -222,6 +222,91 @@ __global__ __launch_bounds__(256) void k_q4rmv(RArgs a) {
     }
 }
 
+// Gate/up + GELU-tanh that also emits the digit planes of its output (the
+// down projection's input), so no separate planes pass runs between the two.
+// A workgroup of 8 waves owns a block of 32 consecutive rows; wave w takes
+// rows w, w + 8, w + 16, w + 24 of it, one gate/up pair at a time with the
+// next pair in flight, exactly as k_q4rmv<RV_MLP, 1, 1> computes each row.
+// The 32 results meet in LDS; four lanes then quantize the block.  Needs
+// K <= 4096 (one wave per row) and M % 32 == 0.
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_q4rmv_mlp_xp(
+    RArgs a, uint32_t *__restrict__ xo) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t nb = a.nb;
+    const bool ok0 = (uint32_t)lane < nb, ok1 = (uint32_t)(64 + lane) < nb;
+    const uint32_t b0 = ok0 ? lane : 0u, b1 = ok1 ? 64 + lane : 0u;
+    __shared__ float sact[32];
+    const uint32_t nrb = a.M / 32;
+
+    uint32_t P[2][XP_WORDS];
+    float xs[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const bool ok = c ? ok1 : ok0;
+        const uint32_t b = c ? b1 : b0;
+#pragma unroll
+        for (int i = 0; i < XP_WORDS; ++i) P[c][i] = a.xp[(size_t)i * nb + b];
+        xs[c] = ((const float *)(a.xp + (size_t)XP_WORDS * nb))[b];
+#pragma unroll
+        for (int i = 0; i < XP_WORDS; ++i) P[c][i] = ok ? P[c][i] : 0u;
+        xs[c] = ok ? xs[c] : 0.0f;
+    }
+
+    for (uint32_t rb = blockIdx.x; rb < nrb; rb += gridDim.x) {
+        u32x4r nq[2][2];
+        uint16_t sq[2][2];
+        auto load = [&](uint32_t row) {
+            const RMat *m[2] = {&a.m0, &a.m1};
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                const u32x4r *N = m[s]->N + (size_t)row * nb;
+                const uint16_t *S = m[s]->S + (size_t)row * nb;
+                nq[s][0] = __builtin_nontemporal_load(N + b0);
+                nq[s][1] = __builtin_nontemporal_load(N + b1);
+                sq[s][0] = __builtin_nontemporal_load(S + b0);
+                sq[s][1] = __builtin_nontemporal_load(S + b1);
+            }
+        };
+        const uint32_t row0 = rb * 32 + wave;
+        load(row0);
+#pragma unroll 1
+        for (int j = 0; j < 4; ++j) {
+            u32x4r cq[2][2];
+            uint16_t cs[2][2];
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    cq[s][c] = nq[s][c];
+                    cs[s][c] = sq[s][c];
+                }
+            if (j < 3) load(row0 + 8 * (j + 1));
+            float tot[2];
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                float r = 0.0f;
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    const int T = block_idot_r(cq[s][c], P[c]);
+                    const float sf = (float)__builtin_bit_cast(_Float16, cs[s][c]);
+                    r = fmaf((float)T, sf * xs[c], r);
+                }
+                tot[s] = wave_sum64(r);
+            }
+            if (lane == 0) sact[wave + 8 * j] = gelu_tanh(tot[0]) * tot[1];
+        }
+        __syncthreads();
+        if (threadIdx.x < 32) a.y0[rb * 32 + threadIdx.x] = sact[threadIdx.x];
+        if (threadIdx.x < 4) {
+            float o[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[i] = sact[8 * threadIdx.x + i];
+            emit_planes8(o, xo, nrb, rb, threadIdx.x, true);
+        }
+        __syncthreads();   // sact is rewritten by the next block
+    }
+}
+
 // Launch shape (from a sweep on MI355X at the 12B decode shapes with weights
 // cold in HBM): the fewest waves splitting K such that each covers <= 128
 // blocks; one gate/up row pair or two rows per wave; one row group per wave
@@ -293,6 +378,23 @@ int mvr_mlp(chn_ctx *ctx, const void *Wg, const void *Wu, const float *x, float 
     return launch_q4rmv(ctx, RV_MLP, a, x, xp, planes_ready);
 }
 
+int mvr_mlp_xp(chn_ctx *ctx, const void *Wg, const void *Wu, const uint32_t *xp_in, float *act,
+               uint32_t *xp_out, uint32_t M, uint32_t K) {
+    const uint32_t nb = K / 32;
+    if (nb > 128 || M % 32 != 0) {
+        const int rc = mvr_mlp(ctx, Wg, Wu, nullptr, act, M, K, (uint32_t *)xp_in, true);
+        if (rc) return rc;
+        if (launch_xplanes(ctx->stream, act, xp_out, M / 32)) return hip_fail(ctx, hipGetLastError(), "k_xplanes");
+        return CHN_OK;
+    }
+    const RArgs a{host_rmat(Wg, M, nb), host_rmat(Wu, M, nb), {}, act, nullptr, nullptr, xp_in, M, M, M, nb};
+    const uint32_t nrb = M / 32;
+    if (!nrb) return CHN_OK;
+    k_q4rmv_mlp_xp<<<nrb < 1024 ? nrb : 1024, 512, 0, ctx->stream>>>(a, xp_out);
+    CHN_LAUNCHED(ctx, "k_q4rmv_mlp_xp");
+    return CHN_OK;
+}
+
 static int check_r(chn_ctx *ctx, const float *x, uint32_t K) {
     CHN_REQUIRE(ctx, K > 0 && K % 32 == 0 && K <= 16384, "K=%u must be a positive multiple of 32, <= 16384", K);
     CHN_REQUIRE(ctx, x && aligned(x, 16), "x must be non-NULL and 16-byte aligned");
@@ -346,4 +448,44 @@ extern "C" int chn_fused_mlp_q4r(chn_ctx *ctx, const void *Wg, const void *Wu, c
     rc = ensure_workspace(ctx, xplanes_bytes(K / 32));
     if (rc) return rc;
     return mvr_mlp(ctx, Wg, Wu, x, act, M, K, (uint32_t *)ctx->ws, false);
+}
+
+extern "C" int chn_xplanes(chn_ctx *ctx, const float *x, uint32_t K, uint32_t *planes) {
+    if (!ctx) return CHN_E_INVALID;
+    CHN_REQUIRE(ctx, x && planes, "NULL argument");
+    CHN_REQUIRE(ctx, K % 32 == 0, "K=%u must be a multiple of 32", K);
+    CHN_REQUIRE(ctx, aligned(x, 16) && aligned(planes, 4), "x must be 16-byte and planes 4-byte aligned");
+    if (!K) return CHN_OK;
+    if (launch_xplanes(ctx->stream, x, planes, K / 32)) return hip_fail(ctx, hipGetLastError(), "k_xplanes");
+    return CHN_OK;
+}
+
+static int check_xp(chn_ctx *ctx, const uint32_t *planes, uint32_t K) {
+    CHN_REQUIRE(ctx, K > 0 && K % 32 == 0 && K <= 16384, "K=%u must be a positive multiple of 32, <= 16384", K);
+    CHN_REQUIRE(ctx, planes && aligned(planes, 4), "planes must be non-NULL and 4-byte aligned");
+    return CHN_OK;
+}
+
+extern "C" int chn_gemv_q4r_xp(chn_ctx *ctx, const void *W, const uint32_t *planes, float *y, uint32_t M,
+                               uint32_t K) {
+    if (!ctx) return CHN_E_INVALID;
+    int rc = check_xp(ctx, planes, K);
+    if (rc) return rc;
+    CHN_REQUIRE(ctx, W && y && aligned(W, 16), "W/y must be non-NULL, W 16-byte aligned");
+    if (!M) return CHN_OK;
+    return mvr_gemv(ctx, W, nullptr, y, M, K, (uint32_t *)planes, true);
+}
+
+extern "C" int chn_fused_mlp_q4r_xp(chn_ctx *ctx, const void *Wg, const void *Wu, const uint32_t *planes,
+                                    float *act, uint32_t *act_planes, uint32_t M, uint32_t K) {
+    if (!ctx) return CHN_E_INVALID;
+    int rc = check_xp(ctx, planes, K);
+    if (rc) return rc;
+    CHN_REQUIRE(ctx, Wg && Wu && act && aligned(Wg, 16) && aligned(Wu, 16), "NULL or misaligned argument");
+    CHN_REQUIRE(ctx, !act_planes || (M % 32 == 0 && aligned(act_planes, 4)),
+                "act_planes needs M %% 32 == 0 (M=%u) and 4-byte alignment", M);
+    CHN_REQUIRE(ctx, !act_planes || act_planes != planes, "act_planes must not alias planes");
+    if (!M) return CHN_OK;
+    if (act_planes) return mvr_mlp_xp(ctx, Wg, Wu, planes, act, act_planes, M, K);
+    return mvr_mlp(ctx, Wg, Wu, nullptr, act, M, K, (uint32_t *)planes, true);
 }

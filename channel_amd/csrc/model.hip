@@ -44,6 +44,7 @@ struct chn_model {
     uint32_t *step;    // {clock, slot_idx, S_global, S_sliding}
     uint32_t *tok;     // one token id for chn_decode_token
     uint32_t *mv_ws;
+    size_t mv_ws_words;
     float *attn_ws;
     uint64_t *topk_ws;
     // prefill buffers
@@ -173,7 +174,8 @@ static int alloc_runtime(chn_model *m) {
     const uint32_t kmax = H > I ? (H > qd ? H : qd) : (I > qd ? I : qd);
     size_t mvb = mv_ws_bytes(kmax);
     if (xbytes_bytes(H / 32) > mvb) mvb = xbytes_bytes(H / 32);
-    M_ALLOC(m->mv_ws, mvb);
+    m->mv_ws_words = mvb / 4;
+    M_ALLOC(m->mv_ws, 2 * mvb);      // two plane sets: the gate/up input and its output
     M_ALLOC(m->attn_ws, attn_ws_bytes(c.num_heads, md.D, kSlotsMax));
     M_ALLOC(m->topk_ws, topk_ws_bytes(V));
     const uint32_t T = c.max_prefill_tokens;
@@ -261,10 +263,10 @@ static int record_decode(chn_model *m, bool with_logits) {
         if (rc) return rc;       \
     } while (0)
     // Each norm kernel also writes the digit planes of its output into
-    // mv_ws, and attention writes those of its output, so the matvec that
-    // follows reads them directly; only the down projection's input (the
-    // gate/up activations) is converted by a separate pass.
-    uint32_t *xp = m->mv_ws;
+    // mv_ws, attention writes those of its output and gate/up those of the
+    // activations (into the second plane set), so every matvec reads its
+    // input planes directly.
+    uint32_t *xp = m->mv_ws, *xp_act = m->mv_ws + m->mv_ws_words;
     for (uint32_t i = 0; i < c.num_layers; ++i) {
         const auto &l = m->L[i];
         const float theta = l.full ? c.rope_theta_full : c.rope_theta;
@@ -276,8 +278,8 @@ static int record_decode(chn_model *m, bool with_logits) {
         R_(mvr_gemv(ctx, l.Wo, m->attn, m->mlp_out, H, l.qd, xp, true));
         R_(launch_norm_planes(s, m->x, m->mlp_out, l.has_post_attn ? l.post_attn : nullptr, l.pre_ffn, m->normed, xp,
                               H, eps, 1.0f, true));
-        R_(mvr_mlp(ctx, l.Wg, l.Wu, m->normed, m->act, I, H, xp, true));
-        R_(mvr_gemv(ctx, l.Wd, m->act, m->mlp_out, H, I, xp, false));
+        R_(mvr_mlp_xp(ctx, l.Wg, l.Wu, xp, m->act, xp_act, I, H));
+        R_(mvr_gemv(ctx, l.Wd, m->act, m->mlp_out, H, I, xp_act, true));
         const float *next_norm = (i + 1 < c.num_layers) ? m->L[i + 1].in_norm : m->final_norm;
         R_(launch_norm_planes(s, m->x, m->mlp_out, l.has_post_ffn ? l.post_ffn : nullptr, next_norm, m->normed, xp, H,
                               eps, l.scalar, true));

@@ -72,6 +72,20 @@ class Context:
             conv.append(_ptr(a) if t is c_void_p else a)
         return self._check(fn, f(self.handle, *conv))
 
+    def bind(self, fn, *args):
+        """A zero-argument callable for a chn_* call repeated with fixed
+        arguments (converted once), for launch loops where the per-call
+        host cost matters."""
+        f = getattr(lib, fn)
+        conv = tuple(_ptr(a) if t is c_void_p else a for a, t in zip(args, f.argtypes[1:]))
+        h = self.handle
+
+        def call():
+            rc = f(h, *conv)
+            if rc:
+                self._check(fn, rc)
+        return call
+
     def alloc(self, nbytes):
         b = Buffer(self, nbytes)
         self._bufs.append(b)

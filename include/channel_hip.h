@@ -144,6 +144,25 @@ int chn_fused_qkv_q4r(chn_ctx *ctx, const void *Wq, const void *Wk, const void *
 int chn_fused_mlp_q4r(chn_ctx *ctx, const void *Wg, const void *Wu, const float *x, float *act,
                       uint32_t M, uint32_t K);
 
+/* Activation digit planes: the form in which every matvec above reads its
+ * input x (K values in K/32 blocks).  Per block b of nb = K/32: an exponent
+ * e with |x_i| < 2^e, X_i = rint(x_i * 2^(22 - e)) split into six signed
+ * hex digits, stored as plane words [(p*4 + w)*nb + b] (p < 6 digit, w < 4
+ * eight-value group, 4-bit digits XOR 8), then nb float scales 2^(e - 22).
+ * Producing the planes once lets several matvecs share them; the model's
+ * norm and attention kernels write them directly.  No reference
+ * counterpart (the reference multiplies by f32 x in every shader). */
+#define CHN_XPLANES_BYTES(K) ((size_t)((K) / 32) * 25 * 4)
+int chn_xplanes(chn_ctx *ctx, const float *x, uint32_t K, uint32_t *planes);
+
+/* chn_gemv_q4r / chn_fused_mlp_q4r reading planes of x (chn_xplanes)
+ * instead of x.  With act_planes != NULL (M % 32 == 0, not aliasing planes)
+ * the gate/up matvec also writes the planes of act, the down projection's
+ * input, in the same pass; bit-identical to chn_xplanes(act). */
+int chn_gemv_q4r_xp(chn_ctx *ctx, const void *W, const uint32_t *planes, float *y, uint32_t M, uint32_t K);
+int chn_fused_mlp_q4r_xp(chn_ctx *ctx, const void *Wg, const void *Wu, const uint32_t *planes, float *act,
+                         uint32_t *act_planes, uint32_t M, uint32_t K);
+
 /* Y[t][r] = sum_k X[t][k] * W[r][k] for t < n_tok, r < M: X fp32 [n_tok][K]
  * (16-byte aligned), W Q4 [M][K], Y fp32 [n_tok][M].  Operands are rounded
  * to bf16 (X) and bf16(scale*(q-8)) (W, dequantized in LDS) for MFMA with

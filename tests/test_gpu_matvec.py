@@ -186,3 +186,86 @@ def test_q4r_bad_shapes(ctx):
     for K in (0, 48, 16416):
         with pytest.raises(ca.ChannelError):
             ctx.call("chn_gemv_q4r", W, x, x, 4, K)
+
+
+# ---- activation digit planes and the plane-input entries ------------------
+
+def decode_planes(P, K):
+    """Host decoding of chn_xplanes output: integers X and block scales."""
+    nb = K // 32
+    words = P[:24 * nb].reshape(6, 4, nb)                       # [plane][group][block]
+    inv = P[24 * nb:].view(np.float32)
+    sh = np.arange(8, dtype=np.uint32) * 4
+    dig = (((words[..., None] ^ np.uint32(0x88888888)) >> sh) & 15).astype(np.int64) - 8   # [p][w][b][n]
+    X = sum(dig[p] * (16 ** p) for p in range(6))               # [w][b][n]
+    return X.transpose(1, 0, 2).reshape(nb, 32), inv
+
+
+def test_xplanes_reconstruct_exactly(ctx):
+    K = 3840
+    rng = np.random.default_rng(41)
+    xh = rng.standard_normal(K).astype(np.float32)
+    xh[0:32] = 0.0                                   # zero block
+    xh[32:64] *= 1e-30                               # tiny block
+    xh[64:96] = 0.0
+    xh[64 + 5] = 4.0                                 # max exactly a power of two
+    xh[96:128] = -xh[96:128] * 1e3                   # large block
+    x = ctx.upload(xh)
+    P = ctx.alloc(ca.xplanes_bytes(K))
+    say("xplanes 3840")
+    ctx.call("chn_xplanes", x, K, P)
+    X, inv = decode_planes(ctx.download(P, np.uint32, ca.xplanes_bytes(K) // 4), K)
+    xb = xh.reshape(-1, 32).astype(np.float64)
+    for b in range(K // 32):
+        m = np.abs(xb[b]).max()
+        if m == 0.0 or m < 2.0 ** -100:
+            assert inv[b] == 0.0 and np.all(X[b] == 0), b
+            continue
+        e = int(np.log2(inv[b])) + 22                  # inv = 2^(e - 22)
+        assert inv[b] == np.float32(2.0 ** (e - 22)), b
+        assert 2.0 ** (e - 1) <= m < 2.0 ** e, b       # frexp exponent of the block max
+        assert np.array_equal(X[b], np.rint(xb[b] * 2.0 ** (22 - e)).astype(np.int64)), b
+        assert np.abs(X[b] * float(inv[b]) - xb[b]).max() <= 0.5 * float(inv[b])
+
+
+@pytest.mark.parametrize("M,K", [(15360, 3840), (64, 256), (64, 8192), (96, 640)])
+def test_q4r_plane_entries_match(ctx, M, K):
+    """chn_gemv_q4r_xp / chn_fused_mlp_q4r_xp on chn_xplanes(x) give the
+    same bits as the x-input entries; the fused act planes equal
+    chn_xplanes(act) (K = 8192 takes the separate-pass path)."""
+    Wg, Wu = synth_q4_dev(ctx, M, K, 1200 + M), synth_q4_dev(ctx, M, K, 1201 + M)
+    Rg, Ru = repack_dev(ctx, Wg, M, K), repack_dev(ctx, Wu, M, K)
+    x = synth_normal_dev(ctx, K, 1202 + K)
+    P = ctx.alloc(ca.xplanes_bytes(K))
+    say(f"q4r plane entries M={M} K={K}")
+    ctx.call("chn_xplanes", x, K, P)
+    y1, y2 = ctx.alloc(M * 4), ctx.alloc(M * 4)
+    ctx.call("chn_gemv_q4r", Rg, x, y1, M, K)
+    ctx.call("chn_gemv_q4r_xp", Rg, P, y2, M, K)
+    assert np.array_equal(f32_host(ctx, y1, M), f32_host(ctx, y2, M))
+    a1, a2, a3 = ctx.alloc(M * 4), ctx.alloc(M * 4), ctx.alloc(M * 4)
+    ctx.call("chn_fused_mlp_q4r", Rg, Ru, x, a1, M, K)
+    ctx.call("chn_fused_mlp_q4r_xp", Rg, Ru, P, a2, None, M, K)
+    AP = ctx.alloc(ca.xplanes_bytes(M))
+    ctx.call("chn_fused_mlp_q4r_xp", Rg, Ru, P, a3, AP, M, K)
+    h1 = f32_host(ctx, a1, M)
+    assert np.array_equal(h1, f32_host(ctx, a2, M))
+    assert np.array_equal(h1, f32_host(ctx, a3, M))
+    AQ = ctx.alloc(ca.xplanes_bytes(M))
+    ctx.call("chn_xplanes", a1, M, AQ)
+    n = ca.xplanes_bytes(M) // 4
+    assert np.array_equal(ctx.download(AP, np.uint32, n), ctx.download(AQ, np.uint32, n))
+    want = oracle.fused_mlp_q4(q4_host(ctx, Wg, M, K), q4_host(ctx, Wu, M, K), f32_host(ctx, x, K), M, K)
+    assert rel_err(h1, want) < 1e-3
+
+
+def test_q4r_plane_entries_reject(ctx):
+    W = ctx.alloc(1 << 16)
+    P = ctx.alloc(ca.xplanes_bytes(256))
+    a = ctx.alloc(64 * 4)
+    with pytest.raises(ca.ChannelError):
+        ctx.call("chn_fused_mlp_q4r_xp", W, W, P, a, P, 64, 256)        # act planes alias the input planes
+    with pytest.raises(ca.ChannelError):
+        ctx.call("chn_fused_mlp_q4r_xp", W, W, P, a, a, 50, 256)        # M % 32 != 0 with act planes
+    with pytest.raises(ca.ChannelError):
+        ctx.call("chn_xplanes", a, 48, P)                                # K % 32 != 0
