@@ -155,12 +155,15 @@ int launch_gemv_q8(hipStream_t st, const uint32_t *W, const float *x, float *y, 
 }
 
 // ---------------------------------------------------------------------
-// Softcapped top-64: pass 1 sorts 2048-logit tiles (bitonic, descending on
-// a 64-bit key = orderable(value) << 32 | ~index, so ties keep the lower
-// index first) and keeps 64 per tile; pass 2 sorts the survivors.
+// Softcapped top-64 on 64-bit keys orderable(value) << 32 | ~index (unique;
+// descending key order = value descending, ties by ascending index).  Pass
+// 1: a workgroup takes 1024 logits; each wave sorts four 64-key groups with
+// shuffle bitonic networks and merges them to its top 64, and the four
+// waves' lists merge through LDS.  Pass 2: 16 waves fold the sorted tile
+// lists with the same 64 + 64 -> 64 merge, then a four-level tree in LDS.
 // ---------------------------------------------------------------------
 constexpr int kTopK = 64;
-constexpr int kTile = 2048;
+constexpr int kTile = 1024;
 
 __device__ __forceinline__ uint64_t topk_key(float v, uint32_t idx) {
     uint32_t u = __builtin_bit_cast(uint32_t, v);
@@ -173,57 +176,100 @@ __device__ __forceinline__ float key_value(uint64_t k) {
     return __builtin_bit_cast(float, u);
 }
 
-// descending bitonic sort of n (power of two) keys in LDS by nthreads threads
-__device__ void bitonic_desc(uint64_t *k, int n) {
-    for (int size = 2; size <= n; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int t = threadIdx.x; t < n / 2; t += blockDim.x) {
-                const int i = 2 * t - (t & (stride - 1));
-                const int j = i + stride;
-                const bool desc = ((i & size) == 0);
-                const uint64_t a = k[i], b = k[j];
-                if (desc ? (a < b) : (a > b)) { k[i] = b; k[j] = a; }
-            }
-            __syncthreads();
-        }
-    }
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m, 64);
+    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m, 64);
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
+    const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)v, src, 64);
+    const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(v >> 32), src, 64);
+    return ((uint64_t)hi << 32) | lo;
 }
 
-__global__ __launch_bounds__(256) void k_topk_pass1(const float *__restrict__ logits, uint32_t V,
-                                                    uint64_t *__restrict__ cand) {
-    __shared__ uint64_t k[kTile];
-    const uint32_t base = blockIdx.x * kTile;
-    for (int i = threadIdx.x; i < kTile; i += 256) {
-        const uint32_t idx = base + i;
-        if (idx < V) {
-            const float v = logits[idx];
-            const float t = tanhf(v * (1.0f / 30.0f));
-            k[i] = topk_key(30.0f * t, idx);
-        } else {
-            k[i] = 0;   // below every real key
+// The wave's 64 keys (one per lane) sorted descending across lanes.
+__device__ __forceinline__ uint64_t wave_sort64_desc(uint64_t key, int lane) {
+#pragma unroll
+    for (int k = 2; k <= 64; k <<= 1)
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            const uint64_t o = shfl_xor_u64(key, j);
+            const bool desc = (lane & k) == 0, lo = (lane & j) == 0;
+            const uint64_t mx = key > o ? key : o, mn = key > o ? o : key;
+            key = (lo == desc) ? mx : mn;
         }
+    return key;
+}
+
+// Top 64 of two descending 64-key lists, descending: the elementwise max of
+// a and reversed b is a bitonic sequence holding them; half-cleaners sort it.
+__device__ __forceinline__ uint64_t wave_merge64_desc(uint64_t a, uint64_t b, int lane) {
+    const uint64_t br = shfl_u64(b, 63 - lane);
+    uint64_t key = a > br ? a : br;
+#pragma unroll
+    for (int j = 32; j > 0; j >>= 1) {
+        const uint64_t o = shfl_xor_u64(key, j);
+        const uint64_t mx = key > o ? key : o, mn = key > o ? o : key;
+        key = (lane & j) == 0 ? mx : mn;
     }
+    return key;
+}
+
+__global__ __launch_bounds__(256) void k_topk_tile(const float *__restrict__ logits, uint32_t V,
+                                                   uint64_t *__restrict__ cand) {
+    __shared__ uint64_t sh[4][kTopK];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t base = blockIdx.x * kTile + wave * 256;
+    uint64_t k[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const uint32_t idx = base + 64 * u + lane;
+        // padding keys (0) sort below every real key
+        k[u] = idx < V ? topk_key(30.0f * tanhf(logits[idx] * (1.0f / 30.0f)), idx) : 0ull;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) k[u] = wave_sort64_desc(k[u], lane);
+    sh[wave][lane] = wave_merge64_desc(wave_merge64_desc(k[0], k[1], lane), wave_merge64_desc(k[2], k[3], lane), lane);
     __syncthreads();
-    bitonic_desc(k, kTile);
-    if (threadIdx.x < kTopK) cand[(size_t)blockIdx.x * kTopK + threadIdx.x] = k[threadIdx.x];
+    if (wave == 0) {
+        const uint64_t a = wave_merge64_desc(sh[0][lane], sh[1][lane], lane);
+        const uint64_t b = wave_merge64_desc(sh[2][lane], sh[3][lane], lane);
+        cand[(size_t)blockIdx.x * kTopK + lane] = wave_merge64_desc(a, b, lane);
+    }
 }
 
-__global__ __launch_bounds__(1024) void k_topk_pass2(const uint64_t *__restrict__ cand, uint32_t ncand,
+__global__ __launch_bounds__(1024) void k_topk_merge(const uint64_t *__restrict__ cand, uint32_t nlist,
                                                      uint32_t *__restrict__ ids, float *__restrict__ vals) {
-    extern __shared__ uint64_t k2[];
-    uint32_t n = 1;
-    while (n < ncand) n <<= 1;
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) k2[i] = i < ncand ? cand[i] : 0;
+    constexpr int U = 8;                 // lists loaded per wave per batch
+    __shared__ uint64_t sh[16][kTopK];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    uint64_t acc = 0ull;                 // the empty list: below every real key
+    for (uint32_t l0 = wave; l0 < nlist; l0 += 16 * U) {
+        uint64_t c[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t l = l0 + 16 * u;
+            c[u] = l < nlist ? cand[(size_t)l * kTopK + lane] : 0ull;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc = wave_merge64_desc(acc, c[u], lane);
+    }
+    sh[wave][lane] = acc;
     __syncthreads();
-    bitonic_desc(k2, (int)n);
-    if (threadIdx.x < kTopK) {
-        const uint64_t key = k2[threadIdx.x];
-        if (key) {
-            ids[threadIdx.x] = 0xFFFFFFFFu - (uint32_t)key;
-            vals[threadIdx.x] = key_value(key);
+#pragma unroll
+    for (int s = 8; s >= 1; s >>= 1) {
+        if (wave < s) acc = wave_merge64_desc(sh[wave][lane], sh[wave + s][lane], lane);
+        __syncthreads();
+        if (wave < s) sh[wave][lane] = acc;
+        __syncthreads();
+    }
+    if (wave == 0) {
+        if (acc) {
+            ids[lane] = 0xFFFFFFFFu - (uint32_t)acc;
+            vals[lane] = key_value(acc);
         } else {
-            ids[threadIdx.x] = 0;
-            vals[threadIdx.x] = -1e30f;
+            ids[lane] = 0;
+            vals[lane] = -1e30f;
         }
     }
 }
@@ -232,11 +278,8 @@ size_t topk_ws_bytes(uint32_t V) { return (size_t)((V + kTile - 1) / kTile) * kT
 
 int launch_topk64(hipStream_t st, const float *logits, uint32_t V, uint32_t *ids, float *vals, uint64_t *ws) {
     const uint32_t tiles = (V + kTile - 1) / kTile;
-    k_topk_pass1<<<tiles, 256, 0, st>>>(logits, V, ws);
-    const uint32_t ncand = tiles * kTopK;
-    uint32_t n = 1;
-    while (n < ncand) n <<= 1;
-    k_topk_pass2<<<1, 1024, n * 8, st>>>(ws, ncand, ids, vals);
+    if (tiles) k_topk_tile<<<tiles, 256, 0, st>>>(logits, V, ws);
+    k_topk_merge<<<1, 1024, 0, st>>>(ws, tiles, ids, vals);
     return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
 }
 

@@ -68,6 +68,23 @@ def test_topk64_exact(ctx, V):
     assert np.all(np.diff(gv[:k].astype(np.float64)) <= 0)
 
 
+@pytest.mark.parametrize("V", [5000, 1025])
+def test_topk64_all_ties(ctx, V):
+    """Every logit saturates the cap to the same value: the answer is the 64
+    lowest indices, in order, whichever tiles they sit in."""
+    lg = np.full(V, 1000.0, np.float32)
+    d = ctx.upload(lg)
+    ids = ctx.alloc(256)
+    vals = ctx.alloc(256)
+    say(f"topk64 all ties V={V}")
+    ctx.call("chn_topk64", d, V, ids, vals)
+    gi = ctx.download(ids, np.uint32, 64)
+    wi, wv = oracle.topk64(lg)
+    assert np.array_equal(gi, np.arange(64, dtype=np.uint32))
+    assert np.array_equal(gi, wi)
+    assert np.array_equal(ctx.download(vals, np.float32, 64), wv)
+
+
 def test_topk64_small_vocab_padding(ctx):
     """Fewer than 64 logits: the tail is padded (ids 0, value -1e30)."""
     lg = np.array([3.0, -1.0, 7.0, 7.0, 0.5], np.float32)
