@@ -178,46 +178,25 @@ __device__ __forceinline__ void load_q(f4 (&q)[GQA][4 * DV], const float *__rest
 struct RopeArgs {
     const float *k_in, *v_in, *qw, *kw;
     const uint32_t *step;
+    const float2 *tab;      // this layer kind's (cos, sin) for the step's clock
     uint32_t rot;
-    float theta, eps;
+    float eps;
     int k_eq_v;
 };
 
-// One wave: RMSNorm (times w, or unit with w == NULL) of the D values at
-// `in` into LDS row `dst` (lane holds d = lane + 64 j).
-template <int D>
-__device__ __forceinline__ void wave_norm_to_lds(const float *__restrict__ in, const float *__restrict__ w,
-                                                 float *dst, float eps, int lane) {
-    float v[D / 64];
-    float ss = 0.0f;
-#pragma unroll
-    for (int j = 0; j < D / 64; ++j) {
-        v[j] = in[lane + 64 * j];
-        ss += v[j] * v[j];
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
-    const float inv = 1.0f / sqrtf(ss / (float)D + eps);
-#pragma unroll
-    for (int j = 0; j < D / 64; ++j) {
-        const float n = v[j] * inv;
-        dst[lane + 64 * j] = w ? n * w[lane + 64 * j] : n;
-    }
-}
-
-// One wave: RoPE over pairs (d, d + rot/2) of an LDS row in place,
-// freq = 1 / theta^(2d / rot), angle = clock * freq.
-__device__ __forceinline__ void wave_rope_lds(float *row, uint32_t rot, float theta, uint32_t clock, int lane) {
+// One wave: RoPE over pairs (d, d + rot/2) of an LDS row in place; lane
+// holds (cos, sin) of pairs d = lane + 64 k in cs[k].
+template <int NP>
+__device__ __forceinline__ void wave_rope_lds(float *row, uint32_t rot, const float2 (&cs)[NP], int lane) {
     const uint32_t half = rot / 2;
-    for (uint32_t d = lane; d < half; d += 64) {
-        const float v0 = row[d], v1 = row[d + half];
-        const float fe = (2.0f * (float)d) / (float)rot;
-        const float freq = 1.0f / powf(theta, fe);
-        const float ang = (float)clock * freq;
-        float sn, cs;
-        sincosf(ang, &sn, &cs);
-        row[d] = v0 * cs - v1 * sn;
-        row[d + half] = v0 * sn + v1 * cs;
+#pragma unroll
+    for (int k = 0; k < NP; ++k) {
+        const uint32_t d = lane + 64 * k;
+        if (d < half) {
+            const float v0 = row[d], v1 = row[d + half];
+            row[d] = v0 * cs[k].x - v1 * cs[k].y;
+            row[d + half] = v0 * cs[k].y + v1 * cs[k].x;
+        }
     }
 }
 
@@ -251,6 +230,44 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
     __shared__ float sh_q[ROPE ? GQA : 1][ROPE ? D : 4];
     __shared__ float sh_k[ROPE ? D : 4], sh_v[ROPE ? D : 4];
 
+    // The prologue's inputs are loaded first (ROPE): the raw q / k / v of this
+    // wave's items and their norm weights.  Loads complete in issue order, so
+    // the norms below then run while the K/V rows are still in flight.
+    constexpr int NIT = ROPE ? (GQA + 2 + 3) / 4 : 1;   // items per wave
+    constexpr int DPL = D / 64;                          // values per lane
+    float raw[NIT][DPL], nwt[NIT][DPL];
+    float2 rcs[DPL / 2];                                 // (cos, sin) of pairs lane + 64 k
+    if (ROPE) {
+#pragma unroll
+        for (int k = 0; k < DPL / 2; ++k) {
+            const uint32_t d = lane + 64 * k;
+            rcs[k] = d < ra.rot / 2 ? ra.tab[d] : float2{1.0f, 0.0f};
+        }
+        const float *vsrc = ra.k_eq_v ? ra.k_in : ra.v_in;
+#pragma unroll
+        for (int j = 0; j < NIT; ++j) {
+            const int it = wave + 4 * j;
+            const float *src = it < GQA ? Q + (size_t)(qh0 + it) * D
+                                        : (it == GQA ? ra.k_in : vsrc) + (size_t)kvh * D;
+            const float *wsrc = it < GQA ? ra.qw : ra.kw;
+            const bool has = it < GQA + 2, hw = it < GQA + 1;
+#pragma unroll
+            for (int d = 0; d < DPL; ++d) {
+                raw[j][d] = has ? src[lane + 64 * d] : 0.0f;
+                nwt[j][d] = hw ? wsrc[lane + 64 * d] : 1.0f;
+            }
+        }
+    }
+    // splits without entries leave an empty partial (max -1e30, sum 0)
+    auto write_empty = [&]() {
+        float *wm = ws + (size_t)G * num_q_heads * D;
+        float *wl = wm + (size_t)G * num_q_heads;
+        if (threadIdx.x < (uint32_t)GQA) {
+            wm[(size_t)split * num_q_heads + qh0 + threadIdx.x] = kNegBig;
+            wl[(size_t)split * num_q_heads + qh0 + threadIdx.x] = 0.0f;
+        }
+    };
+
     const uint32_t row_ent = 4 * wave + r;
     const uint32_t ntmax = ((max_slots + 15) / 16 + G - 1 - split) / G;   // chunks this split could own
     auto entry = [&](uint32_t t) { return (split + G * t) * 16 + row_ent; };
@@ -264,7 +281,10 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
     const uint32_t nch = (S + 15) / 16;
     const uint32_t iters = split < nch ? (nch - split + G - 1) / G : 0;
     // split 0 always runs when it has to write the new token's K/V
-    if (!iters && !(ROPE && split == 0)) return;
+    if (!iters && !(ROPE && split == 0)) {
+        write_empty();
+        return;
+    }
     const size_t dim0 = (size_t)kvh * D + (size_t)c * 4 * NF;
 
     bool ok[2];
@@ -288,18 +308,30 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
     f4 q[GQA][NF];
     uint32_t new_slot = 0xFFFFFFFFu;
     if (ROPE) {
-        const uint32_t clock = ra.step[0];
         new_slot = ra.step[1];
-        // items: GQA query heads, the new K head, the new V head
-        const float *vsrc = ra.k_eq_v ? ra.k_in : ra.v_in;
-        for (int it = wave; it < GQA + 2; it += 4) {
-            if (it < GQA) wave_norm_to_lds<D>(Q + (size_t)(qh0 + it) * D, ra.qw, sh_q[it], ra.eps, lane);
-            else if (it == GQA) wave_norm_to_lds<D>(ra.k_in + (size_t)kvh * D, ra.kw, sh_k, ra.eps, lane);
-            else wave_norm_to_lds<D>(vsrc + (size_t)kvh * D, nullptr, sh_v, ra.eps, lane);
+        // items: GQA query heads (RMSNorm * q_norm), the new K head
+        // (* k_norm), the new V head (unit RMSNorm), into LDS
+#pragma unroll
+        for (int j = 0; j < NIT; ++j) {
+            const int it = wave + 4 * j;
+            if (it < GQA + 2) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) ss += raw[j][d] * raw[j][d];
+#pragma unroll
+                for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+                const float inv = 1.0f / sqrtf(ss / (float)D + ra.eps);
+                float *dst = it < GQA ? sh_q[it] : (it == GQA ? sh_k : sh_v);
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) {
+                    const float n = raw[j][d] * inv;
+                    dst[lane + 64 * d] = it < GQA + 1 ? n * nwt[j][d] : n;
+                }
+            }
         }
         __syncthreads();
         for (int it = wave; it < GQA + 1; it += 4)
-            wave_rope_lds(it < GQA ? sh_q[it] : sh_k, ra.rot, ra.theta, clock, lane);
+            wave_rope_lds(it < GQA ? sh_q[it] : sh_k, ra.rot, rcs, lane);
         __syncthreads();
         if (split == 0) {
             float *kd = Kc + (size_t)new_slot * kv_dim + (size_t)kvh * D;
@@ -309,7 +341,10 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
                 vd[d] = sh_v[d];
             }
         }
-        if (!iters) return;
+        if (!iters) {
+            write_empty();
+            return;
+        }
 #pragma unroll
         for (int h = 0; h < GQA; ++h)
 #pragma unroll
@@ -418,18 +453,17 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
     }
 }
 
-// Merge of the split partials.  Workgroup (column block, query head) owns 64
-// output values (16 float4 columns); thread (j, col), j = tid / 16, merges
-// splits j, j + 16, ... online (running max, rescaled sums) with all of its
-// loads issued at once, then the 16 running states meet in LDS in a fixed
-// order.  Writes the output and, for the o_proj matvec, its digit planes.
-// S = 0 gives a zero row.
+// Merge of the split partials.  Every split leaves a partial, empty (sum 0)
+// when it had no entries, so the merge needs no slot count.  Workgroup
+// (column block, query head) owns 64 output values (16 float4 columns);
+// thread (j, col), j = tid / 16, merges splits j, j + 16, ... online
+// (running max, rescaled sums) with all of its loads issued at once, then
+// the 16 running states meet in LDS in a fixed order.  Writes the output
+// and, for the o_proj matvec, its digit planes.  S = 0 gives a zero row.
 template <int DV>
-__global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ ws,
-                                                    const uint32_t *__restrict__ n_slots, uint32_t max_slots,
-                                                    uint32_t nsplit, uint32_t num_q_heads,
-                                                    float *__restrict__ out, uint32_t *__restrict__ xp,
-                                                    uint32_t xp_nb) {
+__global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ ws, uint32_t nsplit,
+                                                    uint32_t num_q_heads, float *__restrict__ out,
+                                                    uint32_t *__restrict__ xp, uint32_t xp_nb) {
     constexpr int D = DV * 256;
     constexpr int U = 8;                 // splits per thread per batch of loads
     __shared__ f4 st_t[16][16];
@@ -437,10 +471,6 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ ws
     __shared__ float res[64];
     const uint32_t cb = blockIdx.x, qh = blockIdx.y;
     const int j0 = threadIdx.x >> 4, col = threadIdx.x & 15;
-    uint32_t S = *n_slots;
-    if (S > max_slots) S = max_slots;
-    const uint32_t nch = (S + 15) / 16;
-    const uint32_t ns = nch < nsplit ? nch : nsplit;    // splits that hold a partial
     const float *wacc = ws + (size_t)qh * D + cb * 64 + 4 * col;
     const float *wm = ws + (size_t)nsplit * num_q_heads * D + qh;
     const float *wl = wm + (size_t)nsplit * num_q_heads;
@@ -448,22 +478,24 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ ws
 
     float m = kNegBig, l = 0.0f;
     f4 t = f4{0, 0, 0, 0};
-    for (uint32_t jb = j0; jb < ns; jb += 16 * U) {
+    for (uint32_t jb = j0; jb < nsplit; jb += 16 * U) {
         float mj[U], lj[U];
         f4 aj[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const uint32_t j = jb + 16 * u;
-            const bool v = j < ns;
+            const bool v = j < nsplit;
             mj[u] = v ? wm[(size_t)j * num_q_heads] : kNegBig;
             lj[u] = v ? wl[(size_t)j * num_q_heads] : 0.0f;
             aj[u] = v ? *(const f4 *)(wacc + j * stride) : f4{0, 0, 0, 0};
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
+            // an empty partial's sums were never written: select, not scale
+            const f4 av = lj[u] > 0.0f ? aj[u] : f4{0, 0, 0, 0};
             const float mn = fmaxf(m, mj[u]);
             const float a = expf(m - mn), b = expf(mj[u] - mn);
-            t = t * a + aj[u] * b;
+            t = t * a + av * b;
             l = l * a + lj[u] * b;
             m = mn;
         }
@@ -546,7 +578,7 @@ static int launch_decode_impl(chn_ctx *ctx, const float *q, float *kc, float *vc
     const uint32_t nsplit = dec_splits(max_slots);
     dim3 grid(nsplit, num_kv);
     hipStream_t s = ctx->stream;
-    const RopeArgs rz = ra ? *ra : RopeArgs{nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0.0f, 0.0f, 0};
+    const RopeArgs rz = ra ? *ra : RopeArgs{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0.0f, 0};
 #define CHN_ATTN(DV, G)                                                                                           \
     do {                                                                                                          \
         if (ra)                                                                                                   \
@@ -578,9 +610,9 @@ static int launch_decode_impl(chn_ctx *ctx, const float *q, float *kc, float *vc
     CHN_LAUNCHED(ctx, "k_attn_decode");
     const dim3 mgrid(head_dim / 64, num_q_heads);
     if (head_dim == 256)
-        k_attn_merge<1><<<mgrid, 256, 0, s>>>(ws, n_slots, max_slots, nsplit, num_q_heads, out, xp, xp_nb);
+        k_attn_merge<1><<<mgrid, 256, 0, s>>>(ws, nsplit, num_q_heads, out, xp, xp_nb);
     else
-        k_attn_merge<2><<<mgrid, 256, 0, s>>>(ws, n_slots, max_slots, nsplit, num_q_heads, out, xp, xp_nb);
+        k_attn_merge<2><<<mgrid, 256, 0, s>>>(ws, nsplit, num_q_heads, out, xp, xp_nb);
     CHN_LAUNCHED(ctx, "k_attn_merge");
     return CHN_OK;
 }
@@ -595,9 +627,10 @@ int launch_decode_attn(chn_ctx *ctx, const float *q, const float *kc, const floa
 int launch_rope_decode_attn(chn_ctx *ctx, const float *q_in, const float *k_in, const float *v_in, const float *qw,
                             const float *kw, float *kc, float *vc, const uint32_t *step, const uint32_t *slots,
                             const uint32_t *n_slots, uint32_t max_slots, uint32_t num_q_heads, uint32_t head_dim,
-                            uint32_t kv_dim, uint32_t gqa, uint32_t rot, int k_eq_v, float theta, float eps,
-                            float scale, float *out, float *ws, uint32_t *xp) {
-    const RopeArgs ra{k_in, v_in, qw, kw, step, rot, theta, eps, k_eq_v};
+                            uint32_t kv_dim, uint32_t gqa, uint32_t rot, int k_eq_v, const float2 *rope_tab,
+                            float eps, float scale, float *out, float *ws, uint32_t *xp) {
+    if (rot > 2 * kRopePairs || rot > head_dim) return set_err(ctx, CHN_E_UNSUPPORTED, "rotary_dim %u", rot);
+    const RopeArgs ra{k_in, v_in, qw, kw, step, rope_tab, rot, eps, k_eq_v};
     return launch_decode_impl(ctx, q_in, kc, vc, slots, n_slots, max_slots, num_q_heads, head_dim, kv_dim, gqa, scale,
                               out, ws, xp, &ra);
 }

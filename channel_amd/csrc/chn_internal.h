@@ -96,8 +96,20 @@ int mvr_mlp_xp(chn_ctx *ctx, const void *Wg, const void *Wu, const uint32_t *xp_
 // Decode-step norm with planes: r' = post ? rmsnorm(r) * post_w : r;
 // x = add ? (x + r') * scalar : x; y = rmsnorm(x) * w; planes of y into xp
 // (if non-NULL).  One row, dim % 8 == 0, dim <= 8192.
+// Per-step RoPE table, written by the decode step's first norm kernel and
+// read by every layer's attention: (cos, sin) of clock * theta^(-2d / rot)
+// for d < rot / 2, kind 0 = sliding layers, kind 1 = full layers, each
+// kRopePairs entries (rot <= 512).
+constexpr uint32_t kRopePairs = 256;
+struct RopeTab {
+    const uint32_t *step;   // device {clock, ...}
+    float2 *tab;            // [2][kRopePairs]
+    float theta[2];
+    uint32_t rot[2];
+};
 int launch_norm_planes(hipStream_t s, float *x, const float *r, const float *post_w, const float *w, float *y,
-                       uint32_t *xp, uint32_t dim, float eps, float scalar, bool add);
+                       uint32_t *xp, uint32_t dim, float eps, float scalar, bool add,
+                       const RopeTab *rope = nullptr);
 int launch_qkv_rope(hipStream_t st, const float *q_in, const float *k_in, const float *v_in, const float *qw,
                     const float *kw, float *q_out, float *kc, float *vc, const uint32_t *step, uint32_t num_q,
                     uint32_t num_kv, uint32_t D, uint32_t rot, int k_eq_v, float theta, float eps);
@@ -117,8 +129,8 @@ int launch_decode_attn(chn_ctx *ctx, const float *q, const float *kc, const floa
 int launch_rope_decode_attn(chn_ctx *ctx, const float *q_in, const float *k_in, const float *v_in, const float *qw,
                             const float *kw, float *kc, float *vc, const uint32_t *step, const uint32_t *slots,
                             const uint32_t *n_slots, uint32_t max_slots, uint32_t num_q_heads, uint32_t head_dim,
-                            uint32_t kv_dim, uint32_t gqa, uint32_t rot, int k_eq_v, float theta, float eps,
-                            float scale, float *out, float *ws, uint32_t *xp);
+                            uint32_t kv_dim, uint32_t gqa, uint32_t rot, int k_eq_v, const float2 *rope_tab,
+                            float eps, float scale, float *out, float *ws, uint32_t *xp);
 int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const float *vc, const uint32_t *slots,
                         uint32_t n_tok, uint32_t num_prev, uint32_t num_q_heads, uint32_t head_dim, uint32_t kv_dim,
                         uint32_t gqa, float scale, uint32_t window, float *out);

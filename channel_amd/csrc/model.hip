@@ -45,6 +45,7 @@ struct chn_model {
     uint32_t *tok;     // one token id for chn_decode_token
     uint32_t *mv_ws;
     size_t mv_ws_words;
+    float2 *rope_tab;    // [2][kRopePairs] (cos, sin) for the step's clock
     float *attn_ws;
     uint64_t *topk_ws;
     // prefill buffers
@@ -177,6 +178,7 @@ static int alloc_runtime(chn_model *m) {
     m->mv_ws_words = mvb / 4;
     M_ALLOC(m->mv_ws, 2 * mvb);      // two plane sets: the gate/up input and its output
     M_ALLOC(m->attn_ws, attn_ws_bytes(c.num_heads, md.D, kSlotsMax));
+    M_ALLOC(m->rope_tab, 2 * kRopePairs * sizeof(float2));
     M_ALLOC(m->topk_ws, topk_ws_bytes(V));
     const uint32_t T = c.max_prefill_tokens;
     m->max_tok = T;
@@ -269,12 +271,17 @@ static int record_decode(chn_model *m, bool with_logits) {
     uint32_t *xp = m->mv_ws, *xp_act = m->mv_ws + m->mv_ws_words;
     for (uint32_t i = 0; i < c.num_layers; ++i) {
         const auto &l = m->L[i];
-        const float theta = l.full ? c.rope_theta_full : c.rope_theta;
-        if (i == 0) R_(launch_norm_planes(s, m->x, nullptr, nullptr, l.in_norm, m->normed, xp, H, eps, 1.0f, false));
+        if (i == 0) {
+            // the step's first kernel also writes its RoPE table
+            const RopeTab rt{m->step, m->rope_tab, {c.rope_theta, c.rope_theta_full},
+                             {head_shape(c, false).rot, head_shape(c, true).rot}};
+            R_(launch_norm_planes(s, m->x, nullptr, nullptr, l.in_norm, m->normed, xp, H, eps, 1.0f, false, &rt));
+        }
         R_(mvr_qkv(ctx, l.Wq, l.Wk, l.Wv, m->normed, m->q, m->k, m->v, l.qd, l.kvd, H, xp, true));
         R_(launch_rope_decode_attn(ctx, m->q, m->k, m->v, l.q_norm, l.k_norm, l.kc, l.vc, m->step,
                                    m->slots + (l.full ? 0 : kSlotsMax), m->step + (l.full ? 2 : 3), kSlotsMax, nq, l.D,
-                                   l.kvd, l.gqa, l.rot, (int)c.k_eq_v, theta, eps, 1.0f, m->attn, m->attn_ws, xp));
+                                   l.kvd, l.gqa, l.rot, (int)c.k_eq_v, m->rope_tab + (l.full ? kRopePairs : 0), eps,
+                                   1.0f, m->attn, m->attn_ws, xp));
         R_(mvr_gemv(ctx, l.Wo, m->attn, m->mlp_out, H, l.qd, xp, true));
         R_(launch_norm_planes(s, m->x, m->mlp_out, l.has_post_attn ? l.post_attn : nullptr, l.pre_ffn, m->normed, xp,
                               H, eps, 1.0f, true));

@@ -87,14 +87,29 @@ __device__ __forceinline__ void store8(float *p, uint32_t t, const float (&v)[8]
 // norm), with ADD it is added to x and scaled (add_rmsnorm), then
 // y = rmsnorm(x) * w and the digit planes of y.  One workgroup of
 // ceil(dim / 8) threads rounded up to whole waves, eight values per thread
-// (four threads per 32-block, as the planes want them).
+// (four threads per 32-block, as the planes want them).  With rt.tab set
+// (the step's first norm) the threads also write the step's RoPE table.
 template <bool POST, bool ADD>
 __global__ __launch_bounds__(1024) void k_norm_planes(float *__restrict__ x, const float *__restrict__ r,
                                                       const float *__restrict__ pw, const float *__restrict__ w,
                                                       float *__restrict__ y, uint32_t *__restrict__ xp, uint32_t dim,
-                                                      float eps, float scalar) {
+                                                      float eps, float scalar, RopeTab rt) {
     __shared__ float sh[16];
     const uint32_t t = threadIdx.x;
+    if (rt.tab) {
+        const uint32_t clock = rt.step[0];
+        for (uint32_t i = t; i < 2 * kRopePairs; i += blockDim.x) {
+            const uint32_t kind = i / kRopePairs, d = i % kRopePairs, rot = rt.rot[kind];
+            if (d < rot / 2) {
+                const float fe = (2.0f * (float)d) / (float)rot;
+                const float freq = 1.0f / powf(rt.theta[kind], fe);
+                const float ang = (float)clock * freq;
+                float sn, cs;
+                sincosf(ang, &sn, &cs);
+                rt.tab[i] = float2{cs, sn};
+            }
+        }
+    }
     const bool ok = 8 * t < dim;
     // every load is issued before the first reduction
     float xv[8], rv[8], pv[8], wv[8];
@@ -129,12 +144,14 @@ __global__ __launch_bounds__(1024) void k_norm_planes(float *__restrict__ x, con
 }
 
 int launch_norm_planes(hipStream_t s, float *x, const float *r, const float *post_w, const float *w, float *y,
-                       uint32_t *xp, uint32_t dim, float eps, float scalar, bool add) {
+                       uint32_t *xp, uint32_t dim, float eps, float scalar, bool add, const RopeTab *rope) {
     if (dim % 32 != 0 || dim > 8192) return CHN_E_UNSUPPORTED;
+    if (rope && (rope->rot[0] > 2 * kRopePairs || rope->rot[1] > 2 * kRopePairs)) return CHN_E_UNSUPPORTED;
     const uint32_t nt = ((dim / 8 + 63) / 64) * 64;
-    if (!add) k_norm_planes<false, false><<<1, nt, 0, s>>>(x, r, post_w, w, y, xp, dim, eps, scalar);
-    else if (post_w) k_norm_planes<true, true><<<1, nt, 0, s>>>(x, r, post_w, w, y, xp, dim, eps, scalar);
-    else k_norm_planes<false, true><<<1, nt, 0, s>>>(x, r, post_w, w, y, xp, dim, eps, scalar);
+    const RopeTab rt = rope ? *rope : RopeTab{nullptr, nullptr, {0.0f, 0.0f}, {0u, 0u}};
+    if (!add) k_norm_planes<false, false><<<1, nt, 0, s>>>(x, r, post_w, w, y, xp, dim, eps, scalar, rt);
+    else if (post_w) k_norm_planes<true, true><<<1, nt, 0, s>>>(x, r, post_w, w, y, xp, dim, eps, scalar, rt);
+    else k_norm_planes<false, true><<<1, nt, 0, s>>>(x, r, post_w, w, y, xp, dim, eps, scalar, rt);
     return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
 }
 
