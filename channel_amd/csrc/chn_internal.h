@@ -110,6 +110,42 @@ struct RopeTab {
 int launch_norm_planes(hipStream_t s, float *x, const float *r, const float *post_w, const float *w, float *y,
                        uint32_t *xp, uint32_t dim, float eps, float scalar, bool add,
                        const RopeTab *rope = nullptr);
+
+// The RoPE table entries i = t, t + nt, ... of rt (same arithmetic as the
+// reference's per-element rotation: theta^(2d / rot) by powf, sincosf).
+__device__ __forceinline__ void rope_table(const RopeTab &rt, uint32_t t, uint32_t nt) {
+    const uint32_t clock = rt.step[0];
+    for (uint32_t i = t; i < 2 * kRopePairs; i += nt) {
+        // selects, not rt.rot[kind]: a runtime index into a by-value argument
+        // would copy it to scratch
+        const uint32_t kind = i / kRopePairs, d = i % kRopePairs, rot = kind ? rt.rot[1] : rt.rot[0];
+        if (d < rot / 2) {
+            const float fe = (2.0f * (float)d) / (float)rot;
+            const float freq = 1.0f / powf(kind ? rt.theta[1] : rt.theta[0], fe);
+            const float ang = (float)clock * freq;
+            float sn, cs;
+            sincosf(ang, &sn, &cs);
+            rt.tab[i] = float2{cs, sn};
+        }
+    }
+}
+
+// The decode step's norm, as the fused matvecs recompute it in every
+// workgroup: r' = post ? rmsnorm(r) * pw : r; xn = add ? (x_in + r') *
+// scalar : x_in; y = rmsnorm(xn) * w, whose digit planes feed the matvec.
+// Workgroup 0 writes xn to x_out (never x_in: the other workgroups still
+// read it) and y (if non-NULL).
+enum NormMode { NORM_PLAIN = 0, NORM_ADD = 1, NORM_POST_ADD = 2 };
+struct NormArgs {
+    const float *x_in, *r, *pw, *w;
+    float *x_out, *y;
+    float eps, scalar;
+    RopeTab rope;          // tab != NULL: workgroup 0 also writes the step's RoPE table
+};
+int mvr_qkv_nx(chn_ctx *ctx, const void *Wq, const void *Wk, const void *Wv, float *q, float *k, float *v,
+               uint32_t q_dim, uint32_t kv_dim, uint32_t K, const NormArgs &n, int mode);
+int mvr_mlp_nx(chn_ctx *ctx, const void *Wg, const void *Wu, float *act, uint32_t *xp_out, uint32_t M,
+               uint32_t K, const NormArgs &n, int mode);
 int launch_qkv_rope(hipStream_t st, const float *q_in, const float *k_in, const float *v_in, const float *qw,
                     const float *kw, float *q_out, float *kc, float *vc, const uint32_t *step, uint32_t num_q,
                     uint32_t num_kv, uint32_t D, uint32_t rot, int k_eq_v, float theta, float eps);
@@ -249,8 +285,10 @@ __device__ __forceinline__ float wave_max64(float v) {
 // Digit planes of one 32-block from the four lanes 4k..4k+3 of a wave that
 // hold its words w = lane & 3 (eight consecutive values each).  All four
 // lanes must call (with zeros where ok is false); only ok lanes store.
-__device__ __forceinline__ void emit_planes8(const float (&v)[8], uint32_t *__restrict__ xp, uint32_t nb,
-                                             uint32_t b, uint32_t w, bool ok) {
+// Plane word (p, w) of block b goes to xp[(p * 4 + w) * ws + b * bs], the
+// block's scale to xp[24 * ws + b * bs].
+__device__ __forceinline__ void emit_planes8s(const float (&v)[8], uint32_t *__restrict__ xp, uint32_t ws,
+                                              uint32_t bs, uint32_t b, uint32_t w, bool ok) {
     float m = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
@@ -272,9 +310,16 @@ __device__ __forceinline__ void emit_planes8(const float (&v)[8], uint32_t *__re
         uint32_t word = 0;
 #pragma unroll
         for (int n = 0; n < 8; ++n) word |= ((u[n] >> (4 * p)) & 15u) << (4 * n);
-        xp[(size_t)(p * 4 + w) * nb + b] = word ^ 0x88888888u;
+        xp[(size_t)(p * 4 + w) * ws + (size_t)b * bs] = word ^ 0x88888888u;
     }
-    if (w == 0) ((float *)(xp + (size_t)XP_WORDS * nb))[b] = inv;
+    if (w == 0) ((float *)xp)[(size_t)XP_WORDS * ws + (size_t)b * bs] = inv;
+}
+
+// Planes in the chn_xplanes layout: plane word (p, w) of block b at
+// [(p * 4 + w) * nb + b], the scale at [24 * nb + b].
+__device__ __forceinline__ void emit_planes8(const float (&v)[8], uint32_t *__restrict__ xp, uint32_t nb,
+                                             uint32_t b, uint32_t w, bool ok) {
+    emit_planes8s(v, xp, nb, 1, b, w, ok);
 }
 
 }  // namespace chn

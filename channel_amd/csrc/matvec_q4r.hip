@@ -58,6 +58,11 @@ struct RArgs {
     uint32_t M, seg1, seg2, nb;
 };
 
+// The wave's index in its workgroup, as a wave-uniform (scalar) value, so
+// row pointers derived from it stay in SGPRs and loads take 32-bit lane
+// offsets instead of per-lane 64-bit addresses.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
 // sum_i (q_i - 8) X_i of one block: the signed nibbles times each plane.
 __device__ __forceinline__ int block_idot_r(const u32x4r s, const uint32_t (&P)[XP_WORDS]) {
     int t[XP_PLANES];
@@ -112,7 +117,7 @@ __global__ __launch_bounds__(256) void k_q4rmv(RArgs a) {
     constexpr int NMAT = (MODE == RV_MLP) ? 2 : 1;
     constexpr int V = RPW * NMAT;
     constexpr int G = 4 / WPR;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = wave_id(), lane = threadIdx.x & 63;
     const int grp = wave / WPR, part = wave % WPR;
     const uint32_t nb = a.nb;
     // K range of this wave: blocks [kb0, kb0 + nblk), nblk <= 128
@@ -222,55 +227,251 @@ __global__ __launch_bounds__(256) void k_q4rmv(RArgs a) {
     }
 }
 
-// Gate/up + GELU-tanh that also emits the digit planes of its output (the
-// down projection's input), so no separate planes pass runs between the two.
-// A workgroup of 8 waves owns a block of 32 consecutive rows; wave w takes
-// rows w, w + 8, w + 16, w + 24 of it, one gate/up pair at a time with the
-// next pair in flight, exactly as k_q4rmv<RV_MLP, 1, 1> computes each row.
-// The 32 results meet in LDS; four lanes then quantize the block.  Needs
-// K <= 4096 (one wave per row) and M % 32 == 0.
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_q4rmv_mlp_xp(
-    RArgs a, uint32_t *__restrict__ xo) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const uint32_t nb = a.nb;
-    const bool ok0 = (uint32_t)lane < nb, ok1 = (uint32_t)(64 + lane) < nb;
-    const uint32_t b0 = ok0 ? lane : 0u, b1 = ok1 ? 64 + lane : 0u;
-    __shared__ float sact[32];
-    const uint32_t nrb = a.M / 32;
+// ---- the decode step's norm as a matvec prologue ---------------------------
 
-    uint32_t P[2][XP_WORDS];
-    float xs[2];
+typedef float f32x4r __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void ld8(const float *p, uint32_t t, bool ok, float (&v)[8]) {
+    if (ok) {
+        const f32x4r a = *(const f32x4r *)(p + 8 * (size_t)t), b = *(const f32x4r *)(p + 8 * (size_t)t + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    }
+}
+__device__ __forceinline__ void st8(float *p, uint32_t t, const float (&v)[8]) {
+    *(f32x4r *)(p + 8 * (size_t)t) = f32x4r{v[0], v[1], v[2], v[3]};
+    *(f32x4r *)(p + 8 * (size_t)t + 4) = f32x4r{v[4], v[5], v[6], v[7]};
+}
+// Sum over the workgroup: wave sums, then the wave partials in index order.
+__device__ __forceinline__ float wg_sum(float v, float *sh) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    const int nw = blockDim.x >> 6;
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (int i = 0; i < nw; ++i) t += sh[i];
+    __syncthreads();
+    return t;
+}
+
+// NormArgs' norm over dim values (dim % 32 == 0, dim <= 8 * blockDim), eight
+// per thread, four threads per 32-block: the digit planes of y go to LDS
+// block by block (kLdsBlk words per block: 24 plane words, then the scale;
+// constant offsets from one base per block, and the odd stride keeps a
+// wave's reads of consecutive blocks free of bank conflicts), workgroup 0
+// writes x_out and y.  The same arithmetic, in the same order, as the
+// standalone norm kernel.
+constexpr int kLdsBlk = XP_WORDS + 1;
+// Split in two so that the norm's inputs are requested before the matvec's
+// first weights: loads complete in issue order, so the norm math then runs
+// while the weights are still in flight.
+struct NormIn {
+    float xv[8], rv[8], pv[8], wv[8];
+};
+template <int MODE>
+__device__ __forceinline__ void norm_load(const NormArgs &n, uint32_t dim, NormIn &v) {
+    const uint32_t t = threadIdx.x;
+    const bool ok = 8 * t < dim;
+    ld8(n.x_in, t, ok, v.xv);
+    if (MODE != NORM_PLAIN) ld8(n.r, t, ok, v.rv);
+    if (MODE == NORM_POST_ADD) ld8(n.pw, t, ok, v.pv);
+    ld8(n.w, t, ok, v.wv);
+}
+template <int MODE>
+__device__ __forceinline__ void norm_to_lds(const NormArgs &n, uint32_t dim, NormIn &v, uint32_t *lp, float *sh) {
+    const uint32_t t = threadIdx.x;
+    const bool ok = 8 * t < dim;
+    float(&xv)[8] = v.xv;
+    if (MODE != NORM_PLAIN) {
+        if (MODE == NORM_POST_ADD) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ss += v.rv[i] * v.rv[i];
+            ss = wg_sum(ss, sh);
+            const float inv = 1.0f / sqrtf(ss / (float)dim + n.eps);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v.rv[i] = (v.rv[i] * inv) * v.pv[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xv[i] = (xv[i] + v.rv[i]) * n.scalar;
+    }
+    if (blockIdx.x == 0 && ok) st8(n.x_out, t, xv);
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += xv[i] * xv[i];
+    ss = wg_sum(ss, sh);
+    const float inv = 1.0f / sqrtf(ss / (float)dim + n.eps);
+    float yv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) yv[i] = (xv[i] * inv) * v.wv[i];
+    if (blockIdx.x == 0 && ok && n.y) st8(n.y, t, yv);
+    emit_planes8s(yv, lp, 1, kLdsBlk, t >> 2, t & 3, ok);
+}
+
+// This lane's two blocks of planes from the LDS copy norm_to_lds wrote.
+__device__ __forceinline__ void lane_planes_lds(const uint32_t *lp, uint32_t b0, uint32_t b1, bool ok0, bool ok1,
+                                                uint32_t (&P)[2][XP_WORDS], float (&xs)[2]) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const bool ok = c ? ok1 : ok0;
+        const uint32_t *src = lp + (c ? b1 : b0) * kLdsBlk;
+#pragma unroll
+        for (int i = 0; i < XP_WORDS; ++i) P[c][i] = ok ? src[i] : 0u;
+        xs[c] = ok ? __builtin_bit_cast(float, src[XP_WORDS]) : 0.0f;
+    }
+}
+
+// This lane's two blocks of activation planes from `src` (global or LDS,
+// layout of chn_xplanes); blocks without data read block 0 and are zeroed.
+__device__ __forceinline__ void lane_planes(const uint32_t *src, uint32_t nb, uint32_t b0, uint32_t b1, bool ok0,
+                                            bool ok1, uint32_t (&P)[2][XP_WORDS], float (&xs)[2]) {
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
         const bool ok = c ? ok1 : ok0;
         const uint32_t b = c ? b1 : b0;
 #pragma unroll
-        for (int i = 0; i < XP_WORDS; ++i) P[c][i] = a.xp[(size_t)i * nb + b];
-        xs[c] = ((const float *)(a.xp + (size_t)XP_WORDS * nb))[b];
+        for (int i = 0; i < XP_WORDS; ++i) P[c][i] = src[(size_t)i * nb + b];
+        xs[c] = ((const float *)(src + (size_t)XP_WORDS * nb))[b];
 #pragma unroll
         for (int i = 0; i < XP_WORDS; ++i) P[c][i] = ok ? P[c][i] : 0u;
         xs[c] = ok ? xs[c] : 0.0f;
     }
+}
 
-    for (uint32_t rb = blockIdx.x; rb < nrb; rb += gridDim.x) {
-        u32x4r nq[2][2];
-        uint16_t sq[2][2];
-        auto load = [&](uint32_t row) {
-            const RMat *m[2] = {&a.m0, &a.m1};
+// QKV matvec with the step's norm as its prologue (K <= 4096): 16 waves per
+// workgroup, two rows per wave per group as k_q4rmv<RV_QKV, 2, 1>, the first
+// group's weights in flight while the norm runs.
+template <int NORM>
+__global__ __launch_bounds__(1024) void k_q4rmv_qkv_nx(RArgs a, NormArgs n) {
+    constexpr int RPW = 2, NW = 16;
+    const int wave = wave_id(), lane = threadIdx.x & 63;
+    const uint32_t nb = a.nb;
+    const bool ok0 = (uint32_t)lane < nb, ok1 = (uint32_t)(64 + lane) < nb;
+    const uint32_t b0 = ok0 ? lane : 0u, b1 = ok1 ? 64 + lane : 0u;
+    __shared__ uint32_t lp[128 * kLdsBlk];
+    __shared__ float sh[NW];
+
+    const uint32_t ngroups = (a.M + RPW - 1) / RPW;
+    const uint32_t gstride = gridDim.x * NW;
+    u32x4r nq[RPW][2];
+    uint16_t sq[RPW][2];
+    auto load = [&](uint32_t g) {
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                const u32x4r *N = m[s]->N + (size_t)row * nb;
-                const uint16_t *S = m[s]->S + (size_t)row * nb;
-                nq[s][0] = __builtin_nontemporal_load(N + b0);
-                nq[s][1] = __builtin_nontemporal_load(N + b1);
-                sq[s][0] = __builtin_nontemporal_load(S + b0);
-                sq[s][1] = __builtin_nontemporal_load(S + b1);
+        for (int s = 0; s < RPW; ++s) {
+            uint32_t row = g * RPW + s;
+            row = row < a.M ? row : a.M - 1;
+            const u32x4r *N;
+            const uint16_t *S;
+            row_ptrs<RV_QKV>(a, row, 0, N, S);
+            nq[s][0] = __builtin_nontemporal_load(N + b0);
+            nq[s][1] = __builtin_nontemporal_load(N + b1);
+            sq[s][0] = __builtin_nontemporal_load(S + b0);
+            sq[s][1] = __builtin_nontemporal_load(S + b1);
+        }
+    };
+    NormIn nv;
+    norm_load<NORM>(n, nb * 32, nv);
+    uint32_t g = blockIdx.x * NW + wave;
+    if (g < ngroups) load(g);
+    if (n.rope.tab && blockIdx.x == 0) rope_table(n.rope, threadIdx.x, blockDim.x);
+    norm_to_lds<NORM>(n, nb * 32, nv, lp, sh);
+    __syncthreads();
+    uint32_t P[2][XP_WORDS];
+    float xs[2];
+    lane_planes_lds(lp, b0, b1, ok0, ok1, P, xs);
+
+    for (; g < ngroups; g += gstride) {
+        u32x4r cq[RPW][2];
+        uint16_t cs[RPW][2];
+#pragma unroll
+        for (int s = 0; s < RPW; ++s)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                cq[s][c] = nq[s][c];
+                cs[s][c] = sq[s][c];
             }
-        };
-        const uint32_t row0 = rb * 32 + wave;
-        load(row0);
+        if (g + gstride < ngroups) load(g + gstride);
+#pragma unroll
+        for (int s = 0; s < RPW; ++s) {
+            float r = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const int T = block_idot_r(cq[s][c], P[c]);
+                const float sf = (float)__builtin_bit_cast(_Float16, cs[s][c]);
+                r = fmaf((float)T, sf * xs[c], r);
+            }
+            const float tot = wave_sum64(r);
+            const uint32_t row = g * RPW + s;
+            if (lane == 0 && row < a.M) store_r<RV_QKV>(a, row, tot);
+        }
+    }
+}
+
+// Gate/up + GELU-tanh that also emits the digit planes of its output (the
+// down projection's input), so no separate planes pass runs between the two.
+// A workgroup of NW waves owns blocks of 32 consecutive rows; wave w takes
+// rows w, w + NW, ... of a block, one gate/up pair at a time with the next
+// pair (across blocks too) in flight, each row as k_q4rmv<RV_MLP, 1, 1>
+// computes it.  The 32 results meet in LDS; four lanes then quantize the
+// block.  Input planes come from a.xp (NORM < 0) or from the step's norm as
+// the prologue (NORM = NormMode).  Needs K <= 4096 and M % 32 == 0.
+template <int NW, int NORM>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) void k_q4rmv_mlp_xp(
+    RArgs a, uint32_t *__restrict__ xo, NormArgs n) {
+    constexpr int RW = 32 / NW;   // rows per wave per block
+    const int wave = wave_id(), lane = threadIdx.x & 63;
+    const uint32_t nb = a.nb;
+    const bool ok0 = (uint32_t)lane < nb, ok1 = (uint32_t)(64 + lane) < nb;
+    const uint32_t b0 = ok0 ? lane : 0u, b1 = ok1 ? 64 + lane : 0u;
+    __shared__ float sact[32];
+    __shared__ uint32_t lp[NORM >= 0 ? 128 * kLdsBlk : 1];
+    __shared__ float sh[NW];
+    const uint32_t nrb = a.M / 32;
+
+    u32x4r nq[2][2];
+    uint16_t sq[2][2];
+    auto load = [&](uint32_t row) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const u32x4r *N = (s ? a.m1.N : a.m0.N) + (size_t)row * nb;
+            const uint16_t *S = (s ? a.m1.S : a.m0.S) + (size_t)row * nb;
+            nq[s][0] = __builtin_nontemporal_load(N + b0);
+            nq[s][1] = __builtin_nontemporal_load(N + b1);
+            sq[s][0] = __builtin_nontemporal_load(S + b0);
+            sq[s][1] = __builtin_nontemporal_load(S + b1);
+        }
+    };
+    constexpr int NM = NORM < 0 ? 0 : NORM;
+    NormIn nv;
+    if (NORM >= 0) norm_load<NM>(n, nb * 32, nv);
+    uint32_t rb = blockIdx.x;
+    if (rb < nrb) load(rb * 32 + wave);
+
+    // Input planes: in registers (NORM < 0), or read from LDS per block as
+    // they are used (NORM >= 0), which keeps 48 VGPRs free for the norm.
+    uint32_t P[NORM >= 0 ? 1 : 2][XP_WORDS];
+    float xs[2];
+    if (NORM >= 0) {
+        norm_to_lds<NM>(n, nb * 32, nv, lp, sh);
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+            xs[c] = (c ? ok1 : ok0) ? __builtin_bit_cast(float, lp[(c ? b1 : b0) * kLdsBlk + XP_WORDS]) : 0.0f;
+    } else {
+        uint32_t Pr[2][XP_WORDS];
+        lane_planes(a.xp, nb, b0, b1, ok0, ok1, Pr, xs);
+#pragma unroll
+        for (int c = 0; c < (NORM >= 0 ? 1 : 2); ++c)
+#pragma unroll
+            for (int i = 0; i < XP_WORDS; ++i) P[c][i] = Pr[c][i];
+    }
+
+    for (; rb < nrb; rb += gridDim.x) {
 #pragma unroll 1
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < RW; ++j) {
             u32x4r cq[2][2];
             uint16_t cs[2][2];
 #pragma unroll
@@ -280,28 +481,41 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k
                     cq[s][c] = nq[s][c];
                     cs[s][c] = sq[s][c];
                 }
-            if (j < 3) load(row0 + 8 * (j + 1));
+            if (j + 1 < RW) load(rb * 32 + wave + NW * (j + 1));
+            else if (rb + gridDim.x < nrb) load((rb + gridDim.x) * 32 + wave);
+            float rs[2] = {0.0f, 0.0f};
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                uint32_t Pl[XP_WORDS];
+                if (NORM >= 0) {
+                    const uint32_t b = c ? b1 : b0;
+                    const bool ok = c ? ok1 : ok0;
+#pragma unroll
+                    for (int i = 0; i < XP_WORDS; ++i) Pl[i] = ok ? lp[b * kLdsBlk + i] : 0u;
+                }
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    const int T = block_idot_r(cq[s][c], NORM >= 0 ? Pl : P[NORM >= 0 ? 0 : c]);
+                    const float sf = (float)__builtin_bit_cast(_Float16, cs[s][c]);
+                    rs[s] = fmaf((float)T, sf * xs[c], rs[s]);
+                }
+            }
             float tot[2];
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                float r = 0.0f;
-#pragma unroll
-                for (int c = 0; c < 2; ++c) {
-                    const int T = block_idot_r(cq[s][c], P[c]);
-                    const float sf = (float)__builtin_bit_cast(_Float16, cs[s][c]);
-                    r = fmaf((float)T, sf * xs[c], r);
-                }
-                tot[s] = wave_sum64(r);
-            }
-            if (lane == 0) sact[wave + 8 * j] = gelu_tanh(tot[0]) * tot[1];
+            for (int s = 0; s < 2; ++s) tot[s] = wave_sum64(rs[s]);
+            if (lane == 0) sact[wave + NW * j] = gelu_tanh(tot[0]) * tot[1];
         }
         __syncthreads();
-        if (threadIdx.x < 32) a.y0[rb * 32 + threadIdx.x] = sact[threadIdx.x];
-        if (threadIdx.x < 4) {
+        // an opaque copy of the thread index: otherwise the 24 plane-store
+        // addresses are hoisted out of the block loop and spilled
+        uint32_t tx = threadIdx.x;
+        __asm__ volatile("" : "+v"(tx));
+        if (tx < 32) a.y0[rb * 32 + tx] = sact[tx];
+        if (tx < 4) {
             float o[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) o[i] = sact[8 * threadIdx.x + i];
-            emit_planes8(o, xo, nrb, rb, threadIdx.x, true);
+            for (int i = 0; i < 8; ++i) o[i] = sact[8 * tx + i];
+            emit_planes8(o, xo, nrb, rb, tx, true);
         }
         __syncthreads();   // sact is rewritten by the next block
     }
@@ -390,8 +604,43 @@ int mvr_mlp_xp(chn_ctx *ctx, const void *Wg, const void *Wu, const uint32_t *xp_
     const RArgs a{host_rmat(Wg, M, nb), host_rmat(Wu, M, nb), {}, act, nullptr, nullptr, xp_in, M, M, M, nb};
     const uint32_t nrb = M / 32;
     if (!nrb) return CHN_OK;
-    k_q4rmv_mlp_xp<<<nrb < 1024 ? nrb : 1024, 512, 0, ctx->stream>>>(a, xp_out);
+    k_q4rmv_mlp_xp<8, -1><<<nrb < 1024 ? nrb : 1024, 512, 0, ctx->stream>>>(a, xp_out, NormArgs{});
     CHN_LAUNCHED(ctx, "k_q4rmv_mlp_xp");
+    return CHN_OK;
+}
+
+int mvr_mlp_nx(chn_ctx *ctx, const void *Wg, const void *Wu, float *act, uint32_t *xp_out, uint32_t M, uint32_t K,
+               const NormArgs &n, int mode) {
+    const uint32_t nb = K / 32;
+    if (nb > 128 || M % 32 != 0 || nb == 0) return set_err(ctx, CHN_E_UNSUPPORTED, "fused norm gate/up: K=%u M=%u", K, M);
+    const RArgs a{host_rmat(Wg, M, nb), host_rmat(Wu, M, nb), {}, act, nullptr, nullptr, nullptr, M, M, M, nb};
+    const uint32_t nrb = M / 32;
+    if (!nrb) return CHN_OK;
+    // two 8-wave workgroups per CU (128 VGPRs), row blocks dealt evenly; the
+    // 16-wave form spills at this register budget
+    const uint32_t per = (nrb + 511) / 512, grid = (nrb + per - 1) / per;
+    hipStream_t s = ctx->stream;
+    if (mode == NORM_PLAIN) k_q4rmv_mlp_xp<8, NORM_PLAIN><<<grid, 512, 0, s>>>(a, xp_out, n);
+    else if (mode == NORM_ADD) k_q4rmv_mlp_xp<8, NORM_ADD><<<grid, 512, 0, s>>>(a, xp_out, n);
+    else k_q4rmv_mlp_xp<8, NORM_POST_ADD><<<grid, 512, 0, s>>>(a, xp_out, n);
+    CHN_LAUNCHED(ctx, "k_q4rmv_mlp_xp");
+    return CHN_OK;
+}
+
+int mvr_qkv_nx(chn_ctx *ctx, const void *Wq, const void *Wk, const void *Wv, float *q, float *k, float *v,
+               uint32_t q_dim, uint32_t kv_dim, uint32_t K, const NormArgs &n, int mode) {
+    const uint32_t nb = K / 32;
+    if (nb > 128 || nb == 0) return set_err(ctx, CHN_E_UNSUPPORTED, "fused norm QKV: K=%u", K);
+    const uint32_t M = q_dim + 2 * kv_dim;
+    const RArgs a{host_rmat(Wq, q_dim, nb), host_rmat(Wk, kv_dim, nb), host_rmat(Wv, kv_dim, nb), q, k, v, nullptr,
+                  M, q_dim, q_dim + kv_dim, nb};
+    const uint32_t need = ((M + 1) / 2 + 15) / 16;
+    const uint32_t grid = need < 256 ? (need ? need : 1) : 256;
+    hipStream_t s = ctx->stream;
+    if (mode == NORM_PLAIN) k_q4rmv_qkv_nx<NORM_PLAIN><<<grid, 1024, 0, s>>>(a, n);
+    else if (mode == NORM_ADD) k_q4rmv_qkv_nx<NORM_ADD><<<grid, 1024, 0, s>>>(a, n);
+    else k_q4rmv_qkv_nx<NORM_POST_ADD><<<grid, 1024, 0, s>>>(a, n);
+    CHN_LAUNCHED(ctx, "k_q4rmv_qkv_nx");
     return CHN_OK;
 }
 

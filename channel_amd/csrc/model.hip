@@ -37,7 +37,7 @@ struct chn_model {
     uint16_t *embed_bf16 = nullptr;   // device copy of the tied embedding (input gather)
     float *final_norm = nullptr;
     // decode buffers
-    float *x, *normed, *q, *k, *v, *attn, *mlp_out, *act, *logits;
+    float *x, *x2, *normed, *q, *k, *v, *attn, *mlp_out, *act, *logits;
     uint32_t *topk_ids;
     float *topk_vals;
     uint32_t *slots;   // [8192]: global list at 0, sliding list at 4096
@@ -157,6 +157,7 @@ static int alloc_runtime(chn_model *m) {
         M_ALLOC(l.vc, (size_t)kSlotsMax * l.kvd * 4);
     }
     M_ALLOC(m->x, H * 4);
+    M_ALLOC(m->x2, H * 4);
     M_ALLOC(m->normed, H * 4);
     M_ALLOC(m->q, qd * 4);
     M_ALLOC(m->k, kvd * 4);
@@ -264,33 +265,47 @@ static int record_decode(chn_model *m, bool with_logits) {
         rc = (call);             \
         if (rc) return rc;       \
     } while (0)
-    // Each norm kernel also writes the digit planes of its output into
-    // mv_ws, attention writes those of its output and gate/up those of the
-    // activations (into the second plane set), so every matvec reads its
-    // input planes directly.
+    // Six kernels per layer.  The step's norms run as the prologue of the
+    // matvec that consumes them (every workgroup recomputes the norm into
+    // LDS; workgroup 0 writes the new residual stream, alternating between
+    // x and x2 so no workgroup reads a half-written one): QKV takes the
+    // previous layer's FFN residual and this layer's input norm, gate/up
+    // the attention residual and the pre-FFN norm.  Attention writes the
+    // planes of its output for o_proj (mv_ws) and gate/up those of the
+    // activations for down (the second plane set).
     uint32_t *xp = m->mv_ws, *xp_act = m->mv_ws + m->mv_ws_words;
+    float *xa = m->x, *xb = m->x2;
+    const RopeTab no_rope{nullptr, nullptr, {0.0f, 0.0f}, {0u, 0u}};
     for (uint32_t i = 0; i < c.num_layers; ++i) {
         const auto &l = m->L[i];
+        NormArgs n1{xa, nullptr, nullptr, l.in_norm, xb, m->normed, eps, 1.0f, no_rope};
+        int mode1 = NORM_PLAIN;
         if (i == 0) {
             // the step's first kernel also writes its RoPE table
-            const RopeTab rt{m->step, m->rope_tab, {c.rope_theta, c.rope_theta_full},
-                             {head_shape(c, false).rot, head_shape(c, true).rot}};
-            R_(launch_norm_planes(s, m->x, nullptr, nullptr, l.in_norm, m->normed, xp, H, eps, 1.0f, false, &rt));
+            n1.rope = RopeTab{m->step, m->rope_tab, {c.rope_theta, c.rope_theta_full},
+                              {head_shape(c, false).rot, head_shape(c, true).rot}};
+        } else {
+            const auto &p = m->L[i - 1];
+            n1.r = m->mlp_out;
+            n1.pw = p.has_post_ffn ? p.post_ffn : nullptr;
+            n1.scalar = p.scalar;
+            mode1 = p.has_post_ffn ? NORM_POST_ADD : NORM_ADD;
         }
-        R_(mvr_qkv(ctx, l.Wq, l.Wk, l.Wv, m->normed, m->q, m->k, m->v, l.qd, l.kvd, H, xp, true));
+        R_(mvr_qkv_nx(ctx, l.Wq, l.Wk, l.Wv, m->q, m->k, m->v, l.qd, l.kvd, H, n1, mode1));
         R_(launch_rope_decode_attn(ctx, m->q, m->k, m->v, l.q_norm, l.k_norm, l.kc, l.vc, m->step,
                                    m->slots + (l.full ? 0 : kSlotsMax), m->step + (l.full ? 2 : 3), kSlotsMax, nq, l.D,
                                    l.kvd, l.gqa, l.rot, (int)c.k_eq_v, m->rope_tab + (l.full ? kRopePairs : 0), eps,
                                    1.0f, m->attn, m->attn_ws, xp));
         R_(mvr_gemv(ctx, l.Wo, m->attn, m->mlp_out, H, l.qd, xp, true));
-        R_(launch_norm_planes(s, m->x, m->mlp_out, l.has_post_attn ? l.post_attn : nullptr, l.pre_ffn, m->normed, xp,
-                              H, eps, 1.0f, true));
-        R_(mvr_mlp_xp(ctx, l.Wg, l.Wu, xp, m->act, xp_act, I, H));
+        const NormArgs n2{xb, m->mlp_out, l.has_post_attn ? l.post_attn : nullptr, l.pre_ffn, xa, m->normed,
+                          eps, 1.0f, no_rope};
+        R_(mvr_mlp_nx(ctx, l.Wg, l.Wu, m->act, xp_act, I, H, n2, l.has_post_attn ? NORM_POST_ADD : NORM_ADD));
         R_(mvr_gemv(ctx, l.Wd, m->act, m->mlp_out, H, I, xp_act, true));
-        const float *next_norm = (i + 1 < c.num_layers) ? m->L[i + 1].in_norm : m->final_norm;
-        R_(launch_norm_planes(s, m->x, m->mlp_out, l.has_post_ffn ? l.post_ffn : nullptr, next_norm, m->normed, xp, H,
-                              eps, l.scalar, true));
     }
+    // the last layer's FFN residual (into x) and the final norm
+    const auto &last = m->L[c.num_layers - 1];
+    R_(launch_norm_planes(s, xa, m->mlp_out, last.has_post_ffn ? last.post_ffn : nullptr, m->final_norm, m->normed,
+                          xp, H, eps, last.scalar, true));
     if (with_logits) {
         R_(launch_gemv_q8(s, m->embed_q8, m->normed, m->logits, c.vocab_size, H / 32, m->mv_ws));
         R_(launch_topk64(s, m->logits, c.vocab_size, m->topk_ids, m->topk_vals, m->topk_ws));

@@ -96,20 +96,7 @@ __global__ __launch_bounds__(1024) void k_norm_planes(float *__restrict__ x, con
                                                       float eps, float scalar, RopeTab rt) {
     __shared__ float sh[16];
     const uint32_t t = threadIdx.x;
-    if (rt.tab) {
-        const uint32_t clock = rt.step[0];
-        for (uint32_t i = t; i < 2 * kRopePairs; i += blockDim.x) {
-            const uint32_t kind = i / kRopePairs, d = i % kRopePairs, rot = rt.rot[kind];
-            if (d < rot / 2) {
-                const float fe = (2.0f * (float)d) / (float)rot;
-                const float freq = 1.0f / powf(rt.theta[kind], fe);
-                const float ang = (float)clock * freq;
-                float sn, cs;
-                sincosf(ang, &sn, &cs);
-                rt.tab[i] = float2{cs, sn};
-            }
-        }
-    }
+    if (rt.tab) rope_table(rt, t, blockDim.x);
     const bool ok = 8 * t < dim;
     // every load is issued before the first reduction
     float xv[8], rv[8], pv[8], wv[8];
