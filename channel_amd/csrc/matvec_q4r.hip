@@ -484,21 +484,32 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
             if (j + 1 < RW) load(rb * 32 + wave + NW * (j + 1));
             else if (rb + gridDim.x < nrb) load((rb + gridDim.x) * 32 + wave);
             float rs[2] = {0.0f, 0.0f};
+            if (NORM >= 0) {
+                // block by block: each block's planes read once from LDS for
+                // both matrices
 #pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                uint32_t Pl[XP_WORDS];
-                if (NORM >= 0) {
+                for (int c = 0; c < 2; ++c) {
+                    uint32_t Pl[XP_WORDS];
                     const uint32_t b = c ? b1 : b0;
                     const bool ok = c ? ok1 : ok0;
 #pragma unroll
                     for (int i = 0; i < XP_WORDS; ++i) Pl[i] = ok ? lp[b * kLdsBlk + i] : 0u;
-                }
 #pragma unroll
-                for (int s = 0; s < 2; ++s) {
-                    const int T = block_idot_r(cq[s][c], NORM >= 0 ? Pl : P[NORM >= 0 ? 0 : c]);
-                    const float sf = (float)__builtin_bit_cast(_Float16, cs[s][c]);
-                    rs[s] = fmaf((float)T, sf * xs[c], rs[s]);
+                    for (int s = 0; s < 2; ++s) {
+                        const int T = block_idot_r(cq[s][c], Pl);
+                        const float sf = (float)__builtin_bit_cast(_Float16, cs[s][c]);
+                        rs[s] = fmaf((float)T, sf * xs[c], rs[s]);
+                    }
                 }
+            } else {
+#pragma unroll
+                for (int s = 0; s < 2; ++s)
+#pragma unroll
+                    for (int c = 0; c < 2; ++c) {
+                        const int T = block_idot_r(cq[s][c], P[NORM >= 0 ? 0 : c]);
+                        const float sf = (float)__builtin_bit_cast(_Float16, cs[s][c]);
+                        rs[s] = fmaf((float)T, sf * xs[c], rs[s]);
+                    }
             }
             float tot[2];
 #pragma unroll
