@@ -45,6 +45,7 @@ int launch_q4_repack(hipStream_t s, const uint32_t *W, uint32_t rows, uint32_t K
 }
 
 enum RMode { RV_GEMV = 0, RV_QKV = 1, RV_MLP = 2 };
+constexpr uint32_t kRedIters = 8;   // row groups per workgroup at most, when waves split K
 
 struct RMat {
     const u32x4r *N;
@@ -129,7 +130,10 @@ __global__ __launch_bounds__(256) void k_q4rmv(RArgs a) {
     // blocks without data read block 0 of the row (always valid) and are
     // zeroed through their planes
     const uint32_t b0 = ok0 ? kb0 + lane : 0u, b1 = ok1 ? kb0 + 64 + lane : 0u;
-    __shared__ float red[4][V];
+    // waves that split K park each row group's partial sums here and meet
+    // once, after the loop (at most kRedIters row groups per workgroup)
+    __shared__ float red[4][WPR > 1 ? kRedIters * V : 1];
+    uint32_t it = 0;
 
     const uint32_t ngroups = (a.M + RPW - 1) / RPW;
     const uint32_t gstride = gridDim.x * G;
@@ -206,23 +210,28 @@ __global__ __launch_bounds__(256) void k_q4rmv(RArgs a) {
         } else {
             if (lane == 0) {
 #pragma unroll
-                for (int s = 0; s < V; ++s) red[wave][s] = tot[s];
+                for (int s = 0; s < V; ++s) red[wave][it * V + s] = tot[s];
             }
-            __syncthreads();
-            if (part == 0 && gv && lane < RPW) {
-                float t0 = 0.0f, t1 = 0.0f;
+            ++it;
+        }
+    }
+    if (WPR > 1) {
+        // partial sums of the workgroup's row groups, parts in a fixed order
+        __syncthreads();
+        const uint32_t j = lane / RPW, r = lane % RPW;   // row group j, row r of it
+        const uint32_t gj = blockIdx.x * G + grp + j * gstride;
+        if (part == 0 && j < it && gj < ngroups) {
+            float t0 = 0.0f, t1 = 0.0f;
 #pragma unroll
-                for (int w = 0; w < WPR; ++w) {
-                    t0 += red[grp * WPR + w][lane * NMAT];
-                    if (NMAT == 2) t1 += red[grp * WPR + w][lane * 2 + 1];
-                }
-                const uint32_t row = g * RPW + lane;
-                if (row < a.M) {
-                    if (NMAT == 1) store_r<MODE>(a, row, t0);
-                    else a.y0[row] = gelu_tanh(t0) * t1;
-                }
+            for (int w = 0; w < WPR; ++w) {
+                t0 += red[grp * WPR + w][j * V + r * NMAT];
+                if (NMAT == 2) t1 += red[grp * WPR + w][j * V + r * 2 + 1];
             }
-            __syncthreads();
+            const uint32_t row = gj * RPW + r;
+            if (row < a.M) {
+                if (NMAT == 1) store_r<MODE>(a, row, t0);
+                else a.y0[row] = gelu_tanh(t0) * t1;
+            }
         }
     }
 }
@@ -532,12 +541,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     }
 }
 
-// Launch shape (from a sweep on MI355X at the 12B decode shapes with weights
-// cold in HBM): the fewest waves splitting K such that each covers <= 128
-// blocks; one gate/up row pair or two rows per wave; one row group per wave
-// up to 1024 workgroups (768 when waves split K), looping beyond that.
-// Fewer, longer-lived waves lose: at 8192 x 3840 a 341-workgroup launch
-// takes 10.5 us against 7.3 us at 1024.
+// Launch shape (from sweeps on MI355X at the 12B decode shapes with weights
+// cold in HBM, graph replay): the fewest waves splitting K such that each
+// covers <= 128 blocks; one gate/up row pair or two rows per wave.  Without
+// a K split, one row group per wave up to 1024 workgroups (at 8192 x 3840 a
+// 341-workgroup launch takes 10.5 us against 7.3 us at 1024), two per wave
+// for small matrices (o_proj 3840 x 4096: 4.28 us at 240 against 4.41 at
+// 480); with a K split, four row groups per workgroup.
 template <int MODE, int WPR>
 static void launch_rw(const RArgs &a, int rpw, uint32_t grid, hipStream_t s) {
     if (rpw == 1) k_q4rmv<MODE, 1, WPR><<<grid, 256, 0, s>>>(a);
@@ -554,9 +564,19 @@ static int launch_q4rmv(chn_ctx *ctx, int mode, RArgs a, const float *x, uint32_
     const int rpw = mode == RV_MLP ? 1 : 2;
     const uint32_t G = 4 / wpr;
     const uint32_t ngroups = (a.M + rpw - 1) / rpw;
-    const uint32_t cap = wpr == 1 ? 1024u : 768u;
-    const uint32_t need = (ngroups + G - 1) / G;
-    const uint32_t grid = need < cap ? need : cap;
+    const uint32_t need = (ngroups + G - 1) / G;      // workgroups at one row group per wave
+    uint32_t grid;
+    if (wpr == 1) {
+        // one group per wave up to 1024 workgroups; small matrices two per wave
+        grid = need <= 512 ? (need + 1) / 2 : (need < 1024 ? need : 1024);
+    } else {
+        // waves splitting K: four row groups per workgroup (down at 12B:
+        // 9.4 us against 9.7 at 2.5 groups), never more than kRedIters
+        grid = (need + 3) / 4;
+        const uint32_t lo = (need + kRedIters - 1) / kRedIters;
+        if (grid < lo) grid = lo;
+    }
+    if (!grid) grid = 1;
     hipStream_t s = ctx->stream;
     switch (mode) {
     case RV_GEMV:
