@@ -453,21 +453,44 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
     }
 }
 
+// Running softmax state (max, denominator, sum of p * V) and the merge of
+// two states: rescale both to the larger max.
+struct SoftState {
+    float m, l;
+    f4 t;
+};
+__device__ __forceinline__ SoftState soft_merge(const SoftState &x, const SoftState &y) {
+    const float mn = fmaxf(x.m, y.m);
+    const float a = expf(x.m - mn), b = expf(y.m - mn);
+    return SoftState{mn, x.l * a + y.l * b, x.t * a + y.t * b};
+}
+__device__ __forceinline__ SoftState shfl_xor_state(const SoftState &x, int m) {
+    SoftState y;
+    y.m = __shfl_xor(x.m, m, 64);
+    y.l = __shfl_xor(x.l, m, 64);
+    y.t.x = __shfl_xor(x.t.x, m, 64);
+    y.t.y = __shfl_xor(x.t.y, m, 64);
+    y.t.z = __shfl_xor(x.t.z, m, 64);
+    y.t.w = __shfl_xor(x.t.w, m, 64);
+    return y;
+}
+
 // Merge of the split partials.  Every split leaves a partial, empty (sum 0)
 // when it had no entries, so the merge needs no slot count.  Workgroup
 // (column block, query head) owns 64 output values (16 float4 columns);
 // thread (j, col), j = tid / 16, merges splits j, j + 16, ... online
-// (running max, rescaled sums) with all of its loads issued at once, then
-// the 16 running states meet in LDS in a fixed order.  Writes the output
-// and, for the o_proj matvec, its digit planes.  S = 0 gives a zero row.
-template <int DV>
+// (running max, rescaled sums) with all of its loads issued at once (U per
+// batch).  The 16 running states of a column then meet in a fixed tree:
+// lanes 16 and 32 apart inside each wave by shuffles, then the four waves
+// in LDS.  Writes the output and, for the o_proj matvec, its digit planes.
+// S = 0 gives a zero row.
+template <int DV, int U>
 __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ ws, uint32_t nsplit,
                                                     uint32_t num_q_heads, float *__restrict__ out,
                                                     uint32_t *__restrict__ xp, uint32_t xp_nb) {
     constexpr int D = DV * 256;
-    constexpr int U = 8;                 // splits per thread per batch of loads
-    __shared__ f4 st_t[16][16];
-    __shared__ float st_m[16][16], st_l[16][16];
+    __shared__ f4 st_t[4][16];
+    __shared__ float st_m[4][16], st_l[4][16];
     __shared__ float res[64];
     const uint32_t cb = blockIdx.x, qh = blockIdx.y;
     const int j0 = threadIdx.x >> 4, col = threadIdx.x & 15;
@@ -500,24 +523,23 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ ws
             m = mn;
         }
     }
-    st_t[j0][col] = t;
-    st_m[j0][col] = m;
-    st_l[j0][col] = l;
+    SoftState st{m, l, t};
+    st = soft_merge(st, shfl_xor_state(st, 16));
+    st = soft_merge(st, shfl_xor_state(st, 32));
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) < 16) {
+        st_t[wave][col] = st.t;
+        st_m[wave][col] = st.m;
+        st_l[wave][col] = st.l;
+    }
     __syncthreads();
     if (threadIdx.x < 16) {
         const int cc = threadIdx.x;
-        float M = kNegBig;
+        SoftState w[4];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) M = fmaxf(M, st_m[j][cc]);
-        f4 T = f4{0, 0, 0, 0};
-        float Lt = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const float e = expf(st_m[j][cc] - M);
-            T += e * st_t[j][cc];
-            Lt += e * st_l[j][cc];
-        }
-        T *= 1.0f / (Lt + 1e-9f);
+        for (int i = 0; i < 4; ++i) w[i] = SoftState{st_m[i][cc], st_l[i][cc], st_t[i][cc]};
+        const SoftState f = soft_merge(soft_merge(w[0], w[1]), soft_merge(w[2], w[3]));
+        const f4 T = f.t * (1.0f / (f.l + 1e-9f));
         *(f4 *)(out + (size_t)qh * D + cb * 64 + 4 * cc) = T;
         res[4 * cc + 0] = T.x; res[4 * cc + 1] = T.y; res[4 * cc + 2] = T.z; res[4 * cc + 3] = T.w;
     }
@@ -610,9 +632,9 @@ static int launch_decode_impl(chn_ctx *ctx, const float *q, float *kc, float *vc
     CHN_LAUNCHED(ctx, "k_attn_decode");
     const dim3 mgrid(head_dim / 64, num_q_heads);
     if (head_dim == 256)
-        k_attn_merge<1><<<mgrid, 256, 0, s>>>(ws, nsplit, num_q_heads, out, xp, xp_nb);
+        k_attn_merge<1, kDecGrid / 16><<<mgrid, 256, 0, s>>>(ws, nsplit, num_q_heads, out, xp, xp_nb);
     else
-        k_attn_merge<2><<<mgrid, 256, 0, s>>>(ws, nsplit, num_q_heads, out, xp, xp_nb);
+        k_attn_merge<2, kDecGrid / 16><<<mgrid, 256, 0, s>>>(ws, nsplit, num_q_heads, out, xp, xp_nb);
     CHN_LAUNCHED(ctx, "k_attn_merge");
     return CHN_OK;
 }

@@ -253,16 +253,16 @@ __device__ __forceinline__ void st8(float *p, uint32_t t, const float (&v)[8]) {
     *(f32x4r *)(p + 8 * (size_t)t) = f32x4r{v[0], v[1], v[2], v[3]};
     *(f32x4r *)(p + 8 * (size_t)t + 4) = f32x4r{v[4], v[5], v[6], v[7]};
 }
-// Sum over the workgroup: wave sums, then the wave partials in index order.
+// Sum over the workgroup: DPP wave sums, then the wave partials in index
+// order.  One barrier: each call takes its own 16-float slice of LDS, so
+// no later write can overtake a read of it.
 __device__ __forceinline__ float wg_sum(float v, float *sh) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    v = wave_sum64(v);
     const int nw = blockDim.x >> 6;
     if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
     __syncthreads();
     float t = 0.0f;
     for (int i = 0; i < nw; ++i) t += sh[i];
-    __syncthreads();
     return t;
 }
 
@@ -299,7 +299,7 @@ __device__ __forceinline__ void norm_to_lds(const NormArgs &n, uint32_t dim, Nor
             float ss = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) ss += v.rv[i] * v.rv[i];
-            ss = wg_sum(ss, sh);
+            ss = wg_sum(ss, sh + 16);
             const float inv = 1.0f / sqrtf(ss / (float)dim + n.eps);
 #pragma unroll
             for (int i = 0; i < 8; ++i) v.rv[i] = (v.rv[i] * inv) * v.pv[i];
@@ -361,7 +361,7 @@ __global__ __launch_bounds__(1024) void k_q4rmv_qkv_nx(RArgs a, NormArgs n) {
     const bool ok0 = (uint32_t)lane < nb, ok1 = (uint32_t)(64 + lane) < nb;
     const uint32_t b0 = ok0 ? lane : 0u, b1 = ok1 ? 64 + lane : 0u;
     __shared__ uint32_t lp[128 * kLdsBlk];
-    __shared__ float sh[NW];
+    __shared__ float sh[32];
 
     const uint32_t ngroups = (a.M + RPW - 1) / RPW;
     const uint32_t gstride = gridDim.x * NW;
@@ -437,7 +437,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     const uint32_t b0 = ok0 ? lane : 0u, b1 = ok1 ? 64 + lane : 0u;
     __shared__ float sact[32];
     __shared__ uint32_t lp[NORM >= 0 ? 128 * kLdsBlk : 1];
-    __shared__ float sh[NW];
+    __shared__ float sh[32];
     const uint32_t nrb = a.M / 32;
 
     u32x4r nq[2][2];
