@@ -318,8 +318,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
                 float ss = 0.0f;
 #pragma unroll
                 for (int d = 0; d < DPL; ++d) ss += raw[j][d] * raw[j][d];
-#pragma unroll
-                for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+                ss = wave_sum64(ss);
                 const float inv = 1.0f / sqrtf(ss / (float)D + ra.eps);
                 float *dst = it < GQA ? sh_q[it] : (it == GQA ? sh_k : sh_v);
 #pragma unroll
@@ -387,13 +386,11 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
                 d = fmaf(q[h][f].w, kr[b][f].w, d);
             }
             const float sc = ok[b] ? row16_sum(d) * scale : kNegBig;
-            float mx = fmaxf(sc, __shfl_xor(sc, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float mx = rows4_max(sc);
             const float Mn = fmaxf(M[h], mx);
             const float rs = expf(M[h] - Mn);
             const float p = ok[b] ? expf(sc - Mn) : 0.0f;
-            float psum = p + __shfl_xor(p, 16, 64);
-            psum += __shfl_xor(psum, 32, 64);
+            const float psum = rows4_sum(p);
 #pragma unroll
             for (int f = 0; f < NF; ++f) acc[h][f] = acc[h][f] * rs + p * vr[b][f];
             L[h] = L[h] * rs + psum;
@@ -414,11 +411,8 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
     for (int h = 0; h < GQA; ++h)
 #pragma unroll
         for (int f = 0; f < NF; ++f) {
-            f4 t = acc[h][f];
-            t.x += __shfl_xor(t.x, 16, 64); t.y += __shfl_xor(t.y, 16, 64);
-            t.z += __shfl_xor(t.z, 16, 64); t.w += __shfl_xor(t.w, 16, 64);
-            t.x += __shfl_xor(t.x, 32, 64); t.y += __shfl_xor(t.y, 32, 64);
-            t.z += __shfl_xor(t.z, 32, 64); t.w += __shfl_xor(t.w, 32, 64);
+            const f4 t = f4{rows4_sum(acc[h][f].x), rows4_sum(acc[h][f].y), rows4_sum(acc[h][f].z),
+                            rows4_sum(acc[h][f].w)};
             if (r == 0) sh_acc[wave][h][c * NF + f] = t;
         }
     if (lane < GQA) {
@@ -464,15 +458,14 @@ __device__ __forceinline__ SoftState soft_merge(const SoftState &x, const SoftSt
     const float a = expf(x.m - mn), b = expf(y.m - mn);
     return SoftState{mn, x.l * a + y.l * b, x.t * a + y.t * b};
 }
-__device__ __forceinline__ SoftState shfl_xor_state(const SoftState &x, int m) {
-    SoftState y;
-    y.m = __shfl_xor(x.m, m, 64);
-    y.l = __shfl_xor(x.l, m, 64);
-    y.t.x = __shfl_xor(x.t.x, m, 64);
-    y.t.y = __shfl_xor(x.t.y, m, 64);
-    y.t.z = __shfl_xor(x.t.z, m, 64);
-    y.t.w = __shfl_xor(x.t.w, m, 64);
-    return y;
+template <int M>
+__device__ __forceinline__ float xor_lane(float v) {
+    return M == 16 ? xor16_lane(v) : xor32_lane(v);
+}
+template <int M>
+__device__ __forceinline__ SoftState xor_state(const SoftState &x) {
+    return SoftState{xor_lane<M>(x.m), xor_lane<M>(x.l),
+                     f4{xor_lane<M>(x.t.x), xor_lane<M>(x.t.y), xor_lane<M>(x.t.z), xor_lane<M>(x.t.w)}};
 }
 
 // Merge of the split partials.  Every split leaves a partial, empty (sum 0)
@@ -524,8 +517,8 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ ws
         }
     }
     SoftState st{m, l, t};
-    st = soft_merge(st, shfl_xor_state(st, 16));
-    st = soft_merge(st, shfl_xor_state(st, 32));
+    st = soft_merge(st, xor_state<16>(st));
+    st = soft_merge(st, xor_state<32>(st));
     const int wave = threadIdx.x >> 6;
     if ((threadIdx.x & 63) < 16) {
         st_t[wave][col] = st.t;

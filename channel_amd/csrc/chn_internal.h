@@ -282,6 +282,32 @@ __device__ __forceinline__ float wave_max64(float v) {
                        __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48))));
 }
 
+// Exchanges across the four 16-lane rows of a wave on gfx950's lane-swap
+// instructions (VALU, no LDS crossbar).  permlane16_swap(v, v) returns
+// {rows (0,0,2,2), rows (1,1,3,3)} of v, permlane32_swap(v, v) returns
+// {halves (0,0), halves (1,1)}: the partner value of lane ^ 16 (^ 32) is
+// the element of the other row (half).
+__device__ __forceinline__ float xor16_lane(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                    false, false);
+    return __builtin_bit_cast(float, ((threadIdx.x >> 4) & 1) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float xor32_lane(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                    false, false);
+    return __builtin_bit_cast(float, ((threadIdx.x >> 5) & 1) ? r[0] : r[1]);
+}
+// Sum / max over lanes l, l ^ 16, l ^ 32, l ^ 48 (same position in the four
+// rows), ((r0 op r1) op (r2 op r3)) in every lane.
+__device__ __forceinline__ float rows4_sum(float v) {
+    v += xor16_lane(v);
+    return v + xor32_lane(v);
+}
+__device__ __forceinline__ float rows4_max(float v) {
+    v = fmaxf(v, xor16_lane(v));
+    return fmaxf(v, xor32_lane(v));
+}
+
 // Digit planes of one 32-block from the four lanes 4k..4k+3 of a wave that
 // hold its words w = lane & 3 (eight consecutive values each).  All four
 // lanes must call (with zeros where ok is false); only ok lanes store.

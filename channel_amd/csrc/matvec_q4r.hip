@@ -459,23 +459,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     uint32_t rb = blockIdx.x;
     if (rb < nrb) load(rb * 32 + wave);
 
-    // Input planes: in registers (NORM < 0), or read from LDS per block as
-    // they are used (NORM >= 0), which keeps 48 VGPRs free for the norm.
-    uint32_t P[NORM >= 0 ? 1 : 2][XP_WORDS];
+    // this lane's two blocks of input planes, in registers
+    uint32_t P[2][XP_WORDS];
     float xs[2];
     if (NORM >= 0) {
         norm_to_lds<NM>(n, nb * 32, nv, lp, sh);
         __syncthreads();
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-            xs[c] = (c ? ok1 : ok0) ? __builtin_bit_cast(float, lp[(c ? b1 : b0) * kLdsBlk + XP_WORDS]) : 0.0f;
+        lane_planes_lds(lp, b0, b1, ok0, ok1, P, xs);
     } else {
-        uint32_t Pr[2][XP_WORDS];
-        lane_planes(a.xp, nb, b0, b1, ok0, ok1, Pr, xs);
-#pragma unroll
-        for (int c = 0; c < (NORM >= 0 ? 1 : 2); ++c)
-#pragma unroll
-            for (int i = 0; i < XP_WORDS; ++i) P[c][i] = Pr[c][i];
+        lane_planes(a.xp, nb, b0, b1, ok0, ok1, P, xs);
     }
 
     for (; rb < nrb; rb += gridDim.x) {
@@ -493,33 +485,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
             if (j + 1 < RW) load(rb * 32 + wave + NW * (j + 1));
             else if (rb + gridDim.x < nrb) load((rb + gridDim.x) * 32 + wave);
             float rs[2] = {0.0f, 0.0f};
-            if (NORM >= 0) {
-                // block by block: each block's planes read once from LDS for
-                // both matrices
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
 #pragma unroll
                 for (int c = 0; c < 2; ++c) {
-                    uint32_t Pl[XP_WORDS];
-                    const uint32_t b = c ? b1 : b0;
-                    const bool ok = c ? ok1 : ok0;
-#pragma unroll
-                    for (int i = 0; i < XP_WORDS; ++i) Pl[i] = ok ? lp[b * kLdsBlk + i] : 0u;
-#pragma unroll
-                    for (int s = 0; s < 2; ++s) {
-                        const int T = block_idot_r(cq[s][c], Pl);
-                        const float sf = (float)__builtin_bit_cast(_Float16, cs[s][c]);
-                        rs[s] = fmaf((float)T, sf * xs[c], rs[s]);
-                    }
+                    const int T = block_idot_r(cq[s][c], P[c]);
+                    const float sf = (float)__builtin_bit_cast(_Float16, cs[s][c]);
+                    rs[s] = fmaf((float)T, sf * xs[c], rs[s]);
                 }
-            } else {
-#pragma unroll
-                for (int s = 0; s < 2; ++s)
-#pragma unroll
-                    for (int c = 0; c < 2; ++c) {
-                        const int T = block_idot_r(cq[s][c], P[NORM >= 0 ? 0 : c]);
-                        const float sf = (float)__builtin_bit_cast(_Float16, cs[s][c]);
-                        rs[s] = fmaf((float)T, sf * xs[c], rs[s]);
-                    }
-            }
             float tot[2];
 #pragma unroll
             for (int s = 0; s < 2; ++s) tot[s] = wave_sum64(rs[s]);
