@@ -112,8 +112,12 @@ constexpr int kMaxBlocksPerWave = 128;          // two 64-block passes
 constexpr int kSegWords = kMaxBlocksPerWave * 5; // LDS words per stream
 
 // RPW rows (x NMAT matrices) per wave and row group; WPR waves split K.
-template <int MODE, int RPW, int WPR>
-__global__ __launch_bounds__(256) void k_q4mv(MatvecArgs a) {
+// XIN (WPR == 1, K <= 4096): the workgroup converts x to digit planes in LDS
+// itself (the same planes as k_xplanes), so the call is one launch; x's
+// loads are issued before the first weights, the conversion runs while
+// those are in flight.
+template <int MODE, int RPW, int WPR, bool XIN>
+__global__ __launch_bounds__(256) void k_q4mv(MatvecArgs a, const float *__restrict__ x) {
     constexpr int NMAT = (MODE == MV_MLP) ? 2 : 1;
     constexpr int V = RPW * NMAT;
     constexpr int G = 4 / WPR;
@@ -134,19 +138,26 @@ __global__ __launch_bounds__(256) void k_q4mv(MatvecArgs a) {
 
     __shared__ uint32_t seg[4][V * kSegWords];
     __shared__ float red[4][V];
+    constexpr int kPl = XP_WORDS + 1;             // LDS words per block of planes
+    __shared__ uint32_t lpl[XIN ? 128 * kPl : 1];
     uint32_t *L = seg[wave];
 
-    // this lane's two blocks of activation planes
-    uint32_t P[2][XP_WORDS];
-    float xs[2];
+    // XIN: x's values, four threads per 32-block (eight values each), two passes
+    float xv[XIN ? 2 : 1][8];
+    if (XIN) {
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-        const uint32_t bl = c * 64 + lane;
-        const bool ok = bl < nblk;
-        const uint32_t b = kb0 + bl;
+        for (int ps = 0; ps < 2; ++ps) {
+            const uint32_t b = ps * 64 + (threadIdx.x >> 2), w = threadIdx.x & 3;
+            if (b < nb) {
+                const float4 t0 = *(const float4 *)(x + (size_t)b * 32 + w * 8);
+                const float4 t1 = *(const float4 *)(x + (size_t)b * 32 + w * 8 + 4);
+                xv[ps][0] = t0.x; xv[ps][1] = t0.y; xv[ps][2] = t0.z; xv[ps][3] = t0.w;
+                xv[ps][4] = t1.x; xv[ps][5] = t1.y; xv[ps][6] = t1.z; xv[ps][7] = t1.w;
+            } else {
 #pragma unroll
-        for (int i = 0; i < XP_WORDS; ++i) P[c][i] = ok ? a.xp[(size_t)i * nb + b] : 0u;
-        xs[c] = ok ? ((const float *)(a.xp + (size_t)XP_WORDS * nb))[b] : 0.0f;
+                for (int i = 0; i < 8; ++i) xv[ps][i] = 0.0f;
+            }
+        }
     }
 
     const uint32_t ngroups = (a.M + RPW - 1) / RPW;
@@ -169,6 +180,38 @@ __global__ __launch_bounds__(256) void k_q4mv(MatvecArgs a) {
 
     uint32_t g = blockIdx.x * G + grp;
     if (g < ngroups) load(g);
+
+    // this lane's two blocks of activation planes
+    uint32_t P[2][XP_WORDS];
+    float xs[2];
+    if (XIN) {
+#pragma unroll
+        for (int ps = 0; ps < 2; ++ps) {
+            const uint32_t b = ps * 64 + (threadIdx.x >> 2);
+            emit_planes8s(xv[ps], lpl, 1, kPl, b, threadIdx.x & 3, b < nb);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const uint32_t bl = c * 64 + lane;
+            const bool ok = bl < nblk;
+            const uint32_t *src = lpl + (ok ? bl : 0u) * kPl;
+#pragma unroll
+            for (int i = 0; i < XP_WORDS; ++i) P[c][i] = ok ? src[i] : 0u;
+            xs[c] = ok ? __builtin_bit_cast(float, src[XP_WORDS]) : 0.0f;
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const uint32_t bl = c * 64 + lane;
+            const bool ok = bl < nblk;
+            const uint32_t b = kb0 + bl;
+#pragma unroll
+            for (int i = 0; i < XP_WORDS; ++i) P[c][i] = ok ? a.xp[(size_t)i * nb + b] : 0u;
+            xs[c] = ok ? ((const float *)(a.xp + (size_t)XP_WORDS * nb))[b] : 0.0f;
+        }
+    }
+
     for (uint32_t gb = blockIdx.x * G; gb < ngroups; gb += gstride, g += gstride) {
         const bool gv = g < ngroups;
         if (gv) {
@@ -259,25 +302,28 @@ static MvShape pick_shape(int mode, uint32_t M, uint32_t nb) {
     return s;
 }
 
-template <int MODE, int WPR>
-static bool launch_wpr(int rpw, const MatvecArgs &a, uint32_t grid, hipStream_t st) {
+template <int MODE, int WPR, bool XIN>
+static bool launch_wpr(int rpw, const MatvecArgs &a, const float *x, uint32_t grid, hipStream_t st) {
     constexpr int NMAT = MODE == MV_MLP ? 2 : 1;
     switch (rpw) {
-    case 1: k_q4mv<MODE, 1, WPR><<<grid, 256, 0, st>>>(a); return true;
-    case 2: k_q4mv<MODE, 2, WPR><<<grid, 256, 0, st>>>(a); return true;
+    case 1: k_q4mv<MODE, 1, WPR, XIN><<<grid, 256, 0, st>>>(a, x); return true;
+    case 2: k_q4mv<MODE, 2, WPR, XIN><<<grid, 256, 0, st>>>(a, x); return true;
     case 4:
-        if constexpr (4 * NMAT <= 8) { k_q4mv<MODE, 4, WPR><<<grid, 256, 0, st>>>(a); return true; }
+        if constexpr (4 * NMAT <= 8) { k_q4mv<MODE, 4, WPR, XIN><<<grid, 256, 0, st>>>(a, x); return true; }
         return false;
     }
     return false;
 }
 
+// x != NULL: planes computed in the kernel (one wave per row: nb <= 128);
+// otherwise a.xp holds them.
 template <int MODE>
-static bool launch_mode(const MvShape &s, const MatvecArgs &a, hipStream_t st) {
+static bool launch_mode(const MvShape &s, const MatvecArgs &a, const float *x, hipStream_t st) {
+    if (x) return s.wpr == 1 && launch_wpr<MODE, 1, true>(s.rpw, a, x, s.grid, st);
     switch (s.wpr) {
-    case 1: return launch_wpr<MODE, 1>(s.rpw, a, s.grid, st);
-    case 2: return launch_wpr<MODE, 2>(s.rpw, a, s.grid, st);
-    case 4: return launch_wpr<MODE, 4>(s.rpw, a, s.grid, st);
+    case 1: return launch_wpr<MODE, 1, false>(s.rpw, a, nullptr, s.grid, st);
+    case 2: return launch_wpr<MODE, 2, false>(s.rpw, a, nullptr, s.grid, st);
+    case 4: return launch_wpr<MODE, 4, false>(s.rpw, a, nullptr, s.grid, st);
     }
     return false;
 }
@@ -506,7 +552,8 @@ static int launch_generic(chn_ctx *ctx, int mode, const GenericArgs &a) {
 }
 
 
-// x (fp32, K) -> digit planes in xp_ws (xplanes_bytes(K/32)), then the matvec.
+// x (fp32, K) -> digit planes (in the matvec's own LDS for K <= 4096, else
+// into xp_ws, xplanes_bytes(K/32), by a separate pass), then the matvec.
 int launch_matvec(chn_ctx *ctx, int mode, MatvecArgs a, const float *x, uint32_t *xp_ws, bool planes_ready) {
     const uint32_t nb = a.nb;
     const bool fast = nb % 4 == 0 && nb <= 512 && aligned(a.W0, 16) && (!a.W1 || aligned(a.W1, 16)) &&
@@ -515,16 +562,18 @@ int launch_matvec(chn_ctx *ctx, int mode, MatvecArgs a, const float *x, uint32_t
         GenericArgs g{a.W0, a.W1, a.W2, a.y0, a.y1, a.y2, x, a.M, a.seg1, a.seg2, nb};
         return launch_generic(ctx, mode, g);
     }
+    const MvShape s = pick_shape(mode, a.M, nb);
+    // one wave per row (K <= 4096): the kernel makes the planes itself
+    const float *xin = (!planes_ready && s.wpr == 1) ? x : nullptr;
     uint32_t *xp = xp_ws;
-    if (!planes_ready) {
+    if (!planes_ready && !xin) {
         k_xplanes<<<(4 * nb + 255) / 256, 256, 0, ctx->stream>>>(x, xp, nb);
         CHN_LAUNCHED(ctx, "k_xplanes");
     }
     a.xp = xp;
-    const MvShape s = pick_shape(mode, a.M, nb);
-    bool ok = mode == MV_GEMV ? launch_mode<MV_GEMV>(s, a, ctx->stream)
-            : mode == MV_QKV  ? launch_mode<MV_QKV>(s, a, ctx->stream)
-                              : launch_mode<MV_MLP>(s, a, ctx->stream);
+    bool ok = mode == MV_GEMV ? launch_mode<MV_GEMV>(s, a, xin, ctx->stream)
+            : mode == MV_QKV  ? launch_mode<MV_QKV>(s, a, xin, ctx->stream)
+                              : launch_mode<MV_MLP>(s, a, xin, ctx->stream);
     if (!ok) return set_err(ctx, CHN_E_UNSUPPORTED, "no matvec tile for M=%u nb=%u", a.M, nb);
     CHN_LAUNCHED(ctx, "k_q4mv");
     return CHN_OK;
