@@ -19,17 +19,18 @@
 // operand roundings.
 #include "chn_internal.h"
 
+#include <type_traits>
+
 namespace chn {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
 
 constexpr int GT = 128;          // tokens per workgroup tile
 constexpr int GN = 128;          // features per workgroup tile
-constexpr int GK = 64;           // K per step (two Q4 blocks)
-constexpr int LROW = GK * 2 + 16; // LDS row stride in bytes (padded)
 
 __global__ __launch_bounds__(256) void k_to_bf16(const float *__restrict__ x, __bf16 *__restrict__ y, size_t n) {
     size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
@@ -45,6 +46,8 @@ __global__ __launch_bounds__(256) void k_to_bf16(const float *__restrict__ x, __
         }
     }
 }
+
+constexpr int kGemmKB = 2;      // Q4 blocks per K step of the register-staged GEMM
 
 struct GemmArgs {
     const __bf16 *X;       // [n_tok][K] bf16
@@ -80,10 +83,37 @@ __device__ __forceinline__ void dequant_block_bf16(const uint32_t w0, const u32x
     }
 }
 
+// One nibble word (8 weights) to 8 bf16, given s and -8 s.  The empty asm
+// hides the known-zero bits (so byte extraction lowers to
+// v_cvt_f32_ubyte{0..3}) but lets unused results be removed.
+__device__ __forceinline__ uint32_t opaque_nv(uint32_t v) {
+    __asm__("" : "+v"(v));
+    return v;
+}
+__device__ __forceinline__ u32x4v dequant_word_bf16(const uint32_t q, const float s, const float ms) {
+    const uint32_t lo = opaque_nv(q & 0x0F0F0F0Fu);
+    const uint32_t hi = opaque_nv((q >> 4) & 0x0F0F0F0Fu);
+    u32x4v o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        bf16x2 p = {(__bf16)fmaf((float)((lo >> (8 * j)) & 0xffu), s, ms),
+                    (__bf16)fmaf((float)((hi >> (8 * j)) & 0xffu), s, ms)};
+        o[j] = __builtin_bit_cast(uint32_t, p);
+    }
+    return o;
+}
+
 // REP: weights in the repacked layout (16-byte nibble words, each nibble
 // XOR 8, then f16 scales), un-XORed here so the dequantization is shared.
-template <int NMAT, bool REP>
+// KB Q4 blocks (32 K each) per step: the workgroup's chain of dependent
+// load -> compute steps is K / (32 KB) long, and each step's loads return
+// from L2 / HBM in about a microsecond, far longer than its MFMAs take.
+template <int NMAT, bool REP, int KB>
 __global__ __launch_bounds__(256, 2) void k_q4gemm(GemmArgs a) {
+    constexpr int GK = 32 * KB;                  // K per step
+    constexpr int LROW = GK * 2 + 16;            // LDS row stride in bytes (padded)
+    constexpr int XC = GT * GK / 8 / 256;        // 16-byte X chunks per thread per step
+    constexpr int WB = GN * KB / 256;            // weight blocks per thread per step (consecutive)
     __shared__ __attribute__((aligned(16))) unsigned char lx[GT * LROW];
     __shared__ __attribute__((aligned(16))) unsigned char lw[NMAT][GN * LROW];
 
@@ -94,40 +124,43 @@ __global__ __launch_bounds__(256, 2) void k_q4gemm(GemmArgs a) {
     const uint32_t steps = (a.K + GK - 1) / GK;
 
     // global -> register staging for one K step
-    u32x4v xr[4];                  // 4 x 16 B of X per thread
-    uint32_t ww0[NMAT];
-    u32x4v wq[NMAT];
-    const int w_row = tid >> 1, w_blk = tid & 1;       // weight block handled by this thread
+    u32x4v xr[XC];                 // XC x 16 B of X per thread
+    uint32_t ww0[NMAT][WB];
+    u32x4v wq[NMAT][WB];
+    const int w_row = tid / (KB / WB), w_blk = (tid % (KB / WB)) * WB;   // first weight block of this thread
 
     auto gload = [&](uint32_t ks) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = tid + 256 * i;               // 1024 chunks of 16 B
-            const int row = c >> 3, col = c & 7;       // 8 chunks per 64-wide row
+        for (int i = 0; i < XC; ++i) {
+            const int c = tid + 256 * i;               // chunks of 16 B
+            const int row = c / (GK / 8), col = c % (GK / 8);
             const uint32_t t = t0 + row;
             const uint32_t k = ks * GK + col * 8;
             xr[i] = (t < a.n_tok && k < a.K) ? *(const u32x4v *)(a.X + (size_t)t * a.K + k) : u32x4v{0, 0, 0, 0};
         }
         const uint32_t n = n0 + w_row;
-        const uint32_t b = ks * 2 + w_blk;
 #pragma unroll
         for (int m = 0; m < NMAT; ++m) {
             const uint32_t *W = m == 0 ? a.W0 : a.W1;
-            if (n < a.M && b < nb) {
-                if (REP) {
-                    const size_t i = (size_t)n * nb + b;
-                    const u32x4g qv = ((const u32x4g *)W)[i];
-                    wq[m] = u32x4v{qv[0] ^ 0x88888888u, qv[1] ^ 0x88888888u, qv[2] ^ 0x88888888u,
-                                   qv[3] ^ 0x88888888u};
-                    ww0[m] = ((const uint16_t *)((const unsigned char *)W + (size_t)a.M * nb * 16))[i];
+#pragma unroll
+            for (int j = 0; j < WB; ++j) {
+                const uint32_t b = ks * KB + w_blk + j;
+                if (n < a.M && b < nb) {
+                    if (REP) {
+                        const size_t i = (size_t)n * nb + b;
+                        const u32x4g qv = ((const u32x4g *)W)[i];
+                        wq[m][j] = u32x4v{qv[0] ^ 0x88888888u, qv[1] ^ 0x88888888u, qv[2] ^ 0x88888888u,
+                                          qv[3] ^ 0x88888888u};
+                        ww0[m][j] = ((const uint16_t *)((const unsigned char *)W + (size_t)a.M * nb * 16))[i];
+                    } else {
+                        const uint32_t *p = W + ((size_t)n * nb + b) * 5;
+                        ww0[m][j] = p[0];
+                        wq[m][j] = *(const u32x4_a4 *)(p + 1);
+                    }
                 } else {
-                    const uint32_t *p = W + ((size_t)n * nb + b) * 5;
-                    ww0[m] = p[0];
-                    wq[m] = *(const u32x4_a4 *)(p + 1);
+                    ww0[m][j] = 0;
+                    wq[m][j] = u32x4v{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
                 }
-            } else {
-                ww0[m] = 0;
-                wq[m] = u32x4v{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
             }
         }
     };
@@ -144,23 +177,25 @@ __global__ __launch_bounds__(256, 2) void k_q4gemm(GemmArgs a) {
     for (uint32_t ks = 0; ks < steps; ++ks) {
         __syncthreads();
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < XC; ++i) {
             const int c = tid + 256 * i;
-            *(u32x4v *)(lx + (c >> 3) * LROW + (c & 7) * 16) = xr[i];
+            *(u32x4v *)(lx + (c / (GK / 8)) * LROW + (c % (GK / 8)) * 16) = xr[i];
         }
 #pragma unroll
-        for (int m = 0; m < NMAT; ++m) {
-            u32x4v d[4];
-            dequant_block_bf16(ww0[m], wq[m], d);
-            unsigned char *dst = lw[m] + w_row * LROW + w_blk * 64;
+        for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-            for (int w = 0; w < 4; ++w) *(u32x4v *)(dst + 16 * w) = d[w];
-        }
+            for (int j = 0; j < WB; ++j) {
+                u32x4v d[4];
+                dequant_block_bf16(ww0[m][j], wq[m][j], d);
+                unsigned char *dst = lw[m] + w_row * LROW + (w_blk + j) * 64;
+#pragma unroll
+                for (int w = 0; w < 4; ++w) *(u32x4v *)(dst + 16 * w) = d[w];
+            }
         __syncthreads();
         if (ks + 1 < steps) gload(ks + 1);
 
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
+        for (int kk = 0; kk < KB; ++kk) {
             const int koff = (kk * 32 + (lane >> 4) * 8) * 2;
             bf16x8 af[4], bfm[NMAT][4];
 #pragma unroll
@@ -200,6 +235,365 @@ __global__ __launch_bounds__(256, 2) void k_q4gemm(GemmArgs a) {
         }
 }
 
+// ---------------------------------------------------------------------------
+// Pipelined contraction for K % 64 == 0 (every prefill shape of the model).
+//
+// A workgroup owns 128 tokens x BN features (per matrix) and walks K in steps
+// of 64.  Step j's operands travel as one DMA group straight from global
+// memory into LDS (global_load_lds_dwordx{4,1}: no registers, no ds_write):
+//   X(j)      128 rows x 128 B of bf16, 16-byte chunk c of row r stored at
+//             position c ^ sw(r), sw(r) = (r ^ r >> 3) & 7, so the 16 rows a
+//             fragment read touches fall in distinct banks;
+//   Wraw(j+1) the raw Q4 bytes of the next step: nibble words ([blk][row])
+//             and scales.
+// S groups are in flight in a ring; the wait for group j is an explicit
+// vmcnt that leaves the younger groups outstanding, and the workgroup
+// barrier carries no memory fence (a fenced barrier waits for every
+// outstanding load).  While step j's MFMAs run, the waves dequantize
+// Wraw(j+1) once into a double-buffered bf16 tile, so each weight is
+// dequantized once per 128 tokens.
+// The eight waves form two groups of four: group g multiplies K half g of
+// every step (32 of the 64), each wave a 32-token x BN-feature block with
+// v_mfma_f32_16x16x32_bf16, and the two groups' partial sums meet once, in
+// LDS, at the end.  Two waves per SIMD let one wave's waits and dequant
+// arithmetic overlap the other's MFMAs when the grid has one workgroup per
+// CU.
+// Tiles are dealt to the 8 XCDs in contiguous runs (workgroup i runs on XCD
+// i % 8), with the 128-token tiles of one feature block adjacent, so a
+// weight block's bytes are reused from one L2.
+typedef __attribute__((address_space(3))) void lds_t;
+
+template <int NMAT, int BN, bool REP, int S>
+struct PipeCfg {
+    static constexpr int BT = 128, GK = 64, NTHR = 512;
+    static constexpr int R = NMAT * BN;                    // weight rows per step (64 or 128)
+    static constexpr int NW = R / 64;
+    static constexpr int XSLOT = BT * GK * 2;              // 16 KB of X per step
+    static constexpr int QSLOT = R * 2 * 16;               // nibble words per step, [m][blk][row]
+    static constexpr int SWORDS = REP ? R : R * 2;         // scale words per step
+    static constexpr int SSLOT = SWORDS * 4;
+    static constexpr int WROW = GK * 2 + 16;               // padded bf16 weight row
+    static constexpr int WBUF = R * WROW;
+    static constexpr int OFF_Q = S * XSLOT, OFF_S = OFF_Q + S * QSLOT, OFF_W = OFF_S + S * SSLOT;
+    static constexpr int LDS_MAIN = OFF_W + 2 * WBUF;
+    static constexpr int LDS_RED = BT * R * 4;             // group-1 partial sums at the end
+    static constexpr int LDS = LDS_MAIN > LDS_RED ? LDS_MAIN : LDS_RED;
+    // Every DMA instruction runs with all 64 lanes: waves 0 .. NQ-1 each
+    // load 1 KB of nibble words, waves NQ .. NQ+NS-1 each 256 B of scales,
+    // and every wave 2 KB of X.
+    static constexpr int NQ = QSLOT / 1024, NS = SWORDS / 64;
+    static_assert(NW == 1 || NW == 2, "64 or 128 weight rows per step");
+    static_assert(NQ + NS <= 8, "one weight DMA instruction per wave");
+};
+
+// vmcnt(n) and lgkmcnt(0) (gfx9 encoding: vmcnt[3:0] and [15:14],
+// expcnt[6:4], lgkmcnt[11:8]).
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+    static_assert(N >= 0 && N < 64, "vmcnt immediate");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+
+// Waits until at most `after` DMA groups younger than the one needed are in
+// flight, for a wave that issues PER DMA instructions per group.
+template <int PER>
+__device__ __forceinline__ void wait_groups(uint32_t after) {
+    if (after >= 2) wait_vm_lgkm0<2 * PER>();
+    else if (after == 1) wait_vm_lgkm0<PER>();
+    else wait_vm_lgkm0<0>();
+}
+
+// Workgroup barrier without a memory fence; the compiler may not move
+// memory accesses across it.
+__device__ __forceinline__ void bare_barrier() {
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+}
+
+// LDS reads of DMA-filled memory.  The compiler cannot tell ring slots
+// apart and would make every LDS read wait for the newest DMA group; reads
+// issued as asm are ordered by the explicit waits instead.  Their results
+// must stay in the registers the asm wrote until lds_wait() (a copy made
+// earlier would copy a value not yet loaded): lds_pin() after the wait keeps
+// every use below it.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+template <typename T, int OFF = 0>
+__device__ __forceinline__ T lds_read(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset");
+    T v;
+    if constexpr (sizeof(T) == 16) __asm__ volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    else if constexpr (sizeof(T) == 8) __asm__ volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    else __asm__ volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    return v;
+}
+__device__ __forceinline__ void lds_wait() { __asm__ volatile("s_waitcnt lgkmcnt(0)"); }
+template <typename T>
+__device__ __forceinline__ void lds_pin(T &v) {
+    __asm__ volatile("" : "+v"(v));
+}
+
+template <int NMAT, int BN, bool REP, int S>
+__global__ __launch_bounds__(512) void k_q4gemm_p(GemmArgs a, uint32_t n_ct, uint32_t n_tt) {
+    using C = PipeCfg<NMAT, BN, REP, S>;
+    constexpr int NT = BN / 16;
+    __shared__ __attribute__((aligned(16))) unsigned char sm[C::LDS];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave >> 2, wt = (wave & 3) * 32;       // K half, first token row of this wave
+    const uint32_t ntile = n_ct * n_tt, per = (ntile + 7) / 8;
+    const uint32_t tile = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    if (tile >= ntile) return;
+    const uint32_t n0 = (tile / n_tt) * BN, t0 = (tile % n_tt) * C::BT;
+    const uint32_t K = a.K, nb = K / 32, steps = K / 64;
+    const uint32_t smb = lds_addr(sm);
+
+    // ---- per-lane DMA sources (rows clamped in bounds; their results are not stored)
+    const __bf16 *xg[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int q = (i * 8 + wave) * 64 + lane;          // chunk position in the X slot
+        const int r = q >> 3, c = (q & 7) ^ ((r ^ (r >> 3)) & 7);
+        const uint32_t t = min(t0 + r, a.n_tok - 1);
+        xg[i] = a.X + (size_t)t * K + c * 8;
+    }
+    // weight DMA of this wave: nibble instruction `wave` (wave < NQ), scale
+    // instruction `wave - NQ` (NQ <= wave < NQ + NS), or none
+    const bool w_dma = wave < C::NQ + C::NS;
+    const bool q_dma = wave < C::NQ;
+    const unsigned char *wg;
+    uint32_t w_lds, w_step;
+    {
+        const int qi = q_dma ? wave : 0, si = q_dma ? 0 : (w_dma ? wave - C::NQ : 0);
+        const int q = qi * 64 + lane;                      // nibble chunk, [m][blk][row]
+        const int qm = q / (BN * 2), qblk = (q % (BN * 2)) / BN, qrow = q % BN;
+        const int sq = si * 64 + lane;                     // scale word, REP [m][row], else [m][blk][row]
+        const int sm_ = REP ? sq / BN : sq / (BN * 2), sblk = REP ? 0 : (sq % (BN * 2)) / BN, srow = sq % BN;
+        const int m = q_dma ? qm : sm_, row = q_dma ? qrow : srow;
+        const uint32_t n = min(n0 + row, a.M - 1);
+        const unsigned char *W = (const unsigned char *)(m == 0 ? a.W0 : a.W1);
+        if (q_dma) {
+            wg = REP ? W + ((size_t)n * nb + qblk) * 16 : W + ((size_t)n * nb + qblk) * 20 + 4;
+            w_lds = C::OFF_Q + qi * 1024;
+            w_step = REP ? 32 : 40;
+        } else {
+            wg = REP ? W + (size_t)a.M * nb * 16 + (size_t)n * nb * 2 : W + ((size_t)n * nb + sblk) * 20;
+            w_lds = C::OFF_S + si * 256;
+            w_step = REP ? 4 : 40;
+        }
+    }
+
+    auto issue_w = [&](uint32_t j, int slot) {             // Wraw(j) -> ring slot
+        const uint32_t jj = min(j, steps - 1);
+        if (q_dma)
+            __builtin_amdgcn_global_load_lds(wg + (size_t)jj * w_step, (lds_t *)(sm + w_lds + slot * C::QSLOT), 16, 0, 0);
+        else if (w_dma)
+            __builtin_amdgcn_global_load_lds(wg + (size_t)jj * w_step, (lds_t *)(sm + w_lds + slot * C::SSLOT), 4, 0, 0);
+    };
+    auto issue_group = [&](uint32_t j) {                   // X(j) and Wraw(j + 1)
+        const int xs = j % S;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_global_load_lds(xg[i] + (size_t)j * 64,
+                                             (lds_t *)(sm + xs * C::XSLOT + (i * 8 + wave) * 1024), 16, 0, 0);
+        issue_w(j + 1, (j + 1) % S);
+    };
+
+    // ---- dequantization: thread -> weight row (consecutive lanes, distinct
+    // banks) and NW consecutive nibble words of one block
+    const int drow = tid % C::R, du = tid / C::R;
+    const int dblk = C::NW == 1 ? du >> 2 : du >> 1;
+    const int dword0 = C::NW == 1 ? du & 3 : (du & 1) * 2;
+    const int dm = drow / BN, drw = drow % BN;
+    const uint32_t dq_q = smb + C::OFF_Q + (((dm * 2 + dblk) * BN + drw) * 16 + dword0 * 4);
+    const uint32_t dq_s = smb + C::OFF_S + (REP ? drow : (dm * 2 + dblk) * BN + drw) * 4;
+    const uint32_t dq_w = smb + C::OFF_W + drow * C::WROW + dblk * 64 + dword0 * 16;
+    using RawW = typename std::conditional<C::NW == 1, uint32_t, u32x2v>::type;
+    struct Raw {
+        RawW w;
+        uint32_t sw;
+    };
+    auto dq_load = [&](uint32_t j) {
+        const uint32_t slot = j % S;
+        Raw r;
+        r.w = lds_read<RawW>(dq_q + slot * C::QSLOT);
+        r.sw = lds_read<uint32_t>(dq_s + slot * C::SSLOT);
+        return r;
+    };
+    auto dq_word = [&](const Raw &r, int w, float sc, float ms) {
+        uint32_t q;
+        if constexpr (C::NW == 1) q = r.w;
+        else q = r.w[w];
+        return dequant_word_bf16(REP ? q ^ 0x88888888u : q, sc, ms);
+    };
+    auto dq_scale = [&](const Raw &r, float &sc, float &ms) {
+        sc = f16_lo_to_f32(REP ? r.sw >> (16 * dblk) : r.sw);
+        ms = -8.0f * sc;
+    };
+    auto dq_store = [&](uint32_t j, u32x4v d0, u32x4v d1) {
+        unsigned char *dst = sm + (dq_w - smb) + (j & 1) * C::WBUF;
+        *(u32x4v *)dst = d0;
+        if (C::NW == 2) *(u32x4v *)(dst + 16) = d1;
+    };
+
+    f32x4 acc[NMAT][2][NT];
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < NT; ++j) acc[m][i][j] = f32x4{0, 0, 0, 0};
+
+    // fragment addresses (slot 0 / tile 0); the K half is this wave's group
+    uint32_t xa[2], wa;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        const int r = wt + mt * 16 + (lane & 15);
+        const int c = (grp * 4 + (lane >> 4)) ^ ((r ^ (r >> 3)) & 7);
+        xa[mt] = smb + r * 128 + c * 16;
+    }
+    wa = smb + C::OFF_W + (lane & 15) * C::WROW + (grp * 32 + (lane >> 4) * 8) * 2;
+
+    // ---- prologue: Wraw(0), groups 0 .. S-2, then the first dequantization
+    // The waits count DMA instructions in issue order, so the compiler may
+    // not reorder these issues: Wraw(0) first, then the groups in turn.
+    issue_w(0, 0);
+#pragma unroll
+    for (int g = 0; g < S - 1; ++g) {
+        __asm__ volatile("" ::: "memory");
+        if ((uint32_t)g < steps) issue_group(g);
+    }
+    __asm__ volatile("" ::: "memory");
+    {
+        // Wraw(0) landed; the min(S-1, steps) groups after it may still fly
+        const uint32_t after = min((uint32_t)(S - 1), steps);
+        if (w_dma) wait_groups<3>(after);
+        else wait_groups<2>(after);
+    }
+    bare_barrier();                                        // other waves' DMA of Wraw(0) landed too
+    {
+        Raw r0 = dq_load(0);
+        lds_wait();
+        lds_pin(r0.w);
+        lds_pin(r0.sw);
+        float sc, ms;
+        dq_scale(r0, sc, ms);
+        dq_store(0, dq_word(r0, 0, sc, ms), C::NW == 2 ? dq_word(r0, 1, sc, ms) : u32x4v{0, 0, 0, 0});
+    }
+
+    for (uint32_t s = 0; s < steps; ++s) {
+        // group s landed: the younger groups s+1 .. min(s+S-2, steps-1) may still fly
+        {
+            const uint32_t after = min((uint32_t)(S - 2), steps - 1 - s);
+            if (w_dma) wait_groups<3>(after);
+            else wait_groups<2>(after);
+        }
+        bare_barrier();
+        // Wraw(s+1) -> bf16 tile ((s+1) & 1), which no wave reads this step.
+        // On the last step this converts the in-bounds copy the final group
+        // loaded, into the tile nobody reads again.
+        Raw raw = dq_load(s + 1);
+        const uint32_t xo = (s % S) * C::XSLOT, wo = (s & 1) * C::WBUF;
+        bf16x8 af[2], bfm[NMAT][NT];
+        af[0] = lds_read<bf16x8>(xa[0] + xo);
+        af[1] = lds_read<bf16x8>(xa[1] + xo);
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) {
+            const uint32_t wam = wa + wo + m * BN * C::WROW;
+            bfm[m][0] = lds_read<bf16x8, 0 * 16 * C::WROW>(wam);
+            bfm[m][1] = lds_read<bf16x8, 1 * 16 * C::WROW>(wam);
+            bfm[m][2] = lds_read<bf16x8, 2 * 16 * C::WROW>(wam);
+            bfm[m][3] = lds_read<bf16x8, 3 * 16 * C::WROW>(wam);
+            if constexpr (NT == 8) {
+                bfm[m][4 % NT] = lds_read<bf16x8, 4 * 16 * C::WROW>(wam);
+                bfm[m][5 % NT] = lds_read<bf16x8, 5 * 16 * C::WROW>(wam);
+                bfm[m][6 % NT] = lds_read<bf16x8, 6 * 16 * C::WROW>(wam);
+                bfm[m][7 % NT] = lds_read<bf16x8, 7 * 16 * C::WROW>(wam);
+            }
+        }
+        if (s + S - 1 < steps) issue_group(s + S - 1);
+        lds_wait();
+        lds_pin(raw.w);
+        lds_pin(raw.sw);
+        lds_pin(af[0]);
+        lds_pin(af[1]);
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) lds_pin(bfm[m][nt]);
+
+        float sc, ms;
+        dq_scale(raw, sc, ms);
+        const u32x4v d0 = dq_word(raw, 0, sc, ms);
+        const u32x4v d1 = C::NW == 2 ? dq_word(raw, 1, sc, ms) : u32x4v{0, 0, 0, 0};
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+                    acc[m][mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bfm[m][nt], acc[m][mt][nt], 0, 0, 0);
+        dq_store(s + 1, d0, d1);
+        // one MFMA, then a few VALU ops of the dequantization, in turn
+#pragma unroll
+        for (int i = 0; i < NMAT * 2 * NT; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, C::NW == 1 ? 3 : 3, 0);
+        }
+    }
+
+    // ---- the K halves meet: group 1 parks its sums in LDS, group 0 adds and stores
+    wait_vm_lgkm0<0>();
+    bare_barrier();
+    float *red = (float *)sm;                              // [wave & 3][m][mt][nt][4][64]
+    const int rw = wave & 3;
+    if (grp == 1) {
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+                    *(f32x4 *)(red + ((((rw * NMAT + m) * 2 + mt) * NT + nt) * 64 + lane) * 4) = acc[m][mt][nt];
+    }
+    __syncthreads();
+    if (grp == 1) return;
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+                acc[m][mt][nt] += *(const f32x4 *)(red + ((((rw * NMAT + m) * 2 + mt) * NT + nt) * 64 + lane) * 4);
+
+    // epilogue: lane holds tokens (lane>>4)*4 + i of each 16-row tile, feature lane & 15
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const uint32_t n = n0 + nt * 16 + (lane & 15);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t t = t0 + wt + mt * 16 + (lane >> 4) * 4 + i;
+                if (t < a.n_tok && n < a.M) {
+                    float v = acc[0][mt][nt][i];
+                    if (NMAT == 2) v = gelu_tanh(v) * acc[NMAT - 1][mt][nt][i];
+                    a.Y[(size_t)t * a.M + n] = v;
+                }
+            }
+        }
+}
+
+template <int NMAT, int BN, bool REP, int S>
+static void launch_gemm_p(hipStream_t st, const GemmArgs &a) {
+    const uint32_t n_ct = (a.M + BN - 1) / BN, n_tt = (a.n_tok + 127) / 128;
+    const uint32_t per = (n_ct * n_tt + 7) / 8;
+    k_q4gemm_p<NMAT, BN, REP, S><<<8 * per, 512, 0, st>>>(a, n_ct, n_tt);
+}
+
 int launch_q4gemm(chn_ctx *ctx, int nmat, const float *X, const uint32_t *W0, const uint32_t *W1, float *Y,
                   uint32_t n_tok, uint32_t M, uint32_t K, __bf16 *xb, bool repacked) {
     const size_t n = (size_t)n_tok * K;
@@ -209,13 +603,19 @@ int launch_q4gemm(chn_ctx *ctx, int nmat, const float *X, const uint32_t *W0, co
     k_to_bf16<<<g, 256, 0, ctx->stream>>>(X, xb, n);
     CHN_LAUNCHED(ctx, "k_to_bf16");
     GemmArgs a{xb, W0, W1, Y, n_tok, M, K};
+    if (nmat == 1 && K % 64 == 0) {
+        if (repacked) launch_gemm_p<1, 64, true, 4>(ctx->stream, a);
+        else launch_gemm_p<1, 64, false, 4>(ctx->stream, a);
+        CHN_LAUNCHED(ctx, "k_q4gemm_p");
+        return CHN_OK;
+    }
     dim3 grid((M + GN - 1) / GN, (n_tok + GT - 1) / GT);
     if (repacked) {
-        if (nmat == 1) k_q4gemm<1, true><<<grid, 256, 0, ctx->stream>>>(a);
-        else k_q4gemm<2, true><<<grid, 256, 0, ctx->stream>>>(a);
+        if (nmat == 1) k_q4gemm<1, true, kGemmKB><<<grid, 256, 0, ctx->stream>>>(a);
+        else k_q4gemm<2, true, kGemmKB><<<grid, 256, 0, ctx->stream>>>(a);
     } else {
-        if (nmat == 1) k_q4gemm<1, false><<<grid, 256, 0, ctx->stream>>>(a);
-        else k_q4gemm<2, false><<<grid, 256, 0, ctx->stream>>>(a);
+        if (nmat == 1) k_q4gemm<1, false, kGemmKB><<<grid, 256, 0, ctx->stream>>>(a);
+        else k_q4gemm<2, false, kGemmKB><<<grid, 256, 0, ctx->stream>>>(a);
     }
     CHN_LAUNCHED(ctx, "k_q4gemm");
     return CHN_OK;

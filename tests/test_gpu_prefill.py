@@ -19,6 +19,12 @@ pytestmark = pytest.mark.gpu
     (100, 200, 96, None),      # ragged: tokens, features and K not tile multiples
     (1, 130, 32, None),        # one token, one Q4 block
     (129, 64, 160, None),
+    # K % 64 == 0 takes the DMA-pipelined kernel: ragged tokens and features,
+    # and fewer K steps (1, 2, 3) than DMA groups in flight
+    (100, 200, 128, None),
+    (1, 70, 64, None),
+    (257, 100, 192, None),
+    (130, 64, 448, None),
 ])
 def test_batch_gemm_q4_parity(ctx, n_tok, M, K, sample):
     seed = 9000 + n_tok + M + K
