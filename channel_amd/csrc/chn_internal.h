@@ -181,6 +181,10 @@ int launch_quantize(hipStream_t st, int q8, const uint16_t *src, uint32_t *dst, 
 // W0/W1 in the reference Q4 layout, or in Q4R with repacked.
 int launch_q4gemm(chn_ctx *ctx, int nmat, const float *X, const uint32_t *W0, const uint32_t *W1, float *Y,
                   uint32_t n_tok, uint32_t M, uint32_t K, __bf16 *xb, bool repacked);
+// q, k, v (Q4R) over the same activations in one launch.
+int launch_q4gemm_qkv(chn_ctx *ctx, const float *X, const uint32_t *Wq, const uint32_t *Wk, const uint32_t *Wv,
+                      float *Yq, float *Yk, float *Yv, uint32_t n_tok, uint32_t Mq, uint32_t Mkv, uint32_t K,
+                      __bf16 *xb);
 
 // ---------------------------------------------------------------------
 // Device helpers

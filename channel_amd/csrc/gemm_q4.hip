@@ -32,10 +32,12 @@ typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
 constexpr int GT = 128;          // tokens per workgroup tile
 constexpr int GN = 128;          // features per workgroup tile
 
-__global__ __launch_bounds__(256) void k_to_bf16(const float *__restrict__ x, __bf16 *__restrict__ y, size_t n) {
-    size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+// Activations to bf16 (RNE); also zeroes z[0, nz) (the output of a split-K
+// contraction, whose two halves add into it).
+__global__ __launch_bounds__(256) void k_to_bf16(const float *__restrict__ x, __bf16 *__restrict__ y, size_t n,
+                                                 float *__restrict__ z, size_t nz) {
     const size_t stride = (size_t)gridDim.x * blockDim.x * 4;
-    for (; i < n; i += stride) {
+    for (size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; i < n; i += stride) {
         if (i + 4 <= n) {
             const float4 v = *(const float4 *)(x + i);
             bf16x2 a = {(__bf16)v.x, (__bf16)v.y}, b = {(__bf16)v.z, (__bf16)v.w};
@@ -44,6 +46,11 @@ __global__ __launch_bounds__(256) void k_to_bf16(const float *__restrict__ x, __
         } else {
             for (size_t j = i; j < n; ++j) y[j] = (__bf16)x[j];
         }
+    }
+    for (size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; i < nz; i += stride) {
+        if (i + 4 <= nz) *(float4 *)(z + i) = float4{0.f, 0.f, 0.f, 0.f};
+        else
+            for (size_t j = i; j < nz; ++j) z[j] = 0.f;
     }
 }
 
@@ -54,6 +61,11 @@ struct GemmArgs {
     const uint32_t *W0, *W1; // Q4 [M][K/32][5], or Q4R (W1: up matrix for the fused MLP)
     float *Y;              // [n_tok][M]
     uint32_t n_tok, M, K;
+    // Up to two more single-matrix segments sharing X (one launch for q, k
+    // and v): segment g multiplies Wg[g] into Yg[g] ([n_tok][Mg[g]]).
+    const uint32_t *Wg[2] = {nullptr, nullptr};
+    float *Yg[2] = {nullptr, nullptr};
+    uint32_t Mg[2] = {0, 0};
 };
 
 typedef uint32_t u32x4g __attribute__((ext_vector_type(4)));
@@ -275,13 +287,15 @@ struct PipeCfg {
     static constexpr int WROW = GK * 2 + 16;               // padded bf16 weight row
     static constexpr int WBUF = R * WROW;
     static constexpr int OFF_Q = S * XSLOT, OFF_S = OFF_Q + S * QSLOT, OFF_W = OFF_S + S * SSLOT;
-    static constexpr int LDS_MAIN = OFF_W + 2 * WBUF;
+    static constexpr int OFF_D = OFF_W + 2 * WBUF;          // 256 B written by waves without a weight load
+    static constexpr int LDS_MAIN = OFF_D + 256;
     static constexpr int LDS_RED = BT * R * 4;             // group-1 partial sums at the end
     static constexpr int LDS = LDS_MAIN > LDS_RED ? LDS_MAIN : LDS_RED;
-    // Every DMA instruction runs with all 64 lanes: waves 0 .. NQ-1 each
-    // load 1 KB of nibble words, waves NQ .. NQ+NS-1 each 256 B of scales,
-    // and every wave 2 KB of X.
-    static constexpr int NQ = QSLOT / 1024, NS = SWORDS / 64;
+    // Every DMA instruction runs with all 64 lanes, and every wave issues
+    // PER = 3 per group, so one vmcnt fits all waves: 2 KB of X each, then
+    // waves 0 .. NQ-1 1 KB of nibble words, waves NQ .. NQ+NS-1 256 B of
+    // scales, and the rest 256 B into a dummy area.
+    static constexpr int NQ = QSLOT / 1024, NS = SWORDS / 64, PER = 3;
     static_assert(NW == 1 || NW == 2, "64 or 128 weight rows per step");
     static_assert(NQ + NS <= 8, "one weight DMA instruction per wave");
 };
@@ -294,14 +308,6 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
 }
 
-// Waits until at most `after` DMA groups younger than the one needed are in
-// flight, for a wave that issues PER DMA instructions per group.
-template <int PER>
-__device__ __forceinline__ void wait_groups(uint32_t after) {
-    if (after >= 2) wait_vm_lgkm0<2 * PER>();
-    else if (after == 1) wait_vm_lgkm0<PER>();
-    else wait_vm_lgkm0<0>();
-}
 
 // Workgroup barrier without a memory fence; the compiler may not move
 // memory accesses across it.
@@ -330,25 +336,52 @@ __device__ __forceinline__ T lds_read(uint32_t addr) {
     return v;
 }
 __device__ __forceinline__ void lds_wait() { __asm__ volatile("s_waitcnt lgkmcnt(0)"); }
+template <int N>                                           // all but the newest N LDS operations done
+__device__ __forceinline__ void lds_wait_n() {
+    static_assert(N >= 0 && N < 16, "lgkmcnt immediate");
+    __asm__ volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N));
+}
 template <typename T>
 __device__ __forceinline__ void lds_pin(T &v) {
     __asm__ volatile("" : "+v"(v));
 }
 
 template <int NMAT, int BN, bool REP, int S>
-__global__ __launch_bounds__(512) void k_q4gemm_p(GemmArgs a, uint32_t n_ct, uint32_t n_tt) {
+__global__ __launch_bounds__(512) void k_q4gemm_p(GemmArgs a, uint32_t n_ct, uint32_t n_tt, uint32_t ksplit) {
     using C = PipeCfg<NMAT, BN, REP, S>;
-    constexpr int NT = BN / 16;
+    constexpr int NTW = BN / 32;                           // 16-feature tiles per wave and matrix
     __shared__ __attribute__((aligned(16))) unsigned char sm[C::LDS];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int grp = wave >> 2, wt = (wave & 3) * 32;       // K half, first token row of this wave
-    const uint32_t ntile = n_ct * n_tt, per = (ntile + 7) / 8;
-    const uint32_t tile = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
-    if (tile >= ntile) return;
-    const uint32_t n0 = (tile / n_tt) * BN, t0 = (tile % n_tt) * C::BT;
-    const uint32_t K = a.K, nb = K / 32, steps = K / 64;
+    // group grp multiplies K half grp of each step; within it, 2 x 2 waves of
+    // 64 tokens (wr) x BN/2 features per matrix (wc)
+    const int grp = wave >> 2, wr = (wave >> 1) & 1, wc = wave & 1;
+    const uint32_t ntile = n_ct * n_tt, nwork = ntile * ksplit, per = (nwork + 7) / 8;
+    const uint32_t work = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    if (work >= nwork) return;
+    const uint32_t ks = work / ntile, tile = work % ntile;
+    // column tile -> segment (workgroup-uniform)
+    uint32_t ct = tile / n_tt;
+    const uint32_t *W0 = a.W0;
+    float *Yp = a.Y;
+    uint32_t Mloc = a.M;
+    {
+        const uint32_t c0 = (a.M + BN - 1) / BN, c1 = (a.Mg[0] + BN - 1) / BN;
+        if (ct >= c0) {
+            ct -= c0;
+            const int g = ct >= c1 ? 1 : 0;
+            if (g) ct -= c1;
+            W0 = a.Wg[g];
+            Yp = a.Yg[g];
+            Mloc = a.Mg[g];
+        }
+    }
+    const uint32_t n0 = ct * BN, t0 = (tile % n_tt) * C::BT;
+    const uint32_t K = a.K, nb = K / 32, steps_all = K / 64;
+    // K split between two workgroups: steps [0, h) and [h, steps_all)
+    const uint32_t h = steps_all / 2, s_begin = ks ? h : 0;
+    const uint32_t steps = ksplit == 1 ? steps_all : (ks ? steps_all - h : h);
     const uint32_t smb = lds_addr(sm);
 
     // ---- per-lane DMA sources (rows clamped in bounds; their results are not stored)
@@ -358,48 +391,58 @@ __global__ __launch_bounds__(512) void k_q4gemm_p(GemmArgs a, uint32_t n_ct, uin
         const int q = (i * 8 + wave) * 64 + lane;          // chunk position in the X slot
         const int r = q >> 3, c = (q & 7) ^ ((r ^ (r >> 3)) & 7);
         const uint32_t t = min(t0 + r, a.n_tok - 1);
-        xg[i] = a.X + (size_t)t * K + c * 8;
+        xg[i] = a.X + (size_t)t * K + c * 8 + s_begin * 64;
     }
-    // weight DMA of this wave: nibble instruction `wave` (wave < NQ), scale
-    // instruction `wave - NQ` (NQ <= wave < NQ + NS), or none
-    const bool w_dma = wave < C::NQ + C::NS;
-    const bool q_dma = wave < C::NQ;
+    // weight DMA of this wave: nibble instruction `wave` (role 0), scale
+    // instruction `wave - NQ` (role 1) or the dummy load (role 2)
+    const int role = wave < C::NQ ? 0 : (wave < C::NQ + C::NS ? 1 : 2);
     const unsigned char *wg;
-    uint32_t w_lds, w_step;
+    uint32_t w_lds, w_slot, w_step;
     {
-        const int qi = q_dma ? wave : 0, si = q_dma ? 0 : (w_dma ? wave - C::NQ : 0);
+        const int qi = role == 0 ? wave : 0, si = role == 1 ? wave - C::NQ : 0;
         const int q = qi * 64 + lane;                      // nibble chunk, [m][blk][row]
         const int qm = q / (BN * 2), qblk = (q % (BN * 2)) / BN, qrow = q % BN;
         const int sq = si * 64 + lane;                     // scale word, REP [m][row], else [m][blk][row]
         const int sm_ = REP ? sq / BN : sq / (BN * 2), sblk = REP ? 0 : (sq % (BN * 2)) / BN, srow = sq % BN;
-        const int m = q_dma ? qm : sm_, row = q_dma ? qrow : srow;
-        const uint32_t n = min(n0 + row, a.M - 1);
-        const unsigned char *W = (const unsigned char *)(m == 0 ? a.W0 : a.W1);
-        if (q_dma) {
+        const int m = role == 0 ? qm : sm_, row = role == 0 ? qrow : srow;
+        const uint32_t n = min(n0 + row, Mloc - 1);
+        const unsigned char *W = (const unsigned char *)(m == 0 ? W0 : a.W1);
+        if (role == 0) {
             wg = REP ? W + ((size_t)n * nb + qblk) * 16 : W + ((size_t)n * nb + qblk) * 20 + 4;
             w_lds = C::OFF_Q + qi * 1024;
+            w_slot = C::QSLOT;
             w_step = REP ? 32 : 40;
-        } else {
-            wg = REP ? W + (size_t)a.M * nb * 16 + (size_t)n * nb * 2 : W + ((size_t)n * nb + sblk) * 20;
+        } else if (role == 1) {
+            wg = REP ? W + (size_t)Mloc * nb * 16 + (size_t)n * nb * 2 : W + ((size_t)n * nb + sblk) * 20;
             w_lds = C::OFF_S + si * 256;
+            w_slot = C::SSLOT;
             w_step = REP ? 4 : 40;
+        } else {                                           // first 128 B of X (K >= 64)
+            wg = (const unsigned char *)a.X + (lane * 4) % 128;
+            w_lds = C::OFF_D;
+            w_slot = 0;
+            w_step = 0;
         }
+        wg += (size_t)s_begin * w_step;
     }
 
-    auto issue_w = [&](uint32_t j, int slot) {             // Wraw(j) -> ring slot
+    // Group j: X(j) -> X slot j % S and Wraw(j + 1) -> weight slot (j+1) % S.
+    // Groups past the last step reload the last step's bytes (clamped) into
+    // slots nobody reads again, so every wave issues the same count.
+    auto issue_w = [&](uint32_t j) {
         const uint32_t jj = min(j, steps - 1);
-        if (q_dma)
-            __builtin_amdgcn_global_load_lds(wg + (size_t)jj * w_step, (lds_t *)(sm + w_lds + slot * C::QSLOT), 16, 0, 0);
-        else if (w_dma)
-            __builtin_amdgcn_global_load_lds(wg + (size_t)jj * w_step, (lds_t *)(sm + w_lds + slot * C::SSLOT), 4, 0, 0);
+        lds_t *dst = (lds_t *)(sm + w_lds + (j % S) * w_slot);
+        if (role == 0) __builtin_amdgcn_global_load_lds(wg + (size_t)jj * w_step, dst, 16, 0, 0);
+        else __builtin_amdgcn_global_load_lds(wg + (size_t)jj * w_step, dst, 4, 0, 0);
     };
-    auto issue_group = [&](uint32_t j) {                   // X(j) and Wraw(j + 1)
+    auto issue_group = [&](uint32_t j) {
+        const uint32_t jj = min(j, steps - 1);
         const int xs = j % S;
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-            __builtin_amdgcn_global_load_lds(xg[i] + (size_t)j * 64,
+            __builtin_amdgcn_global_load_lds(xg[i] + (size_t)jj * 64,
                                              (lds_t *)(sm + xs * C::XSLOT + (i * 8 + wave) * 1024), 16, 0, 0);
-        issue_w(j + 1, (j + 1) % S);
+        issue_w(j + 1);
     };
 
     // ---- dequantization: thread -> weight row (consecutive lanes, distinct
@@ -410,7 +453,7 @@ __global__ __launch_bounds__(512) void k_q4gemm_p(GemmArgs a, uint32_t n_ct, uin
     const int dm = drow / BN, drw = drow % BN;
     const uint32_t dq_q = smb + C::OFF_Q + (((dm * 2 + dblk) * BN + drw) * 16 + dword0 * 4);
     const uint32_t dq_s = smb + C::OFF_S + (REP ? drow : (dm * 2 + dblk) * BN + drw) * 4;
-    const uint32_t dq_w = smb + C::OFF_W + drow * C::WROW + dblk * 64 + dword0 * 16;
+    const uint32_t dq_w = C::OFF_W + drow * C::WROW + dblk * 64 + dword0 * 16;
     using RawW = typename std::conditional<C::NW == 1, uint32_t, u32x2v>::type;
     struct Raw {
         RawW w;
@@ -434,181 +477,245 @@ __global__ __launch_bounds__(512) void k_q4gemm_p(GemmArgs a, uint32_t n_ct, uin
         ms = -8.0f * sc;
     };
     auto dq_store = [&](uint32_t j, u32x4v d0, u32x4v d1) {
-        unsigned char *dst = sm + (dq_w - smb) + (j & 1) * C::WBUF;
+        unsigned char *dst = sm + dq_w + (j & 1) * C::WBUF;
         *(u32x4v *)dst = d0;
         if (C::NW == 2) *(u32x4v *)(dst + 16) = d1;
     };
+    auto dq_all = [&](uint32_t j, const Raw &r) {
+        float sc, ms;
+        dq_scale(r, sc, ms);
+        dq_store(j, dq_word(r, 0, sc, ms), C::NW == 2 ? dq_word(r, 1, sc, ms) : u32x4v{0, 0, 0, 0});
+    };
 
-    f32x4 acc[NMAT][2][NT];
+    // ---- fragments: this wave's 32 tokens and the BN features of its K half
+    struct Frag {
+        bf16x8 a[4], b[NMAT][NTW];
+    };
+    uint32_t xa[4], wa;
 #pragma unroll
-    for (int m = 0; m < NMAT; ++m)
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < NT; ++j) acc[m][i][j] = f32x4{0, 0, 0, 0};
-
-    // fragment addresses (slot 0 / tile 0); the K half is this wave's group
-    uint32_t xa[2], wa;
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-        const int r = wt + mt * 16 + (lane & 15);
+    for (int mt = 0; mt < 4; ++mt) {
+        const int r = wr * 64 + mt * 16 + (lane & 15);
         const int c = (grp * 4 + (lane >> 4)) ^ ((r ^ (r >> 3)) & 7);
         xa[mt] = smb + r * 128 + c * 16;
     }
-    wa = smb + C::OFF_W + (lane & 15) * C::WROW + (grp * 32 + (lane >> 4) * 8) * 2;
-
-    // ---- prologue: Wraw(0), groups 0 .. S-2, then the first dequantization
-    // The waits count DMA instructions in issue order, so the compiler may
-    // not reorder these issues: Wraw(0) first, then the groups in turn.
-    issue_w(0, 0);
+    wa = smb + C::OFF_W + (wc * (BN / 2) + (lane & 15)) * C::WROW + (grp * 32 + (lane >> 4) * 8) * 2;
+    auto frag_load = [&](uint32_t j, Frag &f) {            // X slot j % S, bf16 tile j & 1
+        const uint32_t xo = (j % S) * C::XSLOT, wo = (j & 1) * C::WBUF;
 #pragma unroll
-    for (int g = 0; g < S - 1; ++g) {
-        __asm__ volatile("" ::: "memory");
-        if ((uint32_t)g < steps) issue_group(g);
-    }
-    __asm__ volatile("" ::: "memory");
-    {
-        // Wraw(0) landed; the min(S-1, steps) groups after it may still fly
-        const uint32_t after = min((uint32_t)(S - 1), steps);
-        if (w_dma) wait_groups<3>(after);
-        else wait_groups<2>(after);
-    }
-    bare_barrier();                                        // other waves' DMA of Wraw(0) landed too
-    {
-        Raw r0 = dq_load(0);
-        lds_wait();
-        lds_pin(r0.w);
-        lds_pin(r0.sw);
-        float sc, ms;
-        dq_scale(r0, sc, ms);
-        dq_store(0, dq_word(r0, 0, sc, ms), C::NW == 2 ? dq_word(r0, 1, sc, ms) : u32x4v{0, 0, 0, 0});
-    }
-
-    for (uint32_t s = 0; s < steps; ++s) {
-        // group s landed: the younger groups s+1 .. min(s+S-2, steps-1) may still fly
-        {
-            const uint32_t after = min((uint32_t)(S - 2), steps - 1 - s);
-            if (w_dma) wait_groups<3>(after);
-            else wait_groups<2>(after);
-        }
-        bare_barrier();
-        // Wraw(s+1) -> bf16 tile ((s+1) & 1), which no wave reads this step.
-        // On the last step this converts the in-bounds copy the final group
-        // loaded, into the tile nobody reads again.
-        Raw raw = dq_load(s + 1);
-        const uint32_t xo = (s % S) * C::XSLOT, wo = (s & 1) * C::WBUF;
-        bf16x8 af[2], bfm[NMAT][NT];
-        af[0] = lds_read<bf16x8>(xa[0] + xo);
-        af[1] = lds_read<bf16x8>(xa[1] + xo);
+        for (int mt = 0; mt < 4; ++mt) f.a[mt] = lds_read<bf16x8>(xa[mt] + xo);
 #pragma unroll
         for (int m = 0; m < NMAT; ++m) {
             const uint32_t wam = wa + wo + m * BN * C::WROW;
-            bfm[m][0] = lds_read<bf16x8, 0 * 16 * C::WROW>(wam);
-            bfm[m][1] = lds_read<bf16x8, 1 * 16 * C::WROW>(wam);
-            bfm[m][2] = lds_read<bf16x8, 2 * 16 * C::WROW>(wam);
-            bfm[m][3] = lds_read<bf16x8, 3 * 16 * C::WROW>(wam);
-            if constexpr (NT == 8) {
-                bfm[m][4 % NT] = lds_read<bf16x8, 4 * 16 * C::WROW>(wam);
-                bfm[m][5 % NT] = lds_read<bf16x8, 5 * 16 * C::WROW>(wam);
-                bfm[m][6 % NT] = lds_read<bf16x8, 6 * 16 * C::WROW>(wam);
-                bfm[m][7 % NT] = lds_read<bf16x8, 7 * 16 * C::WROW>(wam);
+            f.b[m][0] = lds_read<bf16x8, 0 * 16 * C::WROW>(wam);
+            f.b[m][1] = lds_read<bf16x8, 1 * 16 * C::WROW>(wam);
+            if constexpr (NTW == 4) {
+                f.b[m][2 % NTW] = lds_read<bf16x8, 2 * 16 * C::WROW>(wam);
+                f.b[m][3 % NTW] = lds_read<bf16x8, 3 * 16 * C::WROW>(wam);
             }
         }
-        if (s + S - 1 < steps) issue_group(s + S - 1);
-        lds_wait();
-        lds_pin(raw.w);
-        lds_pin(raw.sw);
-        lds_pin(af[0]);
-        lds_pin(af[1]);
+    };
+    auto frag_pin = [&](Frag &f) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) lds_pin(f.a[mt]);
 #pragma unroll
         for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) lds_pin(bfm[m][nt]);
+            for (int nt = 0; nt < NTW; ++nt) lds_pin(f.b[m][nt]);
+    };
 
-        float sc, ms;
-        dq_scale(raw, sc, ms);
-        const u32x4v d0 = dq_word(raw, 0, sc, ms);
-        const u32x4v d1 = C::NW == 2 ? dq_word(raw, 1, sc, ms) : u32x4v{0, 0, 0, 0};
+    f32x4 acc[NMAT][4][NTW];
 #pragma unroll
-        for (int m = 0; m < NMAT; ++m)
+    for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int nt = 0; nt < NT; ++nt)
-                    acc[m][mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bfm[m][nt], acc[m][mt][nt], 0, 0, 0);
-        dq_store(s + 1, d0, d1);
-        // one MFMA, then a few VALU ops of the dequantization, in turn
+            for (int j = 0; j < NTW; ++j) acc[m][i][j] = f32x4{0, 0, 0, 0};
+
+    // ---- prologue: Wraw(0) and groups 0 .. S-2 in flight, Wraw(0) and
+    // Wraw(1) dequantized, then group S-1 (its Wraw(S) reuses Wraw(0)'s slot).
+    // The waits count DMA instructions in issue order, so the compiler may
+    // not reorder these issues.
+    issue_w(0);
 #pragma unroll
-        for (int i = 0; i < NMAT * 2 * NT; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, C::NW == 1 ? 3 : 3, 0);
-        }
+    for (int g = 0; g < S - 1; ++g) {
+        __asm__ volatile("" ::: "memory");
+        issue_group(g);
     }
+    __asm__ volatile("" ::: "memory");
+    wait_vm_lgkm0<(S - 2) * C::PER>();                    // Wraw(0) and group 0 landed
+    bare_barrier();                                        // ... for every wave's DMA
+    {
+        Raw r0 = dq_load(0), r1 = dq_load(1);
+        lds_wait();
+        lds_pin(r0.w);
+        lds_pin(r0.sw);
+        lds_pin(r1.w);
+        lds_pin(r1.sw);
+        dq_all(0, r0);
+        dq_all(1, r1);
+    }
+    wait_vm_lgkm0<(S - 2) * C::PER>();
+    bare_barrier();                                        // tiles 0, 1 written; Wraw(0)'s slot free
+    issue_group(S - 1);
+    __asm__ volatile("" ::: "memory");
+    Frag fa, fb;
+    frag_load(0, fa);
+    lds_wait();
+    frag_pin(fa);
+
+    // ---- step s: multiply fragments `cur` (step s) while the fragments of
+    // step s+1 load into `nxt` and Wraw(s+2) is dequantized into tile s & 1.
+    // The LDS reads are spread between the MFMAs (a read after every second
+    // MFMA) so that LDS traffic and matrix work overlap instead of running as
+    // two bursts after each barrier.
+    constexpr int NMF = NMAT * 4 * NTW;                    // MFMAs per step
+    constexpr int NFR = 4 + NMAT * NTW;                    // fragment reads per step
+    static_assert(NMF >= NFR, "at least one MFMA per fragment read");
+    auto mfma = [&](int i, Frag &cur) {
+        const int m = i / (4 * NTW), mt = (i / NTW) % 4, nt = i % NTW;
+        acc[m][mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur.a[mt], cur.b[m][nt], acc[m][mt][nt], 0, 0, 0);
+    };
+    auto frag_read = [&](int i, uint32_t j, Frag &f) {     // read i of frag_load(j)
+        const uint32_t xo = (j % S) * C::XSLOT, wo = (j & 1) * C::WBUF;
+        if (i < 4) {
+            f.a[i] = lds_read<bf16x8>(xa[i] + xo);
+        } else {
+            const int m = (i - 4) / NTW, nt = (i - 4) % NTW;
+            f.b[m][nt] = lds_read<bf16x8>(wa + wo + m * BN * C::WROW + nt * 16 * C::WROW);
+        }
+    };
+    auto step = [&](uint32_t s, Frag &cur, Frag &nxt) {
+        wait_vm_lgkm0<(S - 2) * C::PER>();                // group s+1 landed
+        bare_barrier();                                    // ... for every wave; tile s & 1 and X slot s % S free
+        Raw raw = dq_load(s + 2);                          // first: LDS returns in issue order
+        issue_group(s + S);
+        // read r goes after MFMA (r * NMF) / NFR
+#pragma unroll
+        for (int i = 0; i < NMF; ++i) {
+            mfma(i, cur);
+#pragma unroll
+            for (int r = 0; r < NFR; ++r)
+                if ((r * NMF) / NFR == i) {
+                    frag_read(r, s + 1, nxt);
+                    if (r == NFR / 2) {
+                        lds_wait_n<NFR / 2 + 1>();         // raw landed (the newest reads may fly)
+                        lds_pin(raw.w);
+                        lds_pin(raw.sw);
+                    }
+                }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        dq_all(s + 2, raw);
+        lds_wait();                                        // step s+1's fragments and the tile writes
+        frag_pin(nxt);
+    };
+    uint32_t s = 0;
+    for (; s + 1 < steps; s += 2) {
+        step(s, fa, fb);
+        step(s + 1, fb, fa);
+    }
+    if (s < steps) step(s, fa, fb);
 
     // ---- the K halves meet: group 1 parks its sums in LDS, group 0 adds and stores
     wait_vm_lgkm0<0>();
     bare_barrier();
-    float *red = (float *)sm;                              // [wave & 3][m][mt][nt][4][64]
+    float *red = (float *)sm;                              // [wave & 3][m][mt][nt][64 lanes][4]
     const int rw = wave & 3;
     if (grp == 1) {
 #pragma unroll
         for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
+            for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-                for (int nt = 0; nt < NT; ++nt)
-                    *(f32x4 *)(red + ((((rw * NMAT + m) * 2 + mt) * NT + nt) * 64 + lane) * 4) = acc[m][mt][nt];
+                for (int nt = 0; nt < NTW; ++nt)
+                    *(f32x4 *)(red + ((((rw * NMAT + m) * 4 + mt) * NTW + nt) * 64 + lane) * 4) = acc[m][mt][nt];
     }
     __syncthreads();
     if (grp == 1) return;
 #pragma unroll
     for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
-                acc[m][mt][nt] += *(const f32x4 *)(red + ((((rw * NMAT + m) * 2 + mt) * NT + nt) * 64 + lane) * 4);
+            for (int nt = 0; nt < NTW; ++nt)
+                acc[m][mt][nt] += *(const f32x4 *)(red + ((((rw * NMAT + m) * 4 + mt) * NTW + nt) * 64 + lane) * 4);
 
-    // epilogue: lane holds tokens (lane>>4)*4 + i of each 16-row tile, feature lane & 15
+    // epilogue: lane holds tokens (lane>>4)*4 + i of each 16-row tile, feature
+    // lane & 15.  Split K: the two halves add into Y, which starts at zero
+    // (two addends from zero give the same sum in either order).
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            const uint32_t n = n0 + nt * 16 + (lane & 15);
+        for (int nt = 0; nt < NTW; ++nt) {
+            const uint32_t n = n0 + wc * (BN / 2) + nt * 16 + (lane & 15);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const uint32_t t = t0 + wt + mt * 16 + (lane >> 4) * 4 + i;
-                if (t < a.n_tok && n < a.M) {
+                const uint32_t t = t0 + wr * 64 + mt * 16 + (lane >> 4) * 4 + i;
+                if (t < a.n_tok && n < Mloc) {
                     float v = acc[0][mt][nt][i];
                     if (NMAT == 2) v = gelu_tanh(v) * acc[NMAT - 1][mt][nt][i];
-                    a.Y[(size_t)t * a.M + n] = v;
+                    float *y = Yp + (size_t)t * Mloc + n;
+                    if (ksplit == 1) *y = v;
+                    else unsafeAtomicAdd(y, v);
                 }
             }
         }
 }
 
+// ksplit 2 (two workgroups per tile, each half of K) needs Y zeroed first,
+// K >= 128, and NMAT == 1 (the fused epilogue is not additive).
 template <int NMAT, int BN, bool REP, int S>
-static void launch_gemm_p(hipStream_t st, const GemmArgs &a) {
-    const uint32_t n_ct = (a.M + BN - 1) / BN, n_tt = (a.n_tok + 127) / 128;
-    const uint32_t per = (n_ct * n_tt + 7) / 8;
-    k_q4gemm_p<NMAT, BN, REP, S><<<8 * per, 512, 0, st>>>(a, n_ct, n_tt);
+static void launch_gemm_p(hipStream_t st, const GemmArgs &a, uint32_t ksplit = 1) {
+    const uint32_t n_ct = (a.M + BN - 1) / BN + (a.Mg[0] + BN - 1) / BN + (a.Mg[1] + BN - 1) / BN;
+    const uint32_t n_tt = (a.n_tok + 127) / 128;
+    const uint32_t per = (n_ct * n_tt * ksplit + 7) / 8;
+    k_q4gemm_p<NMAT, BN, REP, S><<<8 * per, 512, 0, st>>>(a, n_ct, n_tt, ksplit);
+}
+
+static void launch_to_bf16(hipStream_t st, const float *X, __bf16 *xb, size_t n, float *z, size_t nz) {
+    const size_t m = n > nz ? n : nz;
+    unsigned g = (unsigned)((m / 4 + 255) / 256);
+    if (g > 8192) g = 8192;
+    if (g == 0) g = 1;
+    k_to_bf16<<<g, 256, 0, st>>>(X, xb, n, z, nz);
+}
+
+// Launch shapes for one pipelined single-matrix contraction (K % 64 == 0),
+// from sweeps at 512 tokens: 128-token x 64-feature tiles when they give at
+// least ~200 workgroups; otherwise the same tiles with K split in two; and
+// for long K (>= 8192) 128 x 128 tiles with K split in two, whose larger
+// per-step work pays for itself over the longer loop.
+enum class PipeShape { BN64, BN64_K2, BN128_K2 };
+static PipeShape pipe_shape(uint32_t n_tok, uint32_t M, uint32_t K) {
+    const uint32_t tt = (n_tok + 127) / 128;
+    if (K >= 8192 && 2 * ((M + 127) / 128) * tt >= 192) return PipeShape::BN128_K2;
+    if (((M + 63) / 64) * tt >= 192 || K < 128) return PipeShape::BN64;
+    return PipeShape::BN64_K2;
+}
+
+template <bool REP>
+static void launch_pipe(hipStream_t st, const GemmArgs &a, PipeShape ps) {
+    if (ps == PipeShape::BN64) launch_gemm_p<1, 64, REP, 4>(st, a, 1);
+    else if (ps == PipeShape::BN64_K2) launch_gemm_p<1, 64, REP, 4>(st, a, 2);
+    else launch_gemm_p<1, 128, REP, 4>(st, a, 2);
 }
 
 int launch_q4gemm(chn_ctx *ctx, int nmat, const float *X, const uint32_t *W0, const uint32_t *W1, float *Y,
                   uint32_t n_tok, uint32_t M, uint32_t K, __bf16 *xb, bool repacked) {
     const size_t n = (size_t)n_tok * K;
-    unsigned g = (unsigned)((n / 4 + 255) / 256);
-    if (g > 8192) g = 8192;
-    if (g == 0) g = 1;
-    k_to_bf16<<<g, 256, 0, ctx->stream>>>(X, xb, n);
-    CHN_LAUNCHED(ctx, "k_to_bf16");
     GemmArgs a{xb, W0, W1, Y, n_tok, M, K};
     if (nmat == 1 && K % 64 == 0) {
-        if (repacked) launch_gemm_p<1, 64, true, 4>(ctx->stream, a);
-        else launch_gemm_p<1, 64, false, 4>(ctx->stream, a);
+        const PipeShape ps = pipe_shape(n_tok, M, K);
+        const bool split = ps != PipeShape::BN64;
+        launch_to_bf16(ctx->stream, X, xb, n, split ? Y : nullptr, split ? (size_t)n_tok * M : 0);
+        CHN_LAUNCHED(ctx, "k_to_bf16");
+        if (repacked) launch_pipe<true>(ctx->stream, a, ps);
+        else launch_pipe<false>(ctx->stream, a, ps);
         CHN_LAUNCHED(ctx, "k_q4gemm_p");
         return CHN_OK;
     }
+    launch_to_bf16(ctx->stream, X, xb, n, nullptr, 0);
+    CHN_LAUNCHED(ctx, "k_to_bf16");
     dim3 grid((M + GN - 1) / GN, (n_tok + GT - 1) / GT);
     if (repacked) {
         if (nmat == 1) k_q4gemm<1, true, kGemmKB><<<grid, 256, 0, ctx->stream>>>(a);
@@ -618,6 +725,31 @@ int launch_q4gemm(chn_ctx *ctx, int nmat, const float *X, const uint32_t *W0, co
         else k_q4gemm<2, false, kGemmKB><<<grid, 256, 0, ctx->stream>>>(a);
     }
     CHN_LAUNCHED(ctx, "k_q4gemm");
+    return CHN_OK;
+}
+
+// q, k and v of one layer in one launch: three repacked matrices over the
+// same activations (one bf16 conversion), 128 x 64 tiles.
+int launch_q4gemm_qkv(chn_ctx *ctx, const float *X, const uint32_t *Wq, const uint32_t *Wk, const uint32_t *Wv,
+                      float *Yq, float *Yk, float *Yv, uint32_t n_tok, uint32_t Mq, uint32_t Mkv, uint32_t K,
+                      __bf16 *xb) {
+    if (K % 64 != 0) {
+        int rc = launch_q4gemm(ctx, 1, X, Wq, nullptr, Yq, n_tok, Mq, K, xb, true);
+        if (!rc) rc = launch_q4gemm(ctx, 1, X, Wk, nullptr, Yk, n_tok, Mkv, K, xb, true);
+        if (!rc) rc = launch_q4gemm(ctx, 1, X, Wv, nullptr, Yv, n_tok, Mkv, K, xb, true);
+        return rc;
+    }
+    launch_to_bf16(ctx->stream, X, xb, (size_t)n_tok * K, nullptr, 0);
+    CHN_LAUNCHED(ctx, "k_to_bf16");
+    GemmArgs a{xb, Wq, nullptr, Yq, n_tok, Mq, K};
+    a.Wg[0] = Wk;
+    a.Yg[0] = Yk;
+    a.Mg[0] = Mkv;
+    a.Wg[1] = Wv;
+    a.Yg[1] = Yv;
+    a.Mg[1] = Mkv;
+    launch_gemm_p<1, 64, true, 4>(ctx->stream, a, 1);
+    CHN_LAUNCHED(ctx, "k_q4gemm_p");
     return CHN_OK;
 }
 

@@ -740,9 +740,7 @@ extern "C" int chn_prefill(chn_model *m, const uint32_t *tokens, uint32_t n, con
         const float theta = l.full ? c.rope_theta_full : c.rope_theta;
         if (i == 0) P_(launch_rmsnorm(s, m->px, nullptr, l.in_norm, m->pn, H, n, eps, 1.0f, false));
         const uint32_t D = l.D, nkv = l.nkv, qd = l.qd, kvd = l.kvd, gqa = l.gqa;
-        P_(launch_q4gemm(ctx, 1, m->pn, l.Wq, nullptr, m->pq, n, qd, H, m->pxb, true));
-        P_(launch_q4gemm(ctx, 1, m->pn, l.Wk, nullptr, m->pk, n, kvd, H, m->pxb, true));
-        P_(launch_q4gemm(ctx, 1, m->pn, l.Wv, nullptr, m->pv, n, kvd, H, m->pxb, true));
+        P_(launch_q4gemm_qkv(ctx, m->pn, l.Wq, l.Wk, l.Wv, m->pq, m->pk, m->pv, n, qd, kvd, H, m->pxb));
         P_(launch_batch_qkv_rope(s, m->pq, m->pk, m->pv, l.q_norm, l.k_norm, m->pq, l.kc, l.vc, m->pslots,
                                  num_prev_slots, start_clock, n, nq, nkv, D, l.rot, (int)c.k_eq_v, theta, eps));
         // sliding layers see the last 1024 slots (shaders/batch_causal_attn.wgsl:53)
