@@ -584,6 +584,223 @@ __global__ __launch_bounds__(256) void k_prefill_attn(const float *__restrict__ 
     });
 }
 
+// ---------------------------------------------------------------------
+// Prefill attention on the matrix cores, head_dim 256.
+//
+// Same result as k_prefill_attn (an online softmax over each query's causal
+// window), computed per workgroup for 64 query rows (64 / GQA tokens x the
+// GQA heads of one KV head) against 32-key chunks of the slot list:
+//  * scores are formed transposed, S^T = K Q^T, with
+//    v_mfma_f32_16x16x32_bf16; each fp32 operand is split into bf16 high
+//    and low parts and a product is hi*hi + hi*lo + lo*hi (the dropped lo*lo
+//    term is below 2^-16 of it), so the scores keep close to fp32 accuracy;
+//  * the C layout of S^T puts keys 4g..4g+3 of each 16-key tile, for query
+//    lane & 15, in lane group g = lane >> 4 - exactly the B-operand layout of
+//    O^T = V^T P^T once the chunk's keys are permuted (positions 8g .. 8g+7
+//    hold keys 4g..4g+3 and 16+4g..16+4g+3), so probabilities stay in
+//    registers;
+//  * K (row-major) and V (transposed, permuted) chunks are staged in LDS as
+//    bf16 high/low planes, rows padded against bank conflicts; the next
+//    chunk's rows load into registers while the current one is multiplied.
+typedef __bf16 pbf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 pbf16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t pu32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t pu32x2 __attribute__((ext_vector_type(2)));
+
+// x -> (bf16 hi, bf16 lo) with hi + lo = x to within 2^-18 |x|, two lanes
+// of x per 32-bit word.
+struct HiLo {
+    uint32_t hi, lo;
+};
+__device__ __forceinline__ HiLo split_bf16x2(float a, float b) {
+    const pbf16x2 h = {(__bf16)a, (__bf16)b};
+    const uint32_t hi = __builtin_bit_cast(uint32_t, h);
+    const float ra = a - __builtin_bit_cast(float, hi << 16);
+    const float rb = b - __builtin_bit_cast(float, hi & 0xffff0000u);
+    const pbf16x2 l = {(__bf16)ra, (__bf16)rb};
+    return HiLo{hi, __builtin_bit_cast(uint32_t, l)};
+}
+template <typename V>
+__device__ __forceinline__ void put_hilo(V &h, V &l, int i, float a, float b) {
+    const HiLo t = split_bf16x2(a, b);
+    h[i] = t.hi;
+    l[i] = t.lo;
+}
+
+constexpr int kPaNK = 32;                 // keys per chunk
+constexpr int kPaKRow = 256 * 2 + 16;     // bytes per staged K row (bf16, padded)
+constexpr int kPaVRow = kPaNK * 2 + 16;   // bytes per staged V^T row (bf16, padded)
+
+template <int GQA>
+__global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict__ Q, const float *__restrict__ Kc,
+                                                         const float *__restrict__ Vc,
+                                                         const uint32_t *__restrict__ slots, uint32_t num_prev,
+                                                         uint32_t n_tok, uint32_t num_q_heads, uint32_t kv_dim,
+                                                         float scale, uint32_t window, float *__restrict__ out) {
+    constexpr int D = 256, NK = kPaNK, TQ = 64 / GQA;
+    __shared__ __attribute__((aligned(16))) unsigned char kh_s[NK * kPaKRow], kl_s[NK * kPaKRow];
+    __shared__ __attribute__((aligned(16))) unsigned char vh_s[D * kPaVRow], vl_s[D * kPaVRow];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const uint32_t kvh = blockIdx.y;
+    // this lane's query: column c of the wave's 16 rows
+    const int qi = wave * 16 + c;
+    const uint32_t tq = blockIdx.x * TQ + qi / GQA, head = kvh * GQA + qi % GQA;
+    const uint32_t tqc = min(tq, n_tok - 1);
+    const uint32_t Sq = num_prev + tqc + 1;                        // keys [startq, Sq)
+    const uint32_t startq = (window > 0 && Sq > window) ? Sq - window : 0;
+    // the workgroup's key range: from its first token's start to its last token
+    const uint32_t t_first = blockIdx.x * TQ, t_last = min(t_first + TQ - 1, n_tok - 1);
+    const uint32_t S_first = num_prev + t_first + 1, S_end = num_prev + t_last + 1;
+    const uint32_t k_begin = (window > 0 && S_first > window) ? S_first - window : 0;
+
+    // Q^T operand: lane holds query c, dims 32 j + 8 g .. +8, as hi / lo bf16
+    pbf16x8 qh[8], ql[8];
+    {
+        const float *qrow = Q + ((size_t)tqc * num_q_heads + head) * D + 8 * g;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const f4 a = *(const f4 *)(qrow + 32 * j), b = *(const f4 *)(qrow + 32 * j + 4);
+            pu32x4 h, l;
+            put_hilo(h, l, 0, a.x, a.y);
+            put_hilo(h, l, 1, a.z, a.w);
+            put_hilo(h, l, 2, b.x, b.y);
+            put_hilo(h, l, 3, b.z, b.w);
+            qh[j] = __builtin_bit_cast(pbf16x8, h);
+            ql[j] = __builtin_bit_cast(pbf16x8, l);
+        }
+    }
+
+    // staging assignment: K rows: key tid >> 3, dims (tid & 7) * 32 .. +32;
+    // V: keys 4 (tid >> 5) .. +4, dims (tid & 31) * 8 .. +8
+    const int sk_key = tid >> 3, sk_d0 = (tid & 7) * 32;
+    const int sv_a = tid >> 5, sv_d0 = (tid & 31) * 8;
+    const int sv_p = sv_a < 4 ? 8 * sv_a : 8 * (sv_a - 4) + 4;   // V^T position of key 4 sv_a
+    f4 kreg[8], vreg[8];
+    auto gload = [&](uint32_t c0) {
+        const uint32_t pk = c0 + sk_key;
+        if (pk < S_end) {
+            const float *kr = Kc + (size_t)slots[pk] * kv_dim + kvh * D + sk_d0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) kreg[i] = *(const f4 *)(kr + 4 * i);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) kreg[i] = f4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t pv = c0 + 4 * sv_a + k;
+            if (pv < S_end) {
+                const float *vr = Vc + (size_t)slots[pv] * kv_dim + kvh * D + sv_d0;
+                vreg[2 * k] = *(const f4 *)vr;
+                vreg[2 * k + 1] = *(const f4 *)(vr + 4);
+            } else {
+                vreg[2 * k] = f4{0, 0, 0, 0};
+                vreg[2 * k + 1] = f4{0, 0, 0, 0};
+            }
+        }
+    };
+    auto stage = [&]() {
+        unsigned char *kh = kh_s + sk_key * kPaKRow + sk_d0 * 2, *kl = kl_s + sk_key * kPaKRow + sk_d0 * 2;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            pu32x4 h, l;
+            put_hilo(h, l, 0, kreg[2 * i].x, kreg[2 * i].y);
+            put_hilo(h, l, 1, kreg[2 * i].z, kreg[2 * i].w);
+            put_hilo(h, l, 2, kreg[2 * i + 1].x, kreg[2 * i + 1].y);
+            put_hilo(h, l, 3, kreg[2 * i + 1].z, kreg[2 * i + 1].w);
+            *(pu32x4 *)(kh + 16 * i) = h;
+            *(pu32x4 *)(kl + 16 * i) = l;
+        }
+        // V^T: for each of the 8 dims, keys 4 sv_a .. +4 (4 bf16 = 8 bytes)
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            float v[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[k] = vreg[2 * k + d / 4][d % 4];
+            pu32x2 h, l;
+            put_hilo(h, l, 0, v[0], v[1]);
+            put_hilo(h, l, 1, v[2], v[3]);
+            const int off = (sv_d0 + d) * kPaVRow + sv_p * 2;
+            *(pu32x2 *)(vh_s + off) = h;
+            *(pu32x2 *)(vl_s + off) = l;
+        }
+    };
+
+    f4 o[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[i] = f4{0, 0, 0, 0};
+    float m = -INFINITY, l = 0.0f;
+
+    if (k_begin < S_end) gload(k_begin);
+    for (uint32_t c0 = k_begin; c0 < S_end; c0 += NK) {
+        __syncthreads();                                           // previous chunk's reads done
+        stage();
+        __syncthreads();
+        if (c0 + NK < S_end) gload(c0 + NK);
+
+        // S^T tile tt: keys 16 tt + 4 g + i, query c
+        f4 sacc[2] = {f4{0, 0, 0, 0}, f4{0, 0, 0, 0}};
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int off = (16 * tt + c) * kPaKRow + (32 * j + 8 * g) * 2;
+                const pbf16x8 ah = *(const pbf16x8 *)(kh_s + off), al = *(const pbf16x8 *)(kl_s + off);
+                sacc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, qh[j], sacc[tt], 0, 0, 0);
+                sacc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, ql[j], sacc[tt], 0, 0, 0);
+                sacc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, qh[j], sacc[tt], 0, 0, 0);
+            }
+        // online softmax for query c over this chunk (lane groups g hold 8 keys each)
+        float sv[8];
+        float cmax = -INFINITY;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t kp = c0 + 16 * tt + 4 * g + i;
+                const bool ok = kp >= startq && kp < Sq;
+                const float v = ok ? sacc[tt][i] * scale : -INFINITY;
+                sv[4 * tt + i] = v;
+                cmax = fmaxf(cmax, v);
+            }
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+        const float m_new = fmaxf(m, cmax);
+        const float alpha = (m_new == -INFINITY) ? 1.0f : __expf(m - m_new);
+        float psum = 0.0f, pv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            pv[i] = sv[i] == -INFINITY ? 0.0f : __expf(sv[i] - m_new);
+            psum += pv[i];
+        }
+        psum += __shfl_xor(psum, 16, 64);
+        psum += __shfl_xor(psum, 32, 64);
+        l = l * alpha + psum;
+        m = m_new;
+        pu32x4 ph, pl;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) put_hilo(ph, pl, i, pv[2 * i], pv[2 * i + 1]);
+        const pbf16x8 bh = __builtin_bit_cast(pbf16x8, ph), bl = __builtin_bit_cast(pbf16x8, pl);
+        // O^T tile dt: dims 16 dt + 4 g + i, query c
+#pragma unroll
+        for (int dt = 0; dt < 16; ++dt) {
+            o[dt] *= alpha;
+            const int off = (16 * dt + c) * kPaVRow + 16 * g;
+            const pbf16x8 ah = *(const pbf16x8 *)(vh_s + off), al = *(const pbf16x8 *)(vl_s + off);
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, o[dt], 0, 0, 0);
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, o[dt], 0, 0, 0);
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, o[dt], 0, 0, 0);
+        }
+    }
+    if (tq >= n_tok) return;
+    const float inv = 1.0f / (l + 1e-9f);
+    float *orow = out + ((size_t)tq * num_q_heads + head) * D + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt) *(f4 *)(orow + 16 * dt) = o[dt] * inv;
+}
+
 static int launch_decode_impl(chn_ctx *ctx, const float *q, float *kc, float *vc, const uint32_t *slots,
                               const uint32_t *n_slots, uint32_t max_slots, uint32_t num_q_heads, uint32_t head_dim,
                               uint32_t kv_dim, uint32_t gqa, float scale, float *out, float *ws, uint32_t *xp,
@@ -653,6 +870,20 @@ int launch_rope_decode_attn(chn_ctx *ctx, const float *q_in, const float *k_in, 
 int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const float *vc, const uint32_t *slots,
                         uint32_t n_tok, uint32_t num_prev, uint32_t num_q_heads, uint32_t head_dim, uint32_t kv_dim,
                         uint32_t gqa, float scale, uint32_t window, float *out) {
+    if (head_dim == 256 && (gqa == 1 || gqa == 2 || gqa == 4 || gqa == 8)) {
+        const uint32_t tq = 64 / gqa;
+        const dim3 mgrid((n_tok + tq - 1) / tq, num_q_heads / gqa);
+#define CHN_PATTN_MF(G) \
+    k_prefill_attn_mf<G><<<mgrid, 256, 0, st>>>(q, kc, vc, slots, num_prev, n_tok, num_q_heads, kv_dim, scale, window, out)
+        switch (gqa) {
+        case 1: CHN_PATTN_MF(1); break;
+        case 2: CHN_PATTN_MF(2); break;
+        case 4: CHN_PATTN_MF(4); break;
+        default: CHN_PATTN_MF(8); break;
+        }
+#undef CHN_PATTN_MF
+        return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
+    }
     dim3 grid(n_tok, num_q_heads / gqa);
 #define CHN_PATTN(DV, G) \
     k_prefill_attn<DV, G><<<grid, 256, 0, st>>>(q, kc, vc, slots, num_prev, num_q_heads, kv_dim, scale, window, out)

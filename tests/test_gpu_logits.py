@@ -179,6 +179,9 @@ def test_batch_qkv_rope(ctx, nq, nkv, D, rot, keqv, n, off):
     (8, 4, 256, 5, 300, 0),
     (4, 1, 512, 33, 17, 20),
     (16, 2, 256, 1, 0, 0),
+    (16, 2, 256, 512, 0, 1024),   # 12B 512-token prefill (matrix-core path)
+    (8, 8, 256, 20, 40, 0),       # GQA 8: 8 tokens per tile
+    (4, 1, 256, 45, 10, 30),      # GQA 1, window inside the list
 ])
 def test_batch_causal_attn(ctx, nq, gqa, D, n, prev, window):
     kvh = nq // gqa
