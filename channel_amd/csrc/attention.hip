@@ -673,11 +673,11 @@ __global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict
     }
 
     // staging assignment: K rows: key tid >> 3, dims (tid & 7) * 32 .. +32;
-    // V: keys 4 (tid >> 5) .. +4, dims (tid & 31) * 8 .. +8
+    // V: dim tid, all 32 keys (a V^T row; consecutive lanes read consecutive
+    // dims of one key row and write consecutive padded V^T rows)
     const int sk_key = tid >> 3, sk_d0 = (tid & 7) * 32;
-    const int sv_a = tid >> 5, sv_d0 = (tid & 31) * 8;
-    const int sv_p = sv_a < 4 ? 8 * sv_a : 8 * (sv_a - 4) + 4;   // V^T position of key 4 sv_a
-    f4 kreg[8], vreg[8];
+    f4 kreg[8];
+    float vreg[kPaNK];
     auto gload = [&](uint32_t c0) {
         const uint32_t pk = c0 + sk_key;
         if (pk < S_end) {
@@ -689,16 +689,9 @@ __global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict
             for (int i = 0; i < 8; ++i) kreg[i] = f4{0, 0, 0, 0};
         }
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t pv = c0 + 4 * sv_a + k;
-            if (pv < S_end) {
-                const float *vr = Vc + (size_t)slots[pv] * kv_dim + kvh * D + sv_d0;
-                vreg[2 * k] = *(const f4 *)vr;
-                vreg[2 * k + 1] = *(const f4 *)(vr + 4);
-            } else {
-                vreg[2 * k] = f4{0, 0, 0, 0};
-                vreg[2 * k + 1] = f4{0, 0, 0, 0};
-            }
+        for (int k = 0; k < kPaNK; ++k) {
+            const uint32_t pv = c0 + k;
+            vreg[k] = pv < S_end ? Vc[(size_t)slots[pv] * kv_dim + kvh * D + tid] : 0.0f;
         }
     };
     auto stage = [&]() {
@@ -713,19 +706,26 @@ __global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict
             *(pu32x4 *)(kh + 16 * i) = h;
             *(pu32x4 *)(kl + 16 * i) = l;
         }
-        // V^T: for each of the 8 dims, keys 4 sv_a .. +4 (4 bf16 = 8 bytes)
+        // V^T row `tid`: position 8 q + j holds key 4 q + j (j < 4) or
+        // 16 + 4 q + j - 4 (j >= 4)
 #pragma unroll
-        for (int d = 0; d < 8; ++d) {
-            float v[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) v[k] = vreg[2 * k + d / 4][d % 4];
-            pu32x2 h, l;
-            put_hilo(h, l, 0, v[0], v[1]);
-            put_hilo(h, l, 1, v[2], v[3]);
-            const int off = (sv_d0 + d) * kPaVRow + sv_p * 2;
-            *(pu32x2 *)(vh_s + off) = h;
-            *(pu32x2 *)(vl_s + off) = l;
+        for (int q = 0; q < 4; ++q) {
+            pu32x4 h, l;
+            put_hilo(h, l, 0, vreg[4 * q], vreg[4 * q + 1]);
+            put_hilo(h, l, 1, vreg[4 * q + 2], vreg[4 * q + 3]);
+            put_hilo(h, l, 2, vreg[16 + 4 * q], vreg[16 + 4 * q + 1]);
+            put_hilo(h, l, 3, vreg[16 + 4 * q + 2], vreg[16 + 4 * q + 3]);
+            const int off = tid * kPaVRow + 16 * q;
+            *(pu32x4 *)(vh_s + off) = h;
+            *(pu32x4 *)(vl_s + off) = l;
         }
+    };
+    // Workgroup barrier that orders LDS only: prefetched global loads stay in
+    // flight across it (the compiler waits for them where they are used).
+    auto lds_barrier = [&]() {
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        __asm__ volatile("" ::: "memory");
     };
 
     f4 o[16];
@@ -735,9 +735,9 @@ __global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict
 
     if (k_begin < S_end) gload(k_begin);
     for (uint32_t c0 = k_begin; c0 < S_end; c0 += NK) {
-        __syncthreads();                                           // previous chunk's reads done
+        lds_barrier();                                             // previous chunk's reads done
         stage();
-        __syncthreads();
+        lds_barrier();
         if (c0 + NK < S_end) gload(c0 + NK);
 
         // S^T tile tt: keys 16 tt + 4 g + i, query c

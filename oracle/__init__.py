@@ -71,8 +71,21 @@ def _load():
 lib = _load()
 
 
-def _c(a, dtype):
-    return np.ascontiguousarray(a, dtype=dtype)
+def _c(a, dtype, need=None):
+    """Contiguous array of dtype; with `need`, at least that many elements
+    (the C routines read exactly the sizes their arguments imply)."""
+    out = np.ascontiguousarray(a, dtype=dtype)
+    if need is not None and out.size < need:
+        raise ValueError(f"buffer of {out.size} elements, need {need}")
+    return out
+
+
+def _q4(W, rows, K):
+    return _c(W, np.uint32, rows * (K // 32) * 5)
+
+
+def _q8(W, rows, K):
+    return _c(W, np.uint32, rows * (K // 32) * 9)
 
 
 def f32_to_f16_bits(v):
@@ -106,13 +119,13 @@ def quantize_q8(w_bf16):
 
 def dequant_q4(W, rows, K):
     out = np.zeros((rows, K), dtype=np.float32)
-    lib.orc_dequant_q4(out, _c(W, np.uint32), rows, K)
+    lib.orc_dequant_q4(out, _q4(W, rows, K), rows, K)
     return out
 
 
 def dequant_q8(W, rows, K):
     out = np.zeros((rows, K), dtype=np.float32)
-    lib.orc_dequant_q8(out, _c(W, np.uint32), rows, K)
+    lib.orc_dequant_q8(out, _q8(W, rows, K), rows, K)
     return out
 
 
@@ -122,13 +135,13 @@ def gelu_tanh(x):
 
 def gemv_q4(W, x, M, K):
     y = np.zeros(M, dtype=np.float32)
-    lib.orc_gemv_q4(_c(W, np.uint32), _c(x, np.float32), y, M, K)
+    lib.orc_gemv_q4(_q4(W, M, K), _c(x, np.float32, K), y, M, K)
     return y
 
 
 def gemv_q4_mt(W, x, M, K, nthreads):
     y = np.zeros(M, dtype=np.float32)
-    lib.orc_gemv_q4_mt(_c(W, np.uint32), _c(x, np.float32), y, M, K, int(nthreads))
+    lib.orc_gemv_q4_mt(_q4(W, M, K), _c(x, np.float32, K), y, M, K, int(nthreads))
     return y
 
 
@@ -143,7 +156,7 @@ def fused_qkv_q4(Wq, Wk, Wv, x, q_dim, kv_dim, K):
 
 def fused_mlp_q4(Wg, Wu, x, M, K):
     act = np.zeros(M, np.float32)
-    lib.orc_fused_mlp_q4(_c(Wg, np.uint32), _c(Wu, np.uint32), _c(x, np.float32), act, M, K)
+    lib.orc_fused_mlp_q4(_q4(Wg, M, K), _q4(Wu, M, K), _c(x, np.float32, K), act, M, K)
     return act
 
 
@@ -157,25 +170,25 @@ def fused_mlp_step_mt(Wg, Wu, Wd, x, H, I, nthreads):
 
 def gemv_q8_mt(W, x, M, K, nthreads):
     y = np.zeros(M, dtype=np.float32)
-    lib.orc_gemv_q8_mt(_c(W, np.uint32), _c(x, np.float32), y, M, K, int(nthreads))
+    lib.orc_gemv_q8_mt(_q8(W, M, K), _c(x, np.float32, K), y, M, K, int(nthreads))
     return y
 
 
 def gemv_q8(W, x, M, K):
     y = np.zeros(M, dtype=np.float32)
-    lib.orc_gemv_q8(_c(W, np.uint32), _c(x, np.float32), y, M, K)
+    lib.orc_gemv_q8(_q8(W, M, K), _c(x, np.float32, K), y, M, K)
     return y
 
 
 def batch_gemm_q4(W, X, n_tok, M, K):
     Y = np.zeros((n_tok, M), np.float32)
-    lib.orc_batch_gemm_q4(_c(W, np.uint32), _c(X, np.float32), Y, n_tok, M, K)
+    lib.orc_batch_gemm_q4(_q4(W, M, K), _c(X, np.float32, n_tok * K), Y, n_tok, M, K)
     return Y
 
 
 def batch_gemm_q4_bf16(W, X, n_tok, M, K):
     Y = np.zeros((n_tok, M), np.float32)
-    lib.orc_batch_gemm_q4_bf16(_c(W, np.uint32), _c(X, np.float32), Y, n_tok, M, K)
+    lib.orc_batch_gemm_q4_bf16(_q4(W, M, K), _c(X, np.float32, n_tok * K), Y, n_tok, M, K)
     return Y
 
 
