@@ -676,25 +676,40 @@ __global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict
     // V: dim tid, all 32 keys (a V^T row; consecutive lanes read consecutive
     // dims of one key row and write consecutive padded V^T rows)
     const int sk_key = tid >> 3, sk_d0 = (tid & 7) * 32;
-    f4 kreg[8];
-    float vreg[kPaNK];
-    auto gload = [&](uint32_t c0) {
-        const uint32_t pk = c0 + sk_key;
-        if (pk < S_end) {
-            const float *kr = Kc + (size_t)slots[pk] * kv_dim + kvh * D + sk_d0;
+    // The next chunk's rows load into registers while this chunk is
+    // multiplied.
+    struct Rows {
+        f4 k[8];
+        float v[kPaNK];
+        uint32_t nvalid;                                           // keys of the chunk inside the list
+    };
+    // The chunk's 32 slot indices arrive in one vector load (lane j holds
+    // key j's slot; keys past the list repeat its last slot); rows then take
+    // theirs by shuffle (K, per lane) or readlane (V, uniform).  Every row
+    // load is unconditional, so they issue back to back and their waits fall
+    // where the rows are staged; keys past the list are zeroed there.
+    auto gload = [&](uint32_t c0, Rows &r) {
+        const uint32_t pj = min(c0 + (lane & (kPaNK - 1)), S_end - 1);
+        const uint32_t slj = slots[pj];
+        r.nvalid = min((uint32_t)kPaNK, S_end - c0);
+        const uint32_t ks = (uint32_t)__shfl((int)slj, sk_key, 64);
+        const float *kr = Kc + (size_t)ks * kv_dim + kvh * D + sk_d0;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) kreg[i] = *(const f4 *)(kr + 4 * i);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) kreg[i] = f4{0, 0, 0, 0};
-        }
+        for (int i = 0; i < 8; ++i) r.k[i] = *(const f4 *)(kr + 4 * i);
 #pragma unroll
         for (int k = 0; k < kPaNK; ++k) {
-            const uint32_t pv = c0 + k;
-            vreg[k] = pv < S_end ? Vc[(size_t)slots[pv] * kv_dim + kvh * D + tid] : 0.0f;
+            const uint32_t vs = (uint32_t)__builtin_amdgcn_readlane((int)slj, k);
+            r.v[k] = Vc[(size_t)vs * kv_dim + kvh * D + tid];
         }
     };
-    auto stage = [&]() {
+    auto stage = [&](const Rows &r) {
+        f4 kreg[8];
+        float vreg[kPaNK];
+        const bool kok = (uint32_t)sk_key < r.nvalid;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) kreg[i] = kok ? r.k[i] : f4{0, 0, 0, 0};
+#pragma unroll
+        for (int k = 0; k < kPaNK; ++k) vreg[k] = (uint32_t)k < r.nvalid ? r.v[k] : 0.0f;
         unsigned char *kh = kh_s + sk_key * kPaKRow + sk_d0 * 2, *kl = kl_s + sk_key * kPaKRow + sk_d0 * 2;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -733,12 +748,13 @@ __global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict
     for (int i = 0; i < 16; ++i) o[i] = f4{0, 0, 0, 0};
     float m = -INFINITY, l = 0.0f;
 
-    if (k_begin < S_end) gload(k_begin);
+    Rows rows;
+    gload(k_begin, rows);
     for (uint32_t c0 = k_begin; c0 < S_end; c0 += NK) {
         lds_barrier();                                             // previous chunk's reads done
-        stage();
+        stage(rows);
         lds_barrier();
-        if (c0 + NK < S_end) gload(c0 + NK);
+        if (c0 + NK < S_end) gload(c0 + NK, rows);
 
         // S^T tile tt: keys 16 tt + 4 g + i, query c
         f4 sacc[2] = {f4{0, 0, 0, 0}, f4{0, 0, 0, 0}};
