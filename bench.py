@@ -500,7 +500,7 @@ def bench_gemv(ctx, args):
                    "weight_copies_rotated": ncopy},
         "roofline": {"kernel": "k_q4mv<GEMV> (chn_gemv_q4: one launch, x's digit planes made in the kernel)", "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": load_traffic("k_q4mv<GEMV>", "8192x2048"),
+                     "traffic": load_traffic("k_q4mv<GEMV,XIN>", "8192x2048"),
                      "algorithmic_bytes_per_launch": nbytes, "avg_launch_ms": k_ms},
         "cpu_baseline": cpu,
         "dtype": "fp32 accumulate over Q4 weights",
@@ -537,9 +537,11 @@ def bench_prefill(ctx, args):
         "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": ms,
         "config": {"workload": "batched prefill Q4 GEMM 512 tokens x 3840 -> 15360 (bf16 MFMA)",
                    "tokens": T, "K": K, "N": N, "flop_per_step": flops},
-        "roofline": {"kernel": "k_q4gemm<1> (+ k_to_bf16 pre-pass)", "bound": "mfma",
+        "roofline": {"kernel": "k_q4gemm_p<1,64,REF> (128x64 tiles, DMA-pipelined K walk) + k_to_bf16 pre-pass",
+                     "bound": "mfma",
                      "achieved": achieved, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / MFMA_BF16_PEAK_TFLOPS, "traffic": None,
+                     "frac": achieved / MFMA_BF16_PEAK_TFLOPS,
+                     "traffic": load_traffic("k_q4gemm_p<1,64,REF>", "512x3840 -> 15360"),
                      "algorithmic_flop_per_launch": flops,
                      "avg_launch_ms": gpu_ms / args.steps},
         "cpu_baseline": None,
