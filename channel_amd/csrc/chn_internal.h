@@ -312,6 +312,48 @@ __device__ __forceinline__ float rows4_max(float v) {
     return fmaxf(v, xor32_lane(v));
 }
 
+// Transposed pair sums on one lane swap: permlane32_swap(x, y) leaves
+// {x_lo, y_lo} and {x_hi, y_hi}, so lane l of the low half gets
+// x_l + x_{l+32} and lane l of the high half y_{l-32} + y_l (and likewise
+// for rows 0/1 and 2/3 with permlane16_swap).  The two results pass through
+// an empty asm as integers: this compiler otherwise folds "float of result 0
+// + float of result 1" into result 0 + result 0.
+__device__ __forceinline__ float add_swapped(uint32_t a, uint32_t b) {
+    __asm__("" : "+v"(a), "+v"(b));
+    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float swap_add32(float x, float y) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, y),
+                                                    false, false);
+    return add_swapped(r[0], r[1]);
+}
+__device__ __forceinline__ float swap_add16(float x, float y) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, y),
+                                                    false, false);
+    return add_swapped(r[0], r[1]);
+}
+__device__ __forceinline__ float lane_f(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+// Whole-wave sums of two / four values at once.  Every total is formed by
+// the same tree, ((x_l + x_{l^32}) + (x_{l^16} + x_{l^48})) over the 16
+// lanes of a DPP row, taken from the row's lane 0, so wave_sum2(a, b) and
+// wave_sum4(a, b, ., .) give a and b the same bits.
+__device__ __forceinline__ void wave_sum2(float a, float b, float &ta, float &tb) {
+    float c = swap_add32(a, b);       // half 0: a, half 1: b
+    c = row16_sum(swap_add16(c, c));
+    ta = lane_f(c, 0);
+    tb = lane_f(c, 32);
+}
+__device__ __forceinline__ void wave_sum4(float v0, float v1, float v2, float v3, float (&t)[4]) {
+    const float a = swap_add32(v0, v2), b = swap_add32(v1, v3);   // half 0: v0, v1; half 1: v2, v3
+    const float c = row16_sum(swap_add16(a, b));                   // rows 0..3: v0, v1, v2, v3
+    t[0] = lane_f(c, 0);
+    t[1] = lane_f(c, 16);
+    t[2] = lane_f(c, 32);
+    t[3] = lane_f(c, 48);
+}
+
 // Digit planes of one 32-block from the four lanes 4k..4k+3 of a wave that
 // hold its words w = lane & 3 (eight consecutive values each).  All four
 // lanes must call (with zeros where ok is false); only ok lanes store.

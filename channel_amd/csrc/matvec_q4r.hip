@@ -64,20 +64,41 @@ struct RArgs {
 // offsets instead of per-lane 64-bit addresses.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
-// sum_i (q_i - 8) X_i of one block: the signed nibbles times each plane.
+// sum_i (q_i - 8) X_i of one block: the signed nibbles times each plane,
+// in Horner order from the top plane (one accumulator: the dot's own add
+// carries the running sum, so only the first needs a zero).  Exact: the
+// partial sums stay below 2^30 in magnitude.
 __device__ __forceinline__ int block_idot_r(const u32x4r s, const uint32_t (&P)[XP_WORDS]) {
-    int t[XP_PLANES];
+    int acc = 0;
 #pragma unroll
-    for (int p = 0; p < XP_PLANES; ++p) {
-        int a = 0;
+    for (int p = XP_PLANES - 1; p >= 0; --p) {
+        if (p != XP_PLANES - 1) acc *= 16;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) a = __builtin_amdgcn_sdot8((int)s[w], (int)P[p * 4 + w], a, false);
-        t[p] = a;
+        for (int w = 0; w < 4; ++w) acc = __builtin_amdgcn_sdot8((int)s[w], (int)P[p * 4 + w], acc, false);
     }
-    int T = t[XP_PLANES - 1];
+    return acc;
+}
+
+// Whole-wave sums of V per-lane values; the V = 2 and V = 4 forms give
+// each value the same summation tree (gate and up of one row match between
+// the one-row and the two-row gate/up kernels bit for bit).
+template <int V>
+__device__ __forceinline__ void wave_sums(const float (&r)[V], float (&t)[V]) {
+    if constexpr (V == 1) {
+        t[0] = wave_sum64(r[0]);
+    } else if constexpr (V % 4 == 0) {
 #pragma unroll
-    for (int p = XP_PLANES - 2; p >= 0; --p) T = (T << 4) + t[p];
-    return T;
+        for (int i = 0; i < V; i += 4) {
+            float q[4];
+            wave_sum4(r[i], r[i + 1], r[i + 2], r[i + 3], q);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) t[i + k] = q[k];
+        }
+    } else {
+        static_assert(V % 2 == 0, "V must be 1 or even");
+#pragma unroll
+        for (int i = 0; i < V; i += 2) wave_sum2(r[i], r[i + 1], t[i], t[i + 1]);
+    }
 }
 
 template <int MODE>
@@ -184,7 +205,7 @@ __global__ __launch_bounds__(256) void k_q4rmv(RArgs a) {
                 cs[s][c] = sq[s][c];
             }
         if (g + gstride < ngroups) load(g + gstride);
-        float tot[V];
+        float part[V], tot[V];
 #pragma unroll
         for (int s = 0; s < V; ++s) {
             float r = 0.0f;
@@ -194,8 +215,9 @@ __global__ __launch_bounds__(256) void k_q4rmv(RArgs a) {
                 const float sf = (float)__builtin_bit_cast(_Float16, cs[s][c]);
                 r = fmaf((float)T, sf * xs[c], r);
             }
-            tot[s] = wave_sum64(r);
+            part[s] = r;
         }
+        wave_sums<V>(part, tot);
         if (WPR == 1) {
             if (gv && lane == 0) {
 #pragma unroll
@@ -403,6 +425,7 @@ __global__ __launch_bounds__(1024) void k_q4rmv_qkv_nx(RArgs a, NormArgs n) {
                 cs[s][c] = sq[s][c];
             }
         if (g + gstride < ngroups) load(g + gstride);
+        float part[RPW], tot[RPW];
 #pragma unroll
         for (int s = 0; s < RPW; ++s) {
             float r = 0.0f;
@@ -412,9 +435,13 @@ __global__ __launch_bounds__(1024) void k_q4rmv_qkv_nx(RArgs a, NormArgs n) {
                 const float sf = (float)__builtin_bit_cast(_Float16, cs[s][c]);
                 r = fmaf((float)T, sf * xs[c], r);
             }
-            const float tot = wave_sum64(r);
+            part[s] = r;
+        }
+        wave_sums<RPW>(part, tot);
+#pragma unroll
+        for (int s = 0; s < RPW; ++s) {
             const uint32_t row = g * RPW + s;
-            if (lane == 0 && row < a.M) store_r<RV_QKV>(a, row, tot);
+            if (lane == 0 && row < a.M) store_r<RV_QKV>(a, row, tot[s]);
         }
     }
 }
@@ -440,24 +467,27 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     __shared__ float sh[32];
     const uint32_t nrb = a.M / 32;
 
-    u32x4r nq[2][2];
-    uint16_t sq[2][2];
-    auto load = [&](uint32_t row) {
+    struct RowPair {   // this lane's two blocks of one gate row and one up row
+        u32x4r q[2][2];
+        uint16_t s[2][2];
+    };
+    auto load = [&](RowPair &d, uint32_t row) {
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            const u32x4r *N = (s ? a.m1.N : a.m0.N) + (size_t)row * nb;
-            const uint16_t *S = (s ? a.m1.S : a.m0.S) + (size_t)row * nb;
-            nq[s][0] = __builtin_nontemporal_load(N + b0);
-            nq[s][1] = __builtin_nontemporal_load(N + b1);
-            sq[s][0] = __builtin_nontemporal_load(S + b0);
-            sq[s][1] = __builtin_nontemporal_load(S + b1);
+        for (int m = 0; m < 2; ++m) {
+            const u32x4r *N = (m ? a.m1.N : a.m0.N) + (size_t)row * nb;
+            const uint16_t *S = (m ? a.m1.S : a.m0.S) + (size_t)row * nb;
+            d.q[m][0] = __builtin_nontemporal_load(N + b0);
+            d.q[m][1] = __builtin_nontemporal_load(N + b1);
+            d.s[m][0] = __builtin_nontemporal_load(S + b0);
+            d.s[m][1] = __builtin_nontemporal_load(S + b1);
         }
     };
     constexpr int NM = NORM < 0 ? 0 : NORM;
     NormIn nv;
     if (NORM >= 0) norm_load<NM>(n, nb * 32, nv);
     uint32_t rb = blockIdx.x;
-    if (rb < nrb) load(rb * 32 + wave);
+    RowPair nx;
+    if (rb < nrb) load(nx, rb * 32 + wave);
 
     // this lane's two blocks of input planes, in registers
     uint32_t P[2][XP_WORDS];
@@ -473,30 +503,21 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     for (; rb < nrb; rb += gridDim.x) {
 #pragma unroll 1
         for (int j = 0; j < RW; ++j) {
-            u32x4r cq[2][2];
-            uint16_t cs[2][2];
+            const RowPair cur = nx;
+            if (j + 1 < RW) load(nx, rb * 32 + wave + NW * (j + 1));
+            else if (rb + gridDim.x < nrb) load(nx, (rb + gridDim.x) * 32 + wave);
+            float r[2] = {0.0f, 0.0f};
 #pragma unroll
-            for (int s = 0; s < 2; ++s)
-#pragma unroll
-                for (int c = 0; c < 2; ++c) {
-                    cq[s][c] = nq[s][c];
-                    cs[s][c] = sq[s][c];
-                }
-            if (j + 1 < RW) load(rb * 32 + wave + NW * (j + 1));
-            else if (rb + gridDim.x < nrb) load((rb + gridDim.x) * 32 + wave);
-            float rs[2] = {0.0f, 0.0f};
-#pragma unroll
-            for (int s = 0; s < 2; ++s)
+            for (int m = 0; m < 2; ++m)
 #pragma unroll
                 for (int c = 0; c < 2; ++c) {
-                    const int T = block_idot_r(cq[s][c], P[c]);
-                    const float sf = (float)__builtin_bit_cast(_Float16, cs[s][c]);
-                    rs[s] = fmaf((float)T, sf * xs[c], rs[s]);
+                    const int T = block_idot_r(cur.q[m][c], P[c]);
+                    const float sf = (float)__builtin_bit_cast(_Float16, cur.s[m][c]);
+                    r[m] = fmaf((float)T, sf * xs[c], r[m]);
                 }
-            float tot[2];
-#pragma unroll
-            for (int s = 0; s < 2; ++s) tot[s] = wave_sum64(rs[s]);
-            if (lane == 0) sact[wave + NW * j] = gelu_tanh(tot[0]) * tot[1];
+            float t[2];
+            wave_sum2(r[0], r[1], t[0], t[1]);
+            if (lane == 0) sact[wave + NW * j] = gelu_tanh(t[0]) * t[1];
         }
         __syncthreads();
         // an opaque copy of the thread index: otherwise the 24 plane-store

@@ -31,3 +31,40 @@ def test_gemm_lds_waits(tmp_path):
     assert res, "no pipelined GEMM kernel found in the assembly"
     bad = {f: h for f, h in res.items() if h}
     assert not bad, bad
+
+
+def _compile(src, out):
+    cmd = [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+           "-packed-fp32-ops", "-fno-gpu-rdc", "--cuda-device-only", "-S", os.path.join(CSRC, src), "-o", str(out)]
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    assert r.returncode == 0, r.stdout[-2000:]
+    return out.read_text()
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not installed")
+def test_swap_sums_read_both_halves(tmp_path):
+    """The matvec reductions add the two results of each lane swap
+    (v_permlane16/32_swap leaves one value in each operand register).  This
+    compiler has folded such a sum into twice the first result; check that
+    the first float add after every swap reads both swapped registers."""
+    import re
+    asm = _compile("matvec_q4r.hip", tmp_path / "matvec_q4r.s").splitlines()
+    swaps = 0
+    for i, line in enumerate(asm):
+        m = re.match(r"\s*v_permlane(16|32)_swap_b32_e32\s+(v\d+),\s*(v\d+)", line)
+        if not m:
+            continue
+        a, b = m.group(2), m.group(3)
+        # the first float add that reads either swapped register
+        add = None
+        for l in asm[i + 1:i + 16]:
+            if "v_add_f32" in l:
+                regs = re.findall(r"\bv\d+\b", l.split(None, 1)[1])[1:]
+                if a in regs or b in regs:
+                    add = (l, regs)
+                    break
+        if add is None:
+            continue          # a swap used for a lane exchange, not a pair sum
+        assert sorted(add[1]) == sorted([a, b]), (line.strip(), add[0].strip())
+        swaps += 1
+    assert swaps > 0, "no swap sums found in the matvec assembly"
