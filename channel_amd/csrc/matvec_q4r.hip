@@ -275,71 +275,95 @@ __device__ __forceinline__ void st8(float *p, uint32_t t, const float (&v)[8]) {
     *(f32x4r *)(p + 8 * (size_t)t) = f32x4r{v[0], v[1], v[2], v[3]};
     *(f32x4r *)(p + 8 * (size_t)t + 4) = f32x4r{v[4], v[5], v[6], v[7]};
 }
-// Sum over the workgroup: DPP wave sums, then the wave partials in index
-// order.  One barrier: each call takes its own 16-float slice of LDS, so
-// no later write can overtake a read of it.
-__device__ __forceinline__ float wg_sum(float v, float *sh) {
-    v = wave_sum64(v);
+// Sum over the workgroup of C values per thread, in the order a workgroup of
+// C x blockDim threads holding one value each would use: value c of thread
+// t counts as thread t + c * blockDim ("virtual wave" w + c * waves).  DPP
+// wave sums, then the virtual wave partials in index order.  One barrier:
+// each call takes its own 16-float slice of LDS.
+template <int C>
+__device__ __forceinline__ float wg_sum_c(const float (&v)[C], float *sh) {
     const int nw = blockDim.x >> 6;
-    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const float w = wave_sum64(v[c]);
+        if ((threadIdx.x & 63) == 0) sh[(threadIdx.x >> 6) + c * nw] = w;
+    }
     __syncthreads();
     float t = 0.0f;
-    for (int i = 0; i < nw; ++i) t += sh[i];
+    for (int i = 0; i < C * nw; ++i) t += sh[i];
     return t;
 }
 
-// NormArgs' norm over dim values (dim % 32 == 0, dim <= 8 * blockDim), eight
-// per thread, four threads per 32-block: the digit planes of y go to LDS
-// block by block (kLdsBlk words per block: 24 plane words, then the scale;
-// constant offsets from one base per block, and the odd stride keeps a
-// wave's reads of consecutive blocks free of bank conflicts), workgroup 0
-// writes x_out and y.  The same arithmetic, in the same order, as the
-// standalone norm kernel.
+// NormArgs' norm over dim values (dim % 32 == 0, dim <= 8 * C * blockDim):
+// thread t holds the eight values 8 (t + c blockDim) .. + 7 of chunk c < C,
+// four threads per 32-block.  The digit planes of y go to LDS block by block
+// (kLdsBlk words per block: 24 plane words, then the scale; constant offsets
+// from one base per block, and the odd stride keeps a wave's reads of
+// consecutive blocks free of bank conflicts), workgroup 0 writes x_out and
+// y.  The same arithmetic, in the same order, as the standalone norm kernel
+// (eight values per thread, the wave partials in order).
 constexpr int kLdsBlk = XP_WORDS + 1;
 // Split in two so that the norm's inputs are requested before the matvec's
 // first weights: loads complete in issue order, so the norm math then runs
 // while the weights are still in flight.
+template <int C>
 struct NormIn {
-    float xv[8], rv[8], pv[8], wv[8];
+    float xv[C][8], rv[C][8], pv[C][8], wv[C][8];
 };
-template <int MODE>
-__device__ __forceinline__ void norm_load(const NormArgs &n, uint32_t dim, NormIn &v) {
-    const uint32_t t = threadIdx.x;
-    const bool ok = 8 * t < dim;
-    ld8(n.x_in, t, ok, v.xv);
-    if (MODE != NORM_PLAIN) ld8(n.r, t, ok, v.rv);
-    if (MODE == NORM_POST_ADD) ld8(n.pw, t, ok, v.pv);
-    ld8(n.w, t, ok, v.wv);
+template <int MODE, int C>
+__device__ __forceinline__ void norm_load(const NormArgs &n, uint32_t dim, NormIn<C> &v) {
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const uint32_t t = threadIdx.x + c * blockDim.x;
+        const bool ok = 8 * t < dim;
+        ld8(n.x_in, t, ok, v.xv[c]);
+        if (MODE != NORM_PLAIN) ld8(n.r, t, ok, v.rv[c]);
+        if (MODE == NORM_POST_ADD) ld8(n.pw, t, ok, v.pv[c]);
+        ld8(n.w, t, ok, v.wv[c]);
+    }
 }
-template <int MODE>
-__device__ __forceinline__ void norm_to_lds(const NormArgs &n, uint32_t dim, NormIn &v, uint32_t *lp, float *sh) {
-    const uint32_t t = threadIdx.x;
-    const bool ok = 8 * t < dim;
-    float(&xv)[8] = v.xv;
+template <int MODE, int C>
+__device__ __forceinline__ void norm_to_lds(const NormArgs &n, uint32_t dim, NormIn<C> &v, uint32_t *lp,
+                                            float *sh) {
+    float ss[C];
     if (MODE != NORM_PLAIN) {
         if (MODE == NORM_POST_ADD) {
-            float ss = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) ss += v.rv[i] * v.rv[i];
-            ss = wg_sum(ss, sh + 16);
-            const float inv = 1.0f / sqrtf(ss / (float)dim + n.eps);
+            for (int c = 0; c < C; ++c) {
+                ss[c] = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v.rv[i] = (v.rv[i] * inv) * v.pv[i];
+                for (int i = 0; i < 8; ++i) ss[c] += v.rv[c][i] * v.rv[c][i];
+            }
+            const float inv = 1.0f / sqrtf(wg_sum_c<C>(ss, sh + 16) / (float)dim + n.eps);
+#pragma unroll
+            for (int c = 0; c < C; ++c)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v.rv[c][i] = (v.rv[c][i] * inv) * v.pv[c][i];
         }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) xv[i] = (xv[i] + v.rv[i]) * n.scalar;
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v.xv[c][i] = (v.xv[c][i] + v.rv[c][i]) * n.scalar;
     }
-    if (blockIdx.x == 0 && ok) st8(n.x_out, t, xv);
-    float ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ss += xv[i] * xv[i];
-    ss = wg_sum(ss, sh);
-    const float inv = 1.0f / sqrtf(ss / (float)dim + n.eps);
-    float yv[8];
+    for (int c = 0; c < C; ++c) {
+        const uint32_t t = threadIdx.x + c * blockDim.x;
+        if (blockIdx.x == 0 && 8 * t < dim) st8(n.x_out, t, v.xv[c]);
+        ss[c] = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) yv[i] = (xv[i] * inv) * v.wv[i];
-    if (blockIdx.x == 0 && ok && n.y) st8(n.y, t, yv);
-    emit_planes8s(yv, lp, 1, kLdsBlk, t >> 2, t & 3, ok);
+        for (int i = 0; i < 8; ++i) ss[c] += v.xv[c][i] * v.xv[c][i];
+    }
+    const float inv = 1.0f / sqrtf(wg_sum_c<C>(ss, sh) / (float)dim + n.eps);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const uint32_t t = threadIdx.x + c * blockDim.x;
+        const bool ok = 8 * t < dim;
+        float yv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) yv[i] = (v.xv[c][i] * inv) * v.wv[c][i];
+        if (blockIdx.x == 0 && ok && n.y) st8(n.y, t, yv);
+        emit_planes8s(yv, lp, 1, kLdsBlk, t >> 2, t & 3, ok);
+    }
 }
 
 // This lane's two blocks of planes from the LDS copy norm_to_lds wrote.
@@ -403,12 +427,12 @@ __global__ __launch_bounds__(1024) void k_q4rmv_qkv_nx(RArgs a, NormArgs n) {
             sq[s][1] = __builtin_nontemporal_load(S + b1);
         }
     };
-    NormIn nv;
-    norm_load<NORM>(n, nb * 32, nv);
+    NormIn<1> nv;
+    norm_load<NORM, 1>(n, nb * 32, nv);
     uint32_t g = blockIdx.x * NW + wave;
     if (g < ngroups) load(g);
     if (n.rope.tab && blockIdx.x == 0) rope_table(n.rope, threadIdx.x, blockDim.x);
-    norm_to_lds<NORM>(n, nb * 32, nv, lp, sh);
+    norm_to_lds<NORM, 1>(n, nb * 32, nv, lp, sh);
     __syncthreads();
     uint32_t P[2][XP_WORDS];
     float xs[2];
@@ -483,8 +507,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
         }
     };
     constexpr int NM = NORM < 0 ? 0 : NORM;
-    NormIn nv;
-    if (NORM >= 0) norm_load<NM>(n, nb * 32, nv);
+    constexpr int NCH = (NORM < 0) ? 1 : (512 + 64 * NW - 1) / (64 * NW);   // norm chunks: K <= 4096
+    NormIn<NCH> nv;
+    if (NORM >= 0) norm_load<NM, NCH>(n, nb * 32, nv);
     uint32_t rb = blockIdx.x;
     RowPair nx;
     if (rb < nrb) load(nx, rb * 32 + wave);
@@ -493,7 +518,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     uint32_t P[2][XP_WORDS];
     float xs[2];
     if (NORM >= 0) {
-        norm_to_lds<NM>(n, nb * 32, nv, lp, sh);
+        norm_to_lds<NM, NCH>(n, nb * 32, nv, lp, sh);
         __syncthreads();
         lane_planes_lds(lp, b0, b1, ok0, ok1, P, xs);
     } else {
@@ -617,6 +642,12 @@ int mvr_mlp(chn_ctx *ctx, const void *Wg, const void *Wu, const float *x, float 
     return launch_q4rmv(ctx, RV_MLP, a, x, xp, planes_ready);
 }
 
+// Gate/up launch shape (sweeps at 15360 x 3840 with weights cold in HBM):
+// one 32-row block per workgroup, at most kMlpGrid workgroups (which then
+// loop over blocks).  From planes: four waves on eight rows each (the next
+// row pair in flight), 14.2 us against 14.6 us for eight waves on four.
+constexpr uint32_t kMlpGrid = 2048;
+
 int mvr_mlp_xp(chn_ctx *ctx, const void *Wg, const void *Wu, const uint32_t *xp_in, float *act,
                uint32_t *xp_out, uint32_t M, uint32_t K) {
     const uint32_t nb = K / 32;
@@ -629,7 +660,7 @@ int mvr_mlp_xp(chn_ctx *ctx, const void *Wg, const void *Wu, const uint32_t *xp_
     const RArgs a{host_rmat(Wg, M, nb), host_rmat(Wu, M, nb), {}, act, nullptr, nullptr, xp_in, M, M, M, nb};
     const uint32_t nrb = M / 32;
     if (!nrb) return CHN_OK;
-    k_q4rmv_mlp_xp<8, -1><<<nrb < 1024 ? nrb : 1024, 512, 0, ctx->stream>>>(a, xp_out, NormArgs{});
+    k_q4rmv_mlp_xp<4, -1><<<nrb < kMlpGrid ? nrb : kMlpGrid, 256, 0, ctx->stream>>>(a, xp_out, NormArgs{});
     CHN_LAUNCHED(ctx, "k_q4rmv_mlp_xp");
     return CHN_OK;
 }
@@ -641,9 +672,10 @@ int mvr_mlp_nx(chn_ctx *ctx, const void *Wg, const void *Wu, float *act, uint32_
     const RArgs a{host_rmat(Wg, M, nb), host_rmat(Wu, M, nb), {}, act, nullptr, nullptr, nullptr, M, M, M, nb};
     const uint32_t nrb = M / 32;
     if (!nrb) return CHN_OK;
-    // two 8-wave workgroups per CU (128 VGPRs), row blocks dealt evenly; the
-    // 16-wave form spills at this register budget
-    const uint32_t per = (nrb + 511) / 512, grid = (nrb + per - 1) / per;
+    // eight-wave workgroups here: the norm prologue, recomputed by every
+    // workgroup, takes twice as long on four waves (16.3 us against 15.4 us
+    // for the whole kernel)
+    const uint32_t grid = nrb < kMlpGrid ? nrb : kMlpGrid;
     hipStream_t s = ctx->stream;
     if (mode == NORM_PLAIN) k_q4rmv_mlp_xp<8, NORM_PLAIN><<<grid, 512, 0, s>>>(a, xp_out, n);
     else if (mode == NORM_ADD) k_q4rmv_mlp_xp<8, NORM_ADD><<<grid, 512, 0, s>>>(a, xp_out, n);
