@@ -45,7 +45,7 @@ def q4_bytes(rows, K):
 
 
 def xplanes_bytes(K):
-    return (K // 32) * 25 * 4
+    return (K // 32) * 21 * 4
 
 
 def q4r_bytes(rows, K):

@@ -23,9 +23,9 @@ def q4r_bytes(rows, K):
 
 
 def xplanes_bytes(K):
-    """Bytes of the activation digit planes of K values (chn_xplanes): 24
+    """Bytes of the activation digit planes of K values (chn_xplanes): 20
     plane words and one float scale per 32 values."""
-    return (K // 32) * 25 * 4
+    return (K // 32) * 21 * 4
 
 
 def q8_bytes(rows, K):

@@ -49,14 +49,21 @@ int ensure_workspace(chn_ctx *ctx, size_t bytes);
 inline bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
 // ---- activation digit planes (the matvec's input format)
-// Per 32-block b of an activation vector: X_i = rint(x_i * 2^(22 - e_b))
-// with |x_i| < 2^e_b, six balanced base-16 digits per X_i, each digit plane
+// Per 32-block b of an activation vector: X_i = rint(x_i * 2^(18 - e_b))
+// with |x_i| < 2^e_b, five balanced base-16 digits per X_i, each digit plane
 // packed as signed 4-bit lanes in the weights' nibble order.  Stored SoA:
 // u32 plane words at [(p * 4 + w) * nb + b] (p = plane, w = 8-element
-// word), then nb float scales 2^(e_b - 22).
-constexpr int XP_PLANES = 6;
-constexpr int XP_FRAC = 22;
+// word), then nb float scales 2^(e_b - 18).  The rounding of x is at most
+// 2^-18 of the block maximum (the size of fp32's own rounding noise over a
+// few thousand accumulated products).
+constexpr int XP_PLANES = 5;
+constexpr int XP_FRAC = 18;
 constexpr int XP_WORDS = XP_PLANES * 4;
+// X + XP_BIAS has digit 8 + D_p in every hex position p < XP_PLANES
+// (|X| < 2^XP_FRAC keeps every digit in [0, 15]).
+constexpr uint32_t XP_BIAS = 0x88888u;
+static_assert(XP_BIAS == (((1u << (4 * XP_PLANES)) - 1u) / 15u) * 8u, "XP_BIAS: 8 in each of XP_PLANES digits");
+static_assert(4 * XP_PLANES - 1 >= XP_FRAC + 1, "digits must cover |X| < 2^XP_FRAC");
 inline size_t xplanes_bytes(uint32_t nb) { return (size_t)nb * (XP_WORDS + 1) * 4; }
 
 // ---- internal launchers (explicit workspaces; usable under graph capture)
@@ -358,7 +365,7 @@ __device__ __forceinline__ void wave_sum4(float v0, float v1, float v2, float v3
 // hold its words w = lane & 3 (eight consecutive values each).  All four
 // lanes must call (with zeros where ok is false); only ok lanes store.
 // Plane word (p, w) of block b goes to xp[(p * 4 + w) * ws + b * bs], the
-// block's scale to xp[24 * ws + b * bs].
+// block's scale to xp[XP_WORDS * ws + b * bs].
 __device__ __forceinline__ void emit_planes8s(const float (&v)[8], uint32_t *__restrict__ xp, uint32_t ws,
                                               uint32_t bs, uint32_t b, uint32_t w, bool ok) {
     float m = 0.0f;
@@ -375,7 +382,7 @@ __device__ __forceinline__ void emit_planes8s(const float (&v)[8], uint32_t *__r
     }
     uint32_t u[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) u[i] = (uint32_t)((int)rintf(v[i] * scale) + 0x888888);
+    for (int i = 0; i < 8; ++i) u[i] = (uint32_t)((int)rintf(v[i] * scale) + (int)XP_BIAS);
     if (!ok) return;
 #pragma unroll
     for (int p = 0; p < XP_PLANES; ++p) {
@@ -388,7 +395,7 @@ __device__ __forceinline__ void emit_planes8s(const float (&v)[8], uint32_t *__r
 }
 
 // Planes in the chn_xplanes layout: plane word (p, w) of block b at
-// [(p * 4 + w) * nb + b], the scale at [24 * nb + b].
+// [(p * 4 + w) * nb + b], the scale at [XP_WORDS * nb + b].
 __device__ __forceinline__ void emit_planes8(const float (&v)[8], uint32_t *__restrict__ xp, uint32_t nb,
                                              uint32_t b, uint32_t w, bool ok) {
     emit_planes8s(v, xp, nb, 1, b, w, ok);

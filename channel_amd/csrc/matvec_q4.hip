@@ -6,15 +6,15 @@
 // near one instruction so that the issue rate never caps the stream:
 //
 //  * Activations are turned once per call into "digit planes": per 32-block
-//    b, X_i = rint(x_i * 2^(22-e_b)) with |x_i| < 2^e_b, written as six
+//    b, X_i = rint(x_i * 2^(18-e_b)) with |x_i| < 2^e_b, written as five
 //    balanced base-16 digits D_p in [-8, 7] (X = sum_p D_p 16^p), and each
 //    digit plane packed as signed 4-bit lanes in the same nibble order as
-//    the weights.  The quantisation error is <= 2^-22 of the block maximum,
-//    i.e. fp32-grade.
+//    the weights.  The quantisation error is <= 2^-18 of the block maximum,
+//    the size of fp32's own rounding noise over a few thousand products.
 //  * A Q4 word XOR 0x88888888 is exactly the eight signed 4-bit values
 //    (q - 8), so sum_i (q_i - 8) X_i is an exact integer computed with
 //    v_dot8c_i32_i4 (8 MACs per instruction), plane by plane in Horner
-//    form; the block result is (float)T * scale_b * 2^(e_b - 22).
+//    form; the block result is (float)T * scale_b * 2^(e_b - 18).
 //  * Weights are streamed with coalesced non-temporal 16-byte loads of whole
 //    row segments (prefetching the next row group into VGPRs while the
 //    current one is computed), transposed through LDS to one lane per

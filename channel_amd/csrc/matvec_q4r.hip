@@ -297,7 +297,7 @@ __device__ __forceinline__ float wg_sum_c(const float (&v)[C], float *sh) {
 // NormArgs' norm over dim values (dim % 32 == 0, dim <= 8 * C * blockDim):
 // thread t holds the eight values 8 (t + c blockDim) .. + 7 of chunk c < C,
 // four threads per 32-block.  The digit planes of y go to LDS block by block
-// (kLdsBlk words per block: 24 plane words, then the scale; constant offsets
+// (kLdsBlk words per block: the plane words, then the scale; constant offsets
 // from one base per block, and the odd stride keeps a wave's reads of
 // consecutive blocks free of bank conflicts), workgroup 0 writes x_out and
 // y.  The same arithmetic, in the same order, as the standalone norm kernel
@@ -545,7 +545,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
             if (lane == 0) sact[wave + NW * j] = gelu_tanh(t[0]) * t[1];
         }
         __syncthreads();
-        // an opaque copy of the thread index: otherwise the 24 plane-store
+        // an opaque copy of the thread index: otherwise the plane-store
         // addresses are hoisted out of the block loop and spilled
         uint32_t tx = threadIdx.x;
         __asm__ volatile("" : "+v"(tx));

@@ -146,13 +146,13 @@ int chn_fused_mlp_q4r(chn_ctx *ctx, const void *Wg, const void *Wu, const float 
 
 /* Activation digit planes: the form in which every matvec above reads its
  * input x (K values in K/32 blocks).  Per block b of nb = K/32: an exponent
- * e with |x_i| < 2^e, X_i = rint(x_i * 2^(22 - e)) split into six signed
- * hex digits, stored as plane words [(p*4 + w)*nb + b] (p < 6 digit, w < 4
- * eight-value group, 4-bit digits XOR 8), then nb float scales 2^(e - 22).
+ * e with |x_i| < 2^e, X_i = rint(x_i * 2^(18 - e)) split into five signed
+ * hex digits, stored as plane words [(p*4 + w)*nb + b] (p < 5 digit, w < 4
+ * eight-value group, 4-bit digits XOR 8), then nb float scales 2^(e - 18).
  * Producing the planes once lets several matvecs share them; the model's
  * norm and attention kernels write them directly.  No reference
  * counterpart (the reference multiplies by f32 x in every shader). */
-#define CHN_XPLANES_BYTES(K) ((size_t)((K) / 32) * 25 * 4)
+#define CHN_XPLANES_BYTES(K) ((size_t)((K) / 32) * 21 * 4)
 int chn_xplanes(chn_ctx *ctx, const float *x, uint32_t K, uint32_t *planes);
 
 /* chn_gemv_q4r / chn_fused_mlp_q4r reading planes of x (chn_xplanes)

@@ -193,11 +193,11 @@ def test_q4r_bad_shapes(ctx):
 def decode_planes(P, K):
     """Host decoding of chn_xplanes output: integers X and block scales."""
     nb = K // 32
-    words = P[:24 * nb].reshape(6, 4, nb)                       # [plane][group][block]
-    inv = P[24 * nb:].view(np.float32)
+    words = P[:20 * nb].reshape(5, 4, nb)                       # [plane][group][block]
+    inv = P[20 * nb:].view(np.float32)
     sh = np.arange(8, dtype=np.uint32) * 4
     dig = (((words[..., None] ^ np.uint32(0x88888888)) >> sh) & 15).astype(np.int64) - 8   # [p][w][b][n]
-    X = sum(dig[p] * (16 ** p) for p in range(6))               # [w][b][n]
+    X = sum(dig[p] * (16 ** p) for p in range(5))               # [w][b][n]
     return X.transpose(1, 0, 2).reshape(nb, 32), inv
 
 
@@ -221,10 +221,10 @@ def test_xplanes_reconstruct_exactly(ctx):
         if m == 0.0 or m < 2.0 ** -100:
             assert inv[b] == 0.0 and np.all(X[b] == 0), b
             continue
-        e = int(np.log2(inv[b])) + 22                  # inv = 2^(e - 22)
-        assert inv[b] == np.float32(2.0 ** (e - 22)), b
+        e = int(np.log2(inv[b])) + 18                  # inv = 2^(e - 18)
+        assert inv[b] == np.float32(2.0 ** (e - 18)), b
         assert 2.0 ** (e - 1) <= m < 2.0 ** e, b       # frexp exponent of the block max
-        assert np.array_equal(X[b], np.rint(xb[b] * 2.0 ** (22 - e)).astype(np.int64)), b
+        assert np.array_equal(X[b], np.rint(xb[b] * 2.0 ** (18 - e)).astype(np.int64)), b
         assert np.abs(X[b] * float(inv[b]) - xb[b]).max() <= 0.5 * float(inv[b])
 
 
