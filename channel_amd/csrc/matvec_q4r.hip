@@ -526,11 +526,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     }
 
     for (; rb < nrb; rb += gridDim.x) {
+        const uint32_t nxt = rb + gridDim.x;
 #pragma unroll 1
         for (int j = 0; j < RW; ++j) {
             const RowPair cur = nx;
             if (j + 1 < RW) load(nx, rb * 32 + wave + NW * (j + 1));
-            else if (rb + gridDim.x < nrb) load(nx, (rb + gridDim.x) * 32 + wave);
+            else if (nxt < nrb) load(nx, nxt * 32 + wave);
             float r[2] = {0.0f, 0.0f};
 #pragma unroll
             for (int m = 0; m < 2; ++m)
