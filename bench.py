@@ -537,11 +537,11 @@ def bench_prefill(ctx, args):
         "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": ms,
         "config": {"workload": "batched prefill Q4 GEMM 512 tokens x 3840 -> 15360 (bf16 MFMA)",
                    "tokens": T, "K": K, "N": N, "flop_per_step": flops},
-        "roofline": {"kernel": "k_q4gemm_p<1,64,REF> (128x64 tiles, DMA-pipelined K walk) + k_to_bf16 pre-pass",
+        "roofline": {"kernel": "k_q4gemm_p<1,128,REF> (128x128 tiles, DMA-pipelined K walk) + k_to_bf16 pre-pass",
                      "bound": "mfma",
                      "achieved": achieved, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / MFMA_BF16_PEAK_TFLOPS,
-                     "traffic": load_traffic("k_q4gemm_p<1,64,REF>", "512x3840 -> 15360"),
+                     "traffic": load_traffic("k_q4gemm_p<1,128,REF>", "512x3840 -> 15360"),
                      "algorithmic_flop_per_launch": flops,
                      "avg_launch_ms": gpu_ms / args.steps},
         "cpu_baseline": None,

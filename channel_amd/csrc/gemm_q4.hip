@@ -681,13 +681,16 @@ static void launch_to_bf16(hipStream_t st, const float *X, __bf16 *xb, size_t n,
 }
 
 // Launch shapes for one pipelined single-matrix contraction (K % 64 == 0),
-// from sweeps at 512 tokens: 128-token x 64-feature tiles when they give at
-// least ~200 workgroups; otherwise the same tiles with K split in two; and
-// for long K (>= 8192) 128 x 128 tiles with K split in two, whose larger
-// per-step work pays for itself over the longer loop.
-enum class PipeShape { BN64, BN64_K2, BN128_K2 };
+// from sweeps at 512 tokens: 128 x 128 tiles when they alone give at least
+// 1.5 workgroups per CU (15360 x 3840: 97 us against 135 us for 128 x 64:
+// half the LDS fragment reads per MFMA); for long K (>= 8192) 128 x 128
+// tiles with K split in two, whose larger per-step work pays for itself over
+// the longer loop; else 128-token x 64-feature tiles when they give at least
+// ~200 workgroups; otherwise the same tiles with K split in two.
+enum class PipeShape { BN64, BN64_K2, BN128, BN128_K2 };
 static PipeShape pipe_shape(uint32_t n_tok, uint32_t M, uint32_t K) {
     const uint32_t tt = (n_tok + 127) / 128;
+    if (((M + 127) / 128) * tt >= 384) return PipeShape::BN128;
     if (K >= 8192 && 2 * ((M + 127) / 128) * tt >= 192) return PipeShape::BN128_K2;
     if (((M + 63) / 64) * tt >= 192 || K < 128) return PipeShape::BN64;
     return PipeShape::BN64_K2;
@@ -697,6 +700,7 @@ template <bool REP>
 static void launch_pipe(hipStream_t st, const GemmArgs &a, PipeShape ps) {
     if (ps == PipeShape::BN64) launch_gemm_p<1, 64, REP, 4>(st, a, 1);
     else if (ps == PipeShape::BN64_K2) launch_gemm_p<1, 64, REP, 4>(st, a, 2);
+    else if (ps == PipeShape::BN128) launch_gemm_p<1, 128, REP, 4>(st, a, 1);
     else launch_gemm_p<1, 128, REP, 4>(st, a, 2);
 }
 
@@ -706,7 +710,7 @@ int launch_q4gemm(chn_ctx *ctx, int nmat, const float *X, const uint32_t *W0, co
     GemmArgs a{xb, W0, W1, Y, n_tok, M, K};
     if (nmat == 1 && K % 64 == 0) {
         const PipeShape ps = pipe_shape(n_tok, M, K);
-        const bool split = ps != PipeShape::BN64;
+        const bool split = ps == PipeShape::BN64_K2 || ps == PipeShape::BN128_K2;
         launch_to_bf16(ctx->stream, X, xb, n, split ? Y : nullptr, split ? (size_t)n_tok * M : 0);
         CHN_LAUNCHED(ctx, "k_to_bf16");
         if (repacked) launch_pipe<true>(ctx->stream, a, ps);

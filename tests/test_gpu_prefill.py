@@ -14,7 +14,8 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("n_tok,M,K,sample", [
-    (512, 15360, 3840, 12),    # config: prefill Q4 GEMM 512 x 3840 -> 15360
+    (512, 15360, 3840, 12),    # config: prefill Q4 GEMM 512 x 3840 -> 15360 (128 x 128 tiles)
+    (300, 16400, 64, None),    # 128 x 128 tiles, ragged tokens and features, one K step
     (512, 3840, 15360, 6),     # down_proj shape (128 x 128 tiles, K split in two)
     (512, 2048, 3840, 6),      # k/v shape (128 x 64 tiles, K split in two)
     (100, 200, 96, None),      # ragged: tokens, features and K not tile multiples
