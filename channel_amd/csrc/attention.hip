@@ -546,6 +546,18 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ ws
     }
 }
 
+// Four consecutive output values at element offset o: fp32 into out, or
+// bf16 into outb when it is set (the operand of the next contraction).
+typedef __bf16 bf16x2a __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void store_out4(float *out, __bf16 *outb, size_t o, f4 v) {
+    if (outb) {
+        *(bf16x2a *)(outb + o) = bf16x2a{(__bf16)v.x, (__bf16)v.y};
+        *(bf16x2a *)(outb + o + 2) = bf16x2a{(__bf16)v.z, (__bf16)v.w};
+    } else {
+        *(f4 *)(out + o) = v;
+    }
+}
+
 // Prefill (shaders/batch_causal_attn.wgsl): one workgroup per (token, KV
 // head) walks slots [start, prev + t + 1) of the list in 64-slot chunks with
 // an online softmax; start = S - window for window > 0 and S > window.
@@ -554,7 +566,8 @@ __global__ __launch_bounds__(256) void k_prefill_attn(const float *__restrict__ 
                                                       const float *__restrict__ Vc,
                                                       const uint32_t *__restrict__ slots, uint32_t num_prev,
                                                       uint32_t num_q_heads, uint32_t kv_dim, float scale,
-                                                      uint32_t window, float *__restrict__ out) {
+                                                      uint32_t window, float *__restrict__ out,
+                                                      __bf16 *__restrict__ outb) {
     constexpr int D = DV * 256;
     const uint32_t t = blockIdx.x, kvh = blockIdx.y;
     const uint32_t S = num_prev + t + 1;
@@ -580,7 +593,8 @@ __global__ __launch_bounds__(256) void k_prefill_attn(const float *__restrict__ 
 #pragma unroll
     for (int h = 0; h < GQA; ++h) inv[h] = 1.0f / (st.l[h] + 1e-9f);
     attn_reduce<DV, GQA>(st, pacc, [&](int h, int col, f4 v) {
-        *(f4 *)(out + q_row + (size_t)(kvh * GQA + h) * D + 4 * col) = v * inv[h];
+        const size_t o = q_row + (size_t)(kvh * GQA + h) * D + 4 * col;
+        store_out4(out, outb, o, v * inv[h]);
     });
 }
 
@@ -636,7 +650,8 @@ __global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict
                                                          const float *__restrict__ Vc,
                                                          const uint32_t *__restrict__ slots, uint32_t num_prev,
                                                          uint32_t n_tok, uint32_t num_q_heads, uint32_t kv_dim,
-                                                         float scale, uint32_t window, float *__restrict__ out) {
+                                                         float scale, uint32_t window, float *__restrict__ out,
+                                                         __bf16 *__restrict__ outb) {
     constexpr int D = 256, NK = kPaNK, TQ = 64 / GQA;
     __shared__ __attribute__((aligned(16))) unsigned char kh_s[NK * kPaKRow], kl_s[NK * kPaKRow];
     __shared__ __attribute__((aligned(16))) unsigned char vh_s[D * kPaVRow], vl_s[D * kPaVRow];
@@ -812,9 +827,9 @@ __global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict
     }
     if (tq >= n_tok) return;
     const float inv = 1.0f / (l + 1e-9f);
-    float *orow = out + ((size_t)tq * num_q_heads + head) * D + 4 * g;
+    const size_t orow = ((size_t)tq * num_q_heads + head) * D + 4 * g;
 #pragma unroll
-    for (int dt = 0; dt < 16; ++dt) *(f4 *)(orow + 16 * dt) = o[dt] * inv;
+    for (int dt = 0; dt < 16; ++dt) store_out4(out, outb, orow + 16 * dt, o[dt] * inv);
 }
 
 static int launch_decode_impl(chn_ctx *ctx, const float *q, float *kc, float *vc, const uint32_t *slots,
@@ -885,12 +900,13 @@ int launch_rope_decode_attn(chn_ctx *ctx, const float *q_in, const float *k_in, 
 
 int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const float *vc, const uint32_t *slots,
                         uint32_t n_tok, uint32_t num_prev, uint32_t num_q_heads, uint32_t head_dim, uint32_t kv_dim,
-                        uint32_t gqa, float scale, uint32_t window, float *out) {
+                        uint32_t gqa, float scale, uint32_t window, float *out, __bf16 *outb) {
     if (head_dim == 256 && (gqa == 1 || gqa == 2 || gqa == 4 || gqa == 8)) {
         const uint32_t tq = 64 / gqa;
         const dim3 mgrid((n_tok + tq - 1) / tq, num_q_heads / gqa);
 #define CHN_PATTN_MF(G) \
-    k_prefill_attn_mf<G><<<mgrid, 256, 0, st>>>(q, kc, vc, slots, num_prev, n_tok, num_q_heads, kv_dim, scale, window, out)
+    k_prefill_attn_mf<G><<<mgrid, 256, 0, st>>>(q, kc, vc, slots, num_prev, n_tok, num_q_heads, kv_dim, scale, window, \
+                                                out, outb)
         switch (gqa) {
         case 1: CHN_PATTN_MF(1); break;
         case 2: CHN_PATTN_MF(2); break;
@@ -902,7 +918,8 @@ int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const f
     }
     dim3 grid(n_tok, num_q_heads / gqa);
 #define CHN_PATTN(DV, G) \
-    k_prefill_attn<DV, G><<<grid, 256, 0, st>>>(q, kc, vc, slots, num_prev, num_q_heads, kv_dim, scale, window, out)
+    k_prefill_attn<DV, G><<<grid, 256, 0, st>>>(q, kc, vc, slots, num_prev, num_q_heads, kv_dim, scale, window, out, \
+                                                outb)
     if (head_dim == 256) {
         switch (gqa) {
         case 1: CHN_PATTN(1, 1); break;

@@ -79,6 +79,13 @@ int mv_mlp(chn_ctx *ctx, const uint32_t *Wg, const uint32_t *Wu, const float *x,
            uint32_t *ws, bool planes_ready = false);
 int launch_rmsnorm(hipStream_t s, float *x, const float *r, const float *w, float *y, uint32_t dim, uint32_t rows,
                    float eps, float scalar, bool add);
+// The prefill's norm chain per token row: with post_w, r' = rmsnorm(r) *
+// post_w (else r' = r); with add, x = (x + r') * scalar (written back);
+// y = rmsnorm(x) * w as bf16 into yb and, if y != NULL, as fp32.  zero_r
+// clears r once read (the output of the next split-K contraction).  The
+// same arithmetic, in the same order, as launch_rmsnorm's two passes.
+int launch_rmsnorm_chain(hipStream_t s, float *x, float *r, const float *post_w, const float *w, __bf16 *yb,
+                         float *y, uint32_t dim, uint32_t rows, float eps, float scalar, bool add, bool zero_r);
 // Digit planes of x (nb 32-blocks) into xp (xplanes_bytes(nb)).
 int launch_xplanes(hipStream_t s, const float *x, uint32_t *xp, uint32_t nb);
 
@@ -174,9 +181,10 @@ int launch_rope_decode_attn(chn_ctx *ctx, const float *q_in, const float *k_in, 
                             const uint32_t *n_slots, uint32_t max_slots, uint32_t num_q_heads, uint32_t head_dim,
                             uint32_t kv_dim, uint32_t gqa, uint32_t rot, int k_eq_v, const float2 *rope_tab,
                             float eps, float scale, float *out, float *ws, uint32_t *xp);
+// out: [n_tok][num_q_heads * head_dim] fp32, or bf16 into outb when set.
 int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const float *vc, const uint32_t *slots,
                         uint32_t n_tok, uint32_t num_prev, uint32_t num_q_heads, uint32_t head_dim, uint32_t kv_dim,
-                        uint32_t gqa, float scale, uint32_t window, float *out);
+                        uint32_t gqa, float scale, uint32_t window, float *out, __bf16 *outb = nullptr);
 size_t xbytes_bytes(uint32_t nb);
 int launch_gemv_q8(hipStream_t st, const uint32_t *W, const float *x, float *y, uint32_t M, uint32_t nb,
                    uint32_t *xp_ws);
@@ -185,10 +193,15 @@ int launch_topk64(hipStream_t st, const float *logits, uint32_t V, uint32_t *ids
 int launch_embed(hipStream_t st, const uint16_t *table, const uint32_t *tokens, uint32_t n, uint32_t H, float scale,
                  float *x);
 int launch_quantize(hipStream_t st, int q8, const uint16_t *src, uint32_t *dst, uint64_t nblk);
-// W0/W1 in the reference Q4 layout, or in Q4R with repacked.
+// W0/W1 in the reference Q4 layout, or in Q4R with repacked.  X (fp32) is
+// converted into xb; with X == NULL, xb already holds the bf16 activations.
+// Yb (two-matrix form only): the result goes to Yb as bf16 instead of Y.
+// y_zeroed: Y already holds zeros, so a split-K shape skips clearing it.
 int launch_q4gemm(chn_ctx *ctx, int nmat, const float *X, const uint32_t *W0, const uint32_t *W1, float *Y,
-                  uint32_t n_tok, uint32_t M, uint32_t K, __bf16 *xb, bool repacked);
-// q, k, v (Q4R) over the same activations in one launch.
+                  uint32_t n_tok, uint32_t M, uint32_t K, __bf16 *xb, bool repacked, __bf16 *Yb = nullptr,
+                  bool y_zeroed = false);
+// q, k, v (Q4R) over the same activations in one launch (X == NULL: xb
+// already holds them).
 int launch_q4gemm_qkv(chn_ctx *ctx, const float *X, const uint32_t *Wq, const uint32_t *Wk, const uint32_t *Wv,
                       float *Yq, float *Yk, float *Yv, uint32_t n_tok, uint32_t Mq, uint32_t Mkv, uint32_t K,
                       __bf16 *xb);

@@ -66,6 +66,9 @@ struct GemmArgs {
     const uint32_t *Wg[2] = {nullptr, nullptr};
     float *Yg[2] = {nullptr, nullptr};
     uint32_t Mg[2] = {0, 0};
+    // Register-staged kernel only: Yb != NULL writes the result as bf16 to
+    // Yb ([n_tok][M]) instead of Y (the next contraction's input).
+    __bf16 *Yb = nullptr;
 };
 
 typedef uint32_t u32x4g __attribute__((ext_vector_type(4)));
@@ -241,7 +244,8 @@ __global__ __launch_bounds__(256, 2) void k_q4gemm(GemmArgs a) {
                 if (t < a.n_tok && n < a.M) {
                     float v = acc[0][mt][nt][i];
                     if (NMAT == 2) v = gelu_tanh(v) * acc[NMAT - 1][mt][nt][i];
-                    a.Y[(size_t)t * a.M + n] = v;
+                    if (a.Yb) a.Yb[(size_t)t * a.M + n] = (__bf16)v;
+                    else a.Y[(size_t)t * a.M + n] = v;
                 }
             }
         }
@@ -705,21 +709,28 @@ static void launch_pipe(hipStream_t st, const GemmArgs &a, PipeShape ps) {
 }
 
 int launch_q4gemm(chn_ctx *ctx, int nmat, const float *X, const uint32_t *W0, const uint32_t *W1, float *Y,
-                  uint32_t n_tok, uint32_t M, uint32_t K, __bf16 *xb, bool repacked) {
-    const size_t n = (size_t)n_tok * K;
+                  uint32_t n_tok, uint32_t M, uint32_t K, __bf16 *xb, bool repacked, __bf16 *Yb, bool y_zeroed) {
+    const size_t n = X ? (size_t)n_tok * K : 0;
     GemmArgs a{xb, W0, W1, Y, n_tok, M, K};
     if (nmat == 1 && K % 64 == 0) {
+        if (Yb) return set_err(ctx, CHN_E_UNSUPPORTED, "bf16 output needs the two-matrix contraction");
         const PipeShape ps = pipe_shape(n_tok, M, K);
         const bool split = ps == PipeShape::BN64_K2 || ps == PipeShape::BN128_K2;
-        launch_to_bf16(ctx->stream, X, xb, n, split ? Y : nullptr, split ? (size_t)n_tok * M : 0);
-        CHN_LAUNCHED(ctx, "k_to_bf16");
+        const bool zero = split && !y_zeroed;
+        if (n || zero) {
+            launch_to_bf16(ctx->stream, X, xb, n, zero ? Y : nullptr, zero ? (size_t)n_tok * M : 0);
+            CHN_LAUNCHED(ctx, "k_to_bf16");
+        }
         if (repacked) launch_pipe<true>(ctx->stream, a, ps);
         else launch_pipe<false>(ctx->stream, a, ps);
         CHN_LAUNCHED(ctx, "k_q4gemm_p");
         return CHN_OK;
     }
-    launch_to_bf16(ctx->stream, X, xb, n, nullptr, 0);
-    CHN_LAUNCHED(ctx, "k_to_bf16");
+    if (n) {
+        launch_to_bf16(ctx->stream, X, xb, n, nullptr, 0);
+        CHN_LAUNCHED(ctx, "k_to_bf16");
+    }
+    a.Yb = Yb;
     dim3 grid((M + GN - 1) / GN, (n_tok + GT - 1) / GT);
     if (repacked) {
         if (nmat == 1) k_q4gemm<1, true, kGemmKB><<<grid, 256, 0, ctx->stream>>>(a);
@@ -733,18 +744,21 @@ int launch_q4gemm(chn_ctx *ctx, int nmat, const float *X, const uint32_t *W0, co
 }
 
 // q, k and v of one layer in one launch: three repacked matrices over the
-// same activations (one bf16 conversion), 128 x 64 tiles.
+// same activations (one bf16 conversion, none when X is NULL and xb already
+// holds them), 128 x 64 tiles.
 int launch_q4gemm_qkv(chn_ctx *ctx, const float *X, const uint32_t *Wq, const uint32_t *Wk, const uint32_t *Wv,
                       float *Yq, float *Yk, float *Yv, uint32_t n_tok, uint32_t Mq, uint32_t Mkv, uint32_t K,
                       __bf16 *xb) {
     if (K % 64 != 0) {
         int rc = launch_q4gemm(ctx, 1, X, Wq, nullptr, Yq, n_tok, Mq, K, xb, true);
-        if (!rc) rc = launch_q4gemm(ctx, 1, X, Wk, nullptr, Yk, n_tok, Mkv, K, xb, true);
-        if (!rc) rc = launch_q4gemm(ctx, 1, X, Wv, nullptr, Yv, n_tok, Mkv, K, xb, true);
+        if (!rc) rc = launch_q4gemm(ctx, 1, nullptr, Wk, nullptr, Yk, n_tok, Mkv, K, xb, true);
+        if (!rc) rc = launch_q4gemm(ctx, 1, nullptr, Wv, nullptr, Yv, n_tok, Mkv, K, xb, true);
         return rc;
     }
-    launch_to_bf16(ctx->stream, X, xb, (size_t)n_tok * K, nullptr, 0);
-    CHN_LAUNCHED(ctx, "k_to_bf16");
+    if (X) {
+        launch_to_bf16(ctx->stream, X, xb, (size_t)n_tok * K, nullptr, 0);
+        CHN_LAUNCHED(ctx, "k_to_bf16");
+    }
     GemmArgs a{xb, Wq, nullptr, Yq, n_tok, Mq, K};
     a.Wg[0] = Wk;
     a.Yg[0] = Yk;

@@ -50,7 +50,7 @@ struct chn_model {
     uint64_t *topk_ws;
     // prefill buffers
     uint32_t max_tok = 0;
-    float *px, *pn, *pq, *pk, *pv, *pattn, *pmlp, *pact;
+    float *px, *pn, *pq, *pk, *pv, *pmlp, *pact;
     __bf16 *pxb;
     uint32_t *pslots, *ptok;
     // pinned staging
@@ -188,10 +188,9 @@ static int alloc_runtime(chn_model *m) {
     M_ALLOC(m->pq, (size_t)T * qd * 4);
     M_ALLOC(m->pk, (size_t)T * kvd * 4);
     M_ALLOC(m->pv, (size_t)T * kvd * 4);
-    M_ALLOC(m->pattn, (size_t)T * qd * 4);
     M_ALLOC(m->pmlp, (size_t)T * H * 4);
     M_ALLOC(m->pact, (size_t)T * I * 4);
-    M_ALLOC(m->pxb, (size_t)T * (I > H ? (I > qd ? I : qd) : (H > qd ? H : qd)) * 2);
+    M_ALLOC(m->pxb, (size_t)T * (H > qd ? H : qd) * 2);   // bf16 operands of width H or qd; act goes to pact
     M_ALLOC(m->pslots, (size_t)(kSlotsMax + T) * 4);
     M_ALLOC(m->ptok, (size_t)T * 4);
     hipError_t e = hipHostMalloc((void **)&m->h_x, H * 4);
@@ -735,25 +734,33 @@ extern "C" int chn_prefill(chn_model *m, const uint32_t *tokens, uint32_t n, con
         rc = (call);             \
         if (rc) return rc;       \
     } while (0)
+    // Every contraction reads bf16 activations that their producer wrote
+    // directly: the norm chains and the attention into pxb, gate/up into the
+    // act buffer (as bf16).  The chain after o_proj also clears pmlp, which
+    // down's split-K halves then add into.
+    __bf16 *xb = m->pxb;
+    __bf16 *actb = (__bf16 *)m->pact;
     for (uint32_t i = 0; i < c.num_layers; ++i) {
         const auto &l = m->L[i];
         const float theta = l.full ? c.rope_theta_full : c.rope_theta;
-        if (i == 0) P_(launch_rmsnorm(s, m->px, nullptr, l.in_norm, m->pn, H, n, eps, 1.0f, false));
+        if (i == 0)
+            P_(launch_rmsnorm_chain(s, m->px, nullptr, nullptr, l.in_norm, xb, nullptr, H, n, eps, 1.0f, false, false));
         const uint32_t D = l.D, nkv = l.nkv, qd = l.qd, kvd = l.kvd, gqa = l.gqa;
-        P_(launch_q4gemm_qkv(ctx, m->pn, l.Wq, l.Wk, l.Wv, m->pq, m->pk, m->pv, n, qd, kvd, H, m->pxb));
+        P_(launch_q4gemm_qkv(ctx, nullptr, l.Wq, l.Wk, l.Wv, m->pq, m->pk, m->pv, n, qd, kvd, H, xb));
         P_(launch_batch_qkv_rope(s, m->pq, m->pk, m->pv, l.q_norm, l.k_norm, m->pq, l.kc, l.vc, m->pslots,
                                  num_prev_slots, start_clock, n, nq, nkv, D, l.rot, (int)c.k_eq_v, theta, eps));
         // sliding layers see the last 1024 slots (shaders/batch_causal_attn.wgsl:53)
         P_(launch_prefill_attn(s, m->pq, l.kc, l.vc, m->pslots, n, num_prev_slots, nq, D, kvd, gqa, 1.0f,
-                               l.full ? 0u : 1024u, m->pattn));
-        P_(launch_q4gemm(ctx, 1, m->pattn, l.Wo, nullptr, m->pmlp, n, H, qd, m->pxb, true));
-        if (l.has_post_attn) P_(launch_rmsnorm(s, m->pmlp, nullptr, l.post_attn, m->pmlp, H, n, eps, 1.0f, false));
-        P_(launch_rmsnorm(s, m->px, m->pmlp, l.pre_ffn, m->pn, H, n, eps, 1.0f, true));
-        P_(launch_q4gemm(ctx, 2, m->pn, l.Wg, l.Wu, m->pact, n, I, H, m->pxb, true));
-        P_(launch_q4gemm(ctx, 1, m->pact, l.Wd, nullptr, m->pmlp, n, H, I, m->pxb, true));
-        if (l.has_post_ffn) P_(launch_rmsnorm(s, m->pmlp, nullptr, l.post_ffn, m->pmlp, H, n, eps, 1.0f, false));
-        const float *next_norm = (i + 1 < c.num_layers) ? m->L[i + 1].in_norm : m->final_norm;
-        P_(launch_rmsnorm(s, m->px, m->pmlp, next_norm, m->pn, H, n, eps, l.scalar, true));
+                               l.full ? 0u : 1024u, nullptr, xb));
+        P_(launch_q4gemm(ctx, 1, nullptr, l.Wo, nullptr, m->pmlp, n, H, qd, xb, true));
+        P_(launch_rmsnorm_chain(s, m->px, m->pmlp, l.has_post_attn ? l.post_attn : nullptr, l.pre_ffn, xb, nullptr,
+                                H, n, eps, 1.0f, true, true));
+        P_(launch_q4gemm(ctx, 2, nullptr, l.Wg, l.Wu, nullptr, n, I, H, xb, true, actb));
+        P_(launch_q4gemm(ctx, 1, nullptr, l.Wd, nullptr, m->pmlp, n, H, I, actb, true, nullptr, true));
+        const bool last = i + 1 == c.num_layers;
+        const float *next_norm = last ? m->final_norm : m->L[i + 1].in_norm;
+        P_(launch_rmsnorm_chain(s, m->px, m->pmlp, l.has_post_ffn ? l.post_ffn : nullptr, next_norm, xb,
+                                last ? m->pn : nullptr, H, n, eps, l.scalar, true, false));
         if ((i + 1) % 4 == 0 || i + 1 == c.num_layers) {
             if (i + 1 == c.num_layers && (logits_out || topk_ids)) {
                 CHN_HIP(ctx, hipMemcpyAsync(m->normed, m->pn + (size_t)(n - 1) * H, H * 4, hipMemcpyDeviceToDevice, s));

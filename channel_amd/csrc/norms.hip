@@ -7,6 +7,7 @@
 namespace chn {
 
 typedef float f4n __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float block_sum_256(float v, float *sh) {
 #pragma unroll
@@ -50,6 +51,67 @@ int launch_rmsnorm(hipStream_t s, float *x, const float *r, const float *w, floa
                    uint32_t rows, float eps, float scalar, bool add) {
     if (add) k_rmsnorm<true><<<rows, 256, 0, s>>>(x, r, w, y, dim, eps, scalar);
     else k_rmsnorm<false><<<rows, 256, 0, s>>>(x, r, w, y, dim, eps, scalar);
+    return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
+}
+
+// The prefill's norm chain on one row per workgroup: the post-norm of the
+// branch (k_rmsnorm<false> on r with post_w), the residual add
+// (k_rmsnorm<true>) and the input norm of the next contraction, whose
+// result is written as bf16 (the contraction's operand) and optionally as
+// fp32.  The per-thread partial sums, their reduction and every product
+// are those of the two k_rmsnorm passes, so x and y are bit-identical to
+// them (r' is formed where it is added, never stored).  POST needs ADD.
+template <bool POST, bool ADD>
+__global__ __launch_bounds__(256) void k_rmsnorm_chain(float *__restrict__ x, float *__restrict__ r,
+                                                       const float *__restrict__ pw, const float *__restrict__ w,
+                                                       __bf16 *__restrict__ yb, float *__restrict__ y, uint32_t dim,
+                                                       float eps, float scalar, int zero_r) {
+    __shared__ float sh[4];
+    const size_t off = (size_t)blockIdx.x * dim;
+    f4n *xr = (f4n *)(x + off);
+    f4n *rr = (f4n *)(r + off);
+    const f4n *pwr = (const f4n *)pw;
+    const f4n *wr = (const f4n *)w;
+    const uint32_t dv = dim / 4;
+    float inv_r = 1.0f;
+    if (POST) {
+        float ss = 0.0f;
+        for (uint32_t i = threadIdx.x; i < dv; i += 256) {
+            const f4n v = rr[i];
+            ss += ((v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w));
+        }
+        ss = block_sum_256(ss, sh);
+        inv_r = 1.0f / sqrtf(ss / (float)dim + eps);
+    }
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < dv; i += 256) {
+        f4n v = xr[i];
+        if (ADD) {
+            f4n b = rr[i];
+            if (POST) b = (b * inv_r) * pwr[i];
+            v = (v + b) * scalar;
+            xr[i] = v;
+            if (zero_r) rr[i] = f4n{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        ss += ((v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w));
+    }
+    ss = block_sum_256(ss, sh);
+    const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+    for (uint32_t i = threadIdx.x; i < dv; i += 256) {
+        const f4n o = (xr[i] * inv) * wr[i];
+        bf16x2 lo = {(__bf16)o.x, (__bf16)o.y}, hi = {(__bf16)o.z, (__bf16)o.w};
+        *(bf16x2 *)(yb + off + 4 * (size_t)i) = lo;
+        *(bf16x2 *)(yb + off + 4 * (size_t)i + 2) = hi;
+        if (y) *(f4n *)(y + off + 4 * (size_t)i) = o;
+    }
+}
+
+int launch_rmsnorm_chain(hipStream_t s, float *x, float *r, const float *post_w, const float *w, __bf16 *yb,
+                         float *y, uint32_t dim, uint32_t rows, float eps, float scalar, bool add, bool zero_r) {
+    const int z = zero_r ? 1 : 0;
+    if (!add) k_rmsnorm_chain<false, false><<<rows, 256, 0, s>>>(x, r, post_w, w, yb, y, dim, eps, scalar, z);
+    else if (post_w) k_rmsnorm_chain<true, true><<<rows, 256, 0, s>>>(x, r, post_w, w, yb, y, dim, eps, scalar, z);
+    else k_rmsnorm_chain<false, true><<<rows, 256, 0, s>>>(x, r, post_w, w, yb, y, dim, eps, scalar, z);
     return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
 }
 
