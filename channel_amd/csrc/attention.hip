@@ -39,6 +39,12 @@ size_t attn_ws_bytes(uint32_t num_q_heads, uint32_t head_dim, uint32_t max_slots
     return (size_t)dec_splits(max_slots) * num_q_heads * ((size_t)head_dim + 2) * 4;
 }
 
+// Prefill key-split workspace: two parts' sums [n_tok][heads][D] and
+// (max, denominator) pairs.
+size_t prefill_attn_ws_bytes(uint32_t n_tok, uint32_t num_q_heads, uint32_t head_dim) {
+    return 2 * (size_t)n_tok * num_q_heads * ((size_t)head_dim + 2) * 4;
+}
+
 // Running softmax state of one lane: lane row r = lane / 16 holds slots
 // r, r+4, r+8, r+12 of each wave's 16, column c = lane % 16 holds 16*DV
 // consecutive dims, so one slot's row (1 KB at D = 256) is read by a
@@ -651,7 +657,7 @@ __global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict
                                                          const uint32_t *__restrict__ slots, uint32_t num_prev,
                                                          uint32_t n_tok, uint32_t num_q_heads, uint32_t kv_dim,
                                                          float scale, uint32_t window, float *__restrict__ out,
-                                                         __bf16 *__restrict__ outb) {
+                                                         __bf16 *__restrict__ outb, float *__restrict__ ws) {
     constexpr int D = 256, NK = kPaNK, TQ = 64 / GQA;
     __shared__ __attribute__((aligned(16))) unsigned char kh_s[NK * kPaKRow], kl_s[NK * kPaKRow];
     __shared__ __attribute__((aligned(16))) unsigned char vh_s[D * kPaVRow], vl_s[D * kPaVRow];
@@ -668,7 +674,14 @@ __global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict
     // the workgroup's key range: from its first token's start to its last token
     const uint32_t t_first = blockIdx.x * TQ, t_last = min(t_first + TQ - 1, n_tok - 1);
     const uint32_t S_first = num_prev + t_first + 1, S_end = num_prev + t_last + 1;
-    const uint32_t k_begin = (window > 0 && S_first > window) ? S_first - window : 0;
+    const uint32_t k_first = (window > 0 && S_first > window) ? S_first - window : 0;
+    // key split (gridDim.z parts): part z walks its share of the 32-key
+    // chunks [k_first, S_end); the parts' partial states meet in
+    // k_prefill_attn_merge
+    const uint32_t nparts = gridDim.z, part = blockIdx.z;
+    const uint32_t nch = (S_end - k_first + NK - 1) / NK, per = (nch + nparts - 1) / nparts;
+    const uint32_t k_begin = min(S_end, k_first + part * per * NK);
+    const uint32_t k_stop = min(S_end, k_first + (part + 1) * per * NK);
 
     // Q^T operand: lane holds query c, dims 32 j + 8 g .. +8, as hi / lo bf16
     pbf16x8 qh[8], ql[8];
@@ -764,12 +777,12 @@ __global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict
     float m = -INFINITY, l = 0.0f;
 
     Rows rows;
-    gload(k_begin, rows);
-    for (uint32_t c0 = k_begin; c0 < S_end; c0 += NK) {
+    if (k_begin < k_stop) gload(k_begin, rows);
+    for (uint32_t c0 = k_begin; c0 < k_stop; c0 += NK) {
         lds_barrier();                                             // previous chunk's reads done
         stage(rows);
         lds_barrier();
-        if (c0 + NK < S_end) gload(c0 + NK, rows);
+        if (c0 + NK < k_stop) gload(c0 + NK, rows);
 
         // S^T tile tt: keys 16 tt + 4 g + i, query c
         f4 sacc[2] = {f4{0, 0, 0, 0}, f4{0, 0, 0, 0}};
@@ -826,10 +839,45 @@ __global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict
         }
     }
     if (tq >= n_tok) return;
-    const float inv = 1.0f / (l + 1e-9f);
     const size_t orow = ((size_t)tq * num_q_heads + head) * D + 4 * g;
+    if (nparts > 1) {
+        // this part's unnormalised state: sums [part][token][head][D], then
+        // (max, denominator) [part][token][head]
+        const size_t nrow = (size_t)n_tok * num_q_heads;
+#pragma unroll
+        for (int dt = 0; dt < 16; ++dt) *(f4 *)(ws + part * nrow * D + orow + 16 * dt) = o[dt];
+        if (g == 0) {
+            float *ml = ws + nparts * nrow * D + 2 * (part * nrow + (size_t)tq * num_q_heads + head);
+            ml[0] = m;
+            ml[1] = l;
+        }
+        return;
+    }
+    const float inv = 1.0f / (l + 1e-9f);
 #pragma unroll
     for (int dt = 0; dt < 16; ++dt) store_out4(out, outb, orow + 16 * dt, o[dt] * inv);
+}
+
+// The key-split parts' states of each (token, head) rescaled to their
+// common maximum and normalised; four values per thread.
+__global__ __launch_bounds__(256) void k_prefill_attn_merge(const float *__restrict__ ws, uint32_t nparts,
+                                                            size_t nrow, uint32_t D, float *__restrict__ out,
+                                                            __bf16 *__restrict__ outb) {
+    const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;   // element of [token][head][D]
+    if (i >= nrow * D) return;
+    const size_t row = i / D;
+    const float *ml = ws + nparts * nrow * D;
+    float mx = -INFINITY;
+    for (uint32_t p = 0; p < nparts; ++p) mx = fmaxf(mx, ml[2 * (p * nrow + row)]);
+    f4 t = f4{0, 0, 0, 0};
+    float den = 0.0f;
+    for (uint32_t p = 0; p < nparts; ++p) {
+        const float mp = ml[2 * (p * nrow + row)], lp = ml[2 * (p * nrow + row) + 1];
+        const float a = mp == -INFINITY ? 0.0f : __expf(mp - mx);
+        t += *(const f4 *)(ws + p * nrow * D + i) * a;
+        den += lp * a;
+    }
+    store_out4(out, outb, i, t * (1.0f / (den + 1e-9f)));
 }
 
 static int launch_decode_impl(chn_ctx *ctx, const float *q, float *kc, float *vc, const uint32_t *slots,
@@ -900,13 +948,19 @@ int launch_rope_decode_attn(chn_ctx *ctx, const float *q_in, const float *k_in, 
 
 int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const float *vc, const uint32_t *slots,
                         uint32_t n_tok, uint32_t num_prev, uint32_t num_q_heads, uint32_t head_dim, uint32_t kv_dim,
-                        uint32_t gqa, float scale, uint32_t window, float *out, __bf16 *outb) {
+                        uint32_t gqa, float scale, uint32_t window, float *out, __bf16 *outb, float *ws) {
     if (head_dim == 256 && (gqa == 1 || gqa == 2 || gqa == 4 || gqa == 8)) {
         const uint32_t tq = 64 / gqa;
-        const dim3 mgrid((n_tok + tq - 1) / tq, num_q_heads / gqa);
+        const uint32_t tiles = (n_tok + tq - 1) / tq;
+        // Causal tiles differ in length (the last one walks every key): with
+        // no more tiles than CUs, each tile's keys are split between two
+        // workgroups, which halves the longest walk and fills the part
+        // (512 tokens: 128 tiles of up to 16 chunks -> 256 of up to 8).
+        const uint32_t nparts = (ws && tiles * (num_q_heads / gqa) <= 256) ? 2 : 1;
+        const dim3 mgrid(tiles, num_q_heads / gqa, nparts);
 #define CHN_PATTN_MF(G) \
     k_prefill_attn_mf<G><<<mgrid, 256, 0, st>>>(q, kc, vc, slots, num_prev, n_tok, num_q_heads, kv_dim, scale, window, \
-                                                out, outb)
+                                                out, outb, ws)
         switch (gqa) {
         case 1: CHN_PATTN_MF(1); break;
         case 2: CHN_PATTN_MF(2); break;
@@ -914,6 +968,10 @@ int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const f
         default: CHN_PATTN_MF(8); break;
         }
 #undef CHN_PATTN_MF
+        if (nparts > 1) {
+            const size_t nrow = (size_t)n_tok * num_q_heads, nq4 = nrow * head_dim / 4;
+            k_prefill_attn_merge<<<(unsigned)((nq4 + 255) / 256), 256, 0, st>>>(ws, nparts, nrow, head_dim, out, outb);
+        }
         return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
     }
     dim3 grid(n_tok, num_q_heads / gqa);
@@ -1129,8 +1187,10 @@ extern "C" int chn_batch_causal_attn(chn_ctx *ctx, const float *q, const float *
     CHN_REQUIRE(ctx, aligned(q, 16) && aligned(k_cache, 16) && aligned(v_cache, 16) && aligned(out, 16),
                 "q, caches and out must be 16-byte aligned");
     if (!n_tok || !num_q_heads) return CHN_OK;
-    int rc = launch_prefill_attn(ctx->stream, q, k_cache, v_cache, slots, n_tok, num_prev_slots, num_q_heads, head_dim,
-                                 kv_dim, gqa_ratio, scale, window, out);
+    int rc = ensure_workspace(ctx, prefill_attn_ws_bytes(n_tok, num_q_heads, head_dim));
+    if (rc) return rc;
+    rc = launch_prefill_attn(ctx->stream, q, k_cache, v_cache, slots, n_tok, num_prev_slots, num_q_heads, head_dim,
+                             kv_dim, gqa_ratio, scale, window, out, nullptr, (float *)ctx->ws);
     if (rc == CHN_E_UNSUPPORTED)
         return set_err(ctx, rc, "head_dim %u / gqa %u unsupported", head_dim, gqa_ratio);
     CHN_LAUNCHED(ctx, "k_prefill_attn");

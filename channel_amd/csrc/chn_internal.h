@@ -182,9 +182,13 @@ int launch_rope_decode_attn(chn_ctx *ctx, const float *q_in, const float *k_in, 
                             uint32_t kv_dim, uint32_t gqa, uint32_t rot, int k_eq_v, const float2 *rope_tab,
                             float eps, float scale, float *out, float *ws, uint32_t *xp);
 // out: [n_tok][num_q_heads * head_dim] fp32, or bf16 into outb when set.
+// ws (prefill_attn_ws_bytes, or NULL): lets short prompts split each query
+// tile's keys between two workgroups.
+size_t prefill_attn_ws_bytes(uint32_t n_tok, uint32_t num_q_heads, uint32_t head_dim);
 int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const float *vc, const uint32_t *slots,
                         uint32_t n_tok, uint32_t num_prev, uint32_t num_q_heads, uint32_t head_dim, uint32_t kv_dim,
-                        uint32_t gqa, float scale, uint32_t window, float *out, __bf16 *outb = nullptr);
+                        uint32_t gqa, float scale, uint32_t window, float *out, __bf16 *outb = nullptr,
+                        float *ws = nullptr);
 size_t xbytes_bytes(uint32_t nb);
 int launch_gemv_q8(hipStream_t st, const uint32_t *W, const float *x, float *y, uint32_t M, uint32_t nb,
                    uint32_t *xp_ws);

@@ -50,7 +50,7 @@ struct chn_model {
     uint64_t *topk_ws;
     // prefill buffers
     uint32_t max_tok = 0;
-    float *px, *pn, *pq, *pk, *pv, *pmlp, *pact;
+    float *px, *pn, *pq, *pk, *pv, *pmlp, *pact, *pattn_ws;
     __bf16 *pxb;
     uint32_t *pslots, *ptok;
     // pinned staging
@@ -189,6 +189,7 @@ static int alloc_runtime(chn_model *m) {
     M_ALLOC(m->pk, (size_t)T * kvd * 4);
     M_ALLOC(m->pv, (size_t)T * kvd * 4);
     M_ALLOC(m->pmlp, (size_t)T * H * 4);
+    M_ALLOC(m->pattn_ws, prefill_attn_ws_bytes(T, c.num_heads, md.D));
     M_ALLOC(m->pact, (size_t)T * I * 4);
     M_ALLOC(m->pxb, (size_t)T * (H > qd ? H : qd) * 2);   // bf16 operands of width H or qd; act goes to pact
     M_ALLOC(m->pslots, (size_t)(kSlotsMax + T) * 4);
@@ -751,7 +752,7 @@ extern "C" int chn_prefill(chn_model *m, const uint32_t *tokens, uint32_t n, con
                                  num_prev_slots, start_clock, n, nq, nkv, D, l.rot, (int)c.k_eq_v, theta, eps));
         // sliding layers see the last 1024 slots (shaders/batch_causal_attn.wgsl:53)
         P_(launch_prefill_attn(s, m->pq, l.kc, l.vc, m->pslots, n, num_prev_slots, nq, D, kvd, gqa, 1.0f,
-                               l.full ? 0u : 1024u, nullptr, xb));
+                               l.full ? 0u : 1024u, nullptr, xb, m->pattn_ws));
         P_(launch_q4gemm(ctx, 1, nullptr, l.Wo, nullptr, m->pmlp, n, H, qd, xb, true));
         P_(launch_rmsnorm_chain(s, m->px, m->pmlp, l.has_post_attn ? l.post_attn : nullptr, l.pre_ffn, xb, nullptr,
                                 H, n, eps, 1.0f, true, true));
