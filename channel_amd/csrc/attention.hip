@@ -39,10 +39,12 @@ size_t attn_ws_bytes(uint32_t num_q_heads, uint32_t head_dim, uint32_t max_slots
     return (size_t)dec_splits(max_slots) * num_q_heads * ((size_t)head_dim + 2) * 4;
 }
 
-// Prefill key-split workspace: two parts' sums [n_tok][heads][D] and
-// (max, denominator) pairs.
+// Prefill key split: up to kPaParts workgroups per query tile; the
+// workspace holds each part's sums [n_tok][heads][D] and (max,
+// denominator) pairs.
+constexpr uint32_t kPaParts = 2;   // 4 measured slower at 512 tokens (20.65 against 20.28 ms)
 size_t prefill_attn_ws_bytes(uint32_t n_tok, uint32_t num_q_heads, uint32_t head_dim) {
-    return 2 * (size_t)n_tok * num_q_heads * ((size_t)head_dim + 2) * 4;
+    return kPaParts * (size_t)n_tok * num_q_heads * ((size_t)head_dim + 2) * 4;
 }
 
 // Running softmax state of one lane: lane row r = lane / 16 holds slots
@@ -952,11 +954,14 @@ int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const f
     if (head_dim == 256 && (gqa == 1 || gqa == 2 || gqa == 4 || gqa == 8)) {
         const uint32_t tq = 64 / gqa;
         const uint32_t tiles = (n_tok + tq - 1) / tq;
-        // Causal tiles differ in length (the last one walks every key): with
-        // no more tiles than CUs, each tile's keys are split between two
-        // workgroups, which halves the longest walk and fills the part
-        // (512 tokens: 128 tiles of up to 16 chunks -> 256 of up to 8).
-        const uint32_t nparts = (ws && tiles * (num_q_heads / gqa) <= 256) ? 2 : 1;
+        // Causal tiles differ in length (the last one walks every key): while
+        // the tiles fill fewer than two workgroups per CU, each tile's keys
+        // are split between up to kPaParts workgroups, which shortens the
+        // longest walk and fills the part (512 tokens: 128 tiles of up to 16
+        // chunks -> 256 of up to 8; 76 -> ~45 us per layer).
+        const uint32_t wgs = tiles * (num_q_heads / gqa);
+        uint32_t nparts = ws ? 512 / (wgs ? wgs : 1) : 1;
+        nparts = nparts < 1 ? 1 : (nparts > kPaParts ? kPaParts : nparts);
         const dim3 mgrid(tiles, num_q_heads / gqa, nparts);
 #define CHN_PATTN_MF(G) \
     k_prefill_attn_mf<G><<<mgrid, 256, 0, st>>>(q, kc, vc, slots, num_prev, n_tok, num_q_heads, kv_dim, scale, window, \
