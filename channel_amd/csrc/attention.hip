@@ -958,7 +958,8 @@ int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const f
         // the tiles fill fewer than two workgroups per CU, each tile's keys
         // are split between up to kPaParts workgroups, which shortens the
         // longest walk and fills the part (512 tokens: 128 tiles of up to 16
-        // chunks -> 256 of up to 8; 76 -> ~45 us per layer).
+        // chunks -> 256 of up to 8: 76 -> 44 us per layer, plus 5.6 us of
+        // merge).
         const uint32_t wgs = tiles * (num_q_heads / gqa);
         uint32_t nparts = ws ? 512 / (wgs ? wgs : 1) : 1;
         nparts = nparts < 1 ? 1 : (nparts > kPaParts ? kPaParts : nparts);
