@@ -1018,7 +1018,8 @@ __device__ __forceinline__ float wave_sum(float v) {
 // RMSNorm * w, then RoPE on pairs (d, d + rot/2) at `clock`, suffix past
 // rot copied (shaders/qkv_rope.wgsl:42-91).
 __device__ void norm_rope_head(const float *__restrict__ in, const float *__restrict__ w, float *__restrict__ out,
-                               uint32_t D, uint32_t rot, float theta, float eps, uint32_t clock, float *buf) {
+                               uint32_t D, uint32_t rot, float theta, float eps, uint32_t clock, float *buf,
+                               const float2 *__restrict__ cs_tab = nullptr) {
     const int lane = threadIdx.x;
     float ss = 0.0f;
     for (uint32_t d = lane; d < D; d += 64) ss += in[d] * in[d];
@@ -1029,10 +1030,18 @@ __device__ void norm_rope_head(const float *__restrict__ in, const float *__rest
     const uint32_t half = rot / 2;
     for (uint32_t d = lane; d < half; d += 64) {
         const float v0 = buf[d], v1 = buf[d + half];
-        const float fe = (2.0f * (float)d) / (float)rot;
-        const float freq = 1.0f / powf(theta, fe);
-        const float ang = (float)clock * freq;
-        const float c = cosf(ang), s = sinf(ang);
+        float c, s;
+        if (cs_tab) {
+            const float2 t = cs_tab[d];
+            c = t.x;
+            s = t.y;
+        } else {
+            const float fe = (2.0f * (float)d) / (float)rot;
+            const float freq = 1.0f / powf(theta, fe);
+            const float ang = (float)clock * freq;
+            c = cosf(ang);
+            s = sinf(ang);
+        }
         out[d] = v0 * c - v1 * s;
         out[d + half] = v0 * s + v1 * c;
     }
@@ -1077,21 +1086,23 @@ __global__ __launch_bounds__(64) void k_batch_qkv_rope(const float *__restrict__
                                                        float *__restrict__ k_cache, float *__restrict__ v_cache,
                                                        const uint32_t *__restrict__ slots, uint32_t slot_offset,
                                                        uint32_t start_clock, uint32_t num_q, uint32_t num_kv,
-                                                       uint32_t D, uint32_t rot, int k_eq_v, float theta, float eps) {
+                                                       uint32_t D, uint32_t rot, int k_eq_v, float theta, float eps,
+                                                       const float2 *__restrict__ tab) {
     __shared__ float buf[512];
     const uint32_t head = blockIdx.x, t = blockIdx.y;
     const uint32_t clock = start_clock + t, slot = slots[slot_offset + t];
     const size_t q_dim = (size_t)num_q * D, kv_dim = (size_t)num_kv * D;
+    const float2 *cs = tab ? tab + (size_t)t * (rot / 2) : nullptr;
     if (head < num_q) {
         norm_rope_head(q_in + t * q_dim + (size_t)head * D, qw, q_out + t * q_dim + (size_t)head * D, D, rot, theta,
-                       eps, clock, buf);
+                       eps, clock, buf, cs);
         return;
     }
     const uint32_t h = head - num_q;
     if (h >= num_kv) return;
     const float *k = k_in + t * kv_dim + (size_t)h * D;
     const float *v = k_eq_v ? k : v_in + t * kv_dim + (size_t)h * D;
-    norm_rope_head(k, kw, k_cache + (size_t)slot * kv_dim + (size_t)h * D, D, rot, theta, eps, clock, buf);
+    norm_rope_head(k, kw, k_cache + (size_t)slot * kv_dim + (size_t)h * D, D, rot, theta, eps, clock, buf, cs);
     const int lane = threadIdx.x;
     float ss = 0.0f;
     for (uint32_t d = lane; d < D; d += 64) ss += v[d] * v[d];
@@ -1112,10 +1123,33 @@ int launch_qkv_rope(hipStream_t st, const float *q_in, const float *k_in, const 
 int launch_batch_qkv_rope(hipStream_t st, const float *q_in, const float *k_in, const float *v_in, const float *qw,
                           const float *kw, float *q_out, float *kc, float *vc, const uint32_t *slots,
                           uint32_t slot_offset, uint32_t start_clock, uint32_t n_tok, uint32_t num_q, uint32_t num_kv,
-                          uint32_t D, uint32_t rot, int k_eq_v, float theta, float eps) {
+                          uint32_t D, uint32_t rot, int k_eq_v, float theta, float eps, const float2 *tab) {
     dim3 grid(num_q + num_kv, n_tok);
     k_batch_qkv_rope<<<grid, 64, 0, st>>>(q_in, k_in, v_in, qw, kw, q_out, kc, vc, slots, slot_offset, start_clock,
-                                          num_q, num_kv, D, rot, k_eq_v, theta, eps);
+                                          num_q, num_kv, D, rot, k_eq_v, theta, eps, tab);
+    return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
+}
+
+// (cos, sin) of (start_clock + t) * theta^(-2d / rot) for t < n_tok, d <
+// rot / 2, at tab[t * rot / 2 + d]: the same expressions the batched
+// rotation evaluates per element, once per prompt instead of per layer.
+__global__ __launch_bounds__(256) void k_rope_tab_batch(float2 *__restrict__ tab, uint32_t start_clock,
+                                                        uint32_t n_tok, uint32_t rot, float theta) {
+    const uint32_t half = rot / 2;
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)n_tok * half) return;
+    const uint32_t t = (uint32_t)(i / half), d = (uint32_t)(i % half);
+    const float fe = (2.0f * (float)d) / (float)rot;
+    const float freq = 1.0f / powf(theta, fe);
+    const float ang = (float)(start_clock + t) * freq;
+    tab[i] = float2{cosf(ang), sinf(ang)};
+}
+
+int launch_rope_tab_batch(hipStream_t st, float2 *tab, uint32_t start_clock, uint32_t n_tok, uint32_t rot,
+                          float theta) {
+    const size_t n = (size_t)n_tok * (rot / 2);
+    if (!n) return CHN_OK;
+    k_rope_tab_batch<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(tab, start_clock, n_tok, rot, theta);
     return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
 }
 

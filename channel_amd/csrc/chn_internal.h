@@ -163,10 +163,14 @@ int mvr_mlp_nx(chn_ctx *ctx, const void *Wg, const void *Wu, float *act, uint32_
 int launch_qkv_rope(hipStream_t st, const float *q_in, const float *k_in, const float *v_in, const float *qw,
                     const float *kw, float *q_out, float *kc, float *vc, const uint32_t *step, uint32_t num_q,
                     uint32_t num_kv, uint32_t D, uint32_t rot, int k_eq_v, float theta, float eps);
+// tab (or NULL): the prompt's (cos, sin) table from launch_rope_tab_batch
+// for this rot and theta.
 int launch_batch_qkv_rope(hipStream_t st, const float *q_in, const float *k_in, const float *v_in, const float *qw,
                           const float *kw, float *q_out, float *kc, float *vc, const uint32_t *slots,
                           uint32_t slot_offset, uint32_t start_clock, uint32_t n_tok, uint32_t num_q, uint32_t num_kv,
-                          uint32_t D, uint32_t rot, int k_eq_v, float theta, float eps);
+                          uint32_t D, uint32_t rot, int k_eq_v, float theta, float eps, const float2 *tab = nullptr);
+int launch_rope_tab_batch(hipStream_t st, float2 *tab, uint32_t start_clock, uint32_t n_tok, uint32_t rot,
+                          float theta);
 size_t attn_ws_bytes(uint32_t num_q_heads, uint32_t head_dim, uint32_t max_slots);
 // ws holds attn_ws_bytes(); xp (nullable) receives the digit planes of out
 // (num_q_heads * head_dim / 32 blocks).

@@ -51,6 +51,7 @@ struct chn_model {
     // prefill buffers
     uint32_t max_tok = 0;
     float *px, *pn, *pq, *pk, *pv, *pmlp, *pact, *pattn_ws;
+    float2 *prope;       // prefill (cos, sin) per token: [2 kinds][T][rot / 2]
     __bf16 *pxb;
     uint32_t *pslots, *ptok;
     // pinned staging
@@ -190,6 +191,7 @@ static int alloc_runtime(chn_model *m) {
     M_ALLOC(m->pv, (size_t)T * kvd * 4);
     M_ALLOC(m->pmlp, (size_t)T * H * 4);
     M_ALLOC(m->pattn_ws, prefill_attn_ws_bytes(T, c.num_heads, md.D));
+    M_ALLOC(m->prope, (size_t)2 * T * kRopePairs * sizeof(float2));
     M_ALLOC(m->pact, (size_t)T * I * 4);
     M_ALLOC(m->pxb, (size_t)T * (H > qd ? H : qd) * 2);   // bf16 operands of width H or qd; act goes to pact
     M_ALLOC(m->pslots, (size_t)(kSlotsMax + T) * 4);
@@ -741,6 +743,11 @@ extern "C" int chn_prefill(chn_model *m, const uint32_t *tokens, uint32_t n, con
     // down's split-K halves then add into.
     __bf16 *xb = m->pxb;
     __bf16 *actb = (__bf16 *)m->pact;
+    // the prompt's rotation angles, once per kind (sliding / full layers)
+    const HeadShape hs[2] = {head_shape(c, false), head_shape(c, true)};
+    const float thetas[2] = {c.rope_theta, c.rope_theta_full};
+    float2 *ptab[2] = {m->prope, m->prope + (size_t)m->max_tok * kRopePairs};
+    for (int k = 0; k < 2; ++k) P_(launch_rope_tab_batch(s, ptab[k], start_clock, n, hs[k].rot, thetas[k]));
     for (uint32_t i = 0; i < c.num_layers; ++i) {
         const auto &l = m->L[i];
         const float theta = l.full ? c.rope_theta_full : c.rope_theta;
@@ -749,7 +756,8 @@ extern "C" int chn_prefill(chn_model *m, const uint32_t *tokens, uint32_t n, con
         const uint32_t D = l.D, nkv = l.nkv, qd = l.qd, kvd = l.kvd, gqa = l.gqa;
         P_(launch_q4gemm_qkv(ctx, nullptr, l.Wq, l.Wk, l.Wv, m->pq, m->pk, m->pv, n, qd, kvd, H, xb));
         P_(launch_batch_qkv_rope(s, m->pq, m->pk, m->pv, l.q_norm, l.k_norm, m->pq, l.kc, l.vc, m->pslots,
-                                 num_prev_slots, start_clock, n, nq, nkv, D, l.rot, (int)c.k_eq_v, theta, eps));
+                                 num_prev_slots, start_clock, n, nq, nkv, D, l.rot, (int)c.k_eq_v, theta, eps,
+                                 ptab[l.full ? 1 : 0]));
         // sliding layers see the last 1024 slots (shaders/batch_causal_attn.wgsl:53)
         P_(launch_prefill_attn(s, m->pq, l.kc, l.vc, m->pslots, n, num_prev_slots, nq, D, kvd, gqa, 1.0f,
                                l.full ? 0u : 1024u, nullptr, xb, m->pattn_ws));
