@@ -685,16 +685,19 @@ static void launch_to_bf16(hipStream_t st, const float *X, __bf16 *xb, size_t n,
 }
 
 // Launch shapes for one pipelined single-matrix contraction (K % 64 == 0),
-// from sweeps at 512 tokens: 128 x 128 tiles when they alone give at least
-// 1.5 workgroups per CU (15360 x 3840: 97 us against 135 us for 128 x 64:
-// half the LDS fragment reads per MFMA); for long K (>= 8192) 128 x 128
-// tiles with K split in two, whose larger per-step work pays for itself over
-// the longer loop; else 128-token x 64-feature tiles when they give at least
-// ~200 workgroups; otherwise the same tiles with K split in two.
+// from sweeps at 512 tokens:
+//  * 128 x 128 tiles when they alone give at least one workgroup per CU
+//    (half the LDS fragment reads per MFMA of 128 x 64 tiles; 15360 x 3840:
+//    97 us against 135 us, q/k/v 8192 x 3840: 54 against 69 us; 128 such
+//    workgroups lose to 256 of 128 x 64);
+//  * for long K (>= 8192) 128 x 128 tiles with K split in two, whose larger
+//    per-step work pays for itself over the longer loop;
+//  * else 128-token x 64-feature tiles when they give at least ~200
+//    workgroups, otherwise the same tiles with K split in two.
 enum class PipeShape { BN64, BN64_K2, BN128, BN128_K2 };
 static PipeShape pipe_shape(uint32_t n_tok, uint32_t M, uint32_t K) {
     const uint32_t tt = (n_tok + 127) / 128;
-    if (((M + 127) / 128) * tt >= 384) return PipeShape::BN128;
+    if (((M + 127) / 128) * tt >= 256) return PipeShape::BN128;
     if (K >= 8192 && 2 * ((M + 127) / 128) * tt >= 192) return PipeShape::BN128_K2;
     if (((M + 63) / 64) * tt >= 192 || K < 128) return PipeShape::BN64;
     return PipeShape::BN64_K2;
@@ -745,7 +748,7 @@ int launch_q4gemm(chn_ctx *ctx, int nmat, const float *X, const uint32_t *W0, co
 
 // q, k and v of one layer in one launch: three repacked matrices over the
 // same activations (one bf16 conversion, none when X is NULL and xb already
-// holds them), 128 x 64 tiles.
+// holds them).
 int launch_q4gemm_qkv(chn_ctx *ctx, const float *X, const uint32_t *Wq, const uint32_t *Wk, const uint32_t *Wv,
                       float *Yq, float *Yk, float *Yv, uint32_t n_tok, uint32_t Mq, uint32_t Mkv, uint32_t K,
                       __bf16 *xb) {
@@ -766,7 +769,10 @@ int launch_q4gemm_qkv(chn_ctx *ctx, const float *X, const uint32_t *Wq, const ui
     a.Wg[1] = Wv;
     a.Yg[1] = Yv;
     a.Mg[1] = Mkv;
-    launch_gemm_p<1, 64, true, 4>(ctx->stream, a, 1);
+    // 128 x 128 tiles once they give a workgroup per CU, as pipe_shape
+    const uint32_t ct128 = (Mq + 127) / 128 + 2 * ((Mkv + 127) / 128), tt = (n_tok + 127) / 128;
+    if (ct128 * tt >= 256) launch_gemm_p<1, 128, true, 4>(ctx->stream, a, 1);
+    else launch_gemm_p<1, 64, true, 4>(ctx->stream, a, 1);
     CHN_LAUNCHED(ctx, "k_q4gemm_p");
     return CHN_OK;
 }
