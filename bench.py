@@ -38,6 +38,13 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 METRIC = "decode tok/s + Q4 GEMV achieved HBM GB/s (% of peak), 12B-class, 1 GPU"
 SEED = 0xC4A77E1
 ROTATE_BYTES = 1 << 30  # >= 4x the 256 MB Infinity Cache
+# What the decode matvecs compute in: Q4 weights times activations rounded
+# to 18-bit block fixed point (per 32-block, 2^-18 of the block's power-of-
+# two bound), exact int32 block dots, fp32 across blocks.
+DTYPE_Q4MV = ("q4 x 18-bit block-fixed-point activations (exact int32 block dots via v_dot8c_i32_i4, "
+              "fp32 across blocks)")
+DTYPE_DECODE = (DTYPE_Q4MV + "; q8 logits x 22-bit block-fixed-point activations; fp32 attention, norms and "
+                "KV cache")
 
 
 def q4_bytes(rows, K):
@@ -195,7 +202,7 @@ def bench_mlp(ctx, args):
                      "algorithmic_bytes_per_launch": gateup_bytes,
                      "avg_launch_ms": k_ms},
         "cpu_baseline": cpu,
-        "dtype": "fp32 accumulate over Q4 weights",
+        "dtype": DTYPE_Q4MV if rep else DTYPE_Q4MV + " (reference layout)",
     }
 
 
@@ -221,13 +228,24 @@ def alloc_gateup_copies(ctx, H, I, min_bytes=ROTATE_BYTES, repacked=False):
     return pairs
 
 
-def time_gateup(ctx, pairs, x, act, H, I, reps, repacked=False):
+def time_gateup(ctx, pairs, x, act, H, I, reps, repacked=False, fused_norm=False):
     """Average duration (ms) of the fused gate/up matvec over back-to-back
-    launches on the library stream, HIP events.  Repacked: the model's
-    kernel alone (k_q4rmv_mlp_xp: planes of x in, act and its planes out),
-    x's planes made once beforehand; reference layout: chn_fused_mlp_q4
-    (its planes pass + matvec)."""
-    if repacked:
+    launches on the library stream, HIP events.  fused_norm: the decode
+    step's launch (chn_ffn_gate_up_q4r = k_q4rmv_mlp_xp<8, NORM_POST_ADD>:
+    post-attention norm, residual add and pre-FFN norm as the prologue,
+    act and its planes out); repacked: the same matvec reading ready-made
+    planes of x (k_q4rmv_mlp_xp<4, -1>, x's planes made once beforehand);
+    reference layout: chn_fused_mlp_q4 (its planes pass + matvec)."""
+    if fused_norm:
+        r = ctx.alloc(H * 4)
+        ctx.call("chn_synth_normal", r, H, SEED + 8, 1.0)
+        ones = ctx.alloc(H * 4)
+        ctx.fill_u32(ones, 0x3F800000, H)
+        x_out, normed = ctx.alloc(H * 4), ctx.alloc(H * 4)
+        act_planes = ctx.alloc(xplanes_bytes(I))
+        calls = [ctx.bind("chn_ffn_gate_up_q4r", g, u, x, r, ones, ones, x_out, normed, act, act_planes, I, H, 1e-6)
+                 for g, u in pairs]
+    elif repacked:
         planes = ctx.alloc(xplanes_bytes(H))
         act_planes = ctx.alloc(xplanes_bytes(I))
         ctx.call("chn_xplanes", x, H, planes)
@@ -242,10 +260,14 @@ def time_gateup(ctx, pairs, x, act, H, I, reps, repacked=False):
     return ctx.timer_stop() / reps
 
 
-def gateup_bytes(H, I, repacked=False):
+def gateup_bytes(H, I, repacked=False, fused_norm=False):
     """Bytes of one gate/up launch: the reference layout's algorithmic count
-    (20 B per 32 weights), or what the repacked layout reads (18 B)."""
+    (20 B per 32 weights), or what the repacked layout reads (18 B); x in,
+    act out.  fused_norm: the decode step's form also reads x_in, r and the
+    two norm weights, writes x_out and the planes of act (84 B per 32)."""
     w = q4r_bytes(I, H) if repacked else q4_bytes(I, H)
+    if fused_norm:
+        return 2 * w + 5 * H * 4 + I * 4 + xplanes_bytes(I)
     return 2 * w + H * 4 + I * 4
 
 
@@ -392,14 +414,14 @@ def bench_decode(ctx, args):
 
     # the same steps driven token by token through the reference-shaped
     # interface (host slot lists uploaded per token, ids copied back)
+    from channel_amd import ring
     window = cfg["sliding_window"]
     tok = int(gen[-1])
     n_api = 32
     t0 = time.perf_counter()
     for _ in range(n_api):
-        n = min(clock + 1, 4096)
-        active = ((np.arange(n, dtype=np.int64) + clock + 1 - n) % 4096).astype(np.uint32)
-        tok, _, _ = m.forward_token_id(tok, clock, clock % 4096, active, active[max(0, n - window):])
+        slot, active, sliding = ring.decode_lists(clock, window)
+        tok, _, _ = m.forward_token_id(tok, clock, slot, active, sliding)
         clock += 1
     api_ms = (time.perf_counter() - t0) * 1e3 / n_api
     mid_ctx = ctx_start + args.steps // 2
@@ -412,8 +434,11 @@ def bench_decode(ctx, args):
     x = ctx.alloc(H * 4)
     ctx.call("chn_synth_normal", x, H, SEED + 7, 1.0)
     act = ctx.alloc(I * 4)
-    k_ms = time_gateup(ctx, pairs, x, act, H, I, max(192, 4 * len(pairs)), repacked=True)
-    achieved = gateup_bytes(H, I) / (k_ms * 1e-3) / 1e9
+    reps = max(192, 4 * len(pairs))
+    k_ms = time_gateup(ctx, pairs, x, act, H, I, reps, repacked=True, fused_norm=True)
+    achieved = gateup_bytes(H, I, fused_norm=True) / (k_ms * 1e-3) / 1e9
+    sa_ms = time_gateup(ctx, pairs, x, act, H, I, reps, repacked=True)
+    sa_gbps = gateup_bytes(H, I) / (sa_ms * 1e-3) / 1e9
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -434,16 +459,22 @@ def bench_decode(ctx, args):
                    "token_roofline_frac": (w_bytes + kv_bytes) / (ms_per_tok * 1e-3) / 1e9 / HBM_PEAK_GBS,
                    "model_create_s": t_create,
                    "decode_launch": "eager kernel launches" if args.eager else "HIP graph replay"},
-        "roofline": {"kernel": "k_q4rmv_mlp_xp (chn_fused_mlp_q4r_xp: gate/up + GELU-tanh + planes of act, "
-                               "15360x3840 x2, repacked weights as the model holds them)",
+        "roofline": {"kernel": "k_q4rmv_mlp_xp<8,NORM_POST_ADD> (chn_ffn_gate_up_q4r, the decode step's "
+                               "launch: post-attention norm + residual + pre-FFN norm prologue, gate/up 15360x3840 "
+                               "x2 + GELU-tanh * up + planes of act, repacked weights as the model holds them)",
                      "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": load_traffic("k_q4rmv_mlp_xp", "gate/up 15360x3840"),
-                     "algorithmic_bytes_per_launch": gateup_bytes(H, I),
-                     "bytes_per_launch_repacked_layout": gateup_bytes(H, I, repacked=True),
-                     "avg_launch_ms": k_ms},
+                     "traffic": load_traffic("k_q4rmv_mlp_xp<8,2>", "gate/up 15360x3840"),
+                     "algorithmic_bytes_per_launch": gateup_bytes(H, I, fused_norm=True),
+                     "bytes_per_launch_repacked_layout": gateup_bytes(H, I, repacked=True, fused_norm=True),
+                     "avg_launch_ms": k_ms,
+                     "standalone_from_planes": {
+                         "kernel": "k_q4rmv_mlp_xp<4,-1> (chn_fused_mlp_q4r_xp: x's planes ready-made)",
+                         "avg_launch_ms": sa_ms, "achieved": sa_gbps, "frac": sa_gbps / HBM_PEAK_GBS,
+                         "algorithmic_bytes_per_launch": gateup_bytes(H, I),
+                         "traffic": load_traffic("k_q4rmv_mlp_xp", "gate/up 15360x3840")}},
         "cpu_baseline": cpu,
-        "dtype": "fp32 accumulate over Q4 weights (Q8 logits)",
+        "dtype": DTYPE_DECODE,
         "data": "synthetic (seeded random-init 12B Q4 weights: codes uniform 0..15, f16 scales "
                 "U(0.005, 0.02), norms 1, bf16 embedding ~ N(0, 0.02) tied to Q8 logits; prompt of "
                 "uniform random token ids)",
@@ -503,7 +534,7 @@ def bench_gemv(ctx, args):
                      "traffic": load_traffic("k_q4mv<GEMV,XIN>", "8192x2048"),
                      "algorithmic_bytes_per_launch": nbytes, "avg_launch_ms": k_ms},
         "cpu_baseline": cpu,
-        "dtype": "fp32 accumulate over Q4 weights",
+        "dtype": DTYPE_Q4MV,
     }
 
 

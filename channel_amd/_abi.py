@@ -54,8 +54,12 @@ PROTOTYPES = {
     "chn_xplanes": (c_int, [c_void_p, c_void_p, c_u32, c_void_p]),
     "chn_gemv_q4r_xp": (c_int, [c_void_p] * 4 + [c_u32, c_u32]),
     "chn_fused_mlp_q4r_xp": (c_int, [c_void_p] * 6 + [c_u32, c_u32]),
+    "chn_ffn_gate_up_q4r": (c_int, [c_void_p] * 11 + [c_u32, c_u32, c_f32]),
     "chn_batch_gemm_q4": (c_int, [c_void_p] * 4 + [c_u32] * 3),
     "chn_batch_fused_mlp_q4": (c_int, [c_void_p] * 5 + [c_u32] * 3),
+    "chn_batch_gemm_q4r": (c_int, [c_void_p] * 4 + [c_u32] * 3),
+    "chn_batch_qkv_q4r": (c_int, [c_void_p] * 8 + [c_u32] * 4),
+    "chn_batch_fused_mlp_q4r": (c_int, [c_void_p] * 6 + [c_u32] * 3),
     "chn_qkv_rope": (c_int, [c_void_p] + [c_void_p] * 9 + [c_u32] * 4 + [c_int, c_f32, c_f32]),
     "chn_decode_attn": (c_int, [c_void_p] + [c_void_p] * 5 + [c_u32] * 5 + [c_f32, c_void_p]),
     "chn_rmsnorm": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_u32, c_f32]),
@@ -79,7 +83,7 @@ PROTOTYPES = {
                                 c_void_p, c_void_p, P(c_u32)]),
     "chn_decode_token": (c_int, [c_void_p, c_u32, c_u32, c_u32, c_void_p, c_u32, c_void_p, c_u32,
                                  c_void_p, c_void_p, P(c_u32)]),
-    "chn_decode_greedy": (c_int, [c_void_p, c_u32, c_u32, c_u32, c_void_p]),
+    "chn_decode_greedy": (c_int, [c_void_p, c_u32, c_u32, c_u32, c_void_p, c_void_p]),
     "chn_prefill": (c_int, [c_void_p, c_void_p, c_u32, c_void_p, c_void_p, c_u32, c_u32, c_u32,
                             c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "chn_kv_read": (c_int, [c_void_p, c_u32, c_u32, c_u32, c_void_p, c_void_p]),

@@ -387,23 +387,35 @@ __device__ __forceinline__ void wave_sum4(float v0, float v1, float v2, float v3
 // lanes must call (with zeros where ok is false); only ok lanes store.
 // Plane word (p, w) of block b goes to xp[(p * 4 + w) * ws + b * bs], the
 // block's scale to xp[XP_WORDS * ws + b * bs].
+// A block holding NaN or Inf gets zero digits and a NaN scale, so every
+// product with it is NaN, as the fp32 products of the reference would be
+// non-finite.  Blocks whose largest magnitude is below 2^-100 contribute
+// zero (their products are below 2^-100 of the weights).
 __device__ __forceinline__ void emit_planes8s(const float (&v)[8], uint32_t *__restrict__ xp, uint32_t ws,
                                               uint32_t bs, uint32_t b, uint32_t w, bool ok) {
     float m = 0.0f;
+    uint32_t bad = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
+    for (int i = 0; i < 8; ++i) {
+        m = fmaxf(m, fabsf(v[i]));
+        bad |= !(fabsf(v[i]) <= 3.4028235e38f);     // NaN or Inf
+    }
     m = fmaxf(m, __shfl_xor(m, 1, 64));
     m = fmaxf(m, __shfl_xor(m, 2, 64));
+    bad |= __shfl_xor(bad, 1, 64);
+    bad |= __shfl_xor(bad, 2, 64);
     int e = 0;
     (void)frexpf(m, &e);           // m = f * 2^e, f in [0.5, 1): |x_i| < 2^e
     float scale = 0.0f, inv = 0.0f;
-    if (m > 0.0f && e > -100) {
+    if (bad) {
+        inv = __builtin_nanf("");
+    } else if (m > 0.0f && e > -100) {
         scale = ldexpf(1.0f, XP_FRAC - e);
         inv = ldexpf(1.0f, e - XP_FRAC);
     }
     uint32_t u[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) u[i] = (uint32_t)((int)rintf(v[i] * scale) + (int)XP_BIAS);
+    for (int i = 0; i < 8; ++i) u[i] = (uint32_t)((int)rintf((bad ? 0.0f : v[i]) * scale) + (int)XP_BIAS);
     if (!ok) return;
 #pragma unroll
     for (int p = 0; p < XP_PLANES; ++p) {

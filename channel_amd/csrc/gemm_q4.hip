@@ -778,15 +778,16 @@ int launch_q4gemm_qkv(chn_ctx *ctx, const float *X, const uint32_t *Wq, const ui
 }
 
 static int gemm_common(chn_ctx *ctx, int nmat, const uint32_t *W0, const uint32_t *W1, const float *X, float *Y,
-                       uint32_t n_tok, uint32_t M, uint32_t K) {
-    CHN_REQUIRE(ctx, W0 && X && Y && (nmat == 1 || W1), "NULL argument");
+                       uint32_t n_tok, uint32_t M, uint32_t K, bool repacked = false, __bf16 *Yb = nullptr) {
+    CHN_REQUIRE(ctx, W0 && X && (Y || Yb) && (nmat == 1 || W1), "NULL argument");
     CHN_REQUIRE(ctx, K > 0 && K % 32 == 0, "K=%u must be a positive multiple of 32", K);
     CHN_REQUIRE(ctx, K % 8 == 0 && aligned(X, 16), "X must be 16-byte aligned");
-    CHN_REQUIRE(ctx, aligned(W0, 4) && (!W1 || aligned(W1, 4)), "weights must be 4-byte aligned");
+    CHN_REQUIRE(ctx, aligned(W0, repacked ? 16 : 4) && (!W1 || aligned(W1, repacked ? 16 : 4)),
+                "weights must be %d-byte aligned", repacked ? 16 : 4);
     if (!n_tok || !M) return CHN_OK;
     int rc = ensure_workspace(ctx, (size_t)n_tok * K * 2);
     if (rc) return rc;
-    return launch_q4gemm(ctx, nmat, X, W0, W1, Y, n_tok, M, K, (__bf16 *)ctx->ws, false);
+    return launch_q4gemm(ctx, nmat, X, W0, W1, Y, n_tok, M, K, (__bf16 *)ctx->ws, repacked, Yb);
 }
 
 }  // namespace chn
@@ -803,4 +804,34 @@ extern "C" int chn_batch_fused_mlp_q4(chn_ctx *ctx, const uint32_t *Wg, const ui
                                       float *Y, uint32_t n_tok, uint32_t M, uint32_t K) {
     if (!ctx) return CHN_E_INVALID;
     return gemm_common(ctx, 2, Wg, Wu, X, Y, n_tok, M, K);
+}
+
+// The model's prefill contractions over repacked (Q4R) weights, as
+// chn_prefill launches them.
+extern "C" int chn_batch_gemm_q4r(chn_ctx *ctx, const void *W, const float *X, float *Y, uint32_t n_tok, uint32_t M,
+                                  uint32_t K) {
+    if (!ctx) return CHN_E_INVALID;
+    return gemm_common(ctx, 1, (const uint32_t *)W, nullptr, X, Y, n_tok, M, K, true);
+}
+
+extern "C" int chn_batch_fused_mlp_q4r(chn_ctx *ctx, const void *Wg, const void *Wu, const float *X, float *Y,
+                                       uint16_t *Y_bf16, uint32_t n_tok, uint32_t M, uint32_t K) {
+    if (!ctx) return CHN_E_INVALID;
+    CHN_REQUIRE(ctx, (Y == nullptr) != (Y_bf16 == nullptr), "exactly one of Y and Y_bf16 must be given");
+    return gemm_common(ctx, 2, (const uint32_t *)Wg, (const uint32_t *)Wu, X, Y, n_tok, M, K, true,
+                       (__bf16 *)Y_bf16);
+}
+
+extern "C" int chn_batch_qkv_q4r(chn_ctx *ctx, const void *Wq, const void *Wk, const void *Wv, const float *X,
+                                 float *Yq, float *Yk, float *Yv, uint32_t n_tok, uint32_t q_dim, uint32_t kv_dim,
+                                 uint32_t K) {
+    if (!ctx) return CHN_E_INVALID;
+    CHN_REQUIRE(ctx, Wq && Wk && Wv && X && Yq && Yk && Yv, "NULL argument");
+    CHN_REQUIRE(ctx, K > 0 && K % 32 == 0, "K=%u must be a positive multiple of 32", K);
+    CHN_REQUIRE(ctx, aligned(X, 16) && aligned(Wq, 16) && aligned(Wk, 16) && aligned(Wv, 16), "misaligned argument");
+    if (!n_tok || !q_dim || !kv_dim) return CHN_OK;
+    int rc = ensure_workspace(ctx, (size_t)n_tok * K * 2);
+    if (rc) return rc;
+    return launch_q4gemm_qkv(ctx, X, (const uint32_t *)Wq, (const uint32_t *)Wk, (const uint32_t *)Wv, Yq, Yk, Yv,
+                             n_tok, q_dim, kv_dim, K, (__bf16 *)ctx->ws);
 }

@@ -29,13 +29,23 @@ __global__ __launch_bounds__(256) void k_xbytes(const float *__restrict__ x, uin
     const bool ok = b < nb;
     float4 v = ok ? *(const float4 *)(x + (size_t)b * 32 + w * 4) : make_float4(0, 0, 0, 0);
     float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    // NaN or Inf in the block: zero digits and a NaN scale (the products of
+    // the reference's fp32 matvec would be non-finite)
+    uint32_t bad = !(fabsf(v.x) <= 3.4028235e38f) | !(fabsf(v.y) <= 3.4028235e38f) |
+                   !(fabsf(v.z) <= 3.4028235e38f) | !(fabsf(v.w) <= 3.4028235e38f);
     m = fmaxf(m, __shfl_xor(m, 1, 64));
     m = fmaxf(m, __shfl_xor(m, 2, 64));
     m = fmaxf(m, __shfl_xor(m, 4, 64));
+    bad |= __shfl_xor(bad, 1, 64);
+    bad |= __shfl_xor(bad, 2, 64);
+    bad |= __shfl_xor(bad, 4, 64);
     int e = 0;
     (void)frexpf(m, &e);
     float scale = 0.0f, inv = 0.0f;
-    if (m > 0.0f && e > -100) {
+    if (bad) {
+        inv = __builtin_nanf("");
+        v = make_float4(0, 0, 0, 0);
+    } else if (m > 0.0f && e > -100) {
         scale = ldexpf(1.0f, XB_FRAC - e);
         inv = ldexpf(1.0f, e - XB_FRAC);
     }

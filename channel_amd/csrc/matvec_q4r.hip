@@ -803,3 +803,23 @@ extern "C" int chn_fused_mlp_q4r_xp(chn_ctx *ctx, const void *Wg, const void *Wu
     if (act_planes) return mvr_mlp_xp(ctx, Wg, Wu, planes, act, act_planes, M, K);
     return mvr_mlp(ctx, Wg, Wu, nullptr, act, M, K, (uint32_t *)planes, true);
 }
+
+// The decode step's pre-FFN block as the model launches it: the
+// post-attention norm of r (post_w != NULL), the residual add, the pre-FFN
+// norm, gate/up + GELU-tanh * up and the digit planes of act, one launch.
+extern "C" int chn_ffn_gate_up_q4r(chn_ctx *ctx, const void *Wg, const void *Wu, const float *x_in, const float *r,
+                                   const float *post_w, const float *pre_w, float *x_out, float *normed_out,
+                                   float *act, uint32_t *act_planes, uint32_t M, uint32_t K, float eps) {
+    if (!ctx) return CHN_E_INVALID;
+    CHN_REQUIRE(ctx, Wg && Wu && x_in && r && pre_w && x_out && act && act_planes, "NULL argument");
+    CHN_REQUIRE(ctx, K > 0 && K % 32 == 0 && K <= 4096, "K=%u must be a positive multiple of 32, <= 4096", K);
+    CHN_REQUIRE(ctx, M > 0 && M % 32 == 0, "M=%u must be a positive multiple of 32", M);
+    CHN_REQUIRE(ctx, aligned(Wg, 16) && aligned(Wu, 16), "weights must be 16-byte aligned");
+    CHN_REQUIRE(ctx, aligned(x_in, 16) && aligned(r, 16) && aligned(pre_w, 16) && aligned(x_out, 16) &&
+                         (!post_w || aligned(post_w, 16)) && (!normed_out || aligned(normed_out, 16)),
+                "vectors must be 16-byte aligned");
+    CHN_REQUIRE(ctx, aligned(act_planes, 4), "act_planes must be 4-byte aligned");
+    CHN_REQUIRE(ctx, x_out != x_in, "x_out must not alias x_in (other workgroups still read x_in)");
+    const NormArgs n{x_in, r, post_w, pre_w, x_out, normed_out, eps, 1.0f, RopeTab{nullptr, nullptr, {0.0f, 0.0f}, {0u, 0u}}};
+    return mvr_mlp_nx(ctx, Wg, Wu, act, act_planes, M, K, n, post_w ? NORM_POST_ADD : NORM_ADD);
+}

@@ -63,6 +63,8 @@ struct chn_model {
     // device-resident greedy decoding: {clock, count, start token}, tokens out
     uint32_t *gen = nullptr, *gen_tokens = nullptr;
     uint32_t *h_gen = nullptr;
+    // ring state the greedy head reads: turn boundaries, recall clocks
+    uint32_t *ring_bounds = nullptr, *ring_recall = nullptr;
     std::vector<void *> allocs;
 };
 
@@ -174,6 +176,8 @@ static int alloc_runtime(chn_model *m) {
     M_ALLOC(m->tok, 64);
     M_ALLOC(m->gen, 64);
     M_ALLOC(m->gen_tokens, (size_t)kGreedyCap * 4);
+    M_ALLOC(m->ring_bounds, 1024 * 4);
+    M_ALLOC(m->ring_recall, 128 * 4);
     const uint32_t kmax = H > I ? (H > qd ? H : qd) : (I > qd ? I : qd);
     size_t mvb = mv_ws_bytes(kmax);
     if (xbytes_bytes(H / 32) > mvb) mvb = xbytes_bytes(H / 32);
@@ -217,29 +221,75 @@ static int alloc_runtime(chn_model *m) {
 }
 
 // ---- device-resident greedy steps
-// Head: the step parameters and the chronological slot lists of a 4096-slot
-// ring without anchors (slot = clock mod 4096; the global list holds the
-// last min(clock + 1, 4096) slots, the sliding list the last `window` of
-// them: getSlotIndexLayer / getActiveSlotsLayer, src/ring_buffer.zig:
-// 118-121,287-333, for num_anchors = 0), and the input token: the start
-// token on the first step, the previous step's argmax after that.
+// The reference's ring (DynamicRingBuffer, src/ring_buffer.zig:17-355):
+// anchors [0, A) keep clocks 0..A-1, the FIFO window [A, 3968) takes clock c
+// at A + (c - A) mod (3968 - A), the recall tier [3968, 4096) holds
+// retrieved entries.  gen = {clock, count, start token, A, n_boundaries,
+// has_recall}.
+static constexpr uint32_t kRecallStart = kSlotsMax - 128;
+static constexpr uint32_t kMaxAnchors = kRecallStart - 64;    // setNumAnchors' cap
+static constexpr uint32_t kMaxBoundaries = 1024;
+static constexpr uint32_t kRecallNone = 0xFFFFFFFFu;
+
+// Head of one greedy step: the step parameters {clock, slot_idx, S_global,
+// S_sliding}, the chronological slot lists that getActiveSlotsLayer gives
+// for a history in which every clock so far was written
+// (src/ring_buffer.zig:291-333: anchors, the window from the snapped start
+// (snapToBoundary, :92-100), then the recall slots whose clock has passed;
+// the sliding list: the newest `window` clocks, anchors included, no
+// recall), and the input token (the start token, then the previous step's
+// argmax).
 __global__ __launch_bounds__(256) void k_greedy_head(const uint32_t *__restrict__ gen,
                                                      const uint32_t *__restrict__ topk_ids,
+                                                     const uint32_t *__restrict__ bounds,
+                                                     const uint32_t *__restrict__ recall,
                                                      uint32_t *__restrict__ step, uint32_t *__restrict__ slots,
                                                      uint32_t *__restrict__ tok, uint32_t window) {
-    const uint32_t clock = gen[0], count = gen[1];
-    const uint32_t n = clock + 1 < kSlotsMax ? clock + 1 : kSlotsMax;
-    const uint32_t ns = n < window ? n : window;
-    if (threadIdx.x == 0) {
+    __shared__ uint32_t s_first, s_cnt[2];
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint32_t clock = gen[0], count = gen[1], A = gen[3], nb = gen[4];
+    const uint32_t W = kRecallStart - A;
+    // global window: raw start, snapped to the first boundary at or after it
+    const uint32_t raw = clock >= W ? clock - W + 1 : 0;
+    if (t == 0) s_first = kRecallNone;
+    __syncthreads();
+    if (raw > A)
+        for (uint32_t i = t; i < nb; i += 256)
+            if (bounds[i] >= raw) atomicMin(&s_first, i);
+    __syncthreads();
+    const uint32_t gmin = s_first == kRecallNone ? raw : bounds[s_first];
+    const uint32_t na = clock + 1 < A ? clock + 1 : A;
+    const uint32_t gs = gmin > A ? gmin : A;
+    const uint32_t nw = clock >= gs ? clock + 1 - gs : 0;
+    for (uint32_t i = t; i < na; i += 256) slots[i] = i;
+    for (uint32_t i = t; i < nw; i += 256) slots[na + i] = A + (gs + i - A) % W;
+    // recall ranks whose clock has passed, in rank order (two waves, ballots)
+    bool f = false;
+    if (t < 128 && gen[5]) {
+        const uint32_t r = recall[t];
+        f = r != kRecallNone && r <= clock;
+    }
+    const uint64_t bal = __ballot(f);
+    if (lane == 0 && wave < 2) s_cnt[wave] = (uint32_t)__popcll(bal);
+    __syncthreads();
+    const uint32_t pre = (uint32_t)__popcll(bal & ((1ull << lane) - 1ull)) + (wave == 1 ? s_cnt[0] : 0u);
+    if (f) slots[na + nw + pre] = kRecallStart + t;
+    // sliding list: the newest `window` clocks whose slot still holds them
+    const uint32_t raws = clock >= window ? clock - window + 1 : 0;
+    const uint32_t nas = na > raws ? na - raws : 0;
+    uint32_t ss = raws > A ? raws : A;
+    ss = raw > ss ? raw : ss;
+    const uint32_t nsw = clock >= ss ? clock + 1 - ss : 0;
+    uint32_t *sl = slots + kSlotsMax;
+    for (uint32_t i = t; i < nas; i += 256) sl[i] = raws + i;
+    for (uint32_t i = t; i < nsw; i += 256) sl[nas + i] = A + (ss + i - A) % W;
+    if (t == 0) {
         step[0] = clock;
-        step[1] = clock % kSlotsMax;
-        step[2] = n;
-        step[3] = ns;
+        step[1] = clock < A ? clock : A + (clock - A) % W;
+        step[2] = na + nw + s_cnt[0] + s_cnt[1];
+        step[3] = nas + nsw;
         tok[0] = count == 0 ? gen[2] : topk_ids[0];
     }
-    const uint32_t first = clock + 1 - n;
-    for (uint32_t i = threadIdx.x; i < n; i += 256) slots[i] = (first + i) % kSlotsMax;
-    for (uint32_t i = threadIdx.x; i < ns; i += 256) slots[kSlotsMax + i] = (clock + 1 - ns + i) % kSlotsMax;
 }
 
 // Tail: append this step's argmax (top-64 ids[0]) and advance the clock.
@@ -319,7 +369,8 @@ static int record_decode(chn_model *m, bool with_logits) {
 static int record_greedy(chn_model *m) {
     hipStream_t s = m->ctx->stream;
     const uint32_t H = m->cfg.hidden_size;
-    k_greedy_head<<<1, 256, 0, s>>>(m->gen, m->topk_ids, m->step, m->slots, m->tok, m->cfg.sliding_window);
+    k_greedy_head<<<1, 256, 0, s>>>(m->gen, m->topk_ids, m->ring_bounds, m->ring_recall, m->step, m->slots, m->tok,
+                                    m->cfg.sliding_window);
     if (hipGetLastError() != hipSuccess) return hip_fail(m->ctx, hipGetLastError(), "k_greedy_head");
     if (launch_embed(s, m->embed_bf16, m->tok, 1, H, sqrtf((float)H), m->x))
         return hip_fail(m->ctx, hipGetLastError(), "k_embed");
@@ -665,19 +716,36 @@ extern "C" int chn_decode_token(chn_model *m, uint32_t token, uint32_t clock, ui
 // n greedy steps on the device (see k_greedy_head): one host round trip
 // for the whole run.
 extern "C" int chn_decode_greedy(chn_model *m, uint32_t token, uint32_t clock, uint32_t n_steps,
-                                 uint32_t *tokens_out) {
+                                 const chn_ring_state *ring, uint32_t *tokens_out) {
     if (!m) return CHN_E_INVALID;
     chn_ctx *ctx = m->ctx;
     hipStream_t s = ctx->stream;
     CHN_REQUIRE(ctx, token < m->cfg.vocab_size, "token %u out of range", token);
     CHN_REQUIRE(ctx, n_steps <= kGreedyCap, "n_steps %u exceeds %u", n_steps, kGreedyCap);
     CHN_REQUIRE(ctx, tokens_out || !n_steps, "NULL tokens_out");
+    const chn_ring_state none{0, 0, nullptr, nullptr};
+    const chn_ring_state &r = ring ? *ring : none;
+    CHN_REQUIRE(ctx, r.num_anchors <= kMaxAnchors, "num_anchors %u exceeds %u", r.num_anchors, kMaxAnchors);
+    CHN_REQUIRE(ctx, r.num_boundaries <= kMaxBoundaries, "%u turn boundaries (at most %u)", r.num_boundaries,
+                kMaxBoundaries);
+    CHN_REQUIRE(ctx, r.boundaries || !r.num_boundaries, "NULL boundaries");
+    CHN_REQUIRE(ctx, (uint64_t)clock + n_steps <= 0xFFFFFFFEull, "clock %u + %u steps overflows", clock, n_steps);
     if (!n_steps) return CHN_OK;
     CHN_HIP(ctx, hipStreamSynchronize(s));
+    // staging in the pinned buffer: gen at 0, boundaries at 16, recall at 16 + 1024
+    uint32_t *hb = m->h_gen + 16, *hr = m->h_gen + 16 + kMaxBoundaries;
     m->h_gen[0] = clock;
     m->h_gen[1] = 0;
     m->h_gen[2] = token;
-    CHN_HIP(ctx, hipMemcpyAsync(m->gen, m->h_gen, 12, hipMemcpyHostToDevice, s));
+    m->h_gen[3] = r.num_anchors;
+    m->h_gen[4] = r.num_boundaries;
+    m->h_gen[5] = r.recall_clocks ? 1u : 0u;
+    if (r.num_boundaries) std::memcpy(hb, r.boundaries, (size_t)r.num_boundaries * 4);
+    if (r.recall_clocks) std::memcpy(hr, r.recall_clocks, 128 * 4);
+    CHN_HIP(ctx, hipMemcpyAsync(m->gen, m->h_gen, 6 * 4, hipMemcpyHostToDevice, s));
+    if (r.num_boundaries)
+        CHN_HIP(ctx, hipMemcpyAsync(m->ring_bounds, hb, (size_t)r.num_boundaries * 4, hipMemcpyHostToDevice, s));
+    if (r.recall_clocks) CHN_HIP(ctx, hipMemcpyAsync(m->ring_recall, hr, 128 * 4, hipMemcpyHostToDevice, s));
     for (uint32_t i = 0; i < n_steps; ++i) {
         if (m->use_graph) {
             CHN_HIP(ctx, hipGraphLaunch(m->exec[2], s));

@@ -67,6 +67,13 @@ def _bf16_ptr(a, keep):
 _PROGRESS = ctypes.CFUNCTYPE(None, ctypes.c_size_t, ctypes.c_size_t, c_void_p)
 
 
+class RingState(ctypes.Structure):
+    """chn_ring_state: the DynamicRingBuffer state (src/ring_buffer.zig:17-355)
+    that decides a contiguous history's slot lists."""
+    _fields_ = [("num_anchors", c_u32), ("num_boundaries", c_u32), ("boundaries", c_void_p),
+                ("recall_clocks", c_void_p)]
+
+
 class Model:
     """A model resident in HBM: Q4 layer weights, Q8 tied embedding, 4096-slot
     fp32 KV caches per layer, the recorded decode graphs."""
@@ -157,12 +164,19 @@ class Model:
             None if vals is None else vals.ctypes.data_as(c_void_p), ctypes.byref(tok)))
         return tok.value, ids, vals
 
-    def decode_greedy(self, token, clock, n_steps):
-        """n_steps greedy steps on the device over an anchor-free 4096-slot
-        ring; returns the generated token ids."""
+    def decode_greedy(self, token, clock, n_steps, num_anchors=0, boundaries=(), recall_clocks=None):
+        """n_steps greedy steps on the device over the reference's 4096-slot
+        ring (chn_ring_state: anchors, turn boundaries oldest first, the
+        clocks of the 128 recall slots or None); returns the generated ids."""
         out = np.zeros(max(int(n_steps), 1), np.uint32)
+        b = np.ascontiguousarray(boundaries, dtype=np.uint32)
+        rc = None if recall_clocks is None else np.ascontiguousarray(recall_clocks, dtype=np.uint32)
+        if rc is not None and rc.size != 128:
+            raise ValueError("recall_clocks must hold 128 entries")
+        st = RingState(int(num_anchors), b.size, b.ctypes.data_as(c_void_p) if b.size else None,
+                       None if rc is None else rc.ctypes.data_as(c_void_p))
         self._check("chn_decode_greedy", lib.chn_decode_greedy(self.handle, int(token), int(clock), int(n_steps),
-                                                               out.ctypes.data_as(c_void_p)))
+                                                               ctypes.byref(st), out.ctypes.data_as(c_void_p)))
         return out[: int(n_steps)]
 
     def prefill_batch(self, tokens, slots, start_clock, num_prev_slots, embed_bf16=None,

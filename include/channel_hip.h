@@ -163,6 +163,18 @@ int chn_gemv_q4r_xp(chn_ctx *ctx, const void *W, const uint32_t *planes, float *
 int chn_fused_mlp_q4r_xp(chn_ctx *ctx, const void *Wg, const void *Wu, const uint32_t *planes, float *act,
                          uint32_t *act_planes, uint32_t M, uint32_t K);
 
+/* The decode step's pre-FFN block in one launch, as the model runs it:
+ * r' = rmsnorm(r) * post_w (post_w != NULL; else r' = r), x_out = x_in + r',
+ * normed = rmsnorm(x_out) * pre_w (written to normed_out if non-NULL),
+ * act[m] = gelu_tanh(Wg[m].normed) * (Wu[m].normed) over Q4R weights, and the
+ * digit planes of act (chn_xplanes layout, CHN_XPLANES_BYTES(M)) for the down
+ * projection.  recordRmsNorm + recordAddRmsNorm + recordGateUpSwiGlu
+ * (src/gpu/model_dispatch.zig:33-40) fused.  K <= 4096, M % 32 == 0;
+ * vectors 16-byte aligned; x_out must not alias x_in. */
+int chn_ffn_gate_up_q4r(chn_ctx *ctx, const void *Wg, const void *Wu, const float *x_in, const float *r,
+                        const float *post_w, const float *pre_w, float *x_out, float *normed_out, float *act,
+                        uint32_t *act_planes, uint32_t M, uint32_t K, float eps);
+
 /* Y[t][r] = sum_k X[t][k] * W[r][k] for t < n_tok, r < M: X fp32 [n_tok][K]
  * (16-byte aligned), W Q4 [M][K], Y fp32 [n_tok][M].  Operands are rounded
  * to bf16 (X) and bf16(scale*(q-8)) (W, dequantized in LDS) for MFMA with
@@ -178,6 +190,22 @@ int chn_batch_gemm_q4(chn_ctx *ctx, const uint32_t *W, const float *X, float *Y,
  * src/gpu/batch_dispatch.zig:121-123). */
 int chn_batch_fused_mlp_q4(chn_ctx *ctx, const uint32_t *Wg, const uint32_t *Wu,
                            const float *X, float *Y, uint32_t n_tok, uint32_t M, uint32_t K);
+
+/* The same contractions over Q4R weights (chn_q4_repack), launched as
+ * chn_prefill launches them: chn_batch_gemm_q4r as the o and down
+ * projections (src/gpu/batch_dispatch.zig:108-109,129-130),
+ * chn_batch_qkv_q4r as q, k and v in one launch over the same activations
+ * (:70-81), chn_batch_fused_mlp_q4r as gate/up with the product written as
+ * fp32 (Y) or as bf16 bits (Y_bf16, the form the down projection reads;
+ * exactly one of the two) (:121-123).  X fp32 [n_tok][K], 16-byte aligned;
+ * weights 16-byte aligned. */
+int chn_batch_gemm_q4r(chn_ctx *ctx, const void *W, const float *X, float *Y, uint32_t n_tok, uint32_t M,
+                       uint32_t K);
+int chn_batch_qkv_q4r(chn_ctx *ctx, const void *Wq, const void *Wk, const void *Wv, const float *X,
+                      float *Yq, float *Yk, float *Yv, uint32_t n_tok, uint32_t q_dim, uint32_t kv_dim,
+                      uint32_t K);
+int chn_batch_fused_mlp_q4r(chn_ctx *ctx, const void *Wg, const void *Wu, const float *X, float *Y,
+                            uint16_t *Y_bf16, uint32_t n_tok, uint32_t M, uint32_t K);
 
 /* ======================================================================
  * Attention, RoPE and norms (src/gpu/kernels.zig:131-164)
@@ -342,15 +370,39 @@ int chn_decode_token(chn_model *m, uint32_t token, uint32_t clock, uint32_t slot
                      const uint32_t *active, uint32_t n_active, const uint32_t *sliding,
                      uint32_t n_sliding, uint32_t *topk_ids, float *topk_vals, uint32_t *token_out);
 
+/* The state of the reference's KV ring (DynamicRingBuffer,
+ * src/ring_buffer.zig:17-355) that decides a decode step's slot lists when
+ * every clock so far was written and nothing was evicted.  The ring holds
+ * 4096 slots: anchors [0, num_anchors) keep clocks 0..num_anchors-1, the FIFO
+ * window [num_anchors, 3968) takes clock c at slot
+ * num_anchors + (c - num_anchors) mod (3968 - num_anchors)
+ * (getSlotIndexLayer, :117-122), the recall tier [3968, 4096) holds
+ * retrieved entries (writeRecallKV, :277-285). */
+#define CHN_RECALL_NONE 0xFFFFFFFFu
+typedef struct chn_ring_state {
+    uint32_t num_anchors;            /* <= 3904 (setNumAnchors' cap, :101-103) */
+    uint32_t num_boundaries;         /* turn boundaries, <= 1024 (markBoundary, :79-90) */
+    const uint32_t *boundaries;      /* host, oldest first; snapToBoundary (:92-100) moves
+                                        the global window's start to the first one at or
+                                        after it */
+    const uint32_t *recall_clocks;   /* host, 128 entries: the clock held by recall slot
+                                        3968 + r, or CHN_RECALL_NONE; NULL = none active */
+} chn_ring_state;
+
 /* n_steps (<= 4096) greedy decode steps without host round trips: the
- * server's decode loop (src/server/decode.zig) over gpuDispatchForwardToken
- * with the slot lists of a 4096-slot ring without anchors (slot = clock mod
- * 4096; global list = the last min(clock + 1, 4096) slots, sliding list =
- * the last cfg.sliding_window of them; src/ring_buffer.zig:118-121,287-333)
- * generated on the device.  Step i feeds token (i = 0) or step i-1's argmax
- * at clock + i; tokens_out[i] = step i's argmax.  Equivalent to n calls of
- * chn_decode_token with those lists.  No direct reference counterpart. */
-int chn_decode_greedy(chn_model *m, uint32_t token, uint32_t clock, uint32_t n_steps, uint32_t *tokens_out);
+ * server's decode loop (src/server/decode.zig:7-27) over forwardToken's GPU
+ * branch (src/model/forward.zig:41-47) with the slot lists generated on the
+ * device.  Step i runs at clock + i with slot_idx = getSlotIndexLayer(clock
+ * + i), the global list = getActiveSlotsLayer(layer 0, full) = the anchors,
+ * the window clocks from the snapped start of the newest 3968 - num_anchors,
+ * then the recall slots whose clock is <= clock + i; the sliding list = the
+ * newest cfg.sliding_window clocks (anchors included, no recall)
+ * (src/ring_buffer.zig:291-333).  Step i feeds token (i = 0) or step i-1's
+ * argmax; tokens_out[i] = step i's argmax.  ring NULL = no anchors, no
+ * boundaries, no recall.  Equivalent to n calls of chn_decode_token with
+ * those lists.  No direct reference counterpart. */
+int chn_decode_greedy(chn_model *m, uint32_t token, uint32_t clock, uint32_t n_steps,
+                      const chn_ring_state *ring, uint32_t *tokens_out);
 
 /* gpuDispatchPrefillBatch: n <= max_prefill_tokens tokens (else
  * CHN_E_BATCH_TOO_LARGE); slots[0..n_slots) lists num_prev_slots earlier

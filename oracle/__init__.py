@@ -54,7 +54,19 @@ _PROTOS = {
     "orc_gemv_q4_mt": (None, [_u32p, _f32p, _f32p, _u32, _u32, _int]),
     "orc_fused_mlp_step_mt": (None, [_u32p, _u32p, _u32p, _f32p, _f32p, _f32p, _u32, _u32, _int]),
     "orc_gemv_q8_mt": (None, [_u32p, _f32p, _f32p, _u32, _u32, _int]),
+    "orc_quantize_matrix_q4_mt": (None, [_u32p, _u16p, _size, _size, _int]),
+    "orc_quantize_matrix_q8_mt": (None, [_u32p, _u16p, _size, _size, _int]),
+    "orc_batch_gemm_q4_bf16_mt": (None, [_u32p, _f32p, _f32p, _u32, _u32, _u32, _int]),
+    "orc_fused_mlp_q4_mt": (None, [_u32p, _u32p, _f32p, _f32p, _u32, _u32, _int]),
+    "orc_batch_causal_attn_mt": (None, [_f32p, _f32p, _f32p, _u32p, _u32, _u32, _u32, _u32, _u32,
+                                        _u32, _f32, _u32, _f32p, _int]),
+    "orc_gelu_tanh_vec": (None, [_f32p, _f32p, _size]),
+    "orc_softcap_vec": (None, [_f32p, _f32p, _size]),
 }
+
+# Threads for the checking forms at full model sizes (results are
+# bit-identical to the serial routines whatever the count).
+NTHREADS = max(1, min(16, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()))
 
 
 def _load():
@@ -100,20 +112,26 @@ def bf16_from_f32(v):
     return np.array([lib.orc_bf16_from_f32(float(x)) for x in np.ravel(v)], dtype=np.uint16)
 
 
-def quantize_q4(w_bf16):
+def quantize_q4(w_bf16, nthreads=1):
     """[rows, cols] bf16 bits -> Q4 words [rows, cols/32*5] (quant.zig:58-98)."""
     w = _c(w_bf16, np.uint16)
     rows, cols = w.shape
     out = np.zeros((rows, (cols + 31) // 32 * 5), dtype=np.uint32)
-    lib.orc_quantize_matrix_q4(out, w, rows, cols)
+    if nthreads > 1:
+        lib.orc_quantize_matrix_q4_mt(out, w, rows, cols, int(nthreads))
+    else:
+        lib.orc_quantize_matrix_q4(out, w, rows, cols)
     return out
 
 
-def quantize_q8(w_bf16):
+def quantize_q8(w_bf16, nthreads=1):
     w = _c(w_bf16, np.uint16)
     rows, cols = w.shape
     out = np.zeros((rows, (cols + 31) // 32 * 9), dtype=np.uint32)
-    lib.orc_quantize_matrix_q8(out, w, rows, cols)
+    if nthreads > 1:
+        lib.orc_quantize_matrix_q8_mt(out, w, rows, cols, int(nthreads))
+    else:
+        lib.orc_quantize_matrix_q8(out, w, rows, cols)
     return out
 
 
@@ -130,12 +148,18 @@ def dequant_q8(W, rows, K):
 
 
 def gelu_tanh(x):
-    return np.array([lib.orc_gelu_tanh(float(v)) for v in np.ravel(x)], dtype=np.float32)
+    a = _c(np.ravel(x), np.float32)
+    y = np.zeros(a.size, np.float32)
+    lib.orc_gelu_tanh_vec(a, y, a.size)
+    return y
 
 
-def gemv_q4(W, x, M, K):
+def gemv_q4(W, x, M, K, nthreads=1):
     y = np.zeros(M, dtype=np.float32)
-    lib.orc_gemv_q4(_q4(W, M, K), _c(x, np.float32, K), y, M, K)
+    if nthreads > 1:
+        lib.orc_gemv_q4_mt(_q4(W, M, K), _c(x, np.float32, K), y, M, K, int(nthreads) - 1)
+    else:
+        lib.orc_gemv_q4(_q4(W, M, K), _c(x, np.float32, K), y, M, K)
     return y
 
 
@@ -145,7 +169,10 @@ def gemv_q4_mt(W, x, M, K, nthreads):
     return y
 
 
-def fused_qkv_q4(Wq, Wk, Wv, x, q_dim, kv_dim, K):
+def fused_qkv_q4(Wq, Wk, Wv, x, q_dim, kv_dim, K, nthreads=1):
+    if nthreads > 1:
+        return (gemv_q4(Wq, x, q_dim, K, nthreads), gemv_q4(Wk, x, kv_dim, K, nthreads),
+                gemv_q4(Wv, x, kv_dim, K, nthreads))
     q = np.zeros(q_dim, np.float32)
     k = np.zeros(kv_dim, np.float32)
     v = np.zeros(kv_dim, np.float32)
@@ -154,9 +181,12 @@ def fused_qkv_q4(Wq, Wk, Wv, x, q_dim, kv_dim, K):
     return q, k, v
 
 
-def fused_mlp_q4(Wg, Wu, x, M, K):
+def fused_mlp_q4(Wg, Wu, x, M, K, nthreads=1):
     act = np.zeros(M, np.float32)
-    lib.orc_fused_mlp_q4(_q4(Wg, M, K), _q4(Wu, M, K), _c(x, np.float32, K), act, M, K)
+    if nthreads > 1:
+        lib.orc_fused_mlp_q4_mt(_q4(Wg, M, K), _q4(Wu, M, K), _c(x, np.float32, K), act, M, K, int(nthreads))
+    else:
+        lib.orc_fused_mlp_q4(_q4(Wg, M, K), _q4(Wu, M, K), _c(x, np.float32, K), act, M, K)
     return act
 
 
@@ -174,9 +204,12 @@ def gemv_q8_mt(W, x, M, K, nthreads):
     return y
 
 
-def gemv_q8(W, x, M, K):
+def gemv_q8(W, x, M, K, nthreads=1):
     y = np.zeros(M, dtype=np.float32)
-    lib.orc_gemv_q8(_q8(W, M, K), _c(x, np.float32, K), y, M, K)
+    if nthreads > 1:
+        lib.orc_gemv_q8_mt(_q8(W, M, K), _c(x, np.float32, K), y, M, K, int(nthreads) - 1)
+    else:
+        lib.orc_gemv_q8(_q8(W, M, K), _c(x, np.float32, K), y, M, K)
     return y
 
 
@@ -186,9 +219,12 @@ def batch_gemm_q4(W, X, n_tok, M, K):
     return Y
 
 
-def batch_gemm_q4_bf16(W, X, n_tok, M, K):
+def batch_gemm_q4_bf16(W, X, n_tok, M, K, nthreads=1):
     Y = np.zeros((n_tok, M), np.float32)
-    lib.orc_batch_gemm_q4_bf16(_q4(W, M, K), _c(X, np.float32, n_tok * K), Y, n_tok, M, K)
+    if nthreads > 1:
+        lib.orc_batch_gemm_q4_bf16_mt(_q4(W, M, K), _c(X, np.float32, n_tok * K), Y, n_tok, M, K, int(nthreads))
+    else:
+        lib.orc_batch_gemm_q4_bf16(_q4(W, M, K), _c(X, np.float32, n_tok * K), Y, n_tok, M, K)
     return Y
 
 
@@ -208,11 +244,14 @@ def decode_attn(Q, Kc, Vc, slots, num_q_heads, head_dim, kv_dim, gqa, scale=1.0)
 
 
 def batch_causal_attn(Q, Kc, Vc, slots, n_tok, num_prev, num_q_heads, head_dim, kv_dim, gqa,
-                      scale=1.0, window=0):
+                      scale=1.0, window=0, nthreads=1):
     out = np.zeros(n_tok * num_q_heads * head_dim, np.float32)
-    lib.orc_batch_causal_attn(_c(Q, np.float32), _c(Kc, np.float32), _c(Vc, np.float32),
-                              _c(slots, np.uint32), n_tok, num_prev, num_q_heads, head_dim, kv_dim,
-                              gqa, scale, window, out)
+    args = (_c(Q, np.float32), _c(Kc, np.float32), _c(Vc, np.float32), _c(slots, np.uint32), n_tok, num_prev,
+            num_q_heads, head_dim, kv_dim, gqa, scale, window, out)
+    if nthreads > 1:
+        lib.orc_batch_causal_attn_mt(*args, int(nthreads))
+    else:
+        lib.orc_batch_causal_attn(*args)
     return out
 
 
@@ -244,7 +283,10 @@ def add_rmsnorm(x, r, w, eps, scalar):
 
 
 def softcap(v):
-    return np.array([lib.orc_softcap(float(x)) for x in np.ravel(v)], dtype=np.float32)
+    a = _c(np.ravel(v), np.float32)
+    y = np.zeros(a.size, np.float32)
+    lib.orc_softcap_vec(a, y, a.size)
+    return y
 
 
 def topk64(logits):

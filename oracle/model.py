@@ -65,6 +65,35 @@ class Weights:
         self.final_norm = (np.ones(H, np.float32) if final_norm_bf16 is None
                            else bf16_to_f32(final_norm_bf16).astype(np.float32))
 
+    @classmethod
+    def synthetic(cls, cfg, seed, embed_bf16, nthreads=1):
+        """The weights chn_model_create_synthetic generates from `seed`:
+        layer i's matrices q, k, v, o, gate, up, down from orc_synth_q4 with
+        seeds seed + 64 (i + 1) + 0..6 (codes uniform, f16 scales
+        U(0.005, 0.02)), every norm 1.0 (post-attention and post-FFN norms
+        present), layer scalar 1.0; the tied embedding is given (bf16 bits)
+        and quantized to Q8 here."""
+        self = cls.__new__(cls)
+        self.cfg = cfg
+        H, I = cfg["hidden_size"], cfg["intermediate_size"]
+        self.layers = []
+        for i in range(cfg["num_layers"]):
+            D, nkv, rot = layer_shape(cfg, i)
+            qd, kvd = cfg["num_heads"] * D, nkv * D
+            ls = seed + 64 * (i + 1)
+            shapes = [("Wq", qd, H), ("Wk", kvd, H), ("Wv", kvd, H), ("Wo", H, qd),
+                      ("Wg", I, H), ("Wu", I, H), ("Wd", H, I)]
+            d = {name: O.synth_q4(r, k, ls + j).reshape(r, -1) for j, (name, r, k) in enumerate(shapes)}
+            ones_h = np.ones(H, np.float32)
+            d.update({"in_norm": ones_h, "q_norm": np.ones(D, np.float32), "k_norm": np.ones(D, np.float32),
+                      "pre_ffn": ones_h, "post_attn": ones_h, "post_ffn": ones_h, "scalar": np.float32(1.0),
+                      "D": D, "nkv": nkv, "rot": rot})
+            self.layers.append(d)
+        self.embed_bf16 = np.asarray(embed_bf16, np.uint16).reshape(cfg["vocab_size"], H)
+        self.embed_q8 = O.quantize_q8(self.embed_bf16, nthreads)
+        self.final_norm = np.ones(H, np.float32)
+        return self
+
     def embed(self, tokens):
         """x = bf16(embed[tok]) * sqrt(H) (src/model/forward.zig:35-37,
         src/gpu/batch_dispatch.zig:14-23)."""
@@ -79,9 +108,10 @@ def new_caches(cfg, nslot=4096):
             [np.zeros(nslot * k, np.float32) for k in kvds])
 
 
-def decode_step(W, kc, vc, x, clock, slot_idx, active, sliding, with_logits=True):
+def decode_step(W, kc, vc, x, clock, slot_idx, active, sliding, with_logits=True, nthreads=1):
     """One token through every layer; kc / vc (per-layer flat arrays) are
-    updated in place.  Returns (x, normed, logits, ids, vals)."""
+    updated in place.  Returns (x, normed, logits, ids, vals).  nthreads > 1
+    uses the threaded matvecs (bit-identical results)."""
     c = W.cfg
     H, I = c["hidden_size"], c["intermediate_size"]
     nq, eps = c["num_heads"], c["rms_norm_eps"]
@@ -92,24 +122,24 @@ def decode_step(W, kc, vc, x, clock, slot_idx, active, sliding, with_logits=True
         theta = c["rope_theta_full"] if full else c["rope_theta"]
         D, nkv = l["D"], l["nkv"]
         qd, kvd = nq * D, nkv * D
-        q, k, v = O.fused_qkv_q4(l["Wq"], l["Wk"], l["Wv"], normed, qd, kvd, H)
+        q, k, v = O.fused_qkv_q4(l["Wq"], l["Wk"], l["Wv"], normed, qd, kvd, H, nthreads)
         q = O.qkv_rope(q, k, v, l["q_norm"], l["k_norm"], kc[i], vc[i], nq, nkv, D, l["rot"],
                        c["k_eq_v"], theta, eps, clock, slot_idx)
         slots = np.asarray(active if full else sliding, np.uint32)
         attn = O.decode_attn(q, kc[i], vc[i], slots, nq, D, kvd, nq // nkv, 1.0)
-        o = O.gemv_q4(l["Wo"], attn, H, qd)
+        o = O.gemv_q4(l["Wo"], attn, H, qd, nthreads)
         if l["post_attn"] is not None:
             o = O.rmsnorm(o, l["post_attn"], eps)
         x, normed = O.add_rmsnorm(x, o, l["pre_ffn"], eps, 1.0)
-        act = O.fused_mlp_q4(l["Wg"], l["Wu"], normed, I, H)
-        d = O.gemv_q4(l["Wd"], act, H, I)
+        act = O.fused_mlp_q4(l["Wg"], l["Wu"], normed, I, H, nthreads)
+        d = O.gemv_q4(l["Wd"], act, H, I, nthreads)
         if l["post_ffn"] is not None:
             d = O.rmsnorm(d, l["post_ffn"], eps)
         nxt = W.layers[i + 1]["in_norm"] if i + 1 < len(W.layers) else W.final_norm
         x, normed = O.add_rmsnorm(x, d, nxt, eps, float(l["scalar"]))
     logits = ids = vals = None
     if with_logits:
-        logits = O.gemv_q8(W.embed_q8, normed, c["vocab_size"], H)
+        logits = O.gemv_q8(W.embed_q8, normed, c["vocab_size"], H, nthreads)
         ids, vals = O.topk64(logits)
     return x, normed, logits, ids, vals
 
@@ -118,14 +148,18 @@ def _rows(fn, X, *args):
     return np.stack([fn(X[t], *args) for t in range(X.shape[0])]).astype(np.float32)
 
 
-def prefill(W, kc, vc, tokens, slots, start_clock, num_prev, bf16_gemm=True, window=1024):
+def prefill(W, kc, vc, tokens, slots, start_clock, num_prev, bf16_gemm=True, window=1024, nthreads=1):
     """gpuDispatchPrefillBatch; GEMMs use the bf16-operand model of the MFMA
     path when bf16_gemm (else fp32).  Returns (X, Xn, logits, ids, vals)."""
     c = W.cfg
     H, I = c["hidden_size"], c["intermediate_size"]
     nq, eps = c["num_heads"], c["rms_norm_eps"]
     n = len(tokens)
-    gemm = O.batch_gemm_q4_bf16 if bf16_gemm else O.batch_gemm_q4
+    if bf16_gemm:
+        def gemm(Wm, X, nt, M, K):
+            return O.batch_gemm_q4_bf16(Wm, X, nt, M, K, nthreads)
+    else:
+        gemm = O.batch_gemm_q4
     slots = np.asarray(slots, np.uint32)
     X = W.embed(tokens)
     Xn = _rows(O.rmsnorm, X, W.layers[0]["in_norm"], eps)
@@ -143,7 +177,7 @@ def prefill(W, kc, vc, tokens, slots, start_clock, num_prev, bf16_gemm=True, win
                                l["rot"], c["k_eq_v"], theta, eps, start_clock + t,
                                int(slots[num_prev + t]))
         A = O.batch_causal_attn(Qr, kc[i], vc[i], slots, n, num_prev, nq, D, kvd, nq // nkv, 1.0,
-                                0 if full else window).reshape(n, qd)
+                                0 if full else window, nthreads).reshape(n, qd)
         Om = gemm(l["Wo"], A, n, H, qd)
         if l["post_attn"] is not None:
             Om = _rows(O.rmsnorm, Om, l["post_attn"], eps)
@@ -161,7 +195,7 @@ def prefill(W, kc, vc, tokens, slots, start_clock, num_prev, bf16_gemm=True, win
         nxt = W.layers[i + 1]["in_norm"] if i + 1 < len(W.layers) else W.final_norm
         Xs, Xn = zip(*[O.add_rmsnorm(X[t], Dn[t], nxt, eps, float(l["scalar"])) for t in range(n)])
         X, Xn = np.stack(Xs), np.stack(Xn)
-    logits = O.gemv_q8(W.embed_q8, Xn[n - 1], c["vocab_size"], H)
+    logits = O.gemv_q8(W.embed_q8, Xn[n - 1], c["vocab_size"], H, nthreads)
     ids, vals = O.topk64(logits)
     return X, Xn, logits, ids, vals
 

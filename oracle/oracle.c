@@ -799,3 +799,200 @@ void orc_gemv_q8_mt(const uint32_t *W, const float *x, float *y, uint32_t M,
     j.W = W; j.x = x; j.y = y; j.rows = M; j.nb = K / 32; j.mode = 2;
     run_pool(&j, nthreads);
 }
+
+/* ======================================================================
+ * Threaded forms for checking at full model sizes.  Each output element
+ * is computed by exactly the serial routine's code, in the same order, so
+ * every result is bit-identical to the serial one; threads only split the
+ * independent rows.
+ * ==================================================================== */
+
+typedef void (*rows_fn)(void *arg, size_t r0, size_t r1);
+typedef struct {
+    rows_fn fn;
+    void *arg;
+    size_t r0, r1;
+} rows_job_t;
+
+static void *rows_worker(void *p) {
+    rows_job_t *j = (rows_job_t *)p;
+    j->fn(j->arg, j->r0, j->r1);
+    return NULL;
+}
+
+/* fn over [0, n) in nthreads contiguous ranges, the caller taking the last. */
+static void par_rows(size_t n, int nthreads, rows_fn fn, void *arg) {
+    if (nthreads < 1) nthreads = 1;
+    if ((size_t)nthreads > n) nthreads = n ? (int)n : 1;
+    rows_job_t *jobs = (rows_job_t *)malloc(sizeof(rows_job_t) * (size_t)nthreads);
+    pthread_t *th = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)nthreads);
+    int *ok = (int *)calloc((size_t)nthreads, sizeof(int));
+    for (int t = 0; t < nthreads; ++t) {
+        jobs[t].fn = fn;
+        jobs[t].arg = arg;
+        jobs[t].r0 = n * (size_t)t / (size_t)nthreads;
+        jobs[t].r1 = n * (size_t)(t + 1) / (size_t)nthreads;
+    }
+    for (int t = 0; t + 1 < nthreads; ++t) ok[t] = pthread_create(&th[t], NULL, rows_worker, &jobs[t]) == 0;
+    for (int t = 0; t + 1 < nthreads; ++t)
+        if (!ok[t]) rows_worker(&jobs[t]);     /* no thread: run it here */
+    rows_worker(&jobs[nthreads - 1]);
+    for (int t = 0; t + 1 < nthreads; ++t)
+        if (ok[t]) pthread_join(th[t], NULL);
+    free(ok);
+    free(th);
+    free(jobs);
+}
+
+typedef struct {
+    uint32_t *dst;
+    const uint16_t *src;
+    size_t cols;
+    int q8;
+} quant_job_t;
+
+static void quant_rows(void *p, size_t r0, size_t r1) {
+    quant_job_t *j = (quant_job_t *)p;
+    size_t rw = ((j->cols + 31) / 32) * (j->q8 ? 9 : 5);
+    for (size_t r = r0; r < r1; ++r) {
+        if (j->q8) orc_quantize_row_q8(j->dst + r * rw, j->src + r * j->cols, j->cols);
+        else orc_quantize_row_q4(j->dst + r * rw, j->src + r * j->cols, j->cols);
+    }
+}
+
+void orc_quantize_matrix_q4_mt(uint32_t *dst, const uint16_t *src, size_t rows, size_t cols, int nthreads) {
+    quant_job_t j = {dst, src, cols, 0};
+    par_rows(rows, nthreads, quant_rows, &j);
+}
+
+void orc_quantize_matrix_q8_mt(uint32_t *dst, const uint16_t *src, size_t rows, size_t cols, int nthreads) {
+    quant_job_t j = {dst, src, cols, 1};
+    par_rows(rows, nthreads, quant_rows, &j);
+}
+
+typedef struct {
+    const uint32_t *W;
+    const float *X;
+    float *Wd, *Xb, *Y;
+    uint32_t n_tok, M, K;
+} bgemm_job_t;
+
+static void bgemm_dequant_rows(void *p, size_t r0, size_t r1) {
+    bgemm_job_t *j = (bgemm_job_t *)p;
+    size_t nb = j->K / 32;
+    orc_dequant_q4(j->Wd + r0 * j->K, j->W + r0 * nb * 5, r1 - r0, j->K);
+    for (size_t i = r0 * j->K; i < r1 * j->K; ++i) j->Wd[i] = orc_bf16_to_f32(orc_bf16_from_f32(j->Wd[i]));
+}
+
+/* Blocks of 8 rows x 4 tokens: the token tile is transposed to [k][4] and
+ * each row keeps a 4-lane vector of sums (one lane per token; lane-wise
+ * multiply, then add, each rounded as the scalar code rounds it), so the
+ * weights of a row block stay in cache across tokens and eight
+ * independent sums are in flight.  Every sum runs over k in ascending
+ * order, as in orc_batch_gemm_q4_bf16. */
+typedef float f32x4 __attribute__((vector_size(16)));
+
+static void bgemm_rows(void *p, size_t r0, size_t r1) {
+    bgemm_job_t *j = (bgemm_job_t *)p;
+    const uint32_t K = j->K;
+    f32x4 *xt = (f32x4 *)aligned_alloc(16, (size_t)K * sizeof(f32x4));
+    for (uint32_t t0 = 0; t0 < j->n_tok; t0 += 4) {
+        const uint32_t nt = j->n_tok - t0 < 4 ? j->n_tok - t0 : 4;
+        for (uint32_t k = 0; k < K; ++k)
+            for (uint32_t c = 0; c < 4; ++c) xt[k][c] = c < nt ? j->Xb[(size_t)(t0 + c) * K + k] : 0.0f;
+        for (size_t r = r0; r < r1; r += 8) {
+            const size_t nr = r1 - r < 8 ? r1 - r : 8;
+            const float *w[8];
+            for (size_t i = 0; i < 8; ++i) w[i] = j->Wd + (r + (i < nr ? i : 0)) * K;
+            f32x4 acc[8];
+            for (int i = 0; i < 8; ++i) acc[i] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+            for (uint32_t k = 0; k < K; ++k) {
+                const f32x4 x = xt[k];
+                for (int i = 0; i < 8; ++i) {
+                    const f32x4 prod = x * w[i][k];
+                    acc[i] = acc[i] + prod;
+                }
+            }
+            for (size_t i = 0; i < nr; ++i)
+                for (uint32_t c = 0; c < nt; ++c) j->Y[(size_t)(t0 + c) * j->M + r + i] = acc[i][c];
+        }
+    }
+    free(xt);
+}
+
+/* orc_batch_gemm_q4_bf16 over threads (output rows split). */
+void orc_batch_gemm_q4_bf16_mt(const uint32_t *W, const float *X, float *Y, uint32_t n_tok, uint32_t M,
+                               uint32_t K, int nthreads) {
+    bgemm_job_t j = {W, X, NULL, NULL, Y, n_tok, M, K};
+    j.Wd = (float *)malloc((size_t)M * K * sizeof(float));
+    j.Xb = (float *)malloc((size_t)n_tok * K * sizeof(float));
+    for (size_t i = 0; i < (size_t)n_tok * K; ++i) j.Xb[i] = orc_bf16_to_f32(orc_bf16_from_f32(X[i]));
+    par_rows(M, nthreads, bgemm_dequant_rows, &j);
+    par_rows(M, nthreads, bgemm_rows, &j);
+    free(j.Wd);
+    free(j.Xb);
+}
+
+typedef struct {
+    const uint32_t *Wg, *Wu;
+    const float *x;
+    float *act;
+    uint32_t nb;
+} mlp_job_t;
+
+static void mlp_rows(void *p, size_t r0, size_t r1) {
+    mlp_job_t *j = (mlp_job_t *)p;
+    for (size_t r = r0; r < r1; ++r) {
+        float g = gemv_q4_row(j->Wg + r * j->nb * 5, j->x, j->nb);
+        float u = gemv_q4_row(j->Wu + r * j->nb * 5, j->x, j->nb);
+        j->act[r] = orc_gelu_tanh(g) * u;
+    }
+}
+
+/* orc_fused_mlp_q4 over threads. */
+void orc_fused_mlp_q4_mt(const uint32_t *Wg, const uint32_t *Wu, const float *x, float *act, uint32_t M,
+                         uint32_t K, int nthreads) {
+    mlp_job_t j = {Wg, Wu, x, act, K / 32};
+    par_rows(M, nthreads, mlp_rows, &j);
+}
+
+/* Elementwise forms of the scalar routines over arrays. */
+void orc_gelu_tanh_vec(const float *x, float *y, size_t n) {
+    for (size_t i = 0; i < n; ++i) y[i] = orc_gelu_tanh(x[i]);
+}
+
+void orc_softcap_vec(const float *x, float *y, size_t n) {
+    for (size_t i = 0; i < n; ++i) y[i] = orc_softcap(x[i]);
+}
+
+typedef struct {
+    const float *Q, *Kc, *Vc;
+    const uint32_t *slots;
+    uint32_t num_prev_slots, num_q_heads, head_dim, kv_dim, gqa_ratio, window;
+    float scale;
+    float *out;
+} cattn_job_t;
+
+static void cattn_rows(void *p, size_t t0, size_t t1) {
+    cattn_job_t *j = (cattn_job_t *)p;
+    const uint32_t q_dim = j->num_q_heads * j->head_dim;
+    float *scores = (float *)malloc((size_t)(j->num_prev_slots + t1) * sizeof(float));
+    for (size_t t = t0; t < t1; ++t) {
+        uint32_t S = j->num_prev_slots + (uint32_t)t + 1;
+        uint32_t start = (j->window > 0 && S > j->window) ? S - j->window : 0;
+        for (uint32_t h = 0; h < j->num_q_heads; ++h)
+            attn_one_head(j->Q + t * q_dim + (size_t)h * j->head_dim, j->Kc, j->Vc, j->slots, start, S, j->head_dim,
+                          j->kv_dim, h / j->gqa_ratio, j->scale, j->out + t * q_dim + (size_t)h * j->head_dim,
+                          scores);
+    }
+    free(scores);
+}
+
+/* orc_batch_causal_attn over threads (tokens split). */
+void orc_batch_causal_attn_mt(const float *Q, const float *Kc, const float *Vc, const uint32_t *slots,
+                              uint32_t n_tok, uint32_t num_prev_slots, uint32_t num_q_heads, uint32_t head_dim,
+                              uint32_t kv_dim, uint32_t gqa_ratio, float scale, uint32_t window, float *out,
+                              int nthreads) {
+    cattn_job_t j = {Q, Kc, Vc, slots, num_prev_slots, num_q_heads, head_dim, kv_dim, gqa_ratio, window, scale, out};
+    par_rows(n_tok, nthreads, cattn_rows, &j);
+}

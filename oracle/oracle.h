@@ -108,6 +108,21 @@ void orc_fused_mlp_step_mt(const uint32_t *Wg, const uint32_t *Wu,
 void orc_gemv_q8_mt(const uint32_t *W, const float *x, float *y, uint32_t M,
                     uint32_t K, int nthreads);
 
+/* ---- threaded forms for checking at full sizes (bit-identical to the
+ *      serial routines: rows split over threads, each row's order kept) --- */
+void orc_quantize_matrix_q4_mt(uint32_t *dst, const uint16_t *src, size_t rows, size_t cols, int nthreads);
+void orc_quantize_matrix_q8_mt(uint32_t *dst, const uint16_t *src, size_t rows, size_t cols, int nthreads);
+void orc_batch_gemm_q4_bf16_mt(const uint32_t *W, const float *X, float *Y, uint32_t n_tok, uint32_t M,
+                               uint32_t K, int nthreads);
+void orc_fused_mlp_q4_mt(const uint32_t *Wg, const uint32_t *Wu, const float *x, float *act, uint32_t M,
+                         uint32_t K, int nthreads);
+void orc_batch_causal_attn_mt(const float *Q, const float *Kc, const float *Vc, const uint32_t *slots,
+                              uint32_t n_tok, uint32_t num_prev_slots, uint32_t num_q_heads, uint32_t head_dim,
+                              uint32_t kv_dim, uint32_t gqa_ratio, float scale, uint32_t window, float *out,
+                              int nthreads);
+void orc_gelu_tanh_vec(const float *x, float *y, size_t n);
+void orc_softcap_vec(const float *x, float *y, size_t n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -39,16 +39,38 @@ def f32_host(ctx, buf, n, byte_offset=0):
     return ctx.download(buf, np.float32, n, byte_offset)
 
 
-def assert_topk_valid(ids, vals, logits_want, tol):
-    """ids/vals are a valid top-64 of softcap(logits_want) under tolerance:
-    values match the exact top-64 within tol * max|value|, ids are distinct,
-    and each id's exact capped value is within 2 * that of the value at its
-    position (so only near-ties may be ordered differently)."""
+def assert_topk_valid(ids, vals, logits_want, tol, label=""):
+    """ids/vals must be the top-64 of softcap(logits_want) up to the error
+    bound atol = tol * max|value|:
+
+    * ids are distinct and every value is within atol of the exact value at
+      its rank;
+    * where the id at a rank differs from the oracle's, the GPU's id must be
+      a near-tie: its exact capped value lies within 2 * atol of the exact
+      value at that rank (each such rank is reported with its margin);
+    * the argmax (rank 0, the greedy token) must equal the oracle's unless
+      the oracle's own top-2 margin is below 2 * atol (reported).
+
+    Returns (number of ranks whose id matches, list of reported ranks)."""
     import oracle
-    capped = oracle.softcap(logits_want)
+    ids = np.asarray(ids, np.int64)
+    capped = oracle.softcap(logits_want).astype(np.float64)
     want_ids, want_vals = oracle.topk64(logits_want)
+    want_vals = want_vals.astype(np.float64)
     atol = tol * float(np.max(np.abs(want_vals)))
-    assert len(set(int(i) for i in ids)) == 64
-    assert np.all(np.abs(np.asarray(vals, np.float64) - want_vals) <= atol)
-    assert np.all(np.abs(capped[np.asarray(ids, np.int64)].astype(np.float64) - want_vals) <= 2 * atol)
-    return int(np.sum(np.asarray(ids) == want_ids))
+    assert len(set(int(i) for i in ids)) == 64, f"{label}: repeated ids"
+    dv = np.abs(np.asarray(vals, np.float64) - want_vals)
+    assert np.all(dv <= atol), f"{label}: value error {dv.max():.3g} > {atol:.3g}"
+    flagged = []
+    for k in np.nonzero(ids != want_ids.astype(np.int64))[0]:
+        margin = abs(capped[ids[k]] - want_vals[k])
+        flagged.append((int(k), int(ids[k]), int(want_ids[k]), margin))
+        say(f"  {label} near-tie at rank {k}: id {ids[k]} for {want_ids[k]}, "
+            f"exact values differ by {margin:.3g} (bound {2 * atol:.3g})")
+        assert margin <= 2 * atol, f"{label}: rank {k} reordered by {margin:.3g} > {2 * atol:.3g}"
+    if ids[0] != want_ids[0]:
+        top2 = want_vals[0] - want_vals[1]
+        assert top2 <= 2 * atol, f"{label}: argmax {ids[0]} != {want_ids[0]} with oracle top-2 margin {top2:.3g}"
+    n_match = 64 - len(flagged)
+    say(f"  {label} top-64: {n_match}/64 ranks identical")
+    return n_match, flagged

@@ -269,3 +269,37 @@ def test_q4r_plane_entries_reject(ctx):
         ctx.call("chn_fused_mlp_q4r_xp", W, W, P, a, a, 50, 256)        # M % 32 != 0 with act planes
     with pytest.raises(ca.ChannelError):
         ctx.call("chn_xplanes", a, 48, P)                                # K % 32 != 0
+
+
+@pytest.mark.parametrize("post", [True, False])
+def test_ffn_gate_up_fused_norm_12b(ctx, post):
+    """chn_ffn_gate_up_q4r, the decode step's pre-FFN launch, at 12B dims
+    (hidden 3840, FFN 15360): post-attention norm, residual add and pre-FFN
+    norm as the prologue of gate/up (src/gpu/model_dispatch.zig:33-40)."""
+    H, I, eps = 3840, 15360, 1e-6
+    rng = np.random.default_rng(8 + post)
+    Wg, Wu = synth_q4_dev(ctx, I, H, 1300), synth_q4_dev(ctx, I, H, 1301)
+    Rg, Ru = repack_dev(ctx, Wg, I, H), repack_dev(ctx, Wu, I, H)
+    xh = (rng.standard_normal(H) * 3).astype(np.float32)
+    rh = rng.standard_normal(H).astype(np.float32)
+    pw = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    fw = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    x, r = ctx.upload(xh), ctx.upload(rh)
+    pwd, fwd = ctx.upload(pw), ctx.upload(fw)
+    xo, nx, act = ctx.alloc(H * 4), ctx.alloc(H * 4), ctx.alloc(I * 4)
+    AP = ctx.alloc(ca.xplanes_bytes(I))
+    say(f"ffn_gate_up fused norm 15360x3840 post={post}")
+    ctx.call("chn_ffn_gate_up_q4r", Rg, Ru, x, r, pwd if post else None, fwd, xo, nx, act, AP, I, H, eps)
+    rr = oracle.rmsnorm(rh, pw, eps) if post else rh
+    x_o, n_o = oracle.add_rmsnorm(xh, rr, fw, eps, 1.0)
+    assert rel_err(f32_host(ctx, xo, H), x_o) < 1e-5
+    assert rel_err(f32_host(ctx, nx, H), n_o) < 1e-5
+    got = f32_host(ctx, act, I)
+    want = oracle.fused_mlp_q4(q4_host(ctx, Wg, I, H), q4_host(ctx, Wu, I, H), n_o, I, H, oracle.NTHREADS)
+    assert rel_err(got, want) < 1e-3
+    AQ = ctx.alloc(ca.xplanes_bytes(I))
+    ctx.call("chn_xplanes", act, I, AQ)
+    n = ca.xplanes_bytes(I) // 4
+    assert np.array_equal(ctx.download(AP, np.uint32, n), ctx.download(AQ, np.uint32, n))
+    with pytest.raises(ca.ChannelError):
+        ctx.call("chn_ffn_gate_up_q4r", Rg, Ru, x, r, None, fwd, x, nx, act, AP, I, H, eps)   # x_out aliases x_in

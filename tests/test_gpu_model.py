@@ -16,6 +16,7 @@ import channel_amd as ca
 from channel_amd.model import Model
 from gpu_util import assert_topk_valid, rel_err, say
 from oracle import model as OM
+from oracle import ring as OR
 
 pytestmark = pytest.mark.gpu
 
@@ -209,38 +210,69 @@ def test_eager_launches_match_graph(ctx):
             assert np.array_equal(xg, xe) and np.array_equal(ng, ne)
 
 
-def ring_lists(clock, window, nslot=4096):
-    """Slot lists of an anchor-free ring: slot = clock mod nslot."""
-    n = min(clock + 1, nslot)
-    active = ((np.arange(n, dtype=np.int64) + clock + 1 - n) % nslot).astype(np.uint32)
-    return active, active[max(0, n - window):]
+def ring_lists(clock, window):
+    """Slot lists of the reference's ring without anchors (slot = clock mod
+    3968), from the ring restatement oracle/ring.py."""
+    from oracle.ring import Ring
+    ring = Ring(1, 0)
+    for c in range(max(0, clock - 3968), clock):
+        ring.activate_slot(0, c)
+    _, active, sliding = OR.decode_lists(ring, clock, window)
+    return np.asarray(active, np.uint32), np.asarray(sliding, np.uint32)
 
 
-@pytest.mark.parametrize("clock0", [0, 4093])
-def test_decode_greedy_matches_token_loop(ctx, clock0):
-    """chn_decode_greedy (device-resident steps, ring slot lists generated on
-    the device) equals the same steps driven from the host, bit for bit; the
-    second case wraps the ring (slots 4093, 4094, 4095, 0, 1)."""
+GREEDY_CASES = [
+    # (clock0, anchors, boundaries, recall {rank: clock})
+    (0, 0, (), None),
+    (3965, 0, (), None),                                    # the window wraps at 3968
+    (3966, 512, (100, 600, 3971), {0: 50, 5: 3968, 9: 9000}),  # snap past the anchors, recall joins
+]
+
+
+@pytest.mark.parametrize("clock0,anchors,bounds,recall", GREEDY_CASES)
+def test_decode_greedy_matches_token_loop(ctx, clock0, anchors, bounds, recall):
+    """chn_decode_greedy (device-resident steps, slot lists generated on the
+    device) equals the same steps driven from the host with the lists of
+    the ring restatement (oracle/ring.py: getSlotIndexLayer /
+    getActiveSlotsLayer after activateSlot, src/model/forward.zig:41-47),
+    bit for bit: tokens, state and the K/V rows written."""
+    from oracle.ring import Ring
     cfg = dict(CFG, num_layers=2, layer_full=[0, 1])
-    say(f"decode_greedy clock0={clock0}")
+    n = 6
+    say(f"decode_greedy clock0={clock0} anchors={anchors}")
+    rc = None
+    ring = Ring(1, anchors)
+    for b in bounds:
+        ring.mark_boundary(b)
+    if recall is not None:
+        rc = np.full(128, 0xFFFFFFFF, np.uint32)
+        for rank, clk in recall.items():
+            rc[rank] = clk
+            ring.write_recall_kv(0, rank, clk)
+    for c in range(clock0):
+        ring.activate_slot(0, c)
     with Model.synthetic(ctx, cfg, 99) as mg, Model.synthetic(ctx, cfg, 99) as mh:
-        toks = mg.decode_greedy(17, clock0, 5)
+        toks = mg.decode_greedy(17, clock0, n, num_anchors=anchors, boundaries=bounds, recall_clocks=rc)
         tok = 17
-        want = []
-        for i in range(5):
+        want, slots = [], []
+        for i in range(n):
             clock = clock0 + i
-            active, sliding = ring_lists(clock, WINDOW)
-            tok, _, _ = mh.forward_token_id(tok, clock, clock % 4096, active, sliding)
+            slot, active, sliding = OR.decode_lists(ring, clock, WINDOW)
+            assert len(active) <= 4096 and max(active) < 4096
+            tok, _, _ = mh.forward_token_id(tok, clock, slot, active, sliding)
             want.append(tok)
+            slots.append(slot)
         assert list(toks) == want
         xg, ng = mg.read_state()
         xh, nh = mh.read_state()
         assert np.array_equal(xg, xh) and np.array_equal(ng, nh)
         for layer in range(2):
-            for clock in range(clock0, clock0 + 5):
-                kg, vg = mg.kv_read(layer, clock % 4096, 1)
-                kh, vh = mh.kv_read(layer, clock % 4096, 1)
+            for slot in slots:
+                kg, vg = mg.kv_read(layer, slot, 1)
+                kh, vh = mh.kv_read(layer, slot, 1)
                 assert np.array_equal(kg, kh) and np.array_equal(vg, vh)
+    if clock0 == 3965:
+        assert slots[3] == 0            # clock 3968 takes slot 0, not 3968
 
 
 def test_created_model_token_path_matches_step(pair):

@@ -468,3 +468,36 @@ def test_synth_distributions():
     assert counts.min() > 0.9 * codes.size / 16 and counts.max() < 1.1 * codes.size / 16
     z = oracle.synth_normal(200000, 9)
     assert abs(z.mean()) < 0.01 and abs(z.std() - 1) < 0.01
+
+
+def test_threaded_forms_equal_serial():
+    """The threaded checking forms split rows over threads and keep every
+    row's arithmetic: results are bit-identical to the serial routines."""
+    rng = np.random.default_rng(77)
+    M, K, T = 96, 256, 5
+    Wb = (rng.integers(0, 1 << 16, (M, K)) & 0xBFFF).astype(np.uint16)   # finite bf16
+    assert np.array_equal(oracle.quantize_q4(Wb, 4), oracle.quantize_q4(Wb))
+    assert np.array_equal(oracle.quantize_q8(Wb, 3), oracle.quantize_q8(Wb))
+    W = oracle.synth_q4(M, K, 5)
+    Wu = oracle.synth_q4(M, K, 6)
+    x = rng.standard_normal(K).astype(np.float32)
+    X = rng.standard_normal((T, K)).astype(np.float32)
+    assert np.array_equal(oracle.gemv_q4(W, x, M, K, 4), oracle.gemv_q4(W, x, M, K))
+    assert np.array_equal(oracle.fused_mlp_q4(W, Wu, x, M, K, 5), oracle.fused_mlp_q4(W, Wu, x, M, K))
+    assert np.array_equal(oracle.batch_gemm_q4_bf16(W, X, T, M, K, 7), oracle.batch_gemm_q4_bf16(W, X, T, M, K))
+    q, k, v = oracle.fused_qkv_q4(W, W, Wu, x, M, M, K, 3)
+    q1, k1, v1 = oracle.fused_qkv_q4(W, W, Wu, x, M, M, K)
+    assert np.array_equal(q, q1) and np.array_equal(k, k1) and np.array_equal(v, v1)
+    E = oracle.quantize_q8(Wb)
+    assert np.array_equal(oracle.gemv_q8(E, x, M, K, 4), oracle.gemv_q8(E, x, M, K))
+    Kc = rng.standard_normal(64 * 512).astype(np.float32)
+    Vc = rng.standard_normal(64 * 512).astype(np.float32)
+    Q = rng.standard_normal(9 * 4 * 256).astype(np.float32)
+    sl = rng.permutation(64).astype(np.uint32)
+    for win in (0, 5):
+        assert np.array_equal(oracle.batch_causal_attn(Q, Kc, Vc, sl, 9, 20, 4, 256, 512, 2, 1.0, win, 4),
+                              oracle.batch_causal_attn(Q, Kc, Vc, sl, 9, 20, 4, 256, 512, 2, 1.0, win))
+    # the array forms of the scalar routines
+    xs = rng.standard_normal(300).astype(np.float32) * 20
+    assert np.array_equal(oracle.gelu_tanh(xs), np.array([oracle.lib.orc_gelu_tanh(float(v)) for v in xs], np.float32))
+    assert np.array_equal(oracle.softcap(xs), np.array([oracle.lib.orc_softcap(float(v)) for v in xs], np.float32))
