@@ -62,6 +62,7 @@ PROTOTYPES = {
     "chn_batch_fused_mlp_q4r": (c_int, [c_void_p] * 6 + [c_u32] * 3),
     "chn_qkv_rope": (c_int, [c_void_p] + [c_void_p] * 9 + [c_u32] * 4 + [c_int, c_f32, c_f32]),
     "chn_decode_attn": (c_int, [c_void_p] + [c_void_p] * 5 + [c_u32] * 5 + [c_f32, c_void_p]),
+    "chn_decode_attn_noalloc": (c_int, [c_void_p] + [c_void_p] * 5 + [c_u32] * 5 + [c_f32, c_void_p]),
     "chn_rmsnorm": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_u32, c_f32]),
     "chn_add_rmsnorm": (c_int, [c_void_p] * 5 + [c_u32, c_f32, c_f32]),
     "chn_batch_rmsnorm": (c_int, [c_void_p] * 4 + [c_u32, c_u32, c_f32]),

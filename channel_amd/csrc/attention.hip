@@ -18,6 +18,8 @@
 // (sum exp(s_j - max) + 1e-9) up to rounding.
 #include "chn_internal.h"
 
+#include <mutex>
+
 namespace chn {
 
 constexpr int kAttnChunk = 64;     // prefill: slots per online-softmax step
@@ -1153,9 +1155,48 @@ int launch_rope_tab_batch(hipStream_t st, float2 *tab, uint32_t start_clock, uin
     return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
 }
 
+// ---- decode attention without allocation (chn_decode_attn_noalloc)
+// The split partials live in a file-scope device array instead of the
+// context workspace.  Each device holds its own copy until the process ends;
+// host code never passes the array's name to a kernel, only the address
+// hipGetSymbolAddress returns for the current device, taken once per device
+// when a context is created on it (noalloc_scratch_init, from chn_init).
+constexpr size_t kNoAllocBytes = (size_t)2 << 20;    // 2 MiB: num_q_heads * (head_dim + 2) <= 16384 at 32 splits
+static __device__ __align__(256) float scratch[kNoAllocBytes / 4];
+constexpr int kMaxDevices = 64;
+static void *g_scratch[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+int noalloc_scratch_init(chn_ctx *ctx) {
+    if (ctx->device < 0 || ctx->device >= kMaxDevices) return CHN_OK;   // the entry point then refuses
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch[ctx->device]) return CHN_OK;
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipGetSymbolAddress(scratch)");
+    if (!p) return set_err(ctx, CHN_E_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch[ctx->device] = p;
+    return CHN_OK;
+}
+
 }  // namespace chn
 
 using namespace chn;
+
+static int check_decode_attn(chn_ctx *ctx, const float *q, const float *k_cache, const float *v_cache,
+                             const uint32_t *slots, const uint32_t *n_slots, uint32_t max_slots,
+                             uint32_t num_q_heads, uint32_t head_dim, uint32_t kv_dim, uint32_t gqa_ratio,
+                             const float *out) {
+    CHN_REQUIRE(ctx, q && k_cache && v_cache && slots && n_slots && out, "NULL argument");
+    CHN_REQUIRE(ctx, gqa_ratio > 0 && num_q_heads % gqa_ratio == 0, "num_q_heads %u not a multiple of gqa %u",
+                num_q_heads, gqa_ratio);
+    CHN_REQUIRE(ctx, kv_dim >= (num_q_heads / gqa_ratio) * head_dim && kv_dim % 4 == 0,
+                "kv_dim %u too small for %u kv heads of %u", kv_dim, num_q_heads / gqa_ratio, head_dim);
+    CHN_REQUIRE(ctx, aligned(q, 16) && aligned(k_cache, 16) && aligned(v_cache, 16) && aligned(out, 16),
+                "q, caches and out must be 16-byte aligned");
+    CHN_REQUIRE(ctx, max_slots > 0 && max_slots <= 4096, "max_slots %u must be in 1..4096", max_slots);
+    return CHN_OK;
+}
 
 extern "C" int chn_qkv_rope(chn_ctx *ctx, const float *q_in, const float *k_in, const float *v_in,
                             const float *q_norm_w, const float *k_norm_w, float *q_out, float *k_cache,
@@ -1181,19 +1222,39 @@ extern "C" int chn_decode_attn(chn_ctx *ctx, const float *q, const float *k_cach
                                uint32_t num_q_heads, uint32_t head_dim, uint32_t kv_dim, uint32_t gqa_ratio,
                                float scale, float *out) {
     if (!ctx) return CHN_E_INVALID;
-    CHN_REQUIRE(ctx, q && k_cache && v_cache && slots && n_slots && out, "NULL argument");
-    CHN_REQUIRE(ctx, gqa_ratio > 0 && num_q_heads % gqa_ratio == 0, "num_q_heads %u not a multiple of gqa %u",
-                num_q_heads, gqa_ratio);
-    CHN_REQUIRE(ctx, kv_dim >= (num_q_heads / gqa_ratio) * head_dim && kv_dim % 4 == 0,
-                "kv_dim %u too small for %u kv heads of %u", kv_dim, num_q_heads / gqa_ratio, head_dim);
-    CHN_REQUIRE(ctx, aligned(q, 16) && aligned(k_cache, 16) && aligned(v_cache, 16) && aligned(out, 16),
-                "q, caches and out must be 16-byte aligned");
-    CHN_REQUIRE(ctx, max_slots > 0 && max_slots <= 4096, "max_slots %u must be in 1..4096", max_slots);
+    int rc = check_decode_attn(ctx, q, k_cache, v_cache, slots, n_slots, max_slots, num_q_heads, head_dim, kv_dim,
+                               gqa_ratio, out);
+    if (rc) return rc;
     if (!num_q_heads) return CHN_OK;
-    int rc = ensure_workspace(ctx, attn_ws_bytes(num_q_heads, head_dim, max_slots));
+    rc = ensure_workspace(ctx, attn_ws_bytes(num_q_heads, head_dim, max_slots));
     if (rc) return rc;
     return launch_decode_attn(ctx, q, k_cache, v_cache, slots, n_slots, max_slots, num_q_heads, head_dim,
                               kv_dim, gqa_ratio, scale, out, (float *)ctx->ws, nullptr);
+}
+
+// chn_decode_attn with the partials in the device's file-scope scratch: no
+// allocation, so it may run where hipMalloc may not (graph capture, serving
+// loops).  Every call on one device shares the array; calls that overlap on
+// one device race.  Every split writes its whole partial before the merge
+// reads it (splits without list entries write an empty one), so nothing
+// needs clearing between calls.
+extern "C" int chn_decode_attn_noalloc(chn_ctx *ctx, const float *q, const float *k_cache, const float *v_cache,
+                                       const uint32_t *slots, const uint32_t *n_slots, uint32_t max_slots,
+                                       uint32_t num_q_heads, uint32_t head_dim, uint32_t kv_dim, uint32_t gqa_ratio,
+                                       float scale, float *out) {
+    if (!ctx) return CHN_E_INVALID;
+    int rc = check_decode_attn(ctx, q, k_cache, v_cache, slots, n_slots, max_slots, num_q_heads, head_dim, kv_dim,
+                               gqa_ratio, out);
+    if (rc) return rc;
+    if (!num_q_heads) return CHN_OK;
+    const size_t need = attn_ws_bytes(num_q_heads, head_dim, max_slots);
+    if (need > kNoAllocBytes)
+        return set_err(ctx, CHN_E_UNSUPPORTED, "decode attention partials need %zu bytes; the allocation-free "
+                       "scratch holds %zu", need, kNoAllocBytes);
+    void *ws = ctx->device >= 0 && ctx->device < kMaxDevices ? g_scratch[ctx->device] : nullptr;
+    if (!ws) return set_err(ctx, CHN_E_UNSUPPORTED, "no scratch address for device %d", ctx->device);
+    return launch_decode_attn(ctx, q, k_cache, v_cache, slots, n_slots, max_slots, num_q_heads, head_dim,
+                              kv_dim, gqa_ratio, scale, out, (float *)ws, nullptr);
 }
 
 extern "C" int chn_batch_qkv_rope(chn_ctx *ctx, const float *q_in, const float *k_in, const float *v_in,

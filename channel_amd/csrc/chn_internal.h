@@ -27,6 +27,9 @@ int set_err(chn_ctx *ctx, int code, const char *fmt, ...);
 int hip_fail(chn_ctx *ctx, hipError_t e, const char *what);
 // Make sure ctx->ws holds at least `bytes`; returns a status code.
 int ensure_workspace(chn_ctx *ctx, size_t bytes);
+// Resolve, once per device (the context's device current), the address of
+// the file-scope scratch chn_decode_attn_noalloc uses.
+int noalloc_scratch_init(chn_ctx *ctx);
 
 #define CHN_HIP(ctx, call)                                   \
     do {                                                     \

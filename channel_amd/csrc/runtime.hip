@@ -85,6 +85,11 @@ extern "C" int chn_init(int device, chn_ctx **out) {
         delete ctx;
         return rc;
     }
+    if (noalloc_scratch_init(ctx) != CHN_OK) {
+        const int rc = set_err(nullptr, CHN_E_HIP, "%s", ctx->err.c_str());
+        chn_destroy(ctx);
+        return rc;
+    }
     *out = ctx;
     return CHN_OK;
 }

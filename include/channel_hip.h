@@ -236,6 +236,23 @@ int chn_decode_attn(chn_ctx *ctx, const float *q, const float *k_cache, const fl
                     uint32_t num_q_heads, uint32_t head_dim, uint32_t kv_dim,
                     uint32_t gqa_ratio, float scale, float *out);
 
+/* chn_decode_attn without any allocation.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops).  The split partials live in a 2 MiB
+ * file-scope device array per GPU (held until the process ends) instead of
+ * the context workspace, which chn_decode_attn may grow with hipMalloc.
+ * The partials take min(ceil(max_slots / 16), 32) * num_q_heads *
+ * (head_dim + 2) * 4 bytes; shapes above 2 MiB (at max_slots > 496:
+ * num_q_heads * (head_dim + 2) > 16384, e.g. 32 query heads at head_dim
+ * 512) return CHN_E_UNSUPPORTED.  All
+ * calls on one GPU share the array: calls that overlap on one GPU (two
+ * contexts or threads on the same device) race.  Results are bit-identical
+ * to chn_decode_attn. */
+int chn_decode_attn_noalloc(chn_ctx *ctx, const float *q, const float *k_cache, const float *v_cache,
+                            const uint32_t *slots, const uint32_t *n_slots, uint32_t max_slots,
+                            uint32_t num_q_heads, uint32_t head_dim, uint32_t kv_dim,
+                            uint32_t gqa_ratio, float scale, float *out);
+
 /* y = x * rsqrt(mean(x^2) + eps) * w over dim (dim % 4 == 0).
  * recordRmsNorm (src/gpu/kernels.zig:139-142) + shaders/rmsnorm.wgsl. */
 int chn_rmsnorm(chn_ctx *ctx, const float *x, const float *w, float *y, uint32_t dim, float eps);
