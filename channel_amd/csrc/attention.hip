@@ -227,7 +227,9 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
                                                      const uint32_t *__restrict__ slots,
                                                      const uint32_t *__restrict__ n_slots, uint32_t max_slots,
                                                      uint32_t num_q_heads, uint32_t kv_dim, float scale,
-                                                     float *__restrict__ ws, RopeArgs ra) {
+                                                     float *__restrict__ ws, RopeArgs ra,
+                                                     const uint32_t *__restrict__ skip) {
+    if (skip && *skip) return;          // a quiescent layer: no K/V write, no attention (uniform)
     constexpr int D = DV * 256;
     constexpr int NF = 4 * DV;          // float4 per lane per row
     const uint32_t split = blockIdx.x, kvh = blockIdx.y, G = gridDim.x;
@@ -490,7 +492,9 @@ __device__ __forceinline__ SoftState xor_state(const SoftState &x) {
 template <int DV, int U>
 __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ ws, uint32_t nsplit,
                                                     uint32_t num_q_heads, float *__restrict__ out,
-                                                    uint32_t *__restrict__ xp, uint32_t xp_nb) {
+                                                    uint32_t *__restrict__ xp, uint32_t xp_nb,
+                                                    const uint32_t *__restrict__ skip) {
+    if (skip && *skip) return;          // a quiescent layer (uniform)
     constexpr int D = DV * 256;
     __shared__ f4 st_t[4][16];
     __shared__ float st_m[4][16], st_l[4][16];
@@ -887,7 +891,7 @@ __global__ __launch_bounds__(256) void k_prefill_attn_merge(const float *__restr
 static int launch_decode_impl(chn_ctx *ctx, const float *q, float *kc, float *vc, const uint32_t *slots,
                               const uint32_t *n_slots, uint32_t max_slots, uint32_t num_q_heads, uint32_t head_dim,
                               uint32_t kv_dim, uint32_t gqa, float scale, float *out, float *ws, uint32_t *xp,
-                              const RopeArgs *ra) {
+                              const RopeArgs *ra, const uint32_t *skip = nullptr) {
     const uint32_t num_kv = num_q_heads / gqa;
     const uint32_t xp_nb = num_q_heads * head_dim / 32;
     const uint32_t nsplit = dec_splits(max_slots);
@@ -898,10 +902,10 @@ static int launch_decode_impl(chn_ctx *ctx, const float *q, float *kc, float *vc
     do {                                                                                                          \
         if (ra)                                                                                                   \
             k_attn_decode<DV, G, true><<<grid, 256, 0, s>>>(q, kc, vc, slots, n_slots, max_slots,        \
-                                                                     num_q_heads, kv_dim, scale, ws, rz);         \
+                                                                     num_q_heads, kv_dim, scale, ws, rz, skip);   \
         else                                                                                                      \
             k_attn_decode<DV, G, false><<<grid, 256, 0, s>>>(q, kc, vc, slots, n_slots, max_slots,       \
-                                                                      num_q_heads, kv_dim, scale, ws, rz);        \
+                                                                      num_q_heads, kv_dim, scale, ws, rz, skip);  \
     } while (0)
     if (head_dim == 256) {
         switch (gqa) {
@@ -925,9 +929,9 @@ static int launch_decode_impl(chn_ctx *ctx, const float *q, float *kc, float *vc
     CHN_LAUNCHED(ctx, "k_attn_decode");
     const dim3 mgrid(head_dim / 64, num_q_heads);
     if (head_dim == 256)
-        k_attn_merge<1, kDecGrid / 16><<<mgrid, 256, 0, s>>>(ws, nsplit, num_q_heads, out, xp, xp_nb);
+        k_attn_merge<1, kDecGrid / 16><<<mgrid, 256, 0, s>>>(ws, nsplit, num_q_heads, out, xp, xp_nb, skip);
     else
-        k_attn_merge<2, kDecGrid / 16><<<mgrid, 256, 0, s>>>(ws, nsplit, num_q_heads, out, xp, xp_nb);
+        k_attn_merge<2, kDecGrid / 16><<<mgrid, 256, 0, s>>>(ws, nsplit, num_q_heads, out, xp, xp_nb, skip);
     CHN_LAUNCHED(ctx, "k_attn_merge");
     return CHN_OK;
 }
@@ -943,11 +947,11 @@ int launch_rope_decode_attn(chn_ctx *ctx, const float *q_in, const float *k_in, 
                             const float *kw, float *kc, float *vc, const uint32_t *step, const uint32_t *slots,
                             const uint32_t *n_slots, uint32_t max_slots, uint32_t num_q_heads, uint32_t head_dim,
                             uint32_t kv_dim, uint32_t gqa, uint32_t rot, int k_eq_v, const float2 *rope_tab,
-                            float eps, float scale, float *out, float *ws, uint32_t *xp) {
+                            float eps, float scale, float *out, float *ws, uint32_t *xp, const uint32_t *skip) {
     if (rot > 2 * kRopePairs || rot > head_dim) return set_err(ctx, CHN_E_UNSUPPORTED, "rotary_dim %u", rot);
     const RopeArgs ra{k_in, v_in, qw, kw, step, rope_tab, rot, eps, k_eq_v};
     return launch_decode_impl(ctx, q_in, kc, vc, slots, n_slots, max_slots, num_q_heads, head_dim, kv_dim, gqa, scale,
-                              out, ws, xp, &ra);
+                              out, ws, xp, &ra, skip);
 }
 
 int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const float *vc, const uint32_t *slots,

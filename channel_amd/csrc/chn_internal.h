@@ -100,8 +100,9 @@ inline size_t q4r_bytes(uint32_t rows, uint32_t K) { return (size_t)rows * (K / 
 int launch_q4_repack(hipStream_t s, const uint32_t *W, uint32_t rows, uint32_t K, void *dst);
 // Matvecs over Q4R weights with activation planes already in xp (or, if
 // !planes_ready, computed from x into xp first).  K % 32 == 0, K <= 16384.
+// skip (or NULL): the layer's quiescence flag; when set the launch does nothing.
 int mvr_gemv(chn_ctx *ctx, const void *W, const float *x, float *y, uint32_t M, uint32_t K, uint32_t *xp,
-             bool planes_ready);
+             bool planes_ready, const uint32_t *skip = nullptr);
 int mvr_qkv(chn_ctx *ctx, const void *Wq, const void *Wk, const void *Wv, const float *x, float *q, float *k,
             float *v, uint32_t q_dim, uint32_t kv_dim, uint32_t K, uint32_t *xp, bool planes_ready);
 int mvr_mlp(chn_ctx *ctx, const void *Wg, const void *Wu, const float *x, float *act, uint32_t M, uint32_t K,
@@ -124,9 +125,11 @@ struct RopeTab {
     float theta[2];
     uint32_t rot[2];
 };
+// skip (or NULL): the last layer's quiescence flag; when set, x keeps its
+// value and the planes are made from y as it stands (the layer wrote none).
 int launch_norm_planes(hipStream_t s, float *x, const float *r, const float *post_w, const float *w, float *y,
                        uint32_t *xp, uint32_t dim, float eps, float scalar, bool add,
-                       const RopeTab *rope = nullptr);
+                       const RopeTab *rope = nullptr, const uint32_t *skip = nullptr);
 
 // The RoPE table entries i = t, t + nt, ... of rt (same arithmetic as the
 // reference's per-element rotation: theta^(2d / rot) by powf, sincosf).
@@ -153,11 +156,24 @@ __device__ __forceinline__ void rope_table(const RopeTab &rt, uint32_t t, uint32
 // Workgroup 0 writes xn to x_out (never x_in: the other workgroups still
 // read it) and y (if non-NULL).
 enum NormMode { NORM_PLAIN = 0, NORM_ADD = 1, NORM_POST_ADD = 2 };
+// Quiescence gating of a decode layer (the reference's indirect dispatch,
+// src/gpu/model_dispatch.zig:47-101, shaders/quiescence_gate.wgsl): a
+// layer whose input stream moved by less than thresh (mean square) since
+// the previous gated step runs none of its kernels.  NULL pointers: not
+// gated.
+struct Quiesce {
+    const uint32_t *prev_skip;   // the previous layer's flag: its FFN residual was not produced
+    uint32_t *skip;              // this layer's flag (written by the QKV kernel, read by the others)
+    float *x_prev;               // this layer's input stream at the previous gated step
+    float thresh;
+    uint32_t first;              // layer 0: no previous layer wrote the normed row
+};
 struct NormArgs {
     const float *x_in, *r, *pw, *w;
     float *x_out, *y;
     float eps, scalar;
     RopeTab rope;          // tab != NULL: workgroup 0 also writes the step's RoPE table
+    Quiesce q;             // zero: no gating
 };
 int mvr_qkv_nx(chn_ctx *ctx, const void *Wq, const void *Wk, const void *Wv, float *q, float *k, float *v,
                uint32_t q_dim, uint32_t kv_dim, uint32_t K, const NormArgs &n, int mode);
@@ -187,7 +203,8 @@ int launch_rope_decode_attn(chn_ctx *ctx, const float *q_in, const float *k_in, 
                             const float *kw, float *kc, float *vc, const uint32_t *step, const uint32_t *slots,
                             const uint32_t *n_slots, uint32_t max_slots, uint32_t num_q_heads, uint32_t head_dim,
                             uint32_t kv_dim, uint32_t gqa, uint32_t rot, int k_eq_v, const float2 *rope_tab,
-                            float eps, float scale, float *out, float *ws, uint32_t *xp);
+                            float eps, float scale, float *out, float *ws, uint32_t *xp,
+                            const uint32_t *skip = nullptr);
 // out: [n_tok][num_q_heads * head_dim] fp32, or bf16 into outb when set.
 // ws (prefill_attn_ws_bytes, or NULL): lets short prompts split each query
 // tile's keys between two workgroups.

@@ -57,6 +57,7 @@ struct RArgs {
     float *y0, *y1, *y2;
     const uint32_t *xp;
     uint32_t M, seg1, seg2, nb;
+    const uint32_t *skip;       // quiescence flag of the layer (NULL: never skipped)
 };
 
 // The wave's index in its workgroup, as a wave-uniform (scalar) value, so
@@ -136,6 +137,7 @@ __device__ __forceinline__ void store_r(const RArgs &a, uint32_t row, float v) {
 
 template <int MODE, int RPW, int WPR>
 __global__ __launch_bounds__(256) void k_q4rmv(RArgs a) {
+    if (a.skip && *a.skip) return;            // a quiescent layer (uniform)
     constexpr int NMAT = (MODE == RV_MLP) ? 2 : 1;
     constexpr int V = RPW * NMAT;
     constexpr int G = 4 / WPR;
@@ -306,12 +308,25 @@ constexpr int kLdsBlk = XP_WORDS + 1;
 // Split in two so that the norm's inputs are requested before the matvec's
 // first weights: loads complete in issue order, so the norm math then runs
 // while the weights are still in flight.
+//
+// QG (quiescence gating) is 0 when the layer is not gated; 1 in the QKV
+// kernel of a gated layer: the residual add is left out when the previous
+// layer was skipped, the mean square of (stream - its value at the previous
+// gated step) decides whether this layer runs (every workgroup computes the
+// same value in the same order, so they agree), workgroup 0 publishes the
+// decision, and y is written only where the reference writes it (by the
+// previous layer's closing add_rmsnorm or by this layer's input norm); 2 in
+// the gate/up kernel of a gated layer: workgroup 0 records the layer's input
+// stream (x_in) as the next step's x_prev.
 template <int C>
 struct NormIn {
-    float xv[C][8], rv[C][8], pv[C][8], wv[C][8];
+    float xv[C][8], rv[C][8], pv[C][8], wv[C][8], qv[C][8];
+    uint32_t pskip;
 };
-template <int MODE, int C>
+template <int MODE, int C, int QG = 0>
 __device__ __forceinline__ void norm_load(const NormArgs &n, uint32_t dim, NormIn<C> &v) {
+    v.pskip = 0;
+    if (QG == 1 && n.q.prev_skip) v.pskip = *n.q.prev_skip;
 #pragma unroll
     for (int c = 0; c < C; ++c) {
         const uint32_t t = threadIdx.x + c * blockDim.x;
@@ -320,13 +335,23 @@ __device__ __forceinline__ void norm_load(const NormArgs &n, uint32_t dim, NormI
         if (MODE != NORM_PLAIN) ld8(n.r, t, ok, v.rv[c]);
         if (MODE == NORM_POST_ADD) ld8(n.pw, t, ok, v.pv[c]);
         ld8(n.w, t, ok, v.wv[c]);
+        if (QG == 1) ld8(n.q.x_prev, t, ok, v.qv[c]);
     }
 }
-template <int MODE, int C>
-__device__ __forceinline__ void norm_to_lds(const NormArgs &n, uint32_t dim, NormIn<C> &v, uint32_t *lp,
+// Returns whether the layer runs (always true unless QG == 1).
+template <int MODE, int C, int QG = 0>
+__device__ __forceinline__ bool norm_to_lds(const NormArgs &n, uint32_t dim, NormIn<C> &v, uint32_t *lp,
                                             float *sh) {
     float ss[C];
-    if (MODE != NORM_PLAIN) {
+    if (QG == 2 && blockIdx.x == 0) {
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            const uint32_t t = threadIdx.x + c * blockDim.x;
+            if (8 * t < dim) st8(n.q.x_prev, t, v.xv[c]);
+        }
+    }
+    const bool add_on = QG != 1 || v.pskip == 0;   // uniform
+    if (MODE != NORM_PLAIN && add_on) {
         if (MODE == NORM_POST_ADD) {
 #pragma unroll
             for (int c = 0; c < C; ++c) {
@@ -345,6 +370,22 @@ __device__ __forceinline__ void norm_to_lds(const NormArgs &n, uint32_t dim, Nor
 #pragma unroll
             for (int i = 0; i < 8; ++i) v.xv[c][i] = (v.xv[c][i] + v.rv[c][i]) * n.scalar;
     }
+    bool active = true;
+    if (QG == 1) {
+        float dd[C];
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            dd[c] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float d = v.xv[c][i] - v.qv[c][i];
+                dd[c] += d * d;
+            }
+        }
+        const float ms = wg_sum_c<C>(dd, sh + 32) / (float)dim;
+        active = ms >= n.q.thresh || n.q.thresh <= 0.0f;
+        if (blockIdx.x == 0 && threadIdx.x == 0) *n.q.skip = active ? 0u : 1u;
+    }
 #pragma unroll
     for (int c = 0; c < C; ++c) {
         const uint32_t t = threadIdx.x + c * blockDim.x;
@@ -354,6 +395,7 @@ __device__ __forceinline__ void norm_to_lds(const NormArgs &n, uint32_t dim, Nor
         for (int i = 0; i < 8; ++i) ss[c] += v.xv[c][i] * v.xv[c][i];
     }
     const float inv = 1.0f / sqrtf(wg_sum_c<C>(ss, sh) / (float)dim + n.eps);
+    const bool write_y = QG != 1 || (add_on && !n.q.first) || active;
 #pragma unroll
     for (int c = 0; c < C; ++c) {
         const uint32_t t = threadIdx.x + c * blockDim.x;
@@ -361,9 +403,10 @@ __device__ __forceinline__ void norm_to_lds(const NormArgs &n, uint32_t dim, Nor
         float yv[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) yv[i] = (v.xv[c][i] * inv) * v.wv[c][i];
-        if (blockIdx.x == 0 && ok && n.y) st8(n.y, t, yv);
+        if (blockIdx.x == 0 && ok && n.y && write_y) st8(n.y, t, yv);
         emit_planes8s(yv, lp, 1, kLdsBlk, t >> 2, t & 3, ok);
     }
+    return active;
 }
 
 // This lane's two blocks of planes from the LDS copy norm_to_lds wrote.
@@ -400,7 +443,7 @@ __device__ __forceinline__ void lane_planes(const uint32_t *src, uint32_t nb, ui
 // workgroup, two rows per wave per group as k_q4rmv<RV_QKV, 2, 1>, the first
 // group's weights in flight while the norm runs, the next group's while a
 // group is reduced.
-template <int NORM, int NW = 8>
+template <int NORM, int NW = 8, int QG = 0>
 __global__ __launch_bounds__(64 * NW) void k_q4rmv_qkv_nx(RArgs a, NormArgs n) {
     constexpr int RPW = 2;
     constexpr int NCH = (512 + 64 * NW - 1) / (64 * NW);   // norm chunks of eight values per thread: K <= 4096
@@ -409,7 +452,7 @@ __global__ __launch_bounds__(64 * NW) void k_q4rmv_qkv_nx(RArgs a, NormArgs n) {
     const bool ok0 = (uint32_t)lane < nb, ok1 = (uint32_t)(64 + lane) < nb;
     const uint32_t b0 = ok0 ? lane : 0u, b1 = ok1 ? 64 + lane : 0u;
     __shared__ uint32_t lp[128 * kLdsBlk];
-    __shared__ float sh[32];
+    __shared__ float sh[48];
 
     const uint32_t ngroups = (a.M + RPW - 1) / RPW;
     const uint32_t gstride = gridDim.x * NW;
@@ -430,11 +473,12 @@ __global__ __launch_bounds__(64 * NW) void k_q4rmv_qkv_nx(RArgs a, NormArgs n) {
         }
     };
     NormIn<NCH> nv;
-    norm_load<NORM, NCH>(n, nb * 32, nv);
+    norm_load<NORM, NCH, QG>(n, nb * 32, nv);
     uint32_t g = blockIdx.x * NW + wave;
     if (g < ngroups) load(g);
     if (n.rope.tab && blockIdx.x == 0) rope_table(n.rope, threadIdx.x, blockDim.x);
-    norm_to_lds<NORM, NCH>(n, nb * 32, nv, lp, sh);
+    const bool active = norm_to_lds<NORM, NCH, QG>(n, nb * 32, nv, lp, sh);
+    if (QG && !active) return;                // a quiescent layer (the same decision in every workgroup)
     __syncthreads();
     uint32_t P[2][XP_WORDS];
     float xs[2];
@@ -480,10 +524,22 @@ __global__ __launch_bounds__(64 * NW) void k_q4rmv_qkv_nx(RArgs a, NormArgs n) {
 // computes it.  The 32 results meet in LDS; four lanes then quantize the
 // block.  Input planes come from a.xp (NORM < 0) or from the step's norm as
 // the prologue (NORM = NormMode).  Needs K <= 4096 and M % 32 == 0.
-template <int NW, int NORM>
+template <int NW, int NORM, int QG = 0>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) void k_q4rmv_mlp_xp(
     RArgs a, uint32_t *__restrict__ xo, NormArgs n) {
     constexpr int RW = 32 / NW;   // rows per wave per block
+    if (QG && *n.q.skip) {
+        // a quiescent layer: the stream passes unchanged; it is also the
+        // layer's input at the next gated step
+        if (blockIdx.x == 0)
+            for (uint32_t i = threadIdx.x; 8 * i < a.nb * 32; i += blockDim.x) {
+                float v[8];
+                ld8(n.x_in, i, true, v);
+                st8(n.x_out, i, v);
+                st8(n.q.x_prev, i, v);
+            }
+        return;
+    }
     const int wave = wave_id(), lane = threadIdx.x & 63;
     const uint32_t nb = a.nb;
     const bool ok0 = (uint32_t)lane < nb, ok1 = (uint32_t)(64 + lane) < nb;
@@ -511,7 +567,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     constexpr int NM = NORM < 0 ? 0 : NORM;
     constexpr int NCH = (NORM < 0) ? 1 : (512 + 64 * NW - 1) / (64 * NW);   // norm chunks: K <= 4096
     NormIn<NCH> nv;
-    if (NORM >= 0) norm_load<NM, NCH>(n, nb * 32, nv);
+    if (NORM >= 0) norm_load<NM, NCH, QG>(n, nb * 32, nv);
     uint32_t rb = blockIdx.x;
     RowPair nx;
     if (rb < nrb) load(nx, rb * 32 + wave);
@@ -520,7 +576,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
     uint32_t P[2][XP_WORDS];
     float xs[2];
     if (NORM >= 0) {
-        norm_to_lds<NM, NCH>(n, nb * 32, nv, lp, sh);
+        norm_to_lds<NM, NCH, QG>(n, nb * 32, nv, lp, sh);
         __syncthreads();
         lane_planes_lds(lp, b0, b1, ok0, ok1, P, xs);
     } else {
@@ -626,9 +682,9 @@ static RMat host_rmat(const void *W, uint32_t rows, uint32_t nb) {
 }
 
 int mvr_gemv(chn_ctx *ctx, const void *W, const float *x, float *y, uint32_t M, uint32_t K, uint32_t *xp,
-             bool planes_ready) {
+             bool planes_ready, const uint32_t *skip) {
     const uint32_t nb = K / 32;
-    RArgs a{host_rmat(W, M, nb), {}, {}, y, nullptr, nullptr, nullptr, M, M, M, nb};
+    RArgs a{host_rmat(W, M, nb), {}, {}, y, nullptr, nullptr, nullptr, M, M, M, nb, skip};
     return launch_q4rmv(ctx, RV_GEMV, a, x, xp, planes_ready);
 }
 int mvr_qkv(chn_ctx *ctx, const void *Wq, const void *Wk, const void *Wv, const float *x, float *q, float *k,
@@ -680,7 +736,11 @@ int mvr_mlp_nx(chn_ctx *ctx, const void *Wg, const void *Wu, float *act, uint32_
     // for the whole kernel)
     const uint32_t grid = nrb < kMlpGrid ? nrb : kMlpGrid;
     hipStream_t s = ctx->stream;
-    if (mode == NORM_PLAIN) k_q4rmv_mlp_xp<8, NORM_PLAIN><<<grid, 512, 0, s>>>(a, xp_out, n);
+    if (n.q.skip) {
+        if (mode == NORM_PLAIN) k_q4rmv_mlp_xp<8, NORM_PLAIN, 2><<<grid, 512, 0, s>>>(a, xp_out, n);
+        else if (mode == NORM_ADD) k_q4rmv_mlp_xp<8, NORM_ADD, 2><<<grid, 512, 0, s>>>(a, xp_out, n);
+        else k_q4rmv_mlp_xp<8, NORM_POST_ADD, 2><<<grid, 512, 0, s>>>(a, xp_out, n);
+    } else if (mode == NORM_PLAIN) k_q4rmv_mlp_xp<8, NORM_PLAIN><<<grid, 512, 0, s>>>(a, xp_out, n);
     else if (mode == NORM_ADD) k_q4rmv_mlp_xp<8, NORM_ADD><<<grid, 512, 0, s>>>(a, xp_out, n);
     else k_q4rmv_mlp_xp<8, NORM_POST_ADD><<<grid, 512, 0, s>>>(a, xp_out, n);
     CHN_LAUNCHED(ctx, "k_q4rmv_mlp_xp");
@@ -702,7 +762,11 @@ int mvr_qkv_nx(chn_ctx *ctx, const void *Wq, const void *Wk, const void *Wv, flo
     uint32_t grid = (need + 1) / 2;
     grid = grid < 1 ? 1 : (grid > 256 ? 256 : grid);
     hipStream_t s = ctx->stream;
-    if (mode == NORM_PLAIN) k_q4rmv_qkv_nx<NORM_PLAIN, 8><<<grid, 512, 0, s>>>(a, n);
+    if (n.q.skip) {
+        if (mode == NORM_PLAIN) k_q4rmv_qkv_nx<NORM_PLAIN, 8, 1><<<grid, 512, 0, s>>>(a, n);
+        else if (mode == NORM_ADD) k_q4rmv_qkv_nx<NORM_ADD, 8, 1><<<grid, 512, 0, s>>>(a, n);
+        else k_q4rmv_qkv_nx<NORM_POST_ADD, 8, 1><<<grid, 512, 0, s>>>(a, n);
+    } else if (mode == NORM_PLAIN) k_q4rmv_qkv_nx<NORM_PLAIN, 8><<<grid, 512, 0, s>>>(a, n);
     else if (mode == NORM_ADD) k_q4rmv_qkv_nx<NORM_ADD, 8><<<grid, 512, 0, s>>>(a, n);
     else k_q4rmv_qkv_nx<NORM_POST_ADD, 8><<<grid, 512, 0, s>>>(a, n);
     CHN_LAUNCHED(ctx, "k_q4rmv_qkv_nx");

@@ -65,6 +65,10 @@ struct chn_model {
     uint32_t *h_gen = nullptr;
     // ring state the greedy head reads: turn boundaries, recall clocks
     uint32_t *ring_bounds = nullptr, *ring_recall = nullptr;
+    // quiescence: per layer a skip flag and the input stream at the previous
+    // gated step ([num_layers][hidden], zero at creation)
+    uint32_t *qflags = nullptr;
+    float *qprev = nullptr;
     std::vector<void *> allocs;
 };
 
@@ -146,6 +150,7 @@ static int validate_config(chn_ctx *ctx, const chn_model_config &c) {
     CHN_REQUIRE(ctx, c.hidden_size <= 4096, "hidden_size %u: the Q8 logits matvec needs K <= 4096", c.hidden_size);
     CHN_REQUIRE(ctx, c.max_prefill_tokens >= 1 && c.max_prefill_tokens <= 4096, "max_prefill_tokens %u invalid",
                 c.max_prefill_tokens);
+    CHN_REQUIRE(ctx, c.quiescence_thresh >= 0.0f && c.quiescence_thresh <= 3.0e38f, "quiescence_thresh must be >= 0");
     return CHN_OK;
 }
 
@@ -178,6 +183,8 @@ static int alloc_runtime(chn_model *m) {
     M_ALLOC(m->gen_tokens, (size_t)kGreedyCap * 4);
     M_ALLOC(m->ring_bounds, 1024 * 4);
     M_ALLOC(m->ring_recall, 128 * 4);
+    M_ALLOC(m->qflags, (size_t)c.num_layers * 4);
+    M_ALLOC(m->qprev, (size_t)c.num_layers * H * 4);
     const uint32_t kmax = H > I ? (H > qd ? H : qd) : (I > qd ? I : qd);
     size_t mvb = mv_ws_bytes(kmax);
     if (xbytes_bytes(H / 32) > mvb) mvb = xbytes_bytes(H / 32);
@@ -217,6 +224,8 @@ static int alloc_runtime(chn_model *m) {
     if (!rc) rc = chn_fill_u32(m->ctx, m->step, 0, 16);
     if (!rc) rc = chn_fill_u32(m->ctx, m->topk_ids, 0, 64);
     if (!rc) rc = chn_fill_u32(m->ctx, m->gen, 0, 16);
+    if (!rc) rc = chn_fill_u32(m->ctx, m->qflags, 0, c.num_layers);
+    if (!rc) rc = chn_fill_u32(m->ctx, m->qprev, 0, (size_t)c.num_layers * H);
     return rc;
 }
 
@@ -328,9 +337,17 @@ static int record_decode(chn_model *m, bool with_logits) {
     uint32_t *xp = m->mv_ws, *xp_act = m->mv_ws + m->mv_ws_words;
     float *xa = m->x, *xb = m->x2;
     const RopeTab no_rope{nullptr, nullptr, {0.0f, 0.0f}, {0u, 0u}};
+    // Quiescence gating (src/gpu/model_dispatch.zig:103-126): only in the
+    // steps that return logits, for layers from num_layers / 3 on.
+    const bool gate_on = with_logits && c.quiescence_thresh > 0.0f;
+    const uint32_t dense_limit = c.num_layers / 3;
+    auto gated = [&](uint32_t i) { return gate_on && i >= dense_limit; };
     for (uint32_t i = 0; i < c.num_layers; ++i) {
         const auto &l = m->L[i];
-        NormArgs n1{xa, nullptr, nullptr, l.in_norm, xb, m->normed, eps, 1.0f, no_rope};
+        uint32_t *skip = gated(i) ? m->qflags + i : nullptr;
+        const Quiesce q{i > 0 && gated(i - 1) ? m->qflags + i - 1 : nullptr, skip,
+                        skip ? m->qprev + (size_t)i * H : nullptr, c.quiescence_thresh, i == 0 ? 1u : 0u};
+        NormArgs n1{xa, nullptr, nullptr, l.in_norm, xb, m->normed, eps, 1.0f, no_rope, skip ? q : Quiesce{}};
         int mode1 = NORM_PLAIN;
         if (i == 0) {
             // the step's first kernel also writes its RoPE table
@@ -347,17 +364,18 @@ static int record_decode(chn_model *m, bool with_logits) {
         R_(launch_rope_decode_attn(ctx, m->q, m->k, m->v, l.q_norm, l.k_norm, l.kc, l.vc, m->step,
                                    m->slots + (l.full ? 0 : kSlotsMax), m->step + (l.full ? 2 : 3), kSlotsMax, nq, l.D,
                                    l.kvd, l.gqa, l.rot, (int)c.k_eq_v, m->rope_tab + (l.full ? kRopePairs : 0), eps,
-                                   1.0f, m->attn, m->attn_ws, xp));
-        R_(mvr_gemv(ctx, l.Wo, m->attn, m->mlp_out, H, l.qd, xp, true));
+                                   1.0f, m->attn, m->attn_ws, xp, skip));
+        R_(mvr_gemv(ctx, l.Wo, m->attn, m->mlp_out, H, l.qd, xp, true, skip));
         const NormArgs n2{xb, m->mlp_out, l.has_post_attn ? l.post_attn : nullptr, l.pre_ffn, xa, m->normed,
-                          eps, 1.0f, no_rope};
+                          eps, 1.0f, no_rope, skip ? Quiesce{nullptr, skip, q.x_prev, q.thresh, 0u} : Quiesce{}};
         R_(mvr_mlp_nx(ctx, l.Wg, l.Wu, m->act, xp_act, I, H, n2, l.has_post_attn ? NORM_POST_ADD : NORM_ADD));
-        R_(mvr_gemv(ctx, l.Wd, m->act, m->mlp_out, H, I, xp_act, true));
+        R_(mvr_gemv(ctx, l.Wd, m->act, m->mlp_out, H, I, xp_act, true, skip));
     }
     // the last layer's FFN residual (into x) and the final norm
     const auto &last = m->L[c.num_layers - 1];
     R_(launch_norm_planes(s, xa, m->mlp_out, last.has_post_ffn ? last.post_ffn : nullptr, m->final_norm, m->normed,
-                          xp, H, eps, last.scalar, true));
+                          xp, H, eps, last.scalar, true, nullptr,
+                          gated(c.num_layers - 1) ? m->qflags + c.num_layers - 1 : nullptr));
     if (with_logits) {
         R_(launch_gemv_q8(s, m->embed_q8, m->normed, m->logits, c.vocab_size, H / 32, m->mv_ws));
         R_(launch_topk64(s, m->logits, c.vocab_size, m->topk_ids, m->topk_vals, m->topk_ws));
@@ -827,8 +845,10 @@ extern "C" int chn_prefill(chn_model *m, const uint32_t *tokens, uint32_t n, con
                                  num_prev_slots, start_clock, n, nq, nkv, D, l.rot, (int)c.k_eq_v, theta, eps,
                                  ptab[l.full ? 1 : 0]));
         // sliding layers see the last 1024 slots (shaders/batch_causal_attn.wgsl:53)
+        // unless the config sets another prefill window
+        const uint32_t pwin = c.prefill_window ? c.prefill_window : 1024u;
         P_(launch_prefill_attn(s, m->pq, l.kc, l.vc, m->pslots, n, num_prev_slots, nq, D, kvd, gqa, 1.0f,
-                               l.full ? 0u : 1024u, nullptr, xb, m->pattn_ws));
+                               l.full ? 0u : pwin, nullptr, xb, m->pattn_ws));
         P_(launch_q4gemm(ctx, 1, nullptr, l.Wo, nullptr, m->pmlp, n, H, qd, xb, true));
         P_(launch_rmsnorm_chain(s, m->px, m->pmlp, l.has_post_attn ? l.post_attn : nullptr, l.pre_ffn, xb, nullptr,
                                 H, n, eps, 1.0f, true, true));

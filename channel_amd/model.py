@@ -26,7 +26,9 @@ class ModelConfig(ctypes.Structure):
         ("rms_norm_eps", c_f32), ("rope_theta", c_f32), ("rope_theta_full", c_f32),
         ("sliding_window", c_u32), ("k_eq_v", c_u32), ("max_prefill_tokens", c_u32),
         ("layer_full", ctypes.c_uint8 * 64),
+        ("quiescence_thresh", c_f32), ("prefill_window", c_u32),
     ]
+    _OPTIONAL = ("global_head_dim", "num_global_kv_heads", "quiescence_thresh", "prefill_window")
 
     @classmethod
     def from_dict(cls, d):
@@ -36,7 +38,7 @@ class ModelConfig(ctypes.Structure):
                 for i, v in enumerate(d["layer_full"]):
                     c.layer_full[i] = 1 if v else 0
             else:
-                setattr(c, name, d.get(name, 0) if name in ("global_head_dim", "num_global_kv_heads") else d[name])
+                setattr(c, name, d.get(name, 0) if name in cls._OPTIONAL else d[name])
         return c
 
     def to_dict(self):

@@ -330,6 +330,16 @@ typedef struct chn_model_config {
     uint32_t k_eq_v;               /* attention_k_eq_v */
     uint32_t max_prefill_tokens;   /* BatchPrefillContext max_tokens (model_gpu.zig:178) */
     uint8_t layer_full[64];        /* 1 = full_attention, 0 = sliding_attention */
+    /* GpuModelContext.init's quiescence_thresh (model_gpu.zig:68,198): > 0
+     * gates layers >= num_layers / 3 of the decode steps that return logits
+     * (model_dispatch.zig:47-126, shaders/quiescence_gate.wgsl): a layer whose
+     * input stream's mean squared change since the previous such step is
+     * below it runs none of its work (no K/V write either); 0 = off. */
+    float quiescence_thresh;
+    /* Prefill attention window of sliding layers: 0 = 1024, the reference's
+     * fixed value (shaders/batch_causal_attn.wgsl:53); sliding_window makes
+     * prefill agree with decode. */
+    uint32_t prefill_window;
 } chn_model_config;
 
 /* LayerWeights (src/model/types.zig:13-41): host bf16 tensors, row-major

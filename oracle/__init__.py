@@ -61,6 +61,7 @@ _PROTOS = {
     "orc_batch_causal_attn_mt": (None, [_f32p, _f32p, _f32p, _u32p, _u32, _u32, _u32, _u32, _u32,
                                         _u32, _f32, _u32, _f32p, _int]),
     "orc_gelu_tanh_vec": (None, [_f32p, _f32p, _size]),
+    "orc_quiescence_gate": (_int, [_f32p, _f32p, _u32, _f32, _f32p]),
     "orc_softcap_vec": (None, [_f32p, _f32p, _size]),
 }
 
@@ -322,3 +323,13 @@ def synth_normal(n, seed, stddev=1.0):
     out = np.zeros(n, np.float32)
     lib.orc_synth_normal(out, n, seed, stddev)
     return out
+
+
+def quiescence_gate(x, x_prev, thresh):
+    """shaders/quiescence_gate.wgsl for one layer: returns (runs, mean
+    square of the change); x_prev (float32, C-contiguous) is overwritten with x."""
+    assert x_prev.dtype == np.float32 and x_prev.flags.c_contiguous
+    xx = _c(x, np.float32, x_prev.size)
+    ms = np.zeros(1, np.float32)
+    runs = bool(lib.orc_quiescence_gate(xx, x_prev, x_prev.size, float(thresh), ms))
+    return runs, float(ms[0])

@@ -108,16 +108,48 @@ def new_caches(cfg, nslot=4096):
             [np.zeros(nslot * k, np.float32) for k in kvds])
 
 
-def decode_step(W, kc, vc, x, clock, slot_idx, active, sliding, with_logits=True, nthreads=1):
+class QuiescenceState:
+    """What the reference's GPU model keeps across decode steps for
+    quiescence gating (src/gpu/model_gpu.zig:131, model_dispatch.zig:47-126):
+    per layer the input stream at the previous gated step (buf_x_prev,
+    zero-initialised) and the normed row buf_normed_x, which a quiescent
+    layer leaves as it was.  `log` collects per step the (layer, runs, mean
+    square) of every gate."""
+
+    def __init__(self, cfg, thresh):
+        H = cfg["hidden_size"]
+        self.thresh = float(thresh)
+        self.x_prev = [np.zeros(H, np.float32) for _ in range(cfg["num_layers"])]
+        self.normed = np.zeros(H, np.float32)
+        self.log = []
+
+
+def decode_step(W, kc, vc, x, clock, slot_idx, active, sliding, with_logits=True, nthreads=1, qstate=None):
     """One token through every layer; kc / vc (per-layer flat arrays) are
     updated in place.  Returns (x, normed, logits, ids, vals).  nthreads > 1
-    uses the threaded matvecs (bit-identical results)."""
+    uses the threaded matvecs (bit-identical results).  With a
+    QuiescenceState whose threshold is positive, the steps with logits gate
+    layers from num_layers / 3 on (recordLayerIndirect): the gate compares
+    the stream with the layer's previous one, and a quiescent layer runs
+    nothing (the stream, the normed row and its K/V slot keep their values);
+    a running one starts from its own input norm."""
     c = W.cfg
     H, I = c["hidden_size"], c["intermediate_size"]
     nq, eps = c["num_heads"], c["rms_norm_eps"]
     x = np.array(x, np.float32)
-    normed = O.rmsnorm(x, W.layers[0]["in_norm"], eps)
+    gate_on = with_logits and qstate is not None and qstate.thresh > 0.0
+    dense = c["num_layers"] // 3
+    normed = qstate.normed.copy() if qstate is not None else None
+    gates = []
     for i, l in enumerate(W.layers):
+        if gate_on and i >= dense:
+            runs, ms = O.quiescence_gate(x, qstate.x_prev[i], qstate.thresh)
+            gates.append((i, runs, ms))
+            if not runs:
+                continue
+            normed = O.rmsnorm(x, l["in_norm"], eps)
+        elif i == 0:
+            normed = O.rmsnorm(x, l["in_norm"], eps)
         full = bool(c["layer_full"][i])
         theta = c["rope_theta_full"] if full else c["rope_theta"]
         D, nkv = l["D"], l["nkv"]
@@ -137,6 +169,9 @@ def decode_step(W, kc, vc, x, clock, slot_idx, active, sliding, with_logits=True
             d = O.rmsnorm(d, l["post_ffn"], eps)
         nxt = W.layers[i + 1]["in_norm"] if i + 1 < len(W.layers) else W.final_norm
         x, normed = O.add_rmsnorm(x, d, nxt, eps, float(l["scalar"]))
+    if qstate is not None:
+        qstate.normed = normed.copy()
+        qstate.log.append(gates)
     logits = ids = vals = None
     if with_logits:
         logits = O.gemv_q8(W.embed_q8, normed, c["vocab_size"], H, nthreads)

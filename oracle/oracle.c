@@ -996,3 +996,28 @@ void orc_batch_causal_attn_mt(const float *Q, const float *Kc, const float *Vc, 
     cattn_job_t j = {Q, Kc, Vc, slots, num_prev_slots, num_q_heads, head_dim, kv_dim, gqa_ratio, window, scale, out};
     par_rows(n_tok, nthreads, cattn_rows, &j);
 }
+
+/* ======================================================================
+ * Quiescence gate (shaders/quiescence_gate.wgsl:17-62, wired in
+ * src/gpu/model_dispatch.zig:47-126): 32 lanes stride the hidden vector
+ * summing (x - x_prev)^2 in order and copying x into x_prev, then a
+ * 16/8/4/2 tree and s[0] + s[1]; the layer runs when the mean is at least
+ * the threshold (or the threshold is not positive).
+ * ==================================================================== */
+int orc_quiescence_gate(const float *x, float *x_prev, uint32_t H, float thresh, float *mean_out) {
+    float s[32];
+    for (uint32_t lane = 0; lane < 32; ++lane) {
+        float acc = 0.0f;
+        for (uint32_t i = lane; i < H; i += 32) {
+            const float d = x[i] - x_prev[i];
+            acc = acc + d * d;
+            x_prev[i] = x[i];
+        }
+        s[lane] = acc;
+    }
+    for (uint32_t off = 16; off >= 2; off >>= 1)
+        for (uint32_t l = 0; l < off; ++l) s[l] = s[l] + s[l + off];
+    const float mean_sq = (s[0] + s[1]) / (float)H;
+    if (mean_out) *mean_out = mean_sq;
+    return (mean_sq >= thresh) || (thresh <= 0.0f);
+}

@@ -99,6 +99,10 @@ void orc_synth_q8(uint32_t *W, uint32_t rows, uint32_t K, uint64_t seed,
                   float smin, float smax);
 void orc_synth_normal(float *dst, size_t n, uint64_t seed, float stddev);
 
+/* ---- quiescence gate (shaders/quiescence_gate.wgsl): returns 1 when the
+ *      layer runs; x_prev <- x ------------------------------------------- */
+int orc_quiescence_gate(const float *x, float *x_prev, uint32_t H, float thresh, float *mean_out);
+
 /* ---- threaded CPU baseline (src/kernels.zig:53-99 scheme) ------------- */
 void orc_gemv_q4_mt(const uint32_t *W, const float *x, float *y, uint32_t M,
                     uint32_t K, int nthreads);

@@ -327,3 +327,119 @@ def test_global_head_shape_model(ctx):
             x_g, _ = m.read_state()
             assert rel_err(x_g, x_o) < 1e-3
             tok = int(ids_g[0])
+
+
+@pytest.mark.parametrize("anchors", [0, 32])
+def test_prefill_chunked_as_the_server_calls_it(pair, anchors):
+    """The server's batched prefill (src/server/prefill.zig:61-97): the
+    prompt in chunks of max_tokens; per chunk the previous slots from
+    getPrefillPrevSlots, then getSlotIndex of each new clock, every layer's
+    slot activated; logits and the top-64 only for the last chunk.  Against
+    the oracle run through the same chunks (ring restatement oracle/ring.py)."""
+    from oracle.ring import Ring
+    W, m = pair
+    max_tok = CFG["max_prefill_tokens"]
+    toks = [int(t) for t in np.random.default_rng(70 + anchors).integers(0, CFG["vocab_size"], 150)]
+    ring = Ring(CFG["num_layers"], 0)
+    ring.set_num_anchors(anchors)
+    kc, vc = OM.new_caches(CFG, 4096)
+    clock, off = 0, 0
+    while off < len(toks):
+        chunk = toks[off:off + max_tok]
+        last = off + len(chunk) == len(toks)
+        prev = ring.prefill_prev_slots(0, clock, len(chunk))
+        c_slots = list(prev)
+        for i in range(len(chunk)):
+            c_slots.append(ring.slot_index(0, clock + i))
+            for layer in range(CFG["num_layers"]):
+                ring.activate_slot(layer, clock + i)
+        say(f"chunked prefill clock={clock} n={len(chunk)} prev={len(prev)} anchors={anchors}")
+        lg, ids, vals = m.prefill_batch(chunk, c_slots, clock, len(prev), embed_bf16=W.embed_bf16,
+                                        logits=last, topk=last)
+        _, _, lg_o, _, _ = OM.prefill(W, kc, vc, chunk, c_slots, clock, len(prev), bf16_gemm=True)
+        clock += len(chunk)
+        off += len(chunk)
+    assert rel_err(lg, lg_o) < 1e-2
+    assert_topk_valid(ids, vals, lg_o, 1e-2, f"chunked prefill, anchors {anchors}")
+
+
+CFG_Q = OM.default_config(hidden_size=256, intermediate_size=512, vocab_size=4096, num_layers=6,
+                          num_heads=4, num_kv_heads=2, head_dim=256, rotary_dim=128,
+                          layer_full=[0, 0, 1, 0, 0, 1], max_prefill_tokens=16, sliding_window=16)
+# (token, clock, with logits): repeated clocks rewrite a slot with the same
+# values, so the stream entering the first gated layer does not move
+STEPS_Q = [(5, 0, True), (5, 0, True), (9, 1, True), (9, 1, False), (9, 1, True), (9, 1, True),
+           (3, 2, True), (4, 3, True), (4, 3, True)]
+
+
+def _quiescence_oracle(W, thresh):
+    """The steps through the oracle; per step its outputs and the K/V rows of
+    slots 0..3 of every layer after it."""
+    qs = OM.QuiescenceState(CFG_Q, thresh)
+    kc, vc = OM.new_caches(CFG_Q, 4096)
+    kvd = CFG_Q["num_kv_heads"] * CFG_Q["head_dim"]
+    outs, kv = [], []
+    for tok, clock, logits in STEPS_Q:
+        act, sl = OM.slot_lists(clock, 16)
+        outs.append(OM.decode_step(W, kc, vc, W.embed([tok])[0], clock, clock, act, sl, with_logits=logits,
+                                   qstate=qs))
+        kv.append([(k[: 4 * kvd].reshape(4, kvd).copy(), v[: 4 * kvd].reshape(4, kvd).copy()) for k, v in zip(kc, vc)])
+    return qs, outs, kv
+
+
+def test_quiescence_gating_matches_oracle(ctx):
+    """Quiescence-gated decode (src/gpu/model_dispatch.zig:47-126,
+    shaders/quiescence_gate.wgsl) against the oracle's gated composition:
+    the stream, the normed row, the top-64 and every K/V row after each step
+    (quiescent layers write no K/V).  The threshold is chosen from the
+    oracle's own gate values, at least 1% away from every one of them, with
+    both outcomes present and some layers quiescent although their stream
+    moved, so rounding cannot flip a decision."""
+    layers, embed, final = OM.random_model(CFG_Q, 41)
+    W = OM.Weights(CFG_Q, layers, embed, final)
+    chosen = None
+    for thresh in np.geomspace(1e-5, 10.0, 61):
+        qs, outs, kv = _quiescence_oracle(W, thresh)
+        gates = [g for step in qs.log for g in step]
+        margin = min((abs(np.log(g[2] / thresh)) for g in gates if g[2] > 0), default=np.inf)
+        moved_skips = sum(1 for g in gates if not g[1] and g[2] > 0)
+        if margin > 0.01 and any(g[1] for g in gates) and moved_skips >= 2:
+            chosen = (float(thresh), qs, outs, kv)
+            break
+    assert chosen is not None
+    thresh, qs, outs, kv_o = chosen
+    say(f"quiescence threshold {thresh:.3g}; quiescent layers per step: "
+        f"{[[g[0] for g in step if not g[1]] for step in qs.log]}")
+    with Model.create(ctx, dict(CFG_Q, quiescence_thresh=thresh), layers, embed, final) as m:
+        for s, (tok, clock, logits) in enumerate(STEPS_Q):
+            act, sl = OM.slot_lists(clock, 16)
+            say(f"gated decode step {s}: token {tok} clock {clock} logits {logits}")
+            _, ids, vals = m.forward_token(W.embed([tok])[0], clock, clock, act, sl, topk=logits)
+            x_o, n_o, lg_o, _, _ = outs[s]
+            x_g, n_g = m.read_state()
+            assert rel_err(x_g, x_o) < 1e-3 and rel_err(n_g, n_o) < 1e-3
+            if logits:
+                assert_topk_valid(ids, vals, lg_o, 1e-3, f"gated step {s}")
+            for i in range(CFG_Q["num_layers"]):
+                k, v = m.kv_read(i, 0, 4)
+                k_o, v_o = kv_o[s][i]
+                assert np.array_equal(k == 0, k_o == 0), (s, i)      # the same rows written
+                assert rel_err(k, k_o) < 1e-3 and rel_err(v, v_o) < 1e-3, (s, i)
+
+
+def test_prefill_window_option(ctx):
+    """prefill_window = sliding_window makes the prefill's sliding layers
+    use the decode window instead of the reference's fixed 1024."""
+    cfg = dict(CFG, prefill_window=WINDOW, num_layers=2, layer_full=[0, 1])
+    layers, embed, final = OM.random_model(cfg, 55)
+    W = OM.Weights(cfg, layers, embed, final)
+    toks = [int(t) for t in np.random.default_rng(55).integers(0, cfg["vocab_size"], 40)]
+    say("prefill with prefill_window 16")
+    with Model.create(ctx, cfg, layers, embed, final) as m:
+        lg, ids, vals = m.prefill_batch(toks, np.arange(40), 0, 0, embed_bf16=W.embed_bf16)
+    kc, vc = OM.new_caches(cfg, 4096)
+    _, _, lg16, _, _ = OM.prefill(W, kc, vc, toks, np.arange(40), 0, 0, bf16_gemm=True, window=WINDOW)
+    kc, vc = OM.new_caches(cfg, 4096)
+    _, _, lg1024, _, _ = OM.prefill(W, kc, vc, toks, np.arange(40), 0, 0, bf16_gemm=True, window=1024)
+    assert rel_err(lg, lg16) < 1e-2
+    assert rel_err(lg16, lg1024) > 1e-2          # the window matters at 40 tokens

@@ -501,3 +501,23 @@ def test_threaded_forms_equal_serial():
     xs = rng.standard_normal(300).astype(np.float32) * 20
     assert np.array_equal(oracle.gelu_tanh(xs), np.array([oracle.lib.orc_gelu_tanh(float(v)) for v in xs], np.float32))
     assert np.array_equal(oracle.softcap(xs), np.array([oracle.lib.orc_softcap(float(v)) for v in xs], np.float32))
+
+
+def test_quiescence_gate_closed_form():
+    """shaders/quiescence_gate.wgsl: the layer runs when mean((x - x_prev)^2)
+    >= threshold (or the threshold is not positive); x_prev becomes x."""
+    rng = np.random.default_rng(5)
+    H = 3840
+    x = rng.standard_normal(H).astype(np.float32)
+    xp0 = (x + 0.01 * rng.standard_normal(H)).astype(np.float32)
+    ms64 = float(np.mean((x.astype(np.float64) - xp0.astype(np.float64)) ** 2))
+    for thresh, want in ((ms64 * 0.99, True), (ms64 * 1.01, False), (0.0, True), (-1.0, True)):
+        xp = xp0.copy()
+        runs, ms = oracle.quiescence_gate(x, xp, thresh)
+        assert runs == want, thresh
+        assert abs(ms - ms64) <= 1e-5 * ms64
+        assert np.array_equal(xp, x)
+    # an unchanged stream is quiescent for any positive threshold
+    xp = x.copy()
+    runs, ms = oracle.quiescence_gate(x, xp, 1e-30)
+    assert not runs and ms == 0.0

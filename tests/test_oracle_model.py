@@ -130,3 +130,48 @@ def test_global_head_shape_layers():
         a, s = OM.slot_lists(t, 1024)
         x, *_ = OM.decode_step(W, kc2, vc2, W.embed([tok])[0], t, t, a, s)
         assert _rel(X[t], x) < 1e-4
+
+
+def _unit_norm_model(seed, num_layers=6):
+    cfg = OM.default_config(hidden_size=256, intermediate_size=512, vocab_size=1024, num_layers=num_layers,
+                            num_heads=4, num_kv_heads=2, head_dim=256, rotary_dim=128, max_prefill_tokens=16,
+                            sliding_window=8, layer_full=[i % 3 == 2 for i in range(num_layers)])
+    layers, embed, _ = OM.random_model(cfg, seed)
+    for l in layers:       # every norm 1.0 (absent post norms are skipped)
+        for k in ("input_layernorm", "q_norm", "k_norm", "pre_feedforward_layernorm"):
+            l[k] = None
+        l["post_attention_layernorm"] = l["post_feedforward_layernorm"] = None
+        l["layer_scalar"] = 1.0
+    return cfg, layers, embed
+
+
+def test_quiescence_composition():
+    """The gated decode step (recordLayerIndirect data flow): threshold 0 or
+    a step without logits changes nothing; an unreachable threshold skips
+    every gated layer, which leaves exactly the model of the first
+    num_layers / 3 layers (all norms 1, so the stale normed row equals the
+    final norm's) and leaves the gated layers' K/V slots untouched."""
+    cfg, layers, embed = _unit_norm_model(3)
+    W = OM.Weights(cfg, layers, embed, None)
+    dense = cfg["num_layers"] // 3
+    x = W.embed([17])[0]
+    act, sl = OM.slot_lists(0, 8)
+    kc0, vc0 = OM.new_caches(cfg, 64)
+    ref = OM.decode_step(W, kc0, vc0, x, 0, 0, act, sl)
+    for thresh, logits in ((0.0, True), (1e30, False)):
+        kc, vc = OM.new_caches(cfg, 64)
+        got = OM.decode_step(W, kc, vc, x, 0, 0, act, sl, with_logits=logits, qstate=OM.QuiescenceState(cfg, thresh))
+        assert np.array_equal(got[0], ref[0]) and np.array_equal(got[1], ref[1])
+    kc, vc = OM.new_caches(cfg, 64)
+    qs = OM.QuiescenceState(cfg, 1e30)
+    got = OM.decode_step(W, kc, vc, x, 0, 0, act, sl, qstate=qs)
+    assert [g[0] for g in qs.log[0]] == list(range(dense, cfg["num_layers"]))
+    assert not any(g[1] for g in qs.log[0])
+    cfg_t = dict(cfg, num_layers=dense, layer_full=cfg["layer_full"][:dense])
+    Wt = OM.Weights(cfg_t, layers[:dense], embed, None)
+    kt, vt = OM.new_caches(cfg_t, 64)
+    want = OM.decode_step(Wt, kt, vt, x, 0, 0, act, sl)
+    for a, b in zip(got, want):
+        assert np.array_equal(a, b)
+    for i in range(dense, cfg["num_layers"]):
+        assert not kc[i].any() and not vc[i].any()
