@@ -10,7 +10,7 @@ This scans every function whose name matches a pattern and reports any
 instruction that touches the VGPRs of a pending ds_read (LDS operations
 retire in issue order, so lgkmcnt(n) retires all but the newest n).
 
-usage: python lds_wait_check.py file.s [name-substring]
+usage: python tests/lds_wait_check.py file.s [name-substring]
 """
 import re
 import sys

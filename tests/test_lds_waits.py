@@ -3,9 +3,7 @@ completion the compiler does not track; this compiles the kernel for gfx950
 and checks that no instruction touches a load's registers before the wait
 that retires it (a copy made earlier copies a value not yet loaded)."""
 import os
-import shutil
 import subprocess
-import sys
 
 import pytest
 
@@ -22,11 +20,7 @@ def test_gemm_lds_waits(tmp_path):
            os.path.join(CSRC, "gemm_q4.hip"), "-o", str(out)]
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     assert r.returncode == 0, r.stdout[-2000:]
-    sys.path.insert(0, CSRC)
-    try:
-        import lds_wait_check
-    finally:
-        sys.path.remove(CSRC)
+    import lds_wait_check
     res = lds_wait_check.check_file(str(out), "k_q4gemm_p")
     assert res, "no pipelined GEMM kernel found in the assembly"
     bad = {f: h for f, h in res.items() if h}
