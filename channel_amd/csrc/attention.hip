@@ -19,11 +19,14 @@
 #include "chn_internal.h"
 
 #include <mutex>
+#include <type_traits>
 
 namespace chn {
 
 constexpr int kAttnChunk = 64;     // prefill: slots per online-softmax step
 constexpr uint32_t kDecGrid = 32;  // decode: workgroups per KV head (at most)
+constexpr int kMaxChunks = 8;      // decode: 16-entry chunks per split at most (4096 / 16 / kDecGrid)
+static_assert(kMaxChunks * 16 * kDecGrid >= 4096, "a split's chunks of the largest list");
 constexpr float kNegBig = -1e30f;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
@@ -285,9 +288,21 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
     auto entry = [&](uint32_t t) { return (split + G * t) * 16 + row_ent; };
     auto slot_at = [&](uint32_t t) {
         const uint32_t e = entry(t);
-        return t < ntmax ? slots[e < max_slots ? e : max_slots - 1] : 0u;
+        const uint32_t v = slots[e < max_slots ? e : max_slots - 1];   // unconditional (exact waits)
+        return t < ntmax ? v : 0u;
     };
-    uint32_t pa = slot_at(0), pb = slot_at(1);
+    // Chunks go in pairs; NSET pairs are in flight: while one pair is reduced
+    // the next one's K/V rows are loading.  Two sets where the registers
+    // allow (D 256, GQA <= 2: 128 VGPRs of rows); they read every list entry
+    // the split can own up front (at most kMaxChunks: 4096 entries in chunks
+    // of 16 over min(256, kDecGrid) splits), one set reads a pair's entries
+    // while the previous pair is reduced.  Either way the first entries are
+    // read together with the count.
+    constexpr int NSET = (DV == 1 && GQA <= 2) ? 2 : 1;
+    constexpr int NSL = NSET == 2 ? kMaxChunks : 2;
+    uint32_t sl[NSL];
+#pragma unroll
+    for (int t = 0; t < NSL; ++t) sl[t] = slot_at(t);
     uint32_t S = *n_slots;
     if (S > max_slots) S = max_slots;
     const uint32_t nch = (S + 15) / 16;
@@ -299,25 +314,37 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
     }
     const size_t dim0 = (size_t)kvh * D + (size_t)c * 4 * NF;
 
-    bool ok[2];
-    f4 kr[2][NF], vr[2][NF];
-    auto issue = [&](uint32_t t) {       // chunks t, t + 1
-        ok[0] = entry(t) < S;
-        ok[1] = t + 1 < iters && entry(t + 1) < S;
-        const float *ka = Kc + (size_t)pa * kv_dim + dim0, *va = Vc + (size_t)pa * kv_dim + dim0;
-        const float *kb = Kc + (size_t)pb * kv_dim + dim0, *vb = Vc + (size_t)pb * kv_dim + dim0;
+    bool ok[2 * NSET];                   // set s: buffers 2 s, 2 s + 1
+    f4 kr[2 * NSET][NF], vr[2 * NSET][NF];
+    // With two sets, rows past the count load cache row 0 instead (every
+    // load unconditional, so the waits count exactly the loads of the set
+    // being reduced); their scores are masked and their V rows replaced by
+    // zeros in reduce.  One set loads zeros for them.
+    auto issue = [&](int set, uint32_t t, uint32_t pa, uint32_t pb) {   // chunks t, t + 1 (t < iters)
+        const int b0 = 2 * set, b1 = b0 + 1;
+        ok[b0] = entry(t) < S;
+        ok[b1] = t + 1 < iters && entry(t + 1) < S;
+        const bool all = NSET == 2;
+        const size_t ra = (size_t)(ok[b0] ? pa : 0u) * kv_dim + dim0;
+        const size_t rb = (size_t)(ok[b1] ? pb : 0u) * kv_dim + dim0;
 #pragma unroll
-        for (int f = 0; f < NF; ++f) kr[0][f] = ok[0] ? *(const f4 *)(ka + 4 * f) : f4{0, 0, 0, 0};
+        for (int f = 0; f < NF; ++f) kr[b0][f] = all || ok[b0] ? *(const f4 *)(Kc + ra + 4 * f) : f4{0, 0, 0, 0};
 #pragma unroll
-        for (int f = 0; f < NF; ++f) kr[1][f] = ok[1] ? *(const f4 *)(kb + 4 * f) : f4{0, 0, 0, 0};
+        for (int f = 0; f < NF; ++f) kr[b1][f] = all || ok[b1] ? *(const f4 *)(Kc + rb + 4 * f) : f4{0, 0, 0, 0};
 #pragma unroll
-        for (int f = 0; f < NF; ++f) vr[0][f] = ok[0] ? *(const f4 *)(va + 4 * f) : f4{0, 0, 0, 0};
+        for (int f = 0; f < NF; ++f) vr[b0][f] = all || ok[b0] ? *(const f4 *)(Vc + ra + 4 * f) : f4{0, 0, 0, 0};
 #pragma unroll
-        for (int f = 0; f < NF; ++f) vr[1][f] = ok[1] ? *(const f4 *)(vb + 4 * f) : f4{0, 0, 0, 0};
+        for (int f = 0; f < NF; ++f) vr[b1][f] = all || ok[b1] ? *(const f4 *)(Vc + rb + 4 * f) : f4{0, 0, 0, 0};
     };
-    if (iters) issue(0);
-
     f4 q[GQA][NF];
+    if (!ROPE) {                         // before the K/V rows: the first score needs q
+#pragma unroll
+        for (int h = 0; h < GQA; ++h)
+#pragma unroll
+            for (int f = 0; f < NF; ++f) q[h][f] = *(const f4 *)(Q + (size_t)(qh0 + h) * D + c * 4 * NF + 4 * f);
+    }
+    if (iters) issue(0, 0, sl[0], sl[1]);
+
     uint32_t new_slot = 0xFFFFFFFFu;
     if (ROPE) {
         new_slot = ra.step[1];
@@ -360,11 +387,6 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
         for (int h = 0; h < GQA; ++h)
 #pragma unroll
             for (int f = 0; f < NF; ++f) q[h][f] = *(const f4 *)&sh_q[h][c * 4 * NF + 4 * f];
-    } else {
-#pragma unroll
-        for (int h = 0; h < GQA; ++h)
-#pragma unroll
-            for (int f = 0; f < NF; ++f) q[h][f] = *(const f4 *)(Q + (size_t)(qh0 + h) * D + c * 4 * NF + 4 * f);
     }
 
     float M[GQA], L[GQA];
@@ -404,19 +426,53 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
             const float p = ok[b] ? expf(sc - Mn) : 0.0f;
             const float psum = rows4_sum(p);
 #pragma unroll
-            for (int f = 0; f < NF; ++f) acc[h][f] = acc[h][f] * rs + p * vr[b][f];
+            for (int f = 0; f < NF; ++f)
+                acc[h][f] = acc[h][f] * rs + p * (NSET == 1 || ok[b] ? vr[b][f] : f4{0, 0, 0, 0});
             L[h] = L[h] * rs + psum;
             M[h] = Mn;
         }
     };
+    // Pair pr = chunks 2 pr, 2 pr + 1 goes to set pr % NSET; once reduced,
+    // the set takes pair pr + NSET.  One straight-line body per pair count
+    // (the count is uniform over the workgroup): no branch between a load
+    // and its use, so each wait leaves the younger set in flight.  A chunk
+    // past `iters` in the last pair is masked by ok[].
+    if constexpr (NSET == 2) {
+        auto run = [&](auto np_) {
+            constexpr int NP = decltype(np_)::value;
+            if constexpr (NP > 1) issue(1, 2, sl[2 % NSL], sl[3 % NSL]);
+#pragma unroll
+            for (int pr = 0; pr < NP; ++pr) {
+                const int set = pr % 2;
+                reduce(2 * set, sl[(2 * pr) % NSL]);
+                reduce(2 * set + 1, sl[(2 * pr + 1) % NSL]);
+                if (pr + 2 < NP) issue(set, 2 * (pr + 2), sl[(2 * pr + 4) % NSL], sl[(2 * pr + 5) % NSL]);
+            }
+        };
+        const uint32_t np = (iters + 1) / 2;
+        if constexpr (kMaxChunks == 4) {
+            if (np <= 1) run(std::integral_constant<int, 1>{});
+            else run(std::integral_constant<int, 2>{});
+        } else {
+            static_assert(kMaxChunks == 8, "one body per pair count");
+            switch (np) {
+            case 1: run(std::integral_constant<int, 1>{}); break;
+            case 2: run(std::integral_constant<int, 2>{}); break;
+            case 3: run(std::integral_constant<int, 3>{}); break;
+            default: run(std::integral_constant<int, 4>{}); break;
+            }
+        }
+    } else {
+        uint32_t pa = sl[0], pb = sl[1];
 #pragma unroll 1
-    for (uint32_t t = 0; t < iters; t += 2) {
-        if (t > 0) issue(t);
-        const uint32_t na = slot_at(t + 2), nb = slot_at(t + 3);
-        reduce(0, pa);
-        if (t + 1 < iters) reduce(1, pb);
-        pa = na;
-        pb = nb;
+        for (uint32_t t = 0; t < iters; t += 2) {
+            if (t > 0) issue(0, t, pa, pb);
+            const uint32_t na = slot_at(t + 2), nb = slot_at(t + 3);
+            reduce(0, pa);
+            if (t + 1 < iters) reduce(1, pb);
+            pa = na;
+            pb = nb;
+        }
     }
     // rows of the wave hold different entries of the same columns
 #pragma unroll
