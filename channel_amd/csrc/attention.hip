@@ -683,9 +683,14 @@ __global__ __launch_bounds__(256) void k_prefill_attn(const float *__restrict__ 
 //    O^T = V^T P^T once the chunk's keys are permuted (positions 8g .. 8g+7
 //    hold keys 4g..4g+3 and 16+4g..16+4g+3), so probabilities stay in
 //    registers;
-//  * K (row-major) and V (transposed, permuted) chunks are staged in LDS as
-//    bf16 high/low planes, rows padded against bank conflicts; the next
-//    chunk's rows load into registers while the current one is multiplied.
+//  * a pre-pass (k_prefill_frags) splits the K and V rows of the keys into
+//    bf16 high/low parts once per layer and stores them in the order the
+//    MFMA operands are read: per 32-key chunk and KV head, 64 KB = K hi, K
+//    lo, V^T hi, V^T lo, each 16 one-KB fragments in which lane l's 16 bytes
+//    lie at 16 l.  The attention copies a chunk into LDS by DMA
+//    (global_load_lds: no registers, no conversion) while the previous chunk
+//    is multiplied, and every fragment read is one contiguous KB, free of
+//    bank conflicts.
 typedef __bf16 pbf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 pbf16x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t pu32x4 __attribute__((ext_vector_type(4)));
@@ -712,21 +717,88 @@ __device__ __forceinline__ void put_hilo(V &h, V &l, int i, float a, float b) {
 }
 
 constexpr int kPaNK = 32;                 // keys per chunk
-constexpr int kPaKRow = 256 * 2 + 16;     // bytes per staged K row (bf16, padded)
-constexpr int kPaVRow = kPaNK * 2 + 16;   // bytes per staged V^T row (bf16, padded)
+constexpr int kPaFrag = 1024;             // one MFMA operand fragment: 64 lanes x 16 B
+constexpr int kPaPlane = 16 * kPaFrag;    // one plane of a chunk: 16 fragments
+constexpr int kPaChunkBytes = 4 * kPaPlane;   // K hi, K lo, V^T hi, V^T lo
 
+// Plane fragments of a chunk.  K planes, fragment f = 8 tt + j: keys
+// 16 tt + (lane & 15), dims 32 j + 8 (lane >> 4) .. +7.  V^T planes,
+// fragment dt: dims 16 dt + (lane & 15), chunk positions 8 (lane >> 4) ..
+// +7, where position 8 q + i holds key 4 q + i (i < 4) or 16 + 4 q + i - 4
+// (the key order of the S^T accumulator layout).
+__device__ __forceinline__ int vt_key(int pos) {
+    const int q = pos >> 3, i = pos & 7;
+    return i < 4 ? 4 * q + i : 16 + 4 * q + i - 4;
+}
+
+size_t prefill_frag_bytes(uint32_t num_kv_heads, uint32_t n_keys) {
+    return (size_t)num_kv_heads * ((n_keys + kPaNK - 1) / kPaNK) * kPaChunkBytes;
+}
+
+// Pre-pass: grid (chunks c_lo .. c_lo + gridDim.x - 1, KV heads, 2): z = 0
+// writes the chunk's K planes, z = 1 its V^T planes; chunk blockIdx.x of KV
+// head kvh goes to F + (kvh * gridDim.x + blockIdx.x) * kPaChunkBytes.  Keys
+// at or past n_keys are zero.
+__global__ __launch_bounds__(256) void k_prefill_frags(const float *__restrict__ Kc, const float *__restrict__ Vc,
+                                                       const uint32_t *__restrict__ slots, uint32_t n_keys,
+                                                       uint32_t c_lo, uint32_t kv_dim, unsigned char *__restrict__ F) {
+    __shared__ f4 rows[kPaNK][64];                         // the chunk's K or V rows, 256 floats each
+    const int tid = threadIdx.x;
+    const uint32_t c = c_lo + blockIdx.x, kvh = blockIdx.y;
+    const bool is_v = blockIdx.z != 0;
+    {
+        const int key = tid >> 3, part = tid & 7;           // 8 threads per row
+        const uint32_t kp = c * kPaNK + key;
+        const bool ok = kp < n_keys;
+        const uint32_t slot = ok ? slots[kp] : 0u;
+        const f4 *src = (const f4 *)((is_v ? Vc : Kc) + (size_t)slot * kv_dim + (size_t)kvh * 256);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int idx = part + 8 * i;
+            rows[key][idx] = ok ? src[idx] : f4{0, 0, 0, 0};
+        }
+    }
+    __syncthreads();
+    unsigned char *Fc = F + ((size_t)kvh * gridDim.x + blockIdx.x) * kPaChunkBytes + (is_v ? 2 * kPaPlane : 0);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int item = tid + 256 * u, f = item >> 6, l = item & 63;   // fragment f, lane l
+        pu32x4 h, lo;
+        if (!is_v) {
+            const int key = 16 * (f >> 3) + (l & 15), d4 = 8 * (f & 7) + 2 * (l >> 4);
+            const f4 x = rows[key][d4], y = rows[key][d4 + 1];
+            put_hilo(h, lo, 0, x.x, x.y);
+            put_hilo(h, lo, 1, x.z, x.w);
+            put_hilo(h, lo, 2, y.x, y.y);
+            put_hilo(h, lo, 3, y.z, y.w);
+        } else {
+            const int dim = 16 * f + (l & 15), g = l >> 4;
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = ((const float *)rows[vt_key(8 * g + i)])[dim];
+            put_hilo(h, lo, 0, v[0], v[1]);
+            put_hilo(h, lo, 1, v[2], v[3]);
+            put_hilo(h, lo, 2, v[4], v[5]);
+            put_hilo(h, lo, 3, v[6], v[7]);
+        }
+        *(pu32x4 *)(Fc + item * 16) = h;
+        *(pu32x4 *)(Fc + kPaPlane + item * 16) = lo;
+    }
+}
+
+// F: the pre-pass output for chunks c_lo .. c_lo + nfch - 1.
 template <int GQA>
-__global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict__ Q, const float *__restrict__ Kc,
-                                                         const float *__restrict__ Vc,
-                                                         const uint32_t *__restrict__ slots, uint32_t num_prev,
-                                                         uint32_t n_tok, uint32_t num_q_heads, uint32_t kv_dim,
-                                                         float scale, uint32_t window, float *__restrict__ out,
-                                                         __bf16 *__restrict__ outb, float *__restrict__ ws) {
+__global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict__ Q,
+                                                         const unsigned char *__restrict__ F, uint32_t c_lo,
+                                                         uint32_t nfch, uint32_t num_prev, uint32_t n_tok,
+                                                         uint32_t num_q_heads, float scale, uint32_t window,
+                                                         float *__restrict__ out, __bf16 *__restrict__ outb,
+                                                         float *__restrict__ ws) {
     constexpr int D = 256, NK = kPaNK, TQ = 64 / GQA;
-    __shared__ __attribute__((aligned(16))) unsigned char kh_s[NK * kPaKRow], kl_s[NK * kPaKRow];
-    __shared__ __attribute__((aligned(16))) unsigned char vh_s[D * kPaVRow], vl_s[D * kPaVRow];
+    __shared__ __attribute__((aligned(16))) unsigned char ring[2][kPaChunkBytes];   // two chunks in flight
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, c = lane & 15;
     const uint32_t kvh = blockIdx.y;
     // this lane's query: column c of the wave's 16 rows
@@ -739,13 +811,13 @@ __global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict
     const uint32_t t_first = blockIdx.x * TQ, t_last = min(t_first + TQ - 1, n_tok - 1);
     const uint32_t S_first = num_prev + t_first + 1, S_end = num_prev + t_last + 1;
     const uint32_t k_first = (window > 0 && S_first > window) ? S_first - window : 0;
-    // key split (gridDim.z parts): part z walks its share of the 32-key
-    // chunks [k_first, S_end); the parts' partial states meet in
+    // key split (gridDim.z parts): part z walks its share of the whole
+    // 32-key chunks over [k_first, S_end); the parts' partial states meet in
     // k_prefill_attn_merge
     const uint32_t nparts = gridDim.z, part = blockIdx.z;
-    const uint32_t nch = (S_end - k_first + NK - 1) / NK, per = (nch + nparts - 1) / nparts;
-    const uint32_t k_begin = min(S_end, k_first + part * per * NK);
-    const uint32_t k_stop = min(S_end, k_first + (part + 1) * per * NK);
+    const uint32_t cf = k_first / NK, ce = (S_end + NK - 1) / NK;
+    const uint32_t per = (ce - cf + nparts - 1) / nparts;
+    const uint32_t c_begin = min(ce, cf + part * per), c_stop = min(ce, c_begin + per);
 
     // Q^T operand: lane holds query c, dims 32 j + 8 g .. +8, as hi / lo bf16
     pbf16x8 qh[8], ql[8];
@@ -764,75 +836,15 @@ __global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict
         }
     }
 
-    // staging assignment: K rows: key tid >> 3, dims (tid & 7) * 32 .. +32;
-    // V: dim tid, all 32 keys (a V^T row; consecutive lanes read consecutive
-    // dims of one key row and write consecutive padded V^T rows)
-    const int sk_key = tid >> 3, sk_d0 = (tid & 7) * 32;
-    // The next chunk's rows load into registers while this chunk is
-    // multiplied.
-    struct Rows {
-        f4 k[8];
-        float v[kPaNK];
-        uint32_t nvalid;                                           // keys of the chunk inside the list
-    };
-    // The chunk's 32 slot indices arrive in one vector load (lane j holds
-    // key j's slot; keys past the list repeat its last slot); rows then take
-    // theirs by shuffle (K, per lane) or readlane (V, uniform).  Every row
-    // load is unconditional, so they issue back to back and their waits fall
-    // where the rows are staged; keys past the list are zeroed there.
-    auto gload = [&](uint32_t c0, Rows &r) {
-        const uint32_t pj = min(c0 + (lane & (kPaNK - 1)), S_end - 1);
-        const uint32_t slj = slots[pj];
-        r.nvalid = min((uint32_t)kPaNK, S_end - c0);
-        const uint32_t ks = (uint32_t)__shfl((int)slj, sk_key, 64);
-        const float *kr = Kc + (size_t)ks * kv_dim + kvh * D + sk_d0;
+    // chunk cc into ring stage st: wave w copies fragments 16 w .. 16 w + 15
+    const unsigned char *Fk = F + (size_t)kvh * nfch * kPaChunkBytes + lane * 16;
+    auto issue = [&](uint32_t cc, int st) {
+        const unsigned char *src = Fk + (size_t)(cc - c_lo) * kPaChunkBytes;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) r.k[i] = *(const f4 *)(kr + 4 * i);
-#pragma unroll
-        for (int k = 0; k < kPaNK; ++k) {
-            const uint32_t vs = (uint32_t)__builtin_amdgcn_readlane((int)slj, k);
-            r.v[k] = Vc[(size_t)vs * kv_dim + kvh * D + tid];
+        for (int i = 0; i < 16; ++i) {
+            const int fr = wave * 16 + i;
+            __builtin_amdgcn_global_load_lds(src + fr * kPaFrag, (lds_t *)(ring[st] + fr * kPaFrag), 16, 0, 0);
         }
-    };
-    auto stage = [&](const Rows &r) {
-        f4 kreg[8];
-        float vreg[kPaNK];
-        const bool kok = (uint32_t)sk_key < r.nvalid;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) kreg[i] = kok ? r.k[i] : f4{0, 0, 0, 0};
-#pragma unroll
-        for (int k = 0; k < kPaNK; ++k) vreg[k] = (uint32_t)k < r.nvalid ? r.v[k] : 0.0f;
-        unsigned char *kh = kh_s + sk_key * kPaKRow + sk_d0 * 2, *kl = kl_s + sk_key * kPaKRow + sk_d0 * 2;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            pu32x4 h, l;
-            put_hilo(h, l, 0, kreg[2 * i].x, kreg[2 * i].y);
-            put_hilo(h, l, 1, kreg[2 * i].z, kreg[2 * i].w);
-            put_hilo(h, l, 2, kreg[2 * i + 1].x, kreg[2 * i + 1].y);
-            put_hilo(h, l, 3, kreg[2 * i + 1].z, kreg[2 * i + 1].w);
-            *(pu32x4 *)(kh + 16 * i) = h;
-            *(pu32x4 *)(kl + 16 * i) = l;
-        }
-        // V^T row `tid`: position 8 q + j holds key 4 q + j (j < 4) or
-        // 16 + 4 q + j - 4 (j >= 4)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            pu32x4 h, l;
-            put_hilo(h, l, 0, vreg[4 * q], vreg[4 * q + 1]);
-            put_hilo(h, l, 1, vreg[4 * q + 2], vreg[4 * q + 3]);
-            put_hilo(h, l, 2, vreg[16 + 4 * q], vreg[16 + 4 * q + 1]);
-            put_hilo(h, l, 3, vreg[16 + 4 * q + 2], vreg[16 + 4 * q + 3]);
-            const int off = tid * kPaVRow + 16 * q;
-            *(pu32x4 *)(vh_s + off) = h;
-            *(pu32x4 *)(vl_s + off) = l;
-        }
-    };
-    // Workgroup barrier that orders LDS only: prefetched global loads stay in
-    // flight across it (the compiler waits for them where they are used).
-    auto lds_barrier = [&]() {
-        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        __asm__ volatile("" ::: "memory");
     };
 
     f4 o[16];
@@ -840,26 +852,46 @@ __global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict
     for (int i = 0; i < 16; ++i) o[i] = f4{0, 0, 0, 0};
     float m = -INFINITY, l = 0.0f;
 
-    Rows rows;
-    if (k_begin < k_stop) gload(k_begin, rows);
-    for (uint32_t c0 = k_begin; c0 < k_stop; c0 += NK) {
-        lds_barrier();                                             // previous chunk's reads done
-        stage(rows);
-        lds_barrier();
-        if (c0 + NK < k_stop) gload(c0 + NK, rows);
+    const uint32_t sm0 = lds_addr(ring[0]) + lane * 16;
+    if (c_begin < c_stop) issue(c_begin, 0);
+    for (uint32_t cc = c_begin; cc < c_stop; ++cc) {
+        const int st = (cc - c_begin) & 1;
+        wait_vm_lgkm0<0>();                                        // this wave's share of chunk cc landed
+        bare_barrier();                                            // ... every wave's; chunk cc-1's reads done
+        if (cc + 1 < c_stop) issue(cc + 1, st ^ 1);
+        __asm__ volatile("" ::: "memory");
+        const uint32_t base = sm0 + st * kPaChunkBytes;
+        const uint32_t c0 = cc * NK;
 
-        // S^T tile tt: keys 16 tt + 4 g + i, query c
+        // S^T tile tt: keys 16 tt + 4 g + i, query c.  Dims slice j's four
+        // fragments (K hi / lo of both tiles) load while slice j-1 multiplies.
         f4 sacc[2] = {f4{0, 0, 0, 0}, f4{0, 0, 0, 0}};
+        pbf16x8 kf[2][4];
+        auto kread = [&](int j, pbf16x8 (&d)[4]) {
+            d[0] = lds_read<pbf16x8>(base + (0 * 8 + j) * kPaFrag);
+            d[1] = lds_read<pbf16x8>(base + kPaPlane + (0 * 8 + j) * kPaFrag);
+            d[2] = lds_read<pbf16x8>(base + (1 * 8 + j) * kPaFrag);
+            d[3] = lds_read<pbf16x8>(base + kPaPlane + (1 * 8 + j) * kPaFrag);
+        };
+        kread(0, kf[0]);
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int off = (16 * tt + c) * kPaKRow + (32 * j + 8 * g) * 2;
-                const pbf16x8 ah = *(const pbf16x8 *)(kh_s + off), al = *(const pbf16x8 *)(kl_s + off);
-                sacc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, qh[j], sacc[tt], 0, 0, 0);
-                sacc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, ql[j], sacc[tt], 0, 0, 0);
-                sacc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, qh[j], sacc[tt], 0, 0, 0);
+        for (int j = 0; j < 8; ++j) {
+            pbf16x8 (&cur)[4] = kf[j & 1];
+            if (j < 7) {
+                kread(j + 1, kf[(j + 1) & 1]);
+                lds_wait_n<4>();                                   // slice j landed (slice j+1 may fly)
+            } else {
+                lds_wait();
             }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) lds_pin(cur[k]);
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                sacc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur[2 * tt], qh[j], sacc[tt], 0, 0, 0);
+                sacc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur[2 * tt], ql[j], sacc[tt], 0, 0, 0);
+                sacc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur[2 * tt + 1], qh[j], sacc[tt], 0, 0, 0);
+            }
+        }
         // online softmax for query c over this chunk (lane groups g hold 8 keys each)
         float sv[8];
         float cmax = -INFINITY;
@@ -891,15 +923,29 @@ __global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict
 #pragma unroll
         for (int i = 0; i < 4; ++i) put_hilo(ph, pl, i, pv[2 * i], pv[2 * i + 1]);
         const pbf16x8 bh = __builtin_bit_cast(pbf16x8, ph), bl = __builtin_bit_cast(pbf16x8, pl);
-        // O^T tile dt: dims 16 dt + 4 g + i, query c
+        // O^T tile dt: dims 16 dt + 4 g + i, query c; tile dt+1's V^T
+        // fragments load while tile dt multiplies
+        pbf16x8 vf[2][2];
+        auto vread = [&](int dt, pbf16x8 (&d)[2]) {
+            d[0] = lds_read<pbf16x8>(base + 2 * kPaPlane + dt * kPaFrag);
+            d[1] = lds_read<pbf16x8>(base + 3 * kPaPlane + dt * kPaFrag);
+        };
+        vread(0, vf[0]);
 #pragma unroll
         for (int dt = 0; dt < 16; ++dt) {
+            pbf16x8 (&cur)[2] = vf[dt & 1];
+            if (dt < 15) {
+                vread(dt + 1, vf[(dt + 1) & 1]);
+                lds_wait_n<2>();
+            } else {
+                lds_wait();
+            }
+            lds_pin(cur[0]);
+            lds_pin(cur[1]);
             o[dt] *= alpha;
-            const int off = (16 * dt + c) * kPaVRow + 16 * g;
-            const pbf16x8 ah = *(const pbf16x8 *)(vh_s + off), al = *(const pbf16x8 *)(vl_s + off);
-            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, o[dt], 0, 0, 0);
-            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, o[dt], 0, 0, 0);
-            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, o[dt], 0, 0, 0);
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur[0], bh, o[dt], 0, 0, 0);
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur[0], bl, o[dt], 0, 0, 0);
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur[1], bh, o[dt], 0, 0, 0);
         }
     }
     if (tq >= n_tok) return;
@@ -1012,8 +1058,16 @@ int launch_rope_decode_attn(chn_ctx *ctx, const float *q_in, const float *k_in, 
 
 int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const float *vc, const uint32_t *slots,
                         uint32_t n_tok, uint32_t num_prev, uint32_t num_q_heads, uint32_t head_dim, uint32_t kv_dim,
-                        uint32_t gqa, float scale, uint32_t window, float *out, __bf16 *outb, float *ws) {
+                        uint32_t gqa, float scale, uint32_t window, float *out, __bf16 *outb, float *ws,
+                        unsigned char *frag, size_t frag_bytes) {
     if (head_dim == 256 && (gqa == 1 || gqa == 2 || gqa == 4 || gqa == 8)) {
+        // the keys' operand fragments, chunks c_lo .. c_hi - 1 (from the
+        // first token's window start to the last key)
+        const uint32_t num_kv = num_q_heads / gqa, n_keys = num_prev + n_tok;
+        const uint32_t k_lo = (window > 0 && num_prev + 1 > window) ? num_prev + 1 - window : 0;
+        const uint32_t c_lo = k_lo / kPaNK, c_hi = (n_keys + kPaNK - 1) / kPaNK, nfch = c_hi - c_lo;
+        if (!frag || frag_bytes < (size_t)num_kv * nfch * kPaChunkBytes) return CHN_E_UNSUPPORTED;
+        k_prefill_frags<<<dim3(nfch, num_kv, 2), 256, 0, st>>>(kc, vc, slots, n_keys, c_lo, kv_dim, frag);
         const uint32_t tq = 64 / gqa;
         const uint32_t tiles = (n_tok + tq - 1) / tq;
         // Causal tiles differ in length (the last one walks every key): while
@@ -1027,8 +1081,8 @@ int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const f
         nparts = nparts < 1 ? 1 : (nparts > kPaParts ? kPaParts : nparts);
         const dim3 mgrid(tiles, num_q_heads / gqa, nparts);
 #define CHN_PATTN_MF(G) \
-    k_prefill_attn_mf<G><<<mgrid, 256, 0, st>>>(q, kc, vc, slots, num_prev, n_tok, num_q_heads, kv_dim, scale, window, \
-                                                out, outb, ws)
+    k_prefill_attn_mf<G><<<mgrid, 256, 0, st>>>(q, frag, c_lo, nfch, num_prev, n_tok, num_q_heads, scale, window, out, \
+                                                outb, ws)
         switch (gqa) {
         case 1: CHN_PATTN_MF(1); break;
         case 2: CHN_PATTN_MF(2); break;
@@ -1348,10 +1402,13 @@ extern "C" int chn_batch_causal_attn(chn_ctx *ctx, const float *q, const float *
     CHN_REQUIRE(ctx, aligned(q, 16) && aligned(k_cache, 16) && aligned(v_cache, 16) && aligned(out, 16),
                 "q, caches and out must be 16-byte aligned");
     if (!n_tok || !num_q_heads) return CHN_OK;
-    int rc = ensure_workspace(ctx, prefill_attn_ws_bytes(n_tok, num_q_heads, head_dim));
+    const size_t pws = prefill_attn_ws_bytes(n_tok, num_q_heads, head_dim);
+    const size_t fb = prefill_frag_bytes(num_q_heads / gqa_ratio, num_prev_slots + n_tok);
+    int rc = ensure_workspace(ctx, pws + fb);
     if (rc) return rc;
     rc = launch_prefill_attn(ctx->stream, q, k_cache, v_cache, slots, n_tok, num_prev_slots, num_q_heads, head_dim,
-                             kv_dim, gqa_ratio, scale, window, out, nullptr, (float *)ctx->ws);
+                             kv_dim, gqa_ratio, scale, window, out, nullptr, (float *)ctx->ws,
+                             (unsigned char *)ctx->ws + pws, fb);
     if (rc == CHN_E_UNSUPPORTED)
         return set_err(ctx, rc, "head_dim %u / gqa %u unsupported", head_dim, gqa_ratio);
     CHN_LAUNCHED(ctx, "k_prefill_attn");

@@ -207,12 +207,15 @@ int launch_rope_decode_attn(chn_ctx *ctx, const float *q_in, const float *k_in, 
                             const uint32_t *skip = nullptr);
 // out: [n_tok][num_q_heads * head_dim] fp32, or bf16 into outb when set.
 // ws (prefill_attn_ws_bytes, or NULL): lets short prompts split each query
-// tile's keys between two workgroups.
+// tile's keys between two workgroups.  frag (prefill_frag_bytes for the
+// KV heads and num_prev + n_tok keys): the keys' bf16 operand fragments,
+// required at head_dim 256.
 size_t prefill_attn_ws_bytes(uint32_t n_tok, uint32_t num_q_heads, uint32_t head_dim);
+size_t prefill_frag_bytes(uint32_t num_kv_heads, uint32_t n_keys);
 int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const float *vc, const uint32_t *slots,
                         uint32_t n_tok, uint32_t num_prev, uint32_t num_q_heads, uint32_t head_dim, uint32_t kv_dim,
-                        uint32_t gqa, float scale, uint32_t window, float *out, __bf16 *outb = nullptr,
-                        float *ws = nullptr);
+                        uint32_t gqa, float scale, uint32_t window, float *out, __bf16 *outb, float *ws,
+                        unsigned char *frag, size_t frag_bytes);
 size_t xbytes_bytes(uint32_t nb);
 int launch_gemv_q8(hipStream_t st, const uint32_t *W, const float *x, float *y, uint32_t M, uint32_t nb,
                    uint32_t *xp_ws);
@@ -452,6 +455,59 @@ __device__ __forceinline__ void emit_planes8s(const float (&v)[8], uint32_t *__r
 __device__ __forceinline__ void emit_planes8(const float (&v)[8], uint32_t *__restrict__ xp, uint32_t nb,
                                              uint32_t b, uint32_t w, bool ok) {
     emit_planes8s(v, xp, nb, 1, b, w, ok);
+}
+
+
+// ---------------------------------------------------------------------
+// DMA into LDS (global_load_lds) and the waits around it, shared by the
+// pipelined prefill kernels.
+// ---------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_t;
+
+// vmcnt(n) and lgkmcnt(0) (gfx9 encoding: vmcnt[3:0] and [15:14],
+// expcnt[6:4], lgkmcnt[11:8]).
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+    static_assert(N >= 0 && N < 64, "vmcnt immediate");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+
+
+// Workgroup barrier without a memory fence; the compiler may not move
+// memory accesses across it.
+__device__ __forceinline__ void bare_barrier() {
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+}
+
+// LDS reads of DMA-filled memory.  The compiler cannot tell ring slots
+// apart and would make every LDS read wait for the newest DMA group; reads
+// issued as asm are ordered by the explicit waits instead.  Their results
+// must stay in the registers the asm wrote until lds_wait() (a copy made
+// earlier would copy a value not yet loaded): lds_pin() after the wait keeps
+// every use below it.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+template <typename T, int OFF = 0>
+__device__ __forceinline__ T lds_read(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset");
+    T v;
+    if constexpr (sizeof(T) == 16) __asm__ volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    else if constexpr (sizeof(T) == 8) __asm__ volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    else __asm__ volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+    return v;
+}
+__device__ __forceinline__ void lds_wait() { __asm__ volatile("s_waitcnt lgkmcnt(0)"); }
+template <int N>                                           // all but the newest N LDS operations done
+__device__ __forceinline__ void lds_wait_n() {
+    static_assert(N >= 0 && N < 16, "lgkmcnt immediate");
+    __asm__ volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N));
+}
+template <typename T>
+__device__ __forceinline__ void lds_pin(T &v) {
+    __asm__ volatile("" : "+v"(v));
 }
 
 }  // namespace chn

@@ -277,8 +277,6 @@ __global__ __launch_bounds__(256, 2) void k_q4gemm(GemmArgs a) {
 // Tiles are dealt to the 8 XCDs in contiguous runs (workgroup i runs on XCD
 // i % 8), with the 128-token tiles of one feature block adjacent, so a
 // weight block's bytes are reused from one L2.
-typedef __attribute__((address_space(3))) void lds_t;
-
 template <int NMAT, int BN, bool REP, int S>
 struct PipeCfg {
     static constexpr int BT = 128, GK = 64, NTHR = 512;
@@ -304,51 +302,6 @@ struct PipeCfg {
     static_assert(NQ + NS <= 8, "one weight DMA instruction per wave");
 };
 
-// vmcnt(n) and lgkmcnt(0) (gfx9 encoding: vmcnt[3:0] and [15:14],
-// expcnt[6:4], lgkmcnt[11:8]).
-template <int N>
-__device__ __forceinline__ void wait_vm_lgkm0() {
-    static_assert(N >= 0 && N < 64, "vmcnt immediate");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
-}
-
-
-// Workgroup barrier without a memory fence; the compiler may not move
-// memory accesses across it.
-__device__ __forceinline__ void bare_barrier() {
-    __asm__ volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    __asm__ volatile("" ::: "memory");
-}
-
-// LDS reads of DMA-filled memory.  The compiler cannot tell ring slots
-// apart and would make every LDS read wait for the newest DMA group; reads
-// issued as asm are ordered by the explicit waits instead.  Their results
-// must stay in the registers the asm wrote until lds_wait() (a copy made
-// earlier would copy a value not yet loaded): lds_pin() after the wait keeps
-// every use below it.
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
-}
-template <typename T, int OFF = 0>
-__device__ __forceinline__ T lds_read(uint32_t addr) {
-    static_assert(OFF >= 0 && OFF < 65536, "ds offset");
-    T v;
-    if constexpr (sizeof(T) == 16) __asm__ volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
-    else if constexpr (sizeof(T) == 8) __asm__ volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
-    else __asm__ volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
-    return v;
-}
-__device__ __forceinline__ void lds_wait() { __asm__ volatile("s_waitcnt lgkmcnt(0)"); }
-template <int N>                                           // all but the newest N LDS operations done
-__device__ __forceinline__ void lds_wait_n() {
-    static_assert(N >= 0 && N < 16, "lgkmcnt immediate");
-    __asm__ volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N));
-}
-template <typename T>
-__device__ __forceinline__ void lds_pin(T &v) {
-    __asm__ volatile("" : "+v"(v));
-}
 
 template <int NMAT, int BN, bool REP, int S>
 __global__ __launch_bounds__(512) void k_q4gemm_p(GemmArgs a, uint32_t n_ct, uint32_t n_tt, uint32_t ksplit) {

@@ -51,6 +51,8 @@ struct chn_model {
     // prefill buffers
     uint32_t max_tok = 0;
     float *px, *pn, *pq, *pk, *pv, *pmlp, *pact, *pattn_ws;
+    unsigned char *pfrag;   // prefill attention: the keys' bf16 operand fragments
+    size_t pfrag_bytes;
     float2 *prope;       // prefill (cos, sin) per token: [2 kinds][T][rot / 2]
     __bf16 *pxb;
     uint32_t *pslots, *ptok;
@@ -202,6 +204,10 @@ static int alloc_runtime(chn_model *m) {
     M_ALLOC(m->pv, (size_t)T * kvd * 4);
     M_ALLOC(m->pmlp, (size_t)T * H * 4);
     M_ALLOC(m->pattn_ws, prefill_attn_ws_bytes(T, c.num_heads, md.D));
+    // every key of a prefill (at most the ring plus the batch) for the KV
+    // heads of the widest 256-dim layer
+    m->pfrag_bytes = prefill_frag_bytes(md.kvd / 256 ? md.kvd / 256 : 1, kSlotsMax + T);
+    M_ALLOC(m->pfrag, m->pfrag_bytes);
     M_ALLOC(m->prope, (size_t)2 * T * kRopePairs * sizeof(float2));
     M_ALLOC(m->pact, (size_t)T * I * 4);
     M_ALLOC(m->pxb, (size_t)T * (H > qd ? H : qd) * 2);   // bf16 operands of width H or qd; act goes to pact
@@ -848,7 +854,7 @@ extern "C" int chn_prefill(chn_model *m, const uint32_t *tokens, uint32_t n, con
         // unless the config sets another prefill window
         const uint32_t pwin = c.prefill_window ? c.prefill_window : 1024u;
         P_(launch_prefill_attn(s, m->pq, l.kc, l.vc, m->pslots, n, num_prev_slots, nq, D, kvd, gqa, 1.0f,
-                               l.full ? 0u : pwin, nullptr, xb, m->pattn_ws));
+                               l.full ? 0u : pwin, nullptr, xb, m->pattn_ws, m->pfrag, m->pfrag_bytes));
         P_(launch_q4gemm(ctx, 1, nullptr, l.Wo, nullptr, m->pmlp, n, H, qd, xb, true));
         P_(launch_rmsnorm_chain(s, m->px, m->pmlp, l.has_post_attn ? l.post_attn : nullptr, l.pre_ffn, xb, nullptr,
                                 H, n, eps, 1.0f, true, true));

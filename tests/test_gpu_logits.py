@@ -183,6 +183,8 @@ def test_batch_qkv_rope(ctx, nq, nkv, D, rot, keqv, n, off):
     (16, 2, 256, 512, 0, 1024),   # 12B 512-token prefill (matrix-core path)
     (8, 8, 256, 20, 40, 0),       # GQA 8: 8 tokens per tile
     (4, 1, 256, 45, 10, 30),      # GQA 1, window inside the list
+    (16, 2, 256, 100, 37, 50),    # window start and list end off the 32-key chunk grid
+    (16, 2, 256, 130, 300, 100),  # long earlier context, window of 100
 ])
 def test_batch_causal_attn(ctx, nq, gqa, D, n, prev, window):
     kvh = nq // gqa

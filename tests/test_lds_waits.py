@@ -1,7 +1,8 @@
-"""The pipelined prefill GEMM reads DMA-filled LDS with asm loads whose
-completion the compiler does not track; this compiles the kernel for gfx950
-and checks that no instruction touches a load's registers before the wait
-that retires it (a copy made earlier copies a value not yet loaded)."""
+"""The pipelined prefill GEMM and the prefill attention read DMA-filled LDS
+with asm loads whose completion the compiler does not track; this compiles
+the kernels for gfx950 and checks that no instruction touches a load's
+registers before the wait that retires it (a copy made earlier copies a
+value not yet loaded)."""
 import os
 import subprocess
 
@@ -23,6 +24,17 @@ def test_gemm_lds_waits(tmp_path):
     import lds_wait_check
     res = lds_wait_check.check_file(str(out), "k_q4gemm_p")
     assert res, "no pipelined GEMM kernel found in the assembly"
+    bad = {f: h for f, h in res.items() if h}
+    assert not bad, bad
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not installed")
+def test_prefill_attn_lds_waits(tmp_path):
+    import lds_wait_check
+    out = tmp_path / "attention.s"
+    _compile("attention.hip", out)
+    res = lds_wait_check.check_file(str(out), "k_prefill_attn_mf")
+    assert len(res) == 4, "expected the four GQA forms of the prefill attention"
     bad = {f: h for f, h in res.items() if h}
     assert not bad, bad
 
