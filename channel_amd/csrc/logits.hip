@@ -169,8 +169,8 @@ int launch_gemv_q8(hipStream_t st, const uint32_t *W, const float *x, float *y, 
 // descending key order = value descending, ties by ascending index).  Pass
 // 1: a workgroup takes 1024 logits; each wave sorts four 64-key groups with
 // shuffle bitonic networks and merges them to its top 64, and the four
-// waves' lists merge through LDS.  Pass 2: 16 waves fold the sorted tile
-// lists with the same 64 + 64 -> 64 merge, then a four-level tree in LDS.
+// waves' lists merge through LDS.  Pass 2 merges the sorted tile lists
+// (below).
 // ---------------------------------------------------------------------
 constexpr int kTopK = 64;
 constexpr int kTile = 1024;
@@ -248,35 +248,100 @@ __global__ __launch_bounds__(256) void k_topk_tile(const float *__restrict__ log
     }
 }
 
+// Pass 2.  With at least 64 lists, the 64th largest list head T bounds the
+// answer from below (the 64 heads at or above it are 64 distinct keys), so
+// only keys >= T matter, and only the 64 lists whose heads are at or above T
+// hold any: each contributes the prefix of its sorted list at or above T
+// (with fewer lists, T = 0 and every key is a candidate).  When the
+// candidates number at most kTopkFast (the usual case: a few keys per list)
+// they are gathered into LDS and each finds its rank by counting the larger
+// ones (keys are unique, so the ranks are exact and the gather order does
+// not matter); otherwise 16 waves fold every list with the 64 + 64 -> 64
+// merge and a four-level tree.  Heads are ranked the same way.
+constexpr int kTopkFast = 1024;
+
 __global__ __launch_bounds__(1024) void k_topk_merge(const uint64_t *__restrict__ cand, uint32_t nlist,
                                                      uint32_t *__restrict__ ids, float *__restrict__ vals) {
-    constexpr int U = 8;                 // lists loaded per wave per batch
+    constexpr int U = 8;                 // lists loaded per wave per batch (full fold)
+    constexpr int kMaxLists = 262144 / kTile;
     __shared__ uint64_t sh[16][kTopK];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    uint64_t acc = 0ull;                 // the empty list: below every real key
-    for (uint32_t l0 = wave; l0 < nlist; l0 += 16 * U) {
-        uint64_t c[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const uint32_t l = l0 + 16 * u;
-            c[u] = l < nlist ? cand[(size_t)l * kTopK + lane] : 0ull;
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) acc = wave_merge64_desc(acc, c[u], lane);
+    __shared__ uint64_t heads[kMaxLists];
+    __shared__ uint64_t cbuf[kTopkFast];
+    __shared__ uint64_t outk[kTopK];
+    __shared__ uint32_t sel[kTopK];
+    __shared__ uint32_t ncand;
+    __shared__ uint64_t thr;
+    const uint32_t tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const uint32_t nsel = nlist < (uint32_t)kTopK ? nlist : (uint32_t)kTopK;
+    if (tid == 0) {
+        ncand = 0;
+        thr = 0ull;
     }
-    sh[wave][lane] = acc;
+    if (tid < (uint32_t)kTopK) outk[tid] = 0ull;
+    if (tid < nlist) heads[tid] = cand[(size_t)tid * kTopK];
     __syncthreads();
+    if (tid < nlist) {
+        const uint64_t h = heads[tid];
+        uint32_t r = 0;
+        for (uint32_t j = 0; j < nlist; ++j) r += heads[j] > h ? 1u : 0u;
+        if (r < (uint32_t)kTopK) sel[r] = tid;                   // the list with the r-th largest head
+        if (nlist >= (uint32_t)kTopK && r == (uint32_t)kTopK - 1) thr = h;
+    }
+    __syncthreads();
+    const uint64_t T = thr;
+    // gather the prefixes at or above T: wave w takes selected lists w, w + 16, ...
 #pragma unroll
-    for (int s = 8; s >= 1; s >>= 1) {
-        if (wave < s) acc = wave_merge64_desc(sh[wave][lane], sh[wave + s][lane], lane);
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t i = wave + 16 * q;
+        if (i >= nsel) continue;                                    // uniform per wave
+        const uint64_t key = cand[(size_t)sel[i] * kTopK + lane];
+        const uint64_t above = __ballot(key >= T);                   // a prefix: the list is sorted
+        const uint32_t cnt = __popcll(above);
+        uint32_t off = 0;
+        if (lane == 0) off = atomicAdd(&ncand, cnt);
+        off = __shfl(off, 0, 64);
+        if ((uint32_t)lane < cnt && off + lane < (uint32_t)kTopkFast) cbuf[off + lane] = key;
+    }
+    __syncthreads();
+    const uint32_t n = ncand;
+    uint64_t res = 0ull;
+    if (n <= (uint32_t)kTopkFast) {
+        if (tid < n) {
+            const uint64_t k = cbuf[tid];
+            uint32_t r = 0;
+            for (uint32_t j = 0; j < n; ++j) r += cbuf[j] > k ? 1u : 0u;
+            if (r < (uint32_t)kTopK) outk[r] = k;               // padding keys (0) all land on one rank
+        }
         __syncthreads();
-        if (wave < s) sh[wave][lane] = acc;
+        if (wave == 0) res = outk[lane];
+    } else {
+        uint64_t acc = 0ull;             // the empty list: below every real key
+        for (uint32_t l0 = wave; l0 < nlist; l0 += 16 * U) {
+            uint64_t c[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint32_t l = l0 + 16 * u;
+                c[u] = l < nlist ? cand[(size_t)l * kTopK + lane] : 0ull;
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) acc = wave_merge64_desc(acc, c[u], lane);
+        }
+        sh[wave][lane] = acc;
         __syncthreads();
+#pragma unroll
+        for (int s = 8; s >= 1; s >>= 1) {
+            if (wave < s) acc = wave_merge64_desc(sh[wave][lane], sh[wave + s][lane], lane);
+            __syncthreads();
+            if (wave < s) sh[wave][lane] = acc;
+            __syncthreads();
+        }
+        res = acc;
     }
     if (wave == 0) {
-        if (acc) {
-            ids[lane] = 0xFFFFFFFFu - (uint32_t)acc;
-            vals[lane] = key_value(acc);
+        if (res) {
+            ids[lane] = 0xFFFFFFFFu - (uint32_t)res;
+            vals[lane] = key_value(res);
         } else {
             ids[lane] = 0;
             vals[lane] = -1e30f;

@@ -86,6 +86,30 @@ def test_topk64_all_ties(ctx, V):
     assert np.array_equal(ctx.download(vals, np.float32, 64), wv)
 
 
+@pytest.mark.parametrize("case", ["clustered", "ramp"])
+def test_topk64_concentrated(ctx, case):
+    """The merge takes its threshold from the tiles' maxima: 'clustered'
+    puts 40 of the top values in each of two tiles (a few lists contribute
+    long prefixes), 'ramp' puts every top value in the last tiles (more
+    candidates than the gathered path holds, so every list is folded)."""
+    V = 262144
+    rng = np.random.default_rng(11)
+    if case == "clustered":
+        lg = (rng.standard_normal(V) * 0.5).astype(np.float32)
+        lg[3 * 1024 + 7: 3 * 1024 + 47] = np.linspace(20.0, 21.0, 40, dtype=np.float32)
+        lg[200 * 1024 + 500: 200 * 1024 + 540] = np.linspace(20.5, 21.5, 40, dtype=np.float32)
+    else:
+        lg = np.linspace(-5.0, 5.0, V, dtype=np.float32)
+    d = ctx.upload(lg)
+    ids = ctx.alloc(256)
+    vals = ctx.alloc(256)
+    say(f"topk64 {case}")
+    ctx.call("chn_topk64", d, V, ids, vals)
+    wi, wv = oracle.topk64(lg)
+    assert np.array_equal(ctx.download(ids, np.uint32, 64), wi)
+    assert np.allclose(ctx.download(vals, np.float32, 64), wv, rtol=1e-6, atol=0)
+
+
 def test_topk64_small_vocab_padding(ctx):
     """Fewer than 64 logits: the tail is padded (ids 0, value -1e30)."""
     lg = np.array([3.0, -1.0, 7.0, 7.0, 0.5], np.float32)
