@@ -1236,10 +1236,105 @@ int launch_qkv_rope(hipStream_t st, const float *q_in, const float *k_in, const 
     return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
 }
 
+// The same with four heads per workgroup, one per wave, for D a multiple of
+// 256 and the angle table given: lane l holds dims 4 l + 256 j .. +3 (one
+// 16-byte access each), the norm reduces across the wave, and each wave
+// pairs (d, d + rot/2) through its own LDS row (a wave reads only what it
+// wrote, so no workgroup barrier is needed).
+template <int DV>
+__device__ __forceinline__ void norm_rope_head4(const float *__restrict__ in, const float *__restrict__ w,
+                                                float *__restrict__ out, uint32_t rot, float eps, float *buf,
+                                                const float2 *__restrict__ cs, int lane) {
+    constexpr int D = 256 * DV;
+    f4 v[DV], wv[DV];
+#pragma unroll
+    for (int j = 0; j < DV; ++j) {
+        v[j] = *(const f4 *)(in + 4 * lane + 256 * j);
+        wv[j] = *(const f4 *)(w + 4 * lane + 256 * j);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < DV; ++j) ss += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
+    ss = wave_sum64(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+#pragma unroll
+    for (int j = 0; j < DV; ++j) {
+        v[j] = (v[j] * inv) * wv[j];
+        *(f4 *)(buf + 4 * lane + 256 * j) = v[j];
+    }
+    __builtin_amdgcn_wave_barrier();
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const uint32_t half = rot / 2;
+#pragma unroll
+    for (int j = 0; j < DV; ++j) {
+        f4 o = v[j];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t d = 4 * lane + 256 * j + e;
+            if (d < rot) {
+                const uint32_t p = d < half ? d : d - half;          // the pair's index
+                const float2 t = cs[p];
+                const float v0 = buf[p], v1 = buf[p + half];
+                o[e] = d < half ? v0 * t.x - v1 * t.y : v0 * t.y + v1 * t.x;
+            }
+        }
+        *(f4 *)(out + 4 * lane + 256 * j) = o;
+    }
+}
+
+template <int DV>
+__global__ __launch_bounds__(256) void k_batch_qkv_rope4(const float *__restrict__ q_in, const float *__restrict__ k_in,
+                                                        const float *__restrict__ v_in, const float *__restrict__ qw,
+                                                        const float *__restrict__ kw, float *__restrict__ q_out,
+                                                        float *__restrict__ k_cache, float *__restrict__ v_cache,
+                                                        const uint32_t *__restrict__ slots, uint32_t slot_offset,
+                                                        uint32_t num_q, uint32_t num_kv, uint32_t rot, int k_eq_v,
+                                                        float eps, const float2 *__restrict__ tab) {
+    constexpr int D = 256 * DV;
+    __shared__ __attribute__((aligned(16))) float buf[4][D];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t head = blockIdx.x * 4 + wave, t = blockIdx.y;
+    if (head >= num_q + num_kv) return;                     // whole waves; no workgroup barrier follows
+    const uint32_t slot = slots[slot_offset + t];
+    const size_t q_dim = (size_t)num_q * D, kv_dim = (size_t)num_kv * D;
+    const float2 *cs = tab + (size_t)t * (rot / 2);
+    if (head < num_q) {
+        norm_rope_head4<DV>(q_in + t * q_dim + (size_t)head * D, qw, q_out + t * q_dim + (size_t)head * D, rot, eps,
+                            buf[wave], cs, lane);
+        return;
+    }
+    const uint32_t h = head - num_q;
+    const float *k = k_in + t * kv_dim + (size_t)h * D;
+    const float *v = k_eq_v ? k : v_in + t * kv_dim + (size_t)h * D;
+    norm_rope_head4<DV>(k, kw, k_cache + (size_t)slot * kv_dim + (size_t)h * D, rot, eps, buf[wave], cs, lane);
+    f4 vv[DV];
+#pragma unroll
+    for (int j = 0; j < DV; ++j) vv[j] = *(const f4 *)(v + 4 * lane + 256 * j);
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < DV; ++j)
+        ss += (vv[j].x * vv[j].x + vv[j].y * vv[j].y) + (vv[j].z * vv[j].z + vv[j].w * vv[j].w);
+    ss = wave_sum64(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+    float *vo = v_cache + (size_t)slot * kv_dim + (size_t)h * D;
+#pragma unroll
+    for (int j = 0; j < DV; ++j) *(f4 *)(vo + 4 * lane + 256 * j) = vv[j] * inv;
+}
+
 int launch_batch_qkv_rope(hipStream_t st, const float *q_in, const float *k_in, const float *v_in, const float *qw,
                           const float *kw, float *q_out, float *kc, float *vc, const uint32_t *slots,
                           uint32_t slot_offset, uint32_t start_clock, uint32_t n_tok, uint32_t num_q, uint32_t num_kv,
                           uint32_t D, uint32_t rot, int k_eq_v, float theta, float eps, const float2 *tab) {
+    if (tab && (D == 256 || D == 512)) {
+        dim3 grid4((num_q + num_kv + 3) / 4, n_tok);
+        if (D == 256)
+            k_batch_qkv_rope4<1><<<grid4, 256, 0, st>>>(q_in, k_in, v_in, qw, kw, q_out, kc, vc, slots, slot_offset,
+                                                        num_q, num_kv, rot, k_eq_v, eps, tab);
+        else
+            k_batch_qkv_rope4<2><<<grid4, 256, 0, st>>>(q_in, k_in, v_in, qw, kw, q_out, kc, vc, slots, slot_offset,
+                                                        num_q, num_kv, rot, k_eq_v, eps, tab);
+        return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
+    }
     dim3 grid(num_q + num_kv, n_tok);
     k_batch_qkv_rope<<<grid, 64, 0, st>>>(q_in, k_in, v_in, qw, kw, q_out, kc, vc, slots, slot_offset, start_clock,
                                           num_q, num_kv, D, rot, k_eq_v, theta, eps, tab);

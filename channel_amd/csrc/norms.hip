@@ -106,12 +106,88 @@ __global__ __launch_bounds__(256) void k_rmsnorm_chain(float *__restrict__ x, fl
     }
 }
 
+// The same chain with the row held in registers (dim <= 4096: four float4
+// per thread): every input is requested at once, so the row costs one
+// memory round trip instead of three, and each element is read once.
+// Thread i handles float4s i, i + 256, ... in that order, so every sum and
+// product is the loop form's.
+template <bool POST, bool ADD>
+__global__ __launch_bounds__(256) void k_rmsnorm_chain_r(float *__restrict__ x, float *__restrict__ r,
+                                                         const float *__restrict__ pw, const float *__restrict__ w,
+                                                         __bf16 *__restrict__ yb, float *__restrict__ y, uint32_t dim,
+                                                         float eps, float scalar, int zero_r) {
+    constexpr int NPT = 4;
+    __shared__ float sh[4];
+    const size_t off = (size_t)blockIdx.x * dim;
+    f4n *xr = (f4n *)(x + off);
+    f4n *rr = (f4n *)(r + off);
+    const f4n *pwr = (const f4n *)pw;
+    const f4n *wr = (const f4n *)w;
+    const uint32_t dv = dim / 4;
+    f4n xv[NPT], rv[NPT], pv[NPT], wv[NPT];
+#pragma unroll
+    for (int k = 0; k < NPT; ++k) {
+        const uint32_t i = threadIdx.x + 256 * k;
+        const bool ok = i < dv;
+        xv[k] = ok ? xr[i] : f4n{0, 0, 0, 0};
+        if (ADD) rv[k] = ok ? rr[i] : f4n{0, 0, 0, 0};
+        if (POST) pv[k] = ok ? pwr[i] : f4n{0, 0, 0, 0};
+        wv[k] = ok ? wr[i] : f4n{0, 0, 0, 0};
+    }
+    float inv_r = 1.0f;
+    if (POST) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NPT; ++k) {
+            const f4n v = rv[k];
+            if (threadIdx.x + 256 * k < dv) ss += ((v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w));
+        }
+        ss = block_sum_256(ss, sh);
+        inv_r = 1.0f / sqrtf(ss / (float)dim + eps);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NPT; ++k) {
+        const uint32_t i = threadIdx.x + 256 * k;
+        if (i >= dv) continue;
+        f4n v = xv[k];
+        if (ADD) {
+            f4n b = rv[k];
+            if (POST) b = (b * inv_r) * pv[k];
+            v = (v + b) * scalar;
+            xv[k] = v;
+            xr[i] = v;
+            if (zero_r) rr[i] = f4n{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        ss += ((v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w));
+    }
+    ss = block_sum_256(ss, sh);
+    const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+#pragma unroll
+    for (int k = 0; k < NPT; ++k) {
+        const uint32_t i = threadIdx.x + 256 * k;
+        if (i >= dv) continue;
+        const f4n o = (xv[k] * inv) * wv[k];
+        bf16x2 lo = {(__bf16)o.x, (__bf16)o.y}, hi = {(__bf16)o.z, (__bf16)o.w};
+        *(bf16x2 *)(yb + off + 4 * (size_t)i) = lo;
+        *(bf16x2 *)(yb + off + 4 * (size_t)i + 2) = hi;
+        if (y) *(f4n *)(y + off + 4 * (size_t)i) = o;
+    }
+}
+
 int launch_rmsnorm_chain(hipStream_t s, float *x, float *r, const float *post_w, const float *w, __bf16 *yb,
                          float *y, uint32_t dim, uint32_t rows, float eps, float scalar, bool add, bool zero_r) {
     const int z = zero_r ? 1 : 0;
-    if (!add) k_rmsnorm_chain<false, false><<<rows, 256, 0, s>>>(x, r, post_w, w, yb, y, dim, eps, scalar, z);
-    else if (post_w) k_rmsnorm_chain<true, true><<<rows, 256, 0, s>>>(x, r, post_w, w, yb, y, dim, eps, scalar, z);
-    else k_rmsnorm_chain<false, true><<<rows, 256, 0, s>>>(x, r, post_w, w, yb, y, dim, eps, scalar, z);
+    if (dim <= 4096) {
+        if (!add) k_rmsnorm_chain_r<false, false><<<rows, 256, 0, s>>>(x, r, post_w, w, yb, y, dim, eps, scalar, z);
+        else if (post_w)
+            k_rmsnorm_chain_r<true, true><<<rows, 256, 0, s>>>(x, r, post_w, w, yb, y, dim, eps, scalar, z);
+        else k_rmsnorm_chain_r<false, true><<<rows, 256, 0, s>>>(x, r, post_w, w, yb, y, dim, eps, scalar, z);
+    } else {
+        if (!add) k_rmsnorm_chain<false, false><<<rows, 256, 0, s>>>(x, r, post_w, w, yb, y, dim, eps, scalar, z);
+        else if (post_w) k_rmsnorm_chain<true, true><<<rows, 256, 0, s>>>(x, r, post_w, w, yb, y, dim, eps, scalar, z);
+        else k_rmsnorm_chain<false, true><<<rows, 256, 0, s>>>(x, r, post_w, w, yb, y, dim, eps, scalar, z);
+    }
     return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
 }
 
