@@ -70,6 +70,8 @@ PROTOTYPES = {
     "chn_batch_qkv_rope": (c_int, [c_void_p] + [c_void_p] * 9 + [c_u32] * 7 + [c_int, c_f32, c_f32]),
     "chn_batch_causal_attn": (c_int, [c_void_p] * 5 + [c_u32] * 6 + [c_f32, c_u32, c_void_p]),
     "chn_gemv_q8": (c_int, [c_void_p] * 4 + [c_u32, c_u32]),
+    "chn_q8_repack": (c_int, [c_void_p, c_void_p, c_u32, c_u32, c_void_p]),
+    "chn_gemv_q8r": (c_int, [c_void_p] * 4 + [c_u32, c_u32]),
     "chn_topk64": (c_int, [c_void_p, c_void_p, c_u32, c_void_p, c_void_p]),
     "chn_quantize_q4": (c_int, [c_void_p] * 3 + [c_u32, c_u32]),
     "chn_quantize_q8": (c_int, [c_void_p] * 3 + [c_u32, c_u32]),

@@ -154,6 +154,116 @@ __global__ __launch_bounds__(256) void k_q8mv(const uint32_t *__restrict__ W, co
     }
 }
 
+// Q8R: the Q8_0 blocks repacked for aligned streaming, codes first ([rows *
+// nb][32] int8, two 16-byte words per block, order kept), then the f32
+// scales ([rows * nb]); 36 bytes per block as before.
+__global__ __launch_bounds__(256) void k_repack_q8(const uint32_t *__restrict__ src, u32x4q *__restrict__ D,
+                                                   float *__restrict__ S, size_t nblk) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblk) return;
+    const uint32_t *p = src + i * 9;
+    D[2 * i] = u32x4q{p[1], p[2], p[3], p[4]};
+    D[2 * i + 1] = u32x4q{p[5], p[6], p[7], p[8]};
+    S[i] = __builtin_bit_cast(float, p[0]);
+}
+
+int launch_q8_repack(hipStream_t st, const uint32_t *W, uint32_t rows, uint32_t nb, void *dst) {
+    const size_t nblk = (size_t)rows * nb;
+    if (!nblk) return CHN_OK;
+    k_repack_q8<<<(unsigned)((nblk + 255) / 256), 256, 0, st>>>(W, (u32x4q *)dst,
+                                                               (float *)((unsigned char *)dst + nblk * 32), nblk);
+    return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
+}
+
+// The Q8 matvec over Q8R: lane l owns blocks l and l + 64 of each row (K <=
+// 4096) and reads them straight from the stream (two 16-byte codes words and
+// the scale), no LDS; RPW rows per group, the next group in flight while
+// one is reduced.  Per block and row the arithmetic, its order and the
+// reduction are k_q8mv's, so the two give identical results.
+template <int RPW>
+__global__ __launch_bounds__(256) void k_q8rmv(const u32x4q *__restrict__ D, const float *__restrict__ S,
+                                               const uint32_t *__restrict__ xp, float *__restrict__ y, uint32_t M,
+                                               uint32_t nb) {
+    constexpr int LV = RPW == 1 ? 0 : (RPW == 2 ? 1 : 2);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    uint32_t P[2][XB_WORDS];
+    float xs[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const uint32_t b = c * 64 + lane;
+        const bool ok = b < nb;
+#pragma unroll
+        for (int i = 0; i < XB_WORDS; ++i) P[c][i] = ok ? xp[(size_t)i * nb + b] : 0u;
+        xs[c] = ok ? ((const float *)(xp + (size_t)XB_WORDS * nb))[b] : 0.0f;
+    }
+    const uint32_t ngroups = (M + RPW - 1) / RPW;
+    const uint32_t gstride = gridDim.x * 4;
+    struct Grp {
+        u32x4q d[RPW][2][2];
+        float s[RPW][2];
+    };
+    auto load = [&](Grp &q, uint32_t g) {
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const uint32_t row = g * RPW + r;
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const uint32_t b = c * 64 + lane;
+                const bool ok = row < M && b < nb;
+                const size_t i = (size_t)(ok ? row : 0) * nb + (ok ? b : 0);
+                q.d[r][c][0] = ok ? __builtin_nontemporal_load(D + 2 * i) : u32x4q{0, 0, 0, 0};
+                q.d[r][c][1] = ok ? __builtin_nontemporal_load(D + 2 * i + 1) : u32x4q{0, 0, 0, 0};
+                q.s[r][c] = ok ? __builtin_nontemporal_load(S + i) : 0.0f;
+            }
+        }
+    };
+    uint32_t g = blockIdx.x * 4 + wave;
+    Grp nx;
+    if (g < ngroups) load(nx, g);
+    for (; g < ngroups; g += gstride) {
+        const Grp cur = nx;
+        if (g + gstride < ngroups) load(nx, g + gstride);
+        float acc[RPW];
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const uint32_t b = c * 64 + lane;
+            if (b < nb) {
+#pragma unroll
+                for (int r = 0; r < RPW; ++r) {
+                    int pl[XB_PLANES];
+#pragma unroll
+                    for (int q = 0; q < XB_PLANES; ++q) {
+                        int t = 0;
+#pragma unroll
+                        for (int w = 0; w < 8; ++w)
+                            t = __builtin_amdgcn_sdot4((int)cur.d[r][c][w >> 2][w & 3], (int)P[c][q * 8 + w], t, false);
+                        pl[q] = t;
+                    }
+                    const float T = fmaf((float)pl[2], 65536.0f, fmaf((float)pl[1], 256.0f, (float)pl[0]));
+                    acc[r] = fmaf(T, cur.s[r][c] * xs[c], acc[r]);
+                }
+            }
+        }
+        const float sum = wave_reduce_v<RPW>(acc, lane);
+        const int vi = lane >> (6 - LV);
+        if ((lane & ((64 >> LV) - 1)) == 0 && g * RPW + vi < M) y[g * RPW + vi] = sum;
+    }
+}
+
+int launch_gemv_q8r(hipStream_t st, const void *R, const float *x, float *y, uint32_t M, uint32_t nb,
+                    uint32_t *xp_ws) {
+    k_xbytes<<<(8 * nb + 255) / 256, 256, 0, st>>>(x, xp_ws, nb);
+    const uint32_t ngroups = (M + 3) / 4;
+    uint32_t grid = (ngroups + 3) / 4;
+    if (grid > 1024) grid = 1024;
+    const u32x4q *D = (const u32x4q *)R;
+    const float *S = (const float *)((const unsigned char *)R + (size_t)M * nb * 32);
+    k_q8rmv<4><<<grid, 256, 0, st>>>(D, S, xp_ws, y, M, nb);
+    return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
+}
+
 int launch_gemv_q8(hipStream_t st, const uint32_t *W, const float *x, float *y, uint32_t M, uint32_t nb,
                    uint32_t *xp_ws) {
     k_xbytes<<<(8 * nb + 255) / 256, 256, 0, st>>>(x, xp_ws, nb);
@@ -473,6 +583,28 @@ extern "C" int chn_gemv_q8(chn_ctx *ctx, const uint32_t *W, const float *x, floa
     if (rc) return rc;
     launch_gemv_q8(ctx->stream, W, x, y, M, K / 32, (uint32_t *)ctx->ws);
     CHN_LAUNCHED(ctx, "k_q8mv");
+    return CHN_OK;
+}
+
+extern "C" int chn_q8_repack(chn_ctx *ctx, const uint32_t *W, uint32_t rows, uint32_t K, void *dst) {
+    if (!ctx) return CHN_E_INVALID;
+    CHN_REQUIRE(ctx, W && dst, "NULL argument");
+    CHN_REQUIRE(ctx, K % 32 == 0, "K=%u must be a multiple of 32", K);
+    CHN_REQUIRE(ctx, aligned(dst, 16), "dst must be 16-byte aligned");
+    if (launch_q8_repack(ctx->stream, W, rows, K / 32, dst)) return hip_fail(ctx, hipGetLastError(), "k_repack_q8");
+    return CHN_OK;
+}
+
+extern "C" int chn_gemv_q8r(chn_ctx *ctx, const void *R, const float *x, float *y, uint32_t M, uint32_t K) {
+    if (!ctx) return CHN_E_INVALID;
+    CHN_REQUIRE(ctx, R && x && y, "NULL argument");
+    CHN_REQUIRE(ctx, K % 128 == 0 && K > 0 && K <= 4096, "K=%u: the Q8 matvec needs K %% 128 == 0, K <= 4096", K);
+    CHN_REQUIRE(ctx, aligned(R, 16) && aligned(x, 16), "R and x must be 16-byte aligned");
+    if (!M) return CHN_OK;
+    int rc = ensure_workspace(ctx, xbytes_bytes(K / 32));
+    if (rc) return rc;
+    launch_gemv_q8r(ctx->stream, R, x, y, M, K / 32, (uint32_t *)ctx->ws);
+    CHN_LAUNCHED(ctx, "k_q8rmv");
     return CHN_OK;
 }
 

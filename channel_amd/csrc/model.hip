@@ -33,7 +33,7 @@ struct chn_model {
         uint32_t D, nkv, qd, kvd, rot, gqa;
     };
     std::vector<Layer> L;
-    uint32_t *embed_q8 = nullptr;
+    uint32_t *embed_q8 = nullptr;      // tied embedding, Q8R (Q8_0 repacked for aligned streaming)
     uint16_t *embed_bf16 = nullptr;   // device copy of the tied embedding (input gather)
     float *final_norm = nullptr;
     // decode buffers
@@ -383,7 +383,7 @@ static int record_decode(chn_model *m, bool with_logits) {
                           xp, H, eps, last.scalar, true, nullptr,
                           gated(c.num_layers - 1) ? m->qflags + c.num_layers - 1 : nullptr));
     if (with_logits) {
-        R_(launch_gemv_q8(s, m->embed_q8, m->normed, m->logits, c.vocab_size, H / 32, m->mv_ws));
+        R_(launch_gemv_q8r(s, m->embed_q8, m->normed, m->logits, c.vocab_size, H / 32, m->mv_ws));
         R_(launch_topk64(s, m->logits, c.vocab_size, m->topk_ids, m->topk_vals, m->topk_ws));
     }
 #undef R_
@@ -439,7 +439,6 @@ static void free_model(chn_model *m) {
     delete m;
 }
 
-// bf16 (host) -> device quantized copy; `tmp` holds at least rows*cols bf16
 // bf16 (host) -> quantizeRowQ4_0 on the device into the reference layout
 // (staging `tq`), then repacked into the model's Q4R matrix.  `tmp` holds
 // at least rows*cols bf16, `tq` rows*cols/32 Q4 blocks.
@@ -452,6 +451,24 @@ static int ingest_q4r(chn_model *m, const uint16_t *src, uint32_t rows, uint32_t
     if (launch_q4_repack(m->ctx->stream, tq, rows, cols, *dst)) return hip_fail(m->ctx, hipGetLastError(), "repack");
     CHN_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
     return CHN_OK;
+}
+
+// The tied embedding for the logits: quantizeRowQ8_0 of the device bf16
+// copy into a staging buffer in the reference layout, then repacked into
+// m->embed_q8 (Q8R, chn_q8_repack's layout).
+static int quantize_embed_q8r(chn_model *m, uint32_t V, uint32_t H) {
+    const size_t nblk = (size_t)V * (H / 32);
+    uint32_t *tq = nullptr;
+    CHN_HIP(m->ctx, hipMalloc((void **)&tq, nblk * 36));
+    int rc = CHN_OK;
+    if (launch_quantize(m->ctx->stream, 1, m->embed_bf16, tq, nblk))
+        rc = hip_fail(m->ctx, hipGetLastError(), "quantize embedding");
+    else if (launch_q8_repack(m->ctx->stream, tq, V, H / 32, m->embed_q8))
+        rc = hip_fail(m->ctx, hipGetLastError(), "repack embedding");
+    const hipError_t e = hipStreamSynchronize(m->ctx->stream);
+    (void)hipFree(tq);
+    if (!rc && e != hipSuccess) rc = hip_fail(m->ctx, e, "quantize embedding");
+    return rc;
 }
 
 // bf16 norm weights -> fp32; missing norms -> 1.0 (createNormBuffer,
@@ -535,10 +552,7 @@ extern "C" int chn_model_create(chn_ctx *ctx, const chn_model_config *cfg, const
     C_(m_alloc(m, (size_t)cfg->vocab_size * H * 2, (void **)&m->embed_bf16));
     C_(chn_upload(ctx, m->embed_bf16, embed_bf16, (size_t)cfg->vocab_size * H * 2));
     C_(m_alloc(m, (size_t)cfg->vocab_size * (H / 32) * 36, (void **)&m->embed_q8));
-    if (launch_quantize(ctx->stream, 1, m->embed_bf16, m->embed_q8, (uint64_t)cfg->vocab_size * (H / 32))) {
-        rc = hip_fail(ctx, hipGetLastError(), "quantize embedding");
-        goto fail;
-    }
+    C_(quantize_embed_q8r(m, cfg->vocab_size, H));
     C_(ingest_norm(m, final_norm_bf16, H, &m->final_norm));
     C_(alloc_runtime(m));
     C_(build_graphs(m));
@@ -635,10 +649,7 @@ extern "C" int chn_model_create_synthetic(chn_ctx *ctx, const chn_model_config *
         (void)hipFree(tmpf);
         if (rc) goto fail;
         C_(m_alloc(m, (size_t)V * (H / 32) * 36, (void **)&m->embed_q8));
-        if (launch_quantize(ctx->stream, 1, m->embed_bf16, m->embed_q8, (uint64_t)V * (H / 32))) {
-            rc = hip_fail(ctx, hipGetLastError(), "quantize embedding");
-            goto fail;
-        }
+        C_(quantize_embed_q8r(m, V, H));
     }
     C_(fill_ones(m, H, &m->final_norm));
     C_(alloc_runtime(m));
@@ -867,7 +878,7 @@ extern "C" int chn_prefill(chn_model *m, const uint32_t *tokens, uint32_t n, con
         if ((i + 1) % 4 == 0 || i + 1 == c.num_layers) {
             if (i + 1 == c.num_layers && (logits_out || topk_ids)) {
                 CHN_HIP(ctx, hipMemcpyAsync(m->normed, m->pn + (size_t)(n - 1) * H, H * 4, hipMemcpyDeviceToDevice, s));
-                P_(launch_gemv_q8(s, m->embed_q8, m->normed, m->logits, c.vocab_size, H / 32, m->mv_ws));
+                P_(launch_gemv_q8r(s, m->embed_q8, m->normed, m->logits, c.vocab_size, H / 32, m->mv_ws));
                 P_(launch_topk64(s, m->logits, c.vocab_size, m->topk_ids, m->topk_vals, m->topk_ws));
             }
             CHN_HIP(ctx, hipStreamSynchronize(s));

@@ -298,6 +298,18 @@ int chn_batch_causal_attn(chn_ctx *ctx, const float *q, const float *k_cache, co
  * shaders/gemv_q8.wgsl. */
 int chn_gemv_q8(chn_ctx *ctx, const uint32_t *W, const float *x, float *y, uint32_t M, uint32_t K);
 
+/* Q8R: the Q8_0 blocks of W [rows x K] repacked into dst (rows * K / 32 * 36
+ * bytes, 16-byte aligned) for aligned streaming: the 32 codes of every
+ * block in order, then the f32 scales.  The model holds its tied embedding
+ * this way.  Counterpart of chn_q4_repack for the logits table; the
+ * reference keeps the Q8_0 layout (src/quant.zig:54-98). */
+int chn_q8_repack(chn_ctx *ctx, const uint32_t *W, uint32_t rows, uint32_t K, void *dst);
+
+/* chn_gemv_q8 over Q8R weights (chn_q8_repack): identical results to
+ * chn_gemv_q8 on the same weights.  gemv_q8 (shaders/gemv_q8.wgsl) as the
+ * model's logits run it. */
+int chn_gemv_q8r(chn_ctx *ctx, const void *R, const float *x, float *y, uint32_t M, uint32_t K);
+
 /* Global top-64 of 30*tanh(logit/30), sorted descending, ties by lower
  * index; ids/vals are device arrays of 64.  V <= 262144.  recordTopK
  * (src/gpu/kernels.zig:178-184) + shaders/topk_pass1.wgsl, topk_pass2.wgsl. */

@@ -39,6 +39,30 @@ def test_gemv_q8(ctx, M, K):
     assert np.max(np.abs(got[:r] - want[:r])) <= 1e-5 * scale
 
 
+@pytest.mark.parametrize("M,K", [(262144, 3840), (1001, 128), (7, 4096)])
+def test_gemv_q8r_matches_q8(ctx, M, K):
+    """The model's logits run on Q8R (the Q8_0 blocks repacked: codes, then
+    the f32 scales).  The repack keeps every byte, and the Q8R matvec gives
+    the reference-layout matvec's results bit for bit."""
+    nb = K // 32
+    W = synth_q8_dev(ctx, M, K, 300 + M % 89)
+    R = ctx.alloc(ca.q8_bytes(M, K))
+    ctx.call("chn_q8_repack", W, M, K, R)
+    x = synth_normal_dev(ctx, K, 301 + K)
+    y1, y2 = ctx.alloc(M * 4), ctx.alloc(M * 4)
+    say(f"gemv_q8r M={M} K={K}")
+    ctx.call("chn_gemv_q8", W, x, y1, M, K)
+    ctx.call("chn_gemv_q8r", R, x, y2, M, K)
+    assert np.array_equal(ctx.download(y1, np.uint32, M), ctx.download(y2, np.uint32, M))
+    Wh = ctx.download(W, np.uint32, M * nb * 9).reshape(M * nb, 9)
+    Rh = ctx.download(R, np.uint32, M * nb * 9)
+    assert np.array_equal(Rh[: M * nb * 8].reshape(M * nb, 8), Wh[:, 1:])
+    assert np.array_equal(Rh[M * nb * 8:], Wh[:, 0])
+    if M <= 4096:
+        want = oracle.gemv_q8(Wh.ravel(), f32_host(ctx, x, K), M, K)
+        assert rel_err(f32_host(ctx, y2, M), want) < TOL
+
+
 def test_gemv_q8_shapes_rejected(ctx):
     buf = ctx.alloc(1 << 16)
     for K in (96, 4224, 0):
