@@ -285,6 +285,20 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 // Transposed butterfly: V values per lane (V a power of two <= 64) summed
 // over the 64 lanes.  The sum for value index v ends up in every lane whose
 // top log2(V) lane-index bits equal v, i.e. v = lane >> (6 - log2 V).
+// All ones when ok, else zero, as a value the compiler cannot see through.
+// Masking a loaded value with it (instead of `ok ? v : 0`) keeps the load
+// unconditional: given a select, the compiler sinks the load into an
+// `if (ok)` branch, and the wait after such a branch drains every load
+// issued before it.
+__device__ __forceinline__ uint32_t opaque_mask(bool ok) {
+    uint32_t m = ok ? 0xffffffffu : 0u;
+    __asm__ volatile("" : "+v"(m));
+    return m;
+}
+__device__ __forceinline__ float mask_f(float v, uint32_t m) {
+    return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v) & m);
+}
+
 template <int V>
 __device__ __forceinline__ float wave_reduce_v(const float (&acc)[V], int lane) {
     static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0, "V must be a power of two <= 64");

@@ -263,15 +263,18 @@ __global__ __launch_bounds__(256) void k_q4rmv(RArgs a) {
 // ---- the decode step's norm as a matvec prologue ---------------------------
 
 typedef float f32x4r __attribute__((ext_vector_type(4)));
+// Eight values at 8t, or zeros when !ok.  The load itself is unconditional
+// (chunk 0 when !ok): a branch around it would make the compiler's wait
+// before the first use drain every load issued after it, the matvec's
+// weights included.
 __device__ __forceinline__ void ld8(const float *p, uint32_t t, bool ok, float (&v)[8]) {
-    if (ok) {
-        const f32x4r a = *(const f32x4r *)(p + 8 * (size_t)t), b = *(const f32x4r *)(p + 8 * (size_t)t + 4);
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-    } else {
+    const size_t i = ok ? 8 * (size_t)t : 0;
+    const f32x4r a = *(const f32x4r *)(p + i), b = *(const f32x4r *)(p + i + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    const uint32_t m = opaque_mask(ok);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
-    }
+    for (int k = 0; k < 8; ++k) v[k] = mask_f(v[k], m);
 }
 __device__ __forceinline__ void st8(float *p, uint32_t t, const float (&v)[8]) {
     *(f32x4r *)(p + 8 * (size_t)t) = f32x4r{v[0], v[1], v[2], v[3]};
@@ -414,11 +417,11 @@ __device__ __forceinline__ void lane_planes_lds(const uint32_t *lp, uint32_t b0,
                                                 uint32_t (&P)[2][XP_WORDS], float (&xs)[2]) {
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-        const bool ok = c ? ok1 : ok0;
+        const uint32_t m = opaque_mask(c ? ok1 : ok0);
         const uint32_t *src = lp + (c ? b1 : b0) * kLdsBlk;
 #pragma unroll
-        for (int i = 0; i < XP_WORDS; ++i) P[c][i] = ok ? src[i] : 0u;
-        xs[c] = ok ? __builtin_bit_cast(float, src[XP_WORDS]) : 0.0f;
+        for (int i = 0; i < XP_WORDS; ++i) P[c][i] = src[i] & m;
+        xs[c] = __builtin_bit_cast(float, src[XP_WORDS] & m);
     }
 }
 
@@ -440,9 +443,9 @@ __device__ __forceinline__ void lane_planes(const uint32_t *src, uint32_t nb, ui
 }
 
 // QKV matvec with the step's norm as its prologue (K <= 4096): NW waves per
-// workgroup, two rows per wave per group as k_q4rmv<RV_QKV, 2, 1>, the first
-// group's weights in flight while the norm runs, the next group's while a
-// group is reduced.
+// workgroup, two rows per wave per group as k_q4rmv<RV_QKV, 2, 1>; the
+// wave's first two groups' weights are in flight while the norm runs (the
+// launch gives every wave two groups at the model's shapes).
 template <int NORM, int NW = 8, int QG = 0>
 __global__ __launch_bounds__(64 * NW) void k_q4rmv_qkv_nx(RArgs a, NormArgs n) {
     constexpr int RPW = 2;
@@ -456,9 +459,11 @@ __global__ __launch_bounds__(64 * NW) void k_q4rmv_qkv_nx(RArgs a, NormArgs n) {
 
     const uint32_t ngroups = (a.M + RPW - 1) / RPW;
     const uint32_t gstride = gridDim.x * NW;
-    u32x4r nq[RPW][2];
-    uint16_t sq[RPW][2];
-    auto load = [&](uint32_t g) {
+    struct Grp {   // this lane's two blocks of RPW rows
+        u32x4r q[RPW][2];
+        uint16_t s[RPW][2];
+    };
+    auto load = [&](Grp &d, uint32_t g) {
 #pragma unroll
         for (int s = 0; s < RPW; ++s) {
             uint32_t row = g * RPW + s;
@@ -466,44 +471,24 @@ __global__ __launch_bounds__(64 * NW) void k_q4rmv_qkv_nx(RArgs a, NormArgs n) {
             const u32x4r *N;
             const uint16_t *S;
             row_ptrs<RV_QKV>(a, row, 0, N, S);
-            nq[s][0] = __builtin_nontemporal_load(N + b0);
-            nq[s][1] = __builtin_nontemporal_load(N + b1);
-            sq[s][0] = __builtin_nontemporal_load(S + b0);
-            sq[s][1] = __builtin_nontemporal_load(S + b1);
+            d.q[s][0] = __builtin_nontemporal_load(N + b0);
+            d.q[s][1] = __builtin_nontemporal_load(N + b1);
+            d.s[s][0] = __builtin_nontemporal_load(S + b0);
+            d.s[s][1] = __builtin_nontemporal_load(S + b1);
         }
     };
-    NormIn<NCH> nv;
-    norm_load<NORM, NCH, QG>(n, nb * 32, nv);
-    uint32_t g = blockIdx.x * NW + wave;
-    if (g < ngroups) load(g);
-    if (n.rope.tab && blockIdx.x == 0) rope_table(n.rope, threadIdx.x, blockDim.x);
-    const bool active = norm_to_lds<NORM, NCH, QG>(n, nb * 32, nv, lp, sh);
-    if (QG && !active) return;                // a quiescent layer (the same decision in every workgroup)
-    __syncthreads();
     uint32_t P[2][XP_WORDS];
     float xs[2];
-    lane_planes_lds(lp, b0, b1, ok0, ok1, P, xs);
-
-    for (; g < ngroups; g += gstride) {
-        u32x4r cq[RPW][2];
-        uint16_t cs[RPW][2];
-#pragma unroll
-        for (int s = 0; s < RPW; ++s)
-#pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                cq[s][c] = nq[s][c];
-                cs[s][c] = sq[s][c];
-            }
-        if (g + gstride < ngroups) load(g + gstride);
+    auto dot_store = [&](const Grp &c, uint32_t g) {
         float part[RPW], tot[RPW];
 #pragma unroll
         for (int s = 0; s < RPW; ++s) {
             float r = 0.0f;
 #pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                const int T = block_idot_r(cq[s][c], P[c]);
-                const float sf = (float)__builtin_bit_cast(_Float16, cs[s][c]);
-                r = fmaf((float)T, sf * xs[c], r);
+            for (int k = 0; k < 2; ++k) {
+                const int T = block_idot_r(c.q[s][k], P[k]);
+                const float sf = (float)__builtin_bit_cast(_Float16, c.s[s][k]);
+                r = fmaf((float)T, sf * xs[k], r);
             }
             part[s] = r;
         }
@@ -512,6 +497,36 @@ __global__ __launch_bounds__(64 * NW) void k_q4rmv_qkv_nx(RArgs a, NormArgs n) {
         for (int s = 0; s < RPW; ++s) {
             const uint32_t row = g * RPW + s;
             if (lane == 0 && row < a.M) store_r<RV_QKV>(a, row, tot[s]);
+        }
+    };
+    NormIn<NCH> nv;
+    norm_load<NORM, NCH, QG>(n, nb * 32, nv);
+    // The wave's first two row groups are requested before the norm runs,
+    // unconditionally (the row index is clamped; a wave with one group loads
+    // its own rows twice, from cache), so no branch makes the norm's waits
+    // drain them.
+    uint32_t g = blockIdx.x * NW + wave;
+    const uint32_t g1 = g + gstride;
+    const uint32_t ga = g < ngroups ? g : ngroups - 1;
+    Grp A, B;
+    load(A, ga);
+    load(B, g1 < ngroups ? g1 : ga);
+    if (n.rope.tab && blockIdx.x == 0) rope_table(n.rope, threadIdx.x, blockDim.x);
+    const bool active = norm_to_lds<NORM, NCH, QG>(n, nb * 32, nv, lp, sh);
+    if (QG && !active) return;                // a quiescent layer (the same decision in every workgroup)
+    __syncthreads();
+    lane_planes_lds(lp, b0, b1, ok0, ok1, P, xs);
+    if (g < ngroups) dot_store(A, g);
+    if (g1 < ngroups) dot_store(B, g1);
+
+    // shapes with more than two groups per wave: one group in flight
+    g = g1 + gstride;
+    if (g < ngroups) {
+        load(A, g);
+        for (; g < ngroups; g += gstride) {
+            const Grp c = A;
+            if (g + gstride < ngroups) load(A, g + gstride);
+            dot_store(c, g);
         }
     }
 }
