@@ -44,6 +44,10 @@ PROTOTYPES = {
     "chn_sync": (c_int, [c_void_p]),
     "chn_timer_start": (c_int, [c_void_p]),
     "chn_timer_stop": (c_int, [c_void_p, P(c_f32)]),
+    "chn_record_begin": (c_int, [c_void_p]),
+    "chn_record_end": (c_int, [c_void_p, P(c_void_p)]),
+    "chn_submit": (c_int, [c_void_p, c_void_p]),
+    "chn_recording_free": (None, [c_void_p]),
     "chn_gemv_q4": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_u32, c_u32]),
     "chn_fused_qkv_q4": (c_int, [c_void_p] + [c_void_p] * 7 + [c_u32, c_u32, c_u32]),
     "chn_fused_mlp_q4": (c_int, [c_void_p] + [c_void_p] * 4 + [c_u32, c_u32]),

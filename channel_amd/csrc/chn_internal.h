@@ -16,9 +16,13 @@ struct chn_ctx {
     hipEvent_t t0 = nullptr, t1 = nullptr;
     std::string err;
     // Workspace for kernels that need partials (split-K attention, ...).
-    // Grown on demand outside graph capture; owned by the context.
+    // Grown on demand outside graph capture; owned by the context.  ws_gen
+    // counts reallocations: a recording made at another generation would
+    // read a freed workspace and is refused.
     void *ws = nullptr;
     size_t ws_bytes = 0;
+    uint64_t ws_gen = 0;
+    bool recording = false;     // between chn_record_begin and chn_record_end
 };
 
 namespace chn {

@@ -29,6 +29,12 @@ int hip_fail(chn_ctx *ctx, hipError_t e, const char *what) {
 
 int ensure_workspace(chn_ctx *ctx, size_t bytes) {
     if (ctx->ws_bytes >= bytes) return CHN_OK;
+    if (ctx->recording)
+        return set_err(ctx, CHN_E_UNSUPPORTED,
+                       "the workspace (%zu bytes) must grow to %zu bytes: make one unrecorded call of this shape "
+                       "before recording",
+                       ctx->ws_bytes, bytes);
+    ++ctx->ws_gen;
     if (ctx->ws) {
         CHN_HIP(ctx, hipStreamSynchronize(ctx->stream));
         CHN_HIP(ctx, hipFree(ctx->ws));
@@ -97,6 +103,11 @@ extern "C" int chn_init(int device, chn_ctx **out) {
 extern "C" void chn_destroy(chn_ctx *ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
+    if (ctx->recording) {
+        hipGraph_t g = nullptr;
+        (void)hipStreamEndCapture(ctx->stream, &g);
+        if (g) (void)hipGraphDestroy(g);
+    }
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
     (void)hipEventDestroy(ctx->t0);
@@ -159,6 +170,60 @@ extern "C" int chn_fill_u32(chn_ctx *ctx, void *dst, uint32_t value, size_t coun
     k_fill_u32<<<dim3((unsigned)blocks), dim3(256), 0, ctx->stream>>>((uint32_t *)dst, value, count);
     CHN_LAUNCHED(ctx, "k_fill_u32");
     return CHN_OK;
+}
+
+// ---- recordings (the reference's pre-recorded command buffers) ----------
+
+struct chn_recording {
+    chn_ctx *ctx;
+    hipGraphExec_t exec;
+    uint64_t ws_gen;
+};
+
+extern "C" int chn_record_begin(chn_ctx *ctx) {
+    if (!ctx) return set_err(ctx, CHN_E_INVALID, "NULL ctx");
+    CHN_REQUIRE(ctx, !ctx->recording, "already recording");
+    CHN_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    ctx->recording = true;
+    return CHN_OK;
+}
+
+extern "C" int chn_record_end(chn_ctx *ctx, chn_recording **out) {
+    if (!ctx || !out) return set_err(ctx, CHN_E_INVALID, "NULL argument");
+    *out = nullptr;
+    CHN_REQUIRE(ctx, ctx->recording, "not recording");
+    ctx->recording = false;
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(ctx->stream, &g);
+    if (e != hipSuccess || !g) {
+        if (g) (void)hipGraphDestroy(g);
+        // a call that failed while recording invalidates the capture
+        return hip_fail(ctx, e != hipSuccess ? e : hipErrorStreamCaptureInvalidated, "hipStreamEndCapture");
+    }
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipGraphInstantiate");
+    *out = new chn_recording{ctx, exec, ctx->ws_gen};
+    return CHN_OK;
+}
+
+extern "C" int chn_submit(chn_ctx *ctx, const chn_recording *rec) {
+    if (!ctx || !rec) return set_err(ctx, CHN_E_INVALID, "NULL argument");
+    CHN_REQUIRE(ctx, rec->ctx == ctx, "the recording belongs to another context");
+    CHN_REQUIRE(ctx, !ctx->recording, "cannot submit while recording");
+    CHN_REQUIRE(ctx, rec->ws_gen == ctx->ws_gen,
+                "the context workspace was reallocated after this recording was made: record it again");
+    CHN_HIP(ctx, hipGraphLaunch(rec->exec, ctx->stream));
+    return CHN_OK;
+}
+
+extern "C" void chn_recording_free(chn_recording *rec) {
+    if (!rec) return;
+    (void)hipSetDevice(rec->ctx->device);
+    (void)hipStreamSynchronize(rec->ctx->stream);
+    (void)hipGraphExecDestroy(rec->exec);
+    delete rec;
 }
 
 extern "C" int chn_sync(chn_ctx *ctx) {

@@ -38,6 +38,23 @@ class Buffer:
         return c_void_p(self.ptr)
 
 
+class Recording:
+    """A recorded sequence of calls (chn_record_begin .. chn_record_end), the
+    reference's pre-recorded command buffer; submit() enqueues it again."""
+
+    def __init__(self, ctx, handle):
+        self.ctx = ctx
+        self.handle = handle
+
+    def submit(self):
+        self.ctx._check("chn_submit", lib.chn_submit(self.ctx.handle, self.handle))
+
+    def free(self):
+        if self.handle is not None:
+            lib.chn_recording_free(self.handle)
+            self.handle = None
+
+
 def _ptr(a):
     if a is None:
         return None
@@ -56,6 +73,7 @@ class Context:
             raise ChannelError("chn_init", rc, lib.chn_last_error(None).decode())
         self.handle = h.value
         self._bufs = []
+        self._recs = []
 
     # -- plumbing -----------------------------------------------------
     def _check(self, fn, rc):
@@ -127,9 +145,24 @@ class Context:
         self._check("chn_timer_stop", lib.chn_timer_stop(self.handle, ctypes.byref(ms)))
         return ms.value
 
+    def record_begin(self):
+        """Record the following kernel-level calls instead of running them."""
+        self._check("chn_record_begin", lib.chn_record_begin(self.handle))
+
+    def record_end(self):
+        """End the recording; returns a Recording to submit() any number of times."""
+        h = c_void_p()
+        self._check("chn_record_end", lib.chn_record_end(self.handle, ctypes.byref(h)))
+        r = Recording(self, h.value)
+        self._recs.append(r)
+        return r
+
     def close(self):
         if self.handle is None:
             return
+        for r in self._recs:
+            r.free()
+        self._recs = []
         for b in self._bufs:
             if b.ptr is not None:
                 lib.chn_free(self.handle, b.ptr)

@@ -94,6 +94,31 @@ int chn_sync(chn_ctx *ctx);
 int chn_timer_start(chn_ctx *ctx);
 int chn_timer_stop(chn_ctx *ctx, float *ms);
 
+/* Recordings: the reference's pre-recorded command buffers (GpuEngine.record*
+ * into a VkCommandBuffer, then submitPreRecorded, src/gpu/kernels.zig:89-194;
+ * recordForwardGraph, src/gpu/model_dispatch.zig:103-126).  Between
+ * chn_record_begin and chn_record_end the kernel-level calls on ctx (matvecs,
+ * contractions, attention, norms, logits, chn_copy, chn_fill_u32) are
+ * recorded into a HIP graph instead of run; chn_submit enqueues the recording
+ * on the context stream (chn_sync waits, as submitPreRecorded's fence wait
+ * does) and may be called any number of times.
+ *  - A recording holds the device pointers and sizes it was made with: the
+ *    buffers must stay allocated while it is used, and their contents at
+ *    submission are what the kernels read.
+ *  - Calls that copy to or from the host, synchronize, or would grow the
+ *    context workspace fail while recording (CHN_E_UNSUPPORTED for the
+ *    workspace: make one unrecorded call of the same shapes first, or use
+ *    chn_decode_attn_noalloc); a failed call can invalidate the recording,
+ *    which chn_record_end then reports.
+ *  - chn_submit refuses a recording made before the workspace was last
+ *    reallocated (it would read freed memory), and one from another context.
+ * chn_recording_free waits for the context stream, then releases it. */
+typedef struct chn_recording chn_recording;
+int chn_record_begin(chn_ctx *ctx);
+int chn_record_end(chn_ctx *ctx, chn_recording **out);
+int chn_submit(chn_ctx *ctx, const chn_recording *rec);
+void chn_recording_free(chn_recording *rec);
+
 /* ======================================================================
  * Decode matvecs (GpuEngine.record*, src/gpu/kernels.zig:89-126)
  * ==================================================================== */
