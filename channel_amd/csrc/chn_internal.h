@@ -230,7 +230,16 @@ int launch_q8_repack(hipStream_t st, const uint32_t *W, uint32_t rows, uint32_t 
 int launch_gemv_q8r(hipStream_t st, const void *R, const float *x, float *y, uint32_t M, uint32_t nb,
                     uint32_t *xp_ws);
 size_t topk_ws_bytes(uint32_t V);
-int launch_topk64(hipStream_t st, const float *logits, uint32_t V, uint32_t *ids, float *vals, uint64_t *ws);
+// Optional end of a device-side greedy step, done by the top-64 merge once
+// ids[0] is known: out[gen[1]] = ids[0] (while gen[1] < cap), then gen[1] and
+// the clock gen[0] advance by one.
+struct GreedyTail {
+    uint32_t *gen;
+    uint32_t *out;
+    uint32_t cap;
+};
+int launch_topk64(hipStream_t st, const float *logits, uint32_t V, uint32_t *ids, float *vals, uint64_t *ws,
+                  const GreedyTail *tail = nullptr);
 int launch_embed(hipStream_t st, const uint16_t *table, const uint32_t *tokens, uint32_t n, uint32_t H, float scale,
                  float *x);
 int launch_quantize(hipStream_t st, int q8, const uint16_t *src, uint32_t *dst, uint64_t nblk);

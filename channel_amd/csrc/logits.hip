@@ -371,7 +371,8 @@ __global__ __launch_bounds__(256) void k_topk_tile(const float *__restrict__ log
 constexpr int kTopkFast = 1024;
 
 __global__ __launch_bounds__(1024) void k_topk_merge(const uint64_t *__restrict__ cand, uint32_t nlist,
-                                                     uint32_t *__restrict__ ids, float *__restrict__ vals) {
+                                                     uint32_t *__restrict__ ids, float *__restrict__ vals,
+                                                     GreedyTail tail) {
     constexpr int U = 8;                 // lists loaded per wave per batch (full fold)
     constexpr int kMaxLists = 262144 / kTile;
     __shared__ uint64_t sh[16][kTopK];
@@ -449,22 +450,26 @@ __global__ __launch_bounds__(1024) void k_topk_merge(const uint64_t *__restrict_
         res = acc;
     }
     if (wave == 0) {
-        if (res) {
-            ids[lane] = 0xFFFFFFFFu - (uint32_t)res;
-            vals[lane] = key_value(res);
-        } else {
-            ids[lane] = 0;
-            vals[lane] = -1e30f;
+        const uint32_t id = res ? 0xFFFFFFFFu - (uint32_t)res : 0u;
+        ids[lane] = id;
+        vals[lane] = res ? key_value(res) : -1e30f;
+        if (tail.gen && lane == 0) {
+            // a device-side greedy step: append the argmax, advance the clock
+            const uint32_t count = tail.gen[1];
+            if (count < tail.cap) tail.out[count] = id;
+            tail.gen[1] = count + 1;
+            tail.gen[0] = tail.gen[0] + 1;
         }
     }
 }
 
 size_t topk_ws_bytes(uint32_t V) { return (size_t)((V + kTile - 1) / kTile) * kTopK * 8; }
 
-int launch_topk64(hipStream_t st, const float *logits, uint32_t V, uint32_t *ids, float *vals, uint64_t *ws) {
+int launch_topk64(hipStream_t st, const float *logits, uint32_t V, uint32_t *ids, float *vals, uint64_t *ws,
+                  const GreedyTail *tail) {
     const uint32_t tiles = (V + kTile - 1) / kTile;
     if (tiles) k_topk_tile<<<tiles, 256, 0, st>>>(logits, V, ws);
-    k_topk_merge<<<1, 1024, 0, st>>>(ws, tiles, ids, vals);
+    k_topk_merge<<<1, 1024, 0, st>>>(ws, tiles, ids, vals, tail ? *tail : GreedyTail{nullptr, nullptr, 0});
     return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
 }
 

@@ -253,13 +253,16 @@ static constexpr uint32_t kRecallNone = 0xFFFFFFFFu;
 // (snapToBoundary, :92-100), then the recall slots whose clock has passed;
 // the sliding list: the newest `window` clocks, anchors included, no
 // recall), and the input token (the start token, then the previous step's
-// argmax).
+// argmax), and the step's input row x = bf16(embed[token]) * scale (the
+// embedding gather, expandEmbeddings).
 __global__ __launch_bounds__(256) void k_greedy_head(const uint32_t *__restrict__ gen,
                                                      const uint32_t *__restrict__ topk_ids,
                                                      const uint32_t *__restrict__ bounds,
                                                      const uint32_t *__restrict__ recall,
                                                      uint32_t *__restrict__ step, uint32_t *__restrict__ slots,
-                                                     uint32_t *__restrict__ tok, uint32_t window) {
+                                                     uint32_t *__restrict__ tok, uint32_t window,
+                                                     const uint16_t *__restrict__ embed, uint32_t H, float scale,
+                                                     float *__restrict__ x) {
     __shared__ uint32_t s_first, s_cnt[2];
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const uint32_t clock = gen[0], count = gen[1], A = gen[3], nb = gen[4];
@@ -298,29 +301,21 @@ __global__ __launch_bounds__(256) void k_greedy_head(const uint32_t *__restrict_
     uint32_t *sl = slots + kSlotsMax;
     for (uint32_t i = t; i < nas; i += 256) sl[i] = raws + i;
     for (uint32_t i = t; i < nsw; i += 256) sl[nas + i] = A + (ss + i - A) % W;
+    const uint32_t token = count == 0 ? gen[2] : topk_ids[0];
     if (t == 0) {
         step[0] = clock;
         step[1] = clock < A ? clock : A + (clock - A) % W;
         step[2] = na + nw + s_cnt[0] + s_cnt[1];
         step[3] = nas + nsw;
-        tok[0] = count == 0 ? gen[2] : topk_ids[0];
+        tok[0] = token;
     }
-}
-
-// Tail: append this step's argmax (top-64 ids[0]) and advance the clock.
-__global__ void k_greedy_tail(uint32_t *__restrict__ gen, const uint32_t *__restrict__ topk_ids,
-                              uint32_t *__restrict__ out, uint32_t cap) {
-    if (threadIdx.x == 0 && blockIdx.x == 0) {
-        const uint32_t count = gen[1];
-        if (count < cap) out[count] = topk_ids[0];
-        gen[1] = count + 1;
-        gen[0] = gen[0] + 1;
-    }
+    const uint16_t *row = embed + (size_t)token * H;
+    for (uint32_t i = t; i < H; i += 256) x[i] = __builtin_bit_cast(float, (uint32_t)row[i] << 16) * scale;
 }
 
 // ---- the decode sequence (recordLayerDirect / recordForwardGraph,
 // src/gpu/model_dispatch.zig:10-45,103-126)
-static int record_decode(chn_model *m, bool with_logits) {
+static int record_decode(chn_model *m, bool with_logits, const GreedyTail *tail = nullptr) {
     chn_ctx *ctx = m->ctx;
     hipStream_t s = ctx->stream;
     const chn_model_config &c = m->cfg;
@@ -384,7 +379,7 @@ static int record_decode(chn_model *m, bool with_logits) {
                           gated(c.num_layers - 1) ? m->qflags + c.num_layers - 1 : nullptr));
     if (with_logits) {
         R_(launch_gemv_q8r(s, m->embed_q8, m->normed, m->logits, c.vocab_size, H / 32, m->mv_ws));
-        R_(launch_topk64(s, m->logits, c.vocab_size, m->topk_ids, m->topk_vals, m->topk_ws));
+        R_(launch_topk64(s, m->logits, c.vocab_size, m->topk_ids, m->topk_vals, m->topk_ws, tail));
     }
 #undef R_
     return CHN_OK;
@@ -393,16 +388,13 @@ static int record_decode(chn_model *m, bool with_logits) {
 static int record_greedy(chn_model *m) {
     hipStream_t s = m->ctx->stream;
     const uint32_t H = m->cfg.hidden_size;
+    // the head also gathers the input row; the top-64 merge ends the step
+    // (appends the argmax, advances the clock)
     k_greedy_head<<<1, 256, 0, s>>>(m->gen, m->topk_ids, m->ring_bounds, m->ring_recall, m->step, m->slots, m->tok,
-                                    m->cfg.sliding_window);
+                                    m->cfg.sliding_window, m->embed_bf16, H, sqrtf((float)H), m->x);
     if (hipGetLastError() != hipSuccess) return hip_fail(m->ctx, hipGetLastError(), "k_greedy_head");
-    if (launch_embed(s, m->embed_bf16, m->tok, 1, H, sqrtf((float)H), m->x))
-        return hip_fail(m->ctx, hipGetLastError(), "k_embed");
-    int rc = record_decode(m, true);
-    if (rc) return rc;
-    k_greedy_tail<<<1, 64, 0, s>>>(m->gen, m->topk_ids, m->gen_tokens, kGreedyCap);
-    if (hipGetLastError() != hipSuccess) return hip_fail(m->ctx, hipGetLastError(), "k_greedy_tail");
-    return CHN_OK;
+    const GreedyTail tail{m->gen, m->gen_tokens, kGreedyCap};
+    return record_decode(m, true, &tail);
 }
 
 static int build_graphs(chn_model *m) {
