@@ -175,10 +175,128 @@ __global__ __launch_bounds__(256) void k_rmsnorm_chain_r(float *__restrict__ x, 
     }
 }
 
+// The register form over several rows per workgroup (a grid of at most
+// kChainGrid workgroups striding over the rows), the next row's x and r in
+// flight while a row is reduced and stored, the norm weights loaded once.
+// Loads are unconditional (a row past the end reloads the current one, from
+// cache), so the compiler's waits leave the next row's loads outstanding.
+// Per row, every sum and product is k_rmsnorm_chain_r's.
+constexpr uint32_t kChainGrid = 256;
+template <bool POST, bool ADD>
+__global__ __launch_bounds__(256) void k_rmsnorm_chain_p(float *__restrict__ x, float *__restrict__ r,
+                                                         const float *__restrict__ pw, const float *__restrict__ w,
+                                                         __bf16 *__restrict__ yb, float *__restrict__ y, uint32_t dim,
+                                                         uint32_t rows, float eps, float scalar, int zero_r) {
+    constexpr int NPT = 4;
+    __shared__ float sh[4];
+    const f4n *pwr = (const f4n *)pw;
+    const f4n *wr = (const f4n *)w;
+    const uint32_t dv = dim / 4;
+    struct Row {
+        f4n x[NPT], r[NPT];
+    };
+    f4n pv[NPT], wv[NPT];
+    uint32_t idx[NPT];
+    uint32_t okm[NPT];
+#pragma unroll
+    for (int k = 0; k < NPT; ++k) {
+        const uint32_t i = threadIdx.x + 256 * k;
+        idx[k] = i < dv ? i : 0u;
+        okm[k] = opaque_mask(i < dv);
+    }
+    auto mask4 = [](f4n v, uint32_t m) {
+        return f4n{mask_f(v.x, m), mask_f(v.y, m), mask_f(v.z, m), mask_f(v.w, m)};
+    };
+    auto load = [&](uint32_t row, Row &d) {
+        const f4n *xr = (const f4n *)(x + (size_t)row * dim);
+        const f4n *rr = (const f4n *)(r + (size_t)row * dim);
+#pragma unroll
+        for (int k = 0; k < NPT; ++k) {
+            d.x[k] = xr[idx[k]];
+            if (ADD) d.r[k] = rr[idx[k]];
+        }
+    };
+    uint32_t row = blockIdx.x;
+    Row A, B;
+    load(row, A);
+#pragma unroll
+    for (int k = 0; k < NPT; ++k) {
+        if (POST) pv[k] = pwr[idx[k]];
+        wv[k] = wr[idx[k]];
+    }
+    auto process = [&](uint32_t row, Row &d) {
+        const size_t off = (size_t)row * dim;
+        f4n *xr = (f4n *)(x + off);
+        f4n *rr = (f4n *)(r + off);
+        f4n xv[NPT], rv[NPT];
+#pragma unroll
+        for (int k = 0; k < NPT; ++k) {
+            xv[k] = mask4(d.x[k], okm[k]);
+            if (ADD) rv[k] = mask4(d.r[k], okm[k]);
+        }
+        float inv_r = 1.0f;
+        if (POST) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < NPT; ++k) {
+                const f4n v = rv[k];
+                if (threadIdx.x + 256 * k < dv) ss += ((v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w));
+            }
+            ss = block_sum_256(ss, sh);
+            inv_r = 1.0f / sqrtf(ss / (float)dim + eps);
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NPT; ++k) {
+            const uint32_t i = threadIdx.x + 256 * k;
+            if (i >= dv) continue;
+            f4n v = xv[k];
+            if (ADD) {
+                f4n b = rv[k];
+                if (POST) b = (b * inv_r) * pv[k];
+                v = (v + b) * scalar;
+                xv[k] = v;
+                xr[i] = v;
+                if (zero_r) rr[i] = f4n{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+            ss += ((v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w));
+        }
+        ss = block_sum_256(ss, sh);
+        const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+#pragma unroll
+        for (int k = 0; k < NPT; ++k) {
+            const uint32_t i = threadIdx.x + 256 * k;
+            if (i >= dv) continue;
+            const f4n o = (xv[k] * inv) * wv[k];
+            bf16x2 lo = {(__bf16)o.x, (__bf16)o.y}, hi = {(__bf16)o.z, (__bf16)o.w};
+            *(bf16x2 *)(yb + off + 4 * (size_t)i) = lo;
+            *(bf16x2 *)(yb + off + 4 * (size_t)i + 2) = hi;
+            if (y) *(f4n *)(y + off + 4 * (size_t)i) = o;
+        }
+    };
+    const uint32_t G = gridDim.x;
+    for (;;) {
+        load(row + G < rows ? row + G : row, B);
+        process(row, A);
+        row += G;
+        if (row >= rows) break;
+        load(row + G < rows ? row + G : row, A);
+        process(row, B);
+        row += G;
+        if (row >= rows) break;
+    }
+}
+
 int launch_rmsnorm_chain(hipStream_t s, float *x, float *r, const float *post_w, const float *w, __bf16 *yb,
                          float *y, uint32_t dim, uint32_t rows, float eps, float scalar, bool add, bool zero_r) {
     const int z = zero_r ? 1 : 0;
-    if (dim <= 4096) {
+    if (dim <= 4096 && rows > kChainGrid) {
+        const uint32_t g = kChainGrid;
+        if (!add) k_rmsnorm_chain_p<false, false><<<g, 256, 0, s>>>(x, r, post_w, w, yb, y, dim, rows, eps, scalar, z);
+        else if (post_w)
+            k_rmsnorm_chain_p<true, true><<<g, 256, 0, s>>>(x, r, post_w, w, yb, y, dim, rows, eps, scalar, z);
+        else k_rmsnorm_chain_p<false, true><<<g, 256, 0, s>>>(x, r, post_w, w, yb, y, dim, rows, eps, scalar, z);
+    } else if (dim <= 4096) {
         if (!add) k_rmsnorm_chain_r<false, false><<<rows, 256, 0, s>>>(x, r, post_w, w, yb, y, dim, eps, scalar, z);
         else if (post_w)
             k_rmsnorm_chain_r<true, true><<<rows, 256, 0, s>>>(x, r, post_w, w, yb, y, dim, eps, scalar, z);
