@@ -65,6 +65,9 @@ struct chn_model {
     // device-resident greedy decoding: {clock, count, start token}, tokens out
     uint32_t *gen = nullptr, *gen_tokens = nullptr;
     uint32_t *h_gen = nullptr;
+    // prefill checkpoints: an event after every fourth layer, waited on in
+    // order once the whole prefill is enqueued
+    std::vector<hipEvent_t> pev;
     // ring state the greedy head reads: turn boundaries, recall clocks
     uint32_t *ring_bounds = nullptr, *ring_recall = nullptr;
     // quiescence: per layer a skip flag and the input stream at the previous
@@ -220,6 +223,11 @@ static int alloc_runtime(chn_model *m) {
     if (e == hipSuccess) e = hipHostMalloc((void **)&m->h_vals, 64 * 4);
     if (e == hipSuccess) e = hipHostMalloc((void **)&m->h_gen, (size_t)kGreedyCap * 4);
     if (e != hipSuccess) return hip_fail(m->ctx, e, "hipHostMalloc");
+    m->pev.assign((c.num_layers + 3) / 4, nullptr);
+    for (auto &ev : m->pev) {
+        e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+        if (e != hipSuccess) return hip_fail(m->ctx, e, "hipEventCreate");
+    }
     // zero KV caches and slot buffers with a kernel (no memset nodes anywhere)
     for (auto &l : m->L) {
         int rc = chn_fill_u32(m->ctx, l.kc, 0, (size_t)kSlotsMax * l.kvd);
@@ -428,6 +436,7 @@ static void free_model(chn_model *m) {
     if (m->h_ids) (void)hipHostFree(m->h_ids);
     if (m->h_vals) (void)hipHostFree(m->h_vals);
     if (m->h_gen) (void)hipHostFree(m->h_gen);
+    for (hipEvent_t e : m->pev) (void)hipEventDestroy(e);
     delete m;
 }
 
@@ -873,11 +882,18 @@ extern "C" int chn_prefill(chn_model *m, const uint32_t *tokens, uint32_t n, con
                 P_(launch_gemv_q8r(s, m->embed_q8, m->normed, m->logits, c.vocab_size, H / 32, m->mv_ws));
                 P_(launch_topk64(s, m->logits, c.vocab_size, m->topk_ids, m->topk_vals, m->topk_ws));
             }
-            CHN_HIP(ctx, hipStreamSynchronize(s));
-            if (progress) progress(i + 1, c.num_layers, progress_ctx);
+            CHN_HIP(ctx, hipEventRecord(m->pev[i / 4], s));
         }
     }
 #undef P_
+    // the reference waits on its fence every four layers and reports
+    // progress (src/gpu/batch_dispatch.zig:27-172); here the whole prefill is
+    // already enqueued, so the device runs without gaps while the host waits
+    // on each checkpoint in turn
+    for (uint32_t k = 0; k < (c.num_layers + 3) / 4; ++k) {
+        CHN_HIP(ctx, hipEventSynchronize(m->pev[k]));
+        if (progress) progress(k * 4 + 4 < c.num_layers ? k * 4 + 4 : c.num_layers, c.num_layers, progress_ctx);
+    }
     if (logits_out) CHN_HIP(ctx, hipMemcpy(logits_out, m->logits, (size_t)c.vocab_size * 4, hipMemcpyDeviceToHost));
     if (topk_ids) CHN_HIP(ctx, hipMemcpy(topk_ids, m->topk_ids, 64 * 4, hipMemcpyDeviceToHost));
     if (topk_vals) CHN_HIP(ctx, hipMemcpy(topk_vals, m->topk_vals, 64 * 4, hipMemcpyDeviceToHost));
