@@ -829,9 +829,10 @@ extern "C" int chn_prefill(chn_model *m, const uint32_t *tokens, uint32_t n, con
         CHN_HIP(ctx, hipMemcpyAsync(m->px, hx.data(), hx.size() * 4, hipMemcpyHostToDevice, s));
         CHN_HIP(ctx, hipStreamSynchronize(s));
     } else {
+        // (a copy from pageable memory returns once the bytes are staged, so
+        // the caller's array may change afterwards; no wait is needed here)
         CHN_HIP(ctx, hipMemcpyAsync(m->ptok, tokens, n * 4, hipMemcpyHostToDevice, s));
         if (launch_embed(s, m->embed_bf16, m->ptok, n, H, escale, m->px)) return hip_fail(ctx, hipGetLastError(), "k_embed");
-        CHN_HIP(ctx, hipStreamSynchronize(s));
     }
     CHN_HIP(ctx, hipMemcpyAsync(m->pslots, slots, (size_t)n_slots * 4, hipMemcpyHostToDevice, s));
 
