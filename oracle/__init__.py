@@ -1,7 +1,7 @@
 """numpy/ctypes front end of the CPU oracle (oracle/liboracle.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
-bench.py's cpu_baseline leg, as the checker.  The product (channel_amd/)
+bench.py's cpu_baseline leg, to check results against.  The product (channel_amd/)
 never imports it.  Every function restates reference semantics; see
 oracle.c for the file:line each one follows.
 """

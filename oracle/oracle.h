@@ -1,7 +1,7 @@
 /*
  * CPU oracle for the Q4 inference hot path.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker: it is linked or
+ * TEST INFRASTRUCTURE ONLY.  Results are checked against this library: it is linked or
  * loaded by tests/, by __graft_entry__.smoke() and by bench.py's cpu_baseline
  * leg, never by the product library (channel_amd/).  It restates, in plain
  * C99 with fp32 arithmetic (built with -ffp-contract=off, so every product

@@ -1,7 +1,7 @@
 """Restatement of the reference's KV ring geometry (DynamicRingBuffer,
 src/ring_buffer.zig:17-355): which physical slot a clock's K/V lands in and
 which slots, in which order, a decode step or a prefill chunk attends over.
-TEST INFRASTRUCTURE ONLY (imported by tests/ as the checker).
+TEST INFRASTRUCTURE ONLY (imported by tests/ to check the device's lists).
 
 Only the slot bookkeeping is restated (clocks, active flags, turn
 boundaries); the K/V payload is not, since the GPU caches hold it.  Plain

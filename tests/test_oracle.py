@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (the checker) before anything is compared against it.
+"""Pins the CPU oracle before anything is compared against it.
 
 Each test is chosen so that a plausible restatement mistake fails it: a wrong
 rounding mode, a swapped nibble order, a dropped -8, a transposed operand, a
