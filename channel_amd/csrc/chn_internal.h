@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <string>
+#include <vector>
 
 #include "../../include/channel_hip.h"
 
@@ -23,6 +24,7 @@ struct chn_ctx {
     size_t ws_bytes = 0;
     uint64_t ws_gen = 0;
     bool recording = false;     // between chn_record_begin and chn_record_end
+    std::vector<chn_recording *> recs;   // live recordings, released by chn_destroy
 };
 
 namespace chn {

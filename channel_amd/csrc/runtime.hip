@@ -100,6 +100,19 @@ extern "C" int chn_init(int device, chn_ctx **out) {
     return CHN_OK;
 }
 
+// a recording (chn_record_end): the instantiated graph and the workspace
+// generation it was made at
+struct chn_recording {
+    chn_ctx *ctx;
+    hipGraphExec_t exec;
+    uint64_t ws_gen;
+};
+
+static void release_recording(chn_recording *rec) {
+    (void)hipGraphExecDestroy(rec->exec);
+    delete rec;
+}
+
 extern "C" void chn_destroy(chn_ctx *ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
@@ -108,6 +121,9 @@ extern "C" void chn_destroy(chn_ctx *ctx) {
         (void)hipStreamEndCapture(ctx->stream, &g);
         if (g) (void)hipGraphDestroy(g);
     }
+    (void)hipStreamSynchronize(ctx->stream);
+    for (chn_recording *r : ctx->recs) release_recording(r);
+    ctx->recs.clear();
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
     (void)hipEventDestroy(ctx->t0);
@@ -174,11 +190,6 @@ extern "C" int chn_fill_u32(chn_ctx *ctx, void *dst, uint32_t value, size_t coun
 
 // ---- recordings (the reference's pre-recorded command buffers) ----------
 
-struct chn_recording {
-    chn_ctx *ctx;
-    hipGraphExec_t exec;
-    uint64_t ws_gen;
-};
 
 extern "C" int chn_record_begin(chn_ctx *ctx) {
     if (!ctx) return set_err(ctx, CHN_E_INVALID, "NULL ctx");
@@ -205,6 +216,7 @@ extern "C" int chn_record_end(chn_ctx *ctx, chn_recording **out) {
     (void)hipGraphDestroy(g);
     if (e != hipSuccess) return hip_fail(ctx, e, "hipGraphInstantiate");
     *out = new chn_recording{ctx, exec, ctx->ws_gen};
+    ctx->recs.push_back(*out);
     return CHN_OK;
 }
 
@@ -220,10 +232,15 @@ extern "C" int chn_submit(chn_ctx *ctx, const chn_recording *rec) {
 
 extern "C" void chn_recording_free(chn_recording *rec) {
     if (!rec) return;
-    (void)hipSetDevice(rec->ctx->device);
-    (void)hipStreamSynchronize(rec->ctx->stream);
-    (void)hipGraphExecDestroy(rec->exec);
-    delete rec;
+    chn_ctx *ctx = rec->ctx;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    for (size_t i = 0; i < ctx->recs.size(); ++i)
+        if (ctx->recs[i] == rec) {
+            ctx->recs.erase(ctx->recs.begin() + i);
+            break;
+        }
+    release_recording(rec);
 }
 
 extern "C" int chn_sync(chn_ctx *ctx) {

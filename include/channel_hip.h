@@ -112,7 +112,9 @@ int chn_timer_stop(chn_ctx *ctx, float *ms);
  *    which chn_record_end then reports.
  *  - chn_submit refuses a recording made before the workspace was last
  *    reallocated (it would read freed memory), and one from another context.
- * chn_recording_free waits for the context stream, then releases it. */
+ * chn_recording_free waits for the context stream, then releases it;
+ * chn_destroy releases the recordings still live on its context (they must
+ * not be used or freed afterwards). */
 typedef struct chn_recording chn_recording;
 int chn_record_begin(chn_ctx *ctx);
 int chn_record_end(chn_ctx *ctx, chn_recording **out);

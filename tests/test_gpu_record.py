@@ -97,3 +97,10 @@ def test_recording_misuse_is_refused():
             rec.submit()
         assert "reallocated" in str(ei.value)
         rec.free()
+        # a recording still live when its context is destroyed is released
+        # by chn_destroy
+        c2.record_begin()
+        c2.call("chn_gemv_q4", W, x, y, 64, 256)
+        live = c2.record_end()
+        live.submit()
+        c2._recs.remove(live)
