@@ -1246,12 +1246,24 @@ __device__ __forceinline__ void norm_rope_head4(const float *__restrict__ in, co
                                                 float *__restrict__ out, uint32_t rot, float eps, float *buf,
                                                 const float2 *__restrict__ cs, int lane) {
     constexpr int D = 256 * DV;
+    const uint32_t half = rot / 2;
     f4 v[DV], wv[DV];
+    float2 t[DV][4];
 #pragma unroll
     for (int j = 0; j < DV; ++j) {
         v[j] = *(const f4 *)(in + 4 * lane + 256 * j);
         wv[j] = *(const f4 *)(w + 4 * lane + 256 * j);
     }
+    // the angles too, with the inputs (after the LDS step below the compiler
+    // may not move loads up past its memory clobber)
+#pragma unroll
+    for (int j = 0; j < DV; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t d = 4 * lane + 256 * j + e;
+            const uint32_t p = d < half ? d : d - half;
+            t[j][e] = cs[d < rot ? p : 0u];
+        }
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < DV; ++j) ss += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
@@ -1264,19 +1276,19 @@ __device__ __forceinline__ void norm_rope_head4(const float *__restrict__ in, co
     }
     __builtin_amdgcn_wave_barrier();
     __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    const uint32_t half = rot / 2;
 #pragma unroll
     for (int j = 0; j < DV; ++j) {
         f4 o = v[j];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
+            // branch-free (a branch would let the compiler sink the angle
+            // load into it): past rot the pair indices stay inside the row
+            // and the unrotated value is kept
             const uint32_t d = 4 * lane + 256 * j + e;
-            if (d < rot) {
-                const uint32_t p = d < half ? d : d - half;          // the pair's index
-                const float2 t = cs[p];
-                const float v0 = buf[p], v1 = buf[p + half];
-                o[e] = d < half ? v0 * t.x - v1 * t.y : v0 * t.y + v1 * t.x;
-            }
+            const uint32_t p = d < half ? d : d - half;              // the pair's index
+            const float v0 = buf[p], v1 = buf[p + half];
+            const float r = d < half ? v0 * t[j][e].x - v1 * t[j][e].y : v0 * t[j][e].y + v1 * t[j][e].x;
+            o[e] = d < rot ? r : o[e];
         }
         *(f4 *)(out + 4 * lane + 256 * j) = o;
     }
@@ -1306,10 +1318,11 @@ __global__ __launch_bounds__(256) void k_batch_qkv_rope4(const float *__restrict
     const uint32_t h = head - num_q;
     const float *k = k_in + t * kv_dim + (size_t)h * D;
     const float *v = k_eq_v ? k : v_in + t * kv_dim + (size_t)h * D;
-    norm_rope_head4<DV>(k, kw, k_cache + (size_t)slot * kv_dim + (size_t)h * D, rot, eps, buf[wave], cs, lane);
+    // V's row is requested before K's norm and rotation run
     f4 vv[DV];
 #pragma unroll
     for (int j = 0; j < DV; ++j) vv[j] = *(const f4 *)(v + 4 * lane + 256 * j);
+    norm_rope_head4<DV>(k, kw, k_cache + (size_t)slot * kv_dim + (size_t)h * D, rot, eps, buf[wave], cs, lane);
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < DV; ++j)
