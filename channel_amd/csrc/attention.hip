@@ -9,8 +9,9 @@
 // over 256 workgroups and a full 4096-entry ring gives each eight chunks.
 // A workgroup serves all of its KV head's GQA query heads from one pass over
 // K and V: each 16-lane row of a wave owns one list entry per chunk (a 1 KB
-// row, 64 contiguous bytes per lane), scores reduce inside the row with
-// DPP, and each wave keeps its own online softmax state.  The four waves
+// row, read as four 256-byte runs, 16 bytes per lane each: lane c holds
+// dims 4c + 64f .. + 3), scores reduce inside the row with DPP, and each
+// wave keeps its own online softmax state.  The four waves
 // merge in LDS into one partial (m, l, sum p*V) per query head; a second
 // kernel merges the partials (online, in a fixed order), writes the output
 // and, optionally, its activation digit planes for the o_proj matvec.  The
@@ -312,36 +313,35 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
         write_empty();
         return;
     }
-    const size_t dim0 = (size_t)kvh * D + (size_t)c * 4 * NF;
+    const size_t dim0 = (size_t)kvh * D + (size_t)c * 4;
 
     bool ok[2 * NSET];                   // set s: buffers 2 s, 2 s + 1
     f4 kr[2 * NSET][NF], vr[2 * NSET][NF];
-    // With two sets, rows past the count load cache row 0 instead (every
-    // load unconditional, so the waits count exactly the loads of the set
-    // being reduced); their scores are masked and their V rows replaced by
-    // zeros in reduce.  One set loads zeros for them.
+    // With two sets, rows past the count load cache row 0 instead: every
+    // load is unconditional, so the waits count exactly the loads of the set
+    // being reduced; their scores and V rows are masked in reduce.  One set
+    // loads zeros for them.
     auto issue = [&](int set, uint32_t t, uint32_t pa, uint32_t pb) {   // chunks t, t + 1 (t < iters)
         const int b0 = 2 * set, b1 = b0 + 1;
         ok[b0] = entry(t) < S;
         ok[b1] = t + 1 < iters && entry(t + 1) < S;
-        const bool all = NSET == 2;
         const size_t ra = (size_t)(ok[b0] ? pa : 0u) * kv_dim + dim0;
         const size_t rb = (size_t)(ok[b1] ? pb : 0u) * kv_dim + dim0;
 #pragma unroll
-        for (int f = 0; f < NF; ++f) kr[b0][f] = all || ok[b0] ? *(const f4 *)(Kc + ra + 4 * f) : f4{0, 0, 0, 0};
+        for (int f = 0; f < NF; ++f) kr[b0][f] = NSET == 2 || ok[b0] ? *(const f4 *)(Kc + ra + 64 * f) : f4{0, 0, 0, 0};
 #pragma unroll
-        for (int f = 0; f < NF; ++f) kr[b1][f] = all || ok[b1] ? *(const f4 *)(Kc + rb + 4 * f) : f4{0, 0, 0, 0};
+        for (int f = 0; f < NF; ++f) kr[b1][f] = NSET == 2 || ok[b1] ? *(const f4 *)(Kc + rb + 64 * f) : f4{0, 0, 0, 0};
 #pragma unroll
-        for (int f = 0; f < NF; ++f) vr[b0][f] = all || ok[b0] ? *(const f4 *)(Vc + ra + 4 * f) : f4{0, 0, 0, 0};
+        for (int f = 0; f < NF; ++f) vr[b0][f] = NSET == 2 || ok[b0] ? *(const f4 *)(Vc + ra + 64 * f) : f4{0, 0, 0, 0};
 #pragma unroll
-        for (int f = 0; f < NF; ++f) vr[b1][f] = all || ok[b1] ? *(const f4 *)(Vc + rb + 4 * f) : f4{0, 0, 0, 0};
+        for (int f = 0; f < NF; ++f) vr[b1][f] = NSET == 2 || ok[b1] ? *(const f4 *)(Vc + rb + 64 * f) : f4{0, 0, 0, 0};
     };
     f4 q[GQA][NF];
     if (!ROPE) {                         // before the K/V rows: the first score needs q
 #pragma unroll
         for (int h = 0; h < GQA; ++h)
 #pragma unroll
-            for (int f = 0; f < NF; ++f) q[h][f] = *(const f4 *)(Q + (size_t)(qh0 + h) * D + c * 4 * NF + 4 * f);
+            for (int f = 0; f < NF; ++f) q[h][f] = *(const f4 *)(Q + (size_t)(qh0 + h) * D + c * 4 + 64 * f);
     }
     if (iters) issue(0, 0, sl[0], sl[1]);
 
@@ -386,7 +386,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
 #pragma unroll
         for (int h = 0; h < GQA; ++h)
 #pragma unroll
-            for (int f = 0; f < NF; ++f) q[h][f] = *(const f4 *)&sh_q[h][c * 4 * NF + 4 * f];
+            for (int f = 0; f < NF; ++f) q[h][f] = *(const f4 *)&sh_q[h][c * 4 + 64 * f];
     }
 
     float M[GQA], L[GQA];
@@ -398,16 +398,37 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
 #pragma unroll
         for (int f = 0; f < NF; ++f) acc[h][f] = f4{0, 0, 0, 0};
     }
-    // one chunk of buffer b into the running state
-    auto reduce = [&](int b, uint32_t ps) {
-        // the new token's row comes from LDS (the cache row just loaded may
-        // predate split 0's write)
-        if (ROPE && ok[b] && ps == new_slot) {
+    // One chunk of buffer b into the running state (fresh: the new token's
+    // row, in the rows that held it).  With two sets the rows that do not count (past the
+    // slot count, or, with ROPE, the new token's row: its cache row may
+    // predate split 0's write, so it is added from LDS after the loop) are
+    // masked with bit operations, not selects: given a select the compiler
+    // branches around the dot and copies the V rows into a second set of
+    // registers at the join, which costs registers the two-set shapes do not have.
+    // One set keeps the selects (its rows past the count hold zeros).
+    bool has_new = false;
+    auto reduce = [&](int b, uint32_t ps, bool fresh = false) {
+        bool use = fresh ? has_new : ok[b];
+        if constexpr (NSET == 2) {
+            if (ROPE && !fresh) {
+                has_new = has_new || (use && ps == new_slot);
+                use = use && ps != new_slot;
+            }
+        } else if (ROPE && use && ps == new_slot) {
+            // one set: the new token's row is replaced in place
 #pragma unroll
             for (int f = 0; f < NF; ++f) {
-                kr[b][f] = *(const f4 *)&sh_k[c * 4 * NF + 4 * f];
-                vr[b][f] = *(const f4 *)&sh_v[c * 4 * NF + 4 * f];
+                kr[b][f] = *(const f4 *)&sh_k[c * 4 + 64 * f];
+                vr[b][f] = *(const f4 *)&sh_v[c * 4 + 64 * f];
             }
+        }
+        uint32_t m = 0;
+        if constexpr (NSET == 2) {
+            m = opaque_mask(use);
+#pragma unroll
+            for (int f = 0; f < NF; ++f)
+                vr[b][f] = f4{mask_f(vr[b][f].x, m), mask_f(vr[b][f].y, m), mask_f(vr[b][f].z, m),
+                              mask_f(vr[b][f].w, m)};
         }
 #pragma unroll
         for (int h = 0; h < GQA; ++h) {
@@ -419,15 +440,19 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
                 d = fmaf(q[h][f].z, kr[b][f].z, d);
                 d = fmaf(q[h][f].w, kr[b][f].w, d);
             }
-            const float sc = ok[b] ? row16_sum(d) * scale : kNegBig;
+            float sc;
+            if constexpr (NSET == 2)
+                sc = __builtin_bit_cast(float, (__builtin_bit_cast(uint32_t, row16_sum(d) * scale) & m) |
+                                                   (__builtin_bit_cast(uint32_t, kNegBig) & ~m));
+            else
+                sc = use ? row16_sum(d) * scale : kNegBig;
             const float mx = rows4_max(sc);
             const float Mn = fmaxf(M[h], mx);
             const float rs = expf(M[h] - Mn);
-            const float p = ok[b] ? expf(sc - Mn) : 0.0f;
+            const float p = NSET == 2 ? mask_f(expf(sc - Mn), m) : (use ? expf(sc - Mn) : 0.0f);
             const float psum = rows4_sum(p);
 #pragma unroll
-            for (int f = 0; f < NF; ++f)
-                acc[h][f] = acc[h][f] * rs + p * (NSET == 1 || ok[b] ? vr[b][f] : f4{0, 0, 0, 0});
+            for (int f = 0; f < NF; ++f) acc[h][f] = acc[h][f] * rs + p * vr[b][f];
             L[h] = L[h] * rs + psum;
             M[h] = Mn;
         }
@@ -474,6 +499,16 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
             pb = nb;
         }
     }
+    // two sets: the new token's entry, from LDS, in the rows whose list
+    // entry it is
+    if (ROPE && NSET == 2 && __any(has_new)) {
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            kr[0][f] = *(const f4 *)&sh_k[c * 4 + 64 * f];
+            vr[0][f] = *(const f4 *)&sh_v[c * 4 + 64 * f];
+        }
+        reduce(0, 0u, true);
+    }
     // rows of the wave hold different entries of the same columns
 #pragma unroll
     for (int h = 0; h < GQA; ++h)
@@ -481,7 +516,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
         for (int f = 0; f < NF; ++f) {
             const f4 t = f4{rows4_sum(acc[h][f].x), rows4_sum(acc[h][f].y), rows4_sum(acc[h][f].z),
                             rows4_sum(acc[h][f].w)};
-            if (r == 0) sh_acc[wave][h][c * NF + f] = t;
+            if (r == 0) sh_acc[wave][h][c + 16 * f] = t;
         }
     if (lane < GQA) {
         sh_m[wave][lane] = M[lane];
