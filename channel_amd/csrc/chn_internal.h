@@ -133,9 +133,11 @@ struct RopeTab {
 };
 // skip (or NULL): the last layer's quiescence flag; when set, x keeps its
 // value and the planes are made from y as it stands (the layer wrote none).
+// xb (or NULL) receives the byte planes of y (the Q8 logits matvec's input,
+// launch_gemv_q8r with planes_ready).
 int launch_norm_planes(hipStream_t s, float *x, const float *r, const float *post_w, const float *w, float *y,
                        uint32_t *xp, uint32_t dim, float eps, float scalar, bool add,
-                       const RopeTab *rope = nullptr, const uint32_t *skip = nullptr);
+                       const RopeTab *rope = nullptr, const uint32_t *skip = nullptr, uint32_t *xb = nullptr);
 
 // The RoPE table entries i = t, t + nt, ... of rt (same arithmetic as the
 // reference's per-element rotation: theta^(2d / rot) by powf, sincosf).
@@ -230,7 +232,7 @@ int launch_gemv_q8(hipStream_t st, const uint32_t *W, const float *x, float *y, 
 // launch_gemv_q8 on the same weights).
 int launch_q8_repack(hipStream_t st, const uint32_t *W, uint32_t rows, uint32_t nb, void *dst);
 int launch_gemv_q8r(hipStream_t st, const void *R, const float *x, float *y, uint32_t M, uint32_t nb,
-                    uint32_t *xp_ws);
+                    uint32_t *xp_ws, bool planes_ready = false);
 size_t topk_ws_bytes(uint32_t V);
 // Optional end of a device-side greedy step, done by the top-64 merge once
 // ids[0] is known: out[gen[1]] = ids[0] (while gen[1] < cap), then gen[1] and
@@ -483,6 +485,57 @@ __device__ __forceinline__ void emit_planes8s(const float (&v)[8], uint32_t *__r
         xp[(size_t)(p * 4 + w) * ws + (size_t)b * bs] = word ^ 0x88888888u;
     }
     if (w == 0) ((float *)xp)[(size_t)XP_WORDS * ws + (size_t)b * bs] = inv;
+}
+
+// Byte planes of the Q8 logits matvec's input: per 32-block, three balanced
+// base-256 digits of a 22-bit fixed-point value, plane word (p, w) (four
+// elements 4w .. 4w + 3) at xp[(p * 8 + w) * nb + b], the block's scale
+// 2^(e_b - 22) at xp[XB_WORDS * nb + b] (as float).
+constexpr int XB_PLANES = 3;
+constexpr int XB_FRAC = 22;
+constexpr int XB_WORDS = XB_PLANES * 8;   // 8 int8x4 words per plane per block
+
+// The byte planes of one 32-block from the four lanes 4k..4k+3 of a wave
+// that hold its values 8q .. 8q + 7 (q = lane & 3); all four lanes must
+// call (with zeros where ok is false), only ok lanes store.  The same
+// arithmetic per element as k_xbytes (eight lanes of four values): the
+// block maximum is order-independent, so the planes are identical.
+__device__ __forceinline__ void emit_bytes8(const float (&v)[8], uint32_t *__restrict__ xp, uint32_t nb,
+                                            uint32_t b, uint32_t q, bool ok) {
+    float m = 0.0f;
+    uint32_t bad = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        m = fmaxf(m, fabsf(v[i]));
+        bad |= !(fabsf(v[i]) <= 3.4028235e38f);     // NaN or Inf
+    }
+    m = fmaxf(m, __shfl_xor(m, 1, 64));
+    m = fmaxf(m, __shfl_xor(m, 2, 64));
+    bad |= __shfl_xor(bad, 1, 64);
+    bad |= __shfl_xor(bad, 2, 64);
+    int e = 0;
+    (void)frexpf(m, &e);
+    float scale = 0.0f, inv = 0.0f;
+    if (bad) {
+        inv = __builtin_nanf("");
+    } else if (m > 0.0f && e > -100) {
+        scale = ldexpf(1.0f, XB_FRAC - e);
+        inv = ldexpf(1.0f, e - XB_FRAC);
+    }
+    uint32_t u[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) u[i] = (uint32_t)((int)rintf((bad ? 0.0f : v[i]) * scale) + 0x808080);
+    if (!ok) return;
+#pragma unroll
+    for (int p = 0; p < XB_PLANES; ++p)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) word |= ((u[4 * h + j] >> (8 * p)) & 0xffu) << (8 * j);
+            xp[(size_t)(p * 8 + 2 * q + h) * nb + b] = word ^ 0x80808080u;
+        }
+    if (q == 0) ((float *)(xp + (size_t)XB_WORDS * nb))[b] = inv;
 }
 
 // Planes in the chn_xplanes layout: plane word (p, w) of block b at

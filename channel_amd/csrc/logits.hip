@@ -16,10 +16,6 @@
 
 namespace chn {
 
-constexpr int XB_PLANES = 3;
-constexpr int XB_FRAC = 22;
-constexpr int XB_WORDS = XB_PLANES * 8;   // 8 int8x4 words per plane per block
-
 size_t xbytes_bytes(uint32_t nb) { return (size_t)nb * (XB_WORDS + 1) * 4; }
 
 // Eight threads per 32-block, one per 4-element weight word.
@@ -253,8 +249,8 @@ __global__ __launch_bounds__(256) void k_q8rmv(const u32x4q *__restrict__ D, con
 }
 
 int launch_gemv_q8r(hipStream_t st, const void *R, const float *x, float *y, uint32_t M, uint32_t nb,
-                    uint32_t *xp_ws) {
-    k_xbytes<<<(8 * nb + 255) / 256, 256, 0, st>>>(x, xp_ws, nb);
+                    uint32_t *xp_ws, bool planes_ready) {
+    if (!planes_ready) k_xbytes<<<(8 * nb + 255) / 256, 256, 0, st>>>(x, xp_ws, nb);
     const uint32_t ngroups = (M + 3) / 4;
     uint32_t grid = (ngroups + 3) / 4;
     if (grid > 1024) grid = 1024;

@@ -273,12 +273,30 @@ __global__ __launch_bounds__(256) void k_greedy_head(const uint32_t *__restrict_
                                                      float *__restrict__ x) {
     __shared__ uint32_t s_first, s_cnt[2];
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    if (t == 0) s_first = kRecallNone;
+    __syncthreads();
+    // The loads come in two rounds, each issued at once: the step state,
+    // the last argmax and the recall ranks; then the input row (its address
+    // needs the token) with the turn boundaries.
     const uint32_t clock = gen[0], count = gen[1], A = gen[3], nb = gen[4];
+    const uint32_t tk0 = topk_ids[0];
+    const uint32_t rec0 = t < 128 ? recall[t] : kRecallNone;   // read whether or not recall is on
+    const uint32_t rec = gen[5] ? rec0 : kRecallNone;
+    const uint32_t token = count == 0 ? gen[2] : tk0;
+    const uint16_t *row = embed + (size_t)token * H;
+    constexpr uint32_t kRowLoads = 4;   // 4 x 4 values per thread: H <= 4096
+    const bool vec = H % 4 == 0 && H <= 4 * 256 * kRowLoads;
+    uint2 rv[kRowLoads];
+    if (vec) {
+#pragma unroll
+        for (uint32_t j = 0; j < kRowLoads; ++j) {
+            const uint32_t i = t + 256 * j;
+            rv[j] = i < H / 4 ? ((const uint2 *)row)[i] : make_uint2(0u, 0u);
+        }
+    }
     const uint32_t W = kRecallStart - A;
     // global window: raw start, snapped to the first boundary at or after it
     const uint32_t raw = clock >= W ? clock - W + 1 : 0;
-    if (t == 0) s_first = kRecallNone;
-    __syncthreads();
     if (raw > A)
         for (uint32_t i = t; i < nb; i += 256)
             if (bounds[i] >= raw) atomicMin(&s_first, i);
@@ -290,11 +308,7 @@ __global__ __launch_bounds__(256) void k_greedy_head(const uint32_t *__restrict_
     for (uint32_t i = t; i < na; i += 256) slots[i] = i;
     for (uint32_t i = t; i < nw; i += 256) slots[na + i] = A + (gs + i - A) % W;
     // recall ranks whose clock has passed, in rank order (two waves, ballots)
-    bool f = false;
-    if (t < 128 && gen[5]) {
-        const uint32_t r = recall[t];
-        f = r != kRecallNone && r <= clock;
-    }
+    const bool f = rec != kRecallNone && rec <= clock;
     const uint64_t bal = __ballot(f);
     if (lane == 0 && wave < 2) s_cnt[wave] = (uint32_t)__popcll(bal);
     __syncthreads();
@@ -309,7 +323,6 @@ __global__ __launch_bounds__(256) void k_greedy_head(const uint32_t *__restrict_
     uint32_t *sl = slots + kSlotsMax;
     for (uint32_t i = t; i < nas; i += 256) sl[i] = raws + i;
     for (uint32_t i = t; i < nsw; i += 256) sl[nas + i] = A + (ss + i - A) % W;
-    const uint32_t token = count == 0 ? gen[2] : topk_ids[0];
     if (t == 0) {
         step[0] = clock;
         step[1] = clock < A ? clock : A + (clock - A) % W;
@@ -317,8 +330,18 @@ __global__ __launch_bounds__(256) void k_greedy_head(const uint32_t *__restrict_
         step[3] = nas + nsw;
         tok[0] = token;
     }
-    const uint16_t *row = embed + (size_t)token * H;
-    for (uint32_t i = t; i < H; i += 256) x[i] = __builtin_bit_cast(float, (uint32_t)row[i] << 16) * scale;
+    auto bf = [&](uint32_t b16) { return __builtin_bit_cast(float, b16 << 16) * scale; };
+    if (vec) {
+#pragma unroll
+        for (uint32_t j = 0; j < kRowLoads; ++j) {
+            const uint32_t i = t + 256 * j;
+            if (i < H / 4)
+                *(float4 *)(x + 4 * i) = make_float4(bf(rv[j].x & 0xffffu), bf(rv[j].x >> 16), bf(rv[j].y & 0xffffu),
+                                                     bf(rv[j].y >> 16));
+        }
+    } else {
+        for (uint32_t i = t; i < H; i += 256) x[i] = bf(row[i]);
+    }
 }
 
 // ---- the decode sequence (recordLayerDirect / recordForwardGraph,
@@ -382,11 +405,13 @@ static int record_decode(chn_model *m, bool with_logits, const GreedyTail *tail 
     }
     // the last layer's FFN residual (into x) and the final norm
     const auto &last = m->L[c.num_layers - 1];
+    // (its byte planes are the logits matvec's input)
     R_(launch_norm_planes(s, xa, m->mlp_out, last.has_post_ffn ? last.post_ffn : nullptr, m->final_norm, m->normed,
-                          xp, H, eps, last.scalar, true, nullptr,
-                          gated(c.num_layers - 1) ? m->qflags + c.num_layers - 1 : nullptr));
+                          nullptr, H, eps, last.scalar, true, nullptr,
+                          gated(c.num_layers - 1) ? m->qflags + c.num_layers - 1 : nullptr,
+                          with_logits ? m->mv_ws : nullptr));
     if (with_logits) {
-        R_(launch_gemv_q8r(s, m->embed_q8, m->normed, m->logits, c.vocab_size, H / 32, m->mv_ws));
+        R_(launch_gemv_q8r(s, m->embed_q8, m->normed, m->logits, c.vocab_size, H / 32, m->mv_ws, true));
         R_(launch_topk64(s, m->logits, c.vocab_size, m->topk_ids, m->topk_vals, m->topk_ws, tail));
     }
 #undef R_

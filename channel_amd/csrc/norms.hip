@@ -350,7 +350,8 @@ __global__ __launch_bounds__(1024) void k_norm_planes(float *__restrict__ x, con
                                                       const float *__restrict__ pw, const float *__restrict__ w,
                                                       float *__restrict__ y, uint32_t *__restrict__ xp, uint32_t dim,
                                                       float eps, float scalar, RopeTab rt,
-                                                      const uint32_t *__restrict__ skip) {
+                                                      const uint32_t *__restrict__ skip,
+                                                      uint32_t *__restrict__ xb) {
     __shared__ float sh[16];
     const uint32_t t = threadIdx.x;
     if (rt.tab) rope_table(rt, t, blockDim.x);
@@ -358,10 +359,11 @@ __global__ __launch_bounds__(1024) void k_norm_planes(float *__restrict__ x, con
     if (skip && *skip) {
         // the last layer was quiescent: x keeps its value and y (the normed
         // row the reference's logits read) is whatever was last written
-        if (xp) {
+        if (xp || xb) {
             float yv[8];
             load8(y, t, ok, yv);
-            emit_planes8(yv, xp, dim / 32, t >> 2, t & 3, ok);
+            if (xp) emit_planes8(yv, xp, dim / 32, t >> 2, t & 3, ok);
+            if (xb) emit_bytes8(yv, xb, dim / 32, t >> 2, t & 3, ok);
         }
         return;
     }
@@ -395,18 +397,19 @@ __global__ __launch_bounds__(1024) void k_norm_planes(float *__restrict__ x, con
     for (int i = 0; i < 8; ++i) yv[i] = (xv[i] * inv) * wv[i];
     if (ok) store8(y, t, yv);
     if (xp) emit_planes8(yv, xp, dim / 32, t >> 2, t & 3, ok);
+    if (xb) emit_bytes8(yv, xb, dim / 32, t >> 2, t & 3, ok);
 }
 
 int launch_norm_planes(hipStream_t s, float *x, const float *r, const float *post_w, const float *w, float *y,
                        uint32_t *xp, uint32_t dim, float eps, float scalar, bool add, const RopeTab *rope,
-                       const uint32_t *skip) {
+                       const uint32_t *skip, uint32_t *xb) {
     if (dim % 32 != 0 || dim > 8192) return CHN_E_UNSUPPORTED;
     if (rope && (rope->rot[0] > 2 * kRopePairs || rope->rot[1] > 2 * kRopePairs)) return CHN_E_UNSUPPORTED;
     const uint32_t nt = ((dim / 8 + 63) / 64) * 64;
     const RopeTab rt = rope ? *rope : RopeTab{nullptr, nullptr, {0.0f, 0.0f}, {0u, 0u}};
-    if (!add) k_norm_planes<false, false><<<1, nt, 0, s>>>(x, r, post_w, w, y, xp, dim, eps, scalar, rt, skip);
-    else if (post_w) k_norm_planes<true, true><<<1, nt, 0, s>>>(x, r, post_w, w, y, xp, dim, eps, scalar, rt, skip);
-    else k_norm_planes<false, true><<<1, nt, 0, s>>>(x, r, post_w, w, y, xp, dim, eps, scalar, rt, skip);
+    if (!add) k_norm_planes<false, false><<<1, nt, 0, s>>>(x, r, post_w, w, y, xp, dim, eps, scalar, rt, skip, xb);
+    else if (post_w) k_norm_planes<true, true><<<1, nt, 0, s>>>(x, r, post_w, w, y, xp, dim, eps, scalar, rt, skip, xb);
+    else k_norm_planes<false, true><<<1, nt, 0, s>>>(x, r, post_w, w, y, xp, dim, eps, scalar, rt, skip, xb);
     return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
 }
 
