@@ -15,6 +15,7 @@ import pytest
 import channel_amd as ca
 from channel_amd.model import Model
 from gpu_util import assert_topk_valid, rel_err, say
+import oracle
 from oracle import model as OM
 from oracle import ring as OR
 
@@ -190,6 +191,35 @@ def test_synthetic_model_token_path(ctx):
             tok = int(t1)
             row = ctx.download(p.value + tok * H * 2, np.uint16, H)
             x_in = OM.bf16_to_f32(row) * np.float32(np.sqrt(np.float32(H)))
+
+
+def test_decode_logits_equal_standalone_q8(ctx):
+    """The decode step's final norm writes the byte planes of the normed row
+    that the Q8 logits matvec reads (no separate planes pass).  The step's
+    top-64 must equal, bit for bit, chn_gemv_q8r + chn_topk64 run on the
+    same normed row, which make their planes with the standalone pass."""
+    import ctypes
+    cfg = dict(CFG, num_layers=2, layer_full=[1, 0])
+    H, V = cfg["hidden_size"], cfg["vocab_size"]
+    with Model.synthetic(ctx, cfg, 4321) as m:
+        p = ctypes.c_void_p()
+        assert ca.lib.chn_model_embedding_bf16(m.handle, ctypes.byref(p)) == 0 and p.value
+        emb = ctx.download(p.value, np.uint16, V * H).reshape(V, H)
+        E8 = ctx.upload(oracle.quantize_q8(emb).ravel())
+        R = ctx.alloc(ca.q8_bytes(V, H))
+        ctx.call("chn_q8_repack", E8, V, H, R)
+        y, ids_d, vals_d = ctx.alloc(V * 4), ctx.alloc(256), ctx.alloc(256)
+        tok = 77
+        for clock in range(3):
+            active, sliding = OM.slot_lists(clock, WINDOW)
+            say(f"decode step clock={clock}, logits of the normed row")
+            t, ids, vals = m.forward_token_id(tok, clock, clock, active, sliding)
+            _, normed = m.read_state()
+            ctx.call("chn_gemv_q8r", R, ctx.upload(normed), y, V, H)
+            ctx.call("chn_topk64", y, V, ids_d, vals_d)
+            assert np.array_equal(ids, ctx.download(ids_d, np.uint32, 64))
+            assert np.array_equal(vals.view(np.uint32), ctx.download(vals_d, np.uint32, 64))
+            tok = int(t)
 
 
 def test_eager_launches_match_graph(ctx):
