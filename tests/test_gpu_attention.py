@@ -80,6 +80,34 @@ def test_decode_attn_zero_slots_and_count_from_device(ctx):
     assert rel_err(f32_host(ctx, out, H * D), want) < TOL
 
 
+@pytest.mark.parametrize("gqa,D,S", [(2, 256, 700), (2, 256, 4000), (4, 256, 300), (2, 512, 130)])
+def test_decode_attn_ignores_unlisted_rows(ctx, gqa, D, S):
+    """Cache rows that the first S list entries do not name hold NaN,
+    slot 0 among them: rows past the count are loaded from slot 0 and
+    masked, so the output is finite and equals the oracle's over the listed
+    rows."""
+    nslot, H = 4096, 8
+    kv_dim = H // gqa * D
+    rng = np.random.default_rng(S + gqa)
+    K = rng.standard_normal((nslot, kv_dim)).astype(np.float32)
+    V = rng.standard_normal((nslot, kv_dim)).astype(np.float32)
+    perm = (rng.permutation(nslot - 1) + 1).astype(np.uint32)   # slot 0 never listed
+    listed = perm[:S]
+    unlisted = np.setdiff1d(np.arange(nslot), listed)
+    K[unlisted] = np.nan
+    V[unlisted] = np.nan
+    q = (rng.standard_normal(H * D) * 0.1).astype(np.float32)
+    Kc, Vc, Q = ctx.upload(K.ravel()), ctx.upload(V.ravel()), ctx.upload(q)
+    slots, ns = u32_dev(ctx, np.concatenate([listed, np.zeros(nslot - S, np.uint32)])), u32_dev(ctx, [S])
+    out = ctx.alloc(H * D * 4)
+    say(f"decode_attn NaN outside the list: gqa={gqa} D={D} S={S}")
+    ctx.call("chn_decode_attn", Q, Kc, Vc, slots, ns, nslot, H, D, kv_dim, gqa, 1.0, out)
+    got = f32_host(ctx, out, H * D)
+    assert np.all(np.isfinite(got))
+    want = oracle.decode_attn(q, K.ravel(), V.ravel(), listed, H, D, kv_dim, gqa, 1.0)
+    assert rel_err(got, want) < TOL
+
+
 @pytest.mark.parametrize("nq,nkv,D,rot,k_eq_v,clock", [
     (16, 8, 256, 256, False, 4095),
     (8, 2, 256, 128, False, 77),     # partial rotary: suffix copied normed
