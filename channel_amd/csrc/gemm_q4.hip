@@ -20,6 +20,7 @@
 #include "chn_internal.h"
 
 #include <type_traits>
+#include <utility>
 
 namespace chn {
 
@@ -244,6 +245,244 @@ __global__ __launch_bounds__(256, 2) void k_q4gemm(GemmArgs a) {
                 if (t < a.n_tok && n < a.M) {
                     float v = acc[0][mt][nt][i];
                     if (NMAT == 2) v = gelu_tanh(v) * acc[NMAT - 1][mt][nt][i];
+                    if (a.Yb) a.Yb[(size_t)t * a.M + n] = (__bf16)v;
+                    else a.Y[(size_t)t * a.M + n] = v;
+                }
+            }
+        }
+}
+
+// f(std::integral_constant<int, i>) for i = 0 .. N-1 (compile-time indices,
+// e.g. for the immediate offsets of asm LDS reads).
+template <typename F, int... I>
+__host__ __device__ __forceinline__ void static_for_(F &&f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__host__ __device__ __forceinline__ void static_for(F &&f) {
+    static_for_(f, std::make_integer_sequence<int, N>{});
+}
+
+// ---------------------------------------------------------------------------
+// The fused gate/up (two matrices, GELU-tanh * up epilogue) on 256-token x
+// 128-feature tiles: eight waves (two per SIMD, one workgroup per CU), wave
+// (wr, wc) a 64-token x 64-feature block of both matrices.  Every operand
+// travels by DMA (global_load_lds) straight into LDS, so no register holds
+// a load in flight and the waits are explicit vmcnt immediates:
+//   X(j)      256 rows x 128 B of bf16 (16-byte chunks XOR-swizzled by
+//             row), two slots: one step ahead (X is read from L2);
+//   Wraw(j)   the raw Q4 bytes of both matrices (nibble words, scales),
+//             three slots: two steps ahead, since the weights' first
+//             touch comes from HBM.
+// Each step the 512 threads dequantize Wraw(j) (one 32-block each) into the
+// bf16 weight tile; all LDS reads of the loop are asm and pinned after the
+// waits, and the barriers carry no vmcnt wait.  K % 64 == 0.
+// At 512 x 3840 -> 2 x 15360: 159.6 us against 162-164 us for the
+// register-staged k_q4gemm<2> (128-token tiles, operands one step ahead),
+// which still serves K % 64 != 0.
+template <bool REP>
+struct Gemm2dCfg {
+    static constexpr int BT = 256, GK = 64, SX = 2, SW = 3;
+    static constexpr int LROW = GK * 2 + 16;               // weight tile row stride (padded)
+    static constexpr int XSLOT = BT * GK * 2;              // 32 KB of X per step
+    static constexpr int QSLOT = 2 * 128 * 2 * 16;         // nibble words per step, [m][blk][row]
+    static constexpr int SWORDS = REP ? 2 * 128 : 2 * 128 * 2;   // scale words, REP [m][row] else [m][blk][row]
+    static constexpr int SSLOT = SWORDS * 4;
+    static constexpr int OFF_Q = SX * XSLOT, OFF_S = OFF_Q + SW * QSLOT, OFF_W = OFF_S + SW * SSLOT;
+    static constexpr int OFF_D = OFF_W + 2 * GN * LROW;    // 256 B written by waves without a scale load
+    static constexpr int LDS = OFF_D + 256;
+    static constexpr int NS = SWORDS / 64;                 // scale instructions (one per wave < NS)
+    static constexpr int PER = 6;                          // DMA instructions per wave and step: 4 X, 1 nibble, 1 scale/dummy
+    static constexpr int PER_W = 2;
+    static_assert(NS <= 8, "one scale instruction per wave");
+};
+
+template <bool REP>
+__global__ __launch_bounds__(512) void k_q4gemm2d(GemmArgs a) {
+    using C = Gemm2dCfg<REP>;
+    constexpr int NMAT = 2;
+    __shared__ __attribute__((aligned(16))) unsigned char sm[C::LDS];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr = wave >> 1, wc = wave & 1;
+    const uint32_t n0 = blockIdx.x * GN, t0 = blockIdx.y * C::BT;
+    const uint32_t K = a.K, nb = K / 32, steps = K / C::GK;
+    const uint32_t smb = lds_addr(sm);
+
+    // ---- X by DMA: 32 one-KB instructions per step, four per wave
+    // (a dependent constant inside a DMA builtin's arguments makes the host
+    // pass drop the kernel's launch stub: local copies)
+    constexpr uint32_t GK = C::GK;
+    const __bf16 *Xb = a.X;
+    uint32_t xe[4];                                            // element offsets (n_tok * K < 2^32)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int q = (i * 8 + wave) * 64 + lane;              // chunk position in the slot
+        const int r = q >> 3, c = (q & 7) ^ ((r ^ (r >> 3)) & 7);
+        xe[i] = (t0 + r < a.n_tok ? t0 + r : a.n_tok - 1) * K + c * 8;
+    }
+    auto issue_x = [&](uint32_t j) {                           // X(j) -> slot j % SX (j clamped)
+        const uint32_t jj = j < steps ? j : steps - 1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_global_load_lds(Xb + (xe[i] + jj * GK),
+                                             (lds_t *)(sm + (j % C::SX) * C::XSLOT + (i * 8 + wave) * 1024), 16, 0,
+                                             0);
+    };
+    // ---- raw weights by DMA: nibble chunk `tid` ([m][blk][row]); scale
+    // instruction `wave` (waves >= NS load 256 B of X into a dummy area)
+    const unsigned char *wq_g, *ws_g;
+    uint32_t ws_lds, ws_slot, ws_step;
+    const uint32_t wq_step = REP ? 32 : 40;
+    {
+        const int m = tid >> 8, blk = (tid >> 7) & 1, row = tid & 127;
+        const uint32_t n = n0 + row < a.M ? n0 + row : a.M - 1;
+        const unsigned char *W = (const unsigned char *)(m == 0 ? a.W0 : a.W1);
+        wq_g = REP ? W + ((size_t)n * nb + blk) * 16 : W + ((size_t)n * nb + blk) * 20 + 4;
+        if (wave < C::NS) {
+            const int sq = wave * 64 + lane;                   // REP [m][row], else [m][blk][row]
+            const int sm_ = REP ? sq >> 7 : sq >> 8, sblk = REP ? 0 : (sq >> 7) & 1, srow = sq & 127;
+            const uint32_t ns = n0 + srow < a.M ? n0 + srow : a.M - 1;
+            const unsigned char *Ws = (const unsigned char *)(sm_ == 0 ? a.W0 : a.W1);
+            ws_g = REP ? Ws + (size_t)a.M * nb * 16 + (size_t)ns * nb * 2 : Ws + ((size_t)ns * nb + sblk) * 20;
+            ws_lds = C::OFF_S + wave * 256;
+            ws_slot = C::SSLOT;
+            ws_step = REP ? 4 : 40;
+        } else {
+            ws_g = (const unsigned char *)a.X + (lane * 4) % 128;
+            ws_lds = C::OFF_D;
+            ws_slot = 0;
+            ws_step = 0;
+        }
+    }
+    auto issue_w = [&](uint32_t j) {                           // Wraw(j) -> slot j % SW (j clamped)
+        const uint32_t jj = j < steps ? j : steps - 1;
+        __builtin_amdgcn_global_load_lds(wq_g + (size_t)jj * wq_step,
+                                         (lds_t *)(sm + C::OFF_Q + (j % C::SW) * C::QSLOT + wave * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(ws_g + (size_t)jj * ws_step,
+                                         (lds_t *)(sm + ws_lds + (j % C::SW) * ws_slot), 4, 0, 0);
+    };
+
+    // ---- dequantization: thread tid -> matrix m, block blk, row of nibble chunk tid
+    const int d_m = tid >> 8, d_blk = (tid >> 7) & 1, d_row = tid & 127;
+    const uint32_t dq_q = smb + C::OFF_Q + tid * 16;
+    const uint32_t dq_s = smb + C::OFF_S + (REP ? ((d_m << 7) | d_row) : tid) * 4;
+    const uint32_t dq_w = C::OFF_W + (d_m * GN + d_row) * C::LROW + d_blk * 64;
+    auto dequant = [&](auto slot_) {
+        constexpr int SL = decltype(slot_)::value;
+        u32x4v q = lds_read<u32x4v, SL * C::QSLOT>(dq_q);
+        uint32_t sw = lds_read<uint32_t, SL * C::SSLOT>(dq_s);
+        lds_wait();
+        lds_pin(q);
+        lds_pin(sw);
+        const float sc = f16_lo_to_f32(REP ? sw >> (16 * d_blk) : sw), ms = -8.0f * sc;
+        unsigned char *dst = sm + dq_w;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) *(u32x4v *)(dst + 16 * w) = dequant_word_bf16(REP ? q[w] ^ 0x88888888u : q[w], sc, ms);
+    };
+
+    // ---- fragment addresses: A (row r, chunk (4 kk + lane / 16) ^ sw(r)), B
+    uint32_t xa[2][4];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            const int r = wr * 64 + mt * 16 + (lane & 15);
+            const int c = (4 * kk + (lane >> 4)) ^ ((r ^ (r >> 3)) & 7);
+            xa[kk][mt] = smb + r * 128 + c * 16;
+        }
+    const uint32_t wa = smb + C::OFF_W + (wc * 64 + (lane & 15)) * C::LROW + (lane >> 4) * 16;
+
+    f32x4 acc[NMAT][4][4];
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[m][i][j] = f32x4{0, 0, 0, 0};
+
+    // issue order Wraw(0), X(0), Wraw(1): at every step the wait for X(j)
+    // leaves exactly the PER_W younger instructions of Wraw(j+1) in flight
+    issue_w(0);
+    __asm__ volatile("" ::: "memory");
+    issue_x(0);
+    __asm__ volatile("" ::: "memory");
+    issue_w(1);
+    __asm__ volatile("" ::: "memory");
+
+    // step j: X slot j % 2 (XS), Wraw slot j % 3 (WS)
+    auto step = [&](uint32_t j, auto xs_, auto ws_) {
+        constexpr int XS = decltype(xs_)::value;
+        wait_vm_lgkm0<C::PER_W>();                             // X(j) and Wraw(j) landed
+        bare_barrier();                                        // ... for every wave; step j-1's reads done
+        issue_x(j + 1);                                        // into the X slot step j-1 read
+        __asm__ volatile("" ::: "memory");
+        issue_w(j + 2);                                        // into the Wraw slot step j-1 dequantized
+        __asm__ volatile("" ::: "memory");
+        dequant(ws_);
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this thread's tile writes done
+        bare_barrier();                                        // ... every thread's (no vmcnt wait)
+        static_for<2>([&](auto kk_) {
+            constexpr int KK = decltype(kk_)::value;
+            bf16x8 af[4], bfm[NMAT][4];
+            static_for<4>([&](auto mt_) {
+                constexpr int MT = decltype(mt_)::value;
+                af[MT] = lds_read<bf16x8, XS * C::XSLOT>(xa[KK][MT]);
+            });
+            static_for<NMAT * 4>([&](auto i_) {
+                constexpr int I = decltype(i_)::value, M = I / 4, NT = I % 4;
+                bfm[M][NT] = lds_read<bf16x8, M * GN * C::LROW + NT * 16 * C::LROW + KK * 64>(wa);
+            });
+            lds_wait();
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) lds_pin(af[mt]);
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+                for (int nt = 0; nt < 4; ++nt) lds_pin(bfm[m][nt]);
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                    for (int nt = 0; nt < 4; ++nt)
+                        acc[m][mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bfm[m][nt], acc[m][mt][nt],
+                                                                                  0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);                 // one K half's fragments live at a time
+        });
+    };
+    // six steps per iteration cover every (X slot, Wraw slot) pair
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    uint32_t j = 0;
+    for (; j + 6 <= steps; j += 6) {
+        step(j, I0{}, I0{});
+        step(j + 1, I1{}, I1{});
+        step(j + 2, I0{}, I2{});
+        step(j + 3, I1{}, I0{});
+        step(j + 4, I0{}, I1{});
+        step(j + 5, I1{}, I2{});
+    }
+    if (j < steps) step(j, I0{}, I0{});
+    if (j + 1 < steps) step(j + 1, I1{}, I1{});
+    if (j + 2 < steps) step(j + 2, I0{}, I2{});
+    if (j + 3 < steps) step(j + 3, I1{}, I0{});
+    if (j + 4 < steps) step(j + 4, I0{}, I1{});
+    wait_vm_lgkm0<0>();                                        // no DMA may land after the workgroup ends
+
+    // epilogue: lane holds rows (tokens) (lane>>4)*4 + i, column (feature) lane & 15
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+            const uint32_t n = n0 + wc * 64 + nt * 16 + (lane & 15);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t t = t0 + wr * 64 + mt * 16 + (lane >> 4) * 4 + i;
+                if (t < a.n_tok && n < a.M) {
+                    const float v = gelu_tanh(acc[0][mt][nt][i]) * acc[1][mt][nt][i];
                     if (a.Yb) a.Yb[(size_t)t * a.M + n] = (__bf16)v;
                     else a.Y[(size_t)t * a.M + n] = v;
                 }
@@ -687,6 +926,13 @@ int launch_q4gemm(chn_ctx *ctx, int nmat, const float *X, const uint32_t *W0, co
         CHN_LAUNCHED(ctx, "k_to_bf16");
     }
     a.Yb = Yb;
+    if (nmat == 2 && K % 64 == 0) {
+        const dim3 g2((M + GN - 1) / GN, (n_tok + 255) / 256);
+        if (repacked) k_q4gemm2d<true><<<g2, 512, 0, ctx->stream>>>(a);
+        else k_q4gemm2d<false><<<g2, 512, 0, ctx->stream>>>(a);
+        CHN_LAUNCHED(ctx, "k_q4gemm2d");
+        return CHN_OK;
+    }
     dim3 grid((M + GN - 1) / GN, (n_tok + GT - 1) / GT);
     if (repacked) {
         if (nmat == 1) k_q4gemm<1, true, kGemmKB><<<grid, 256, 0, ctx->stream>>>(a);

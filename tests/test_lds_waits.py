@@ -1,4 +1,4 @@
-"""The pipelined prefill GEMM and the prefill attention read DMA-filled LDS
+"""The pipelined prefill GEMMs and the prefill attention read DMA-filled LDS
 with asm loads whose completion the compiler does not track; this compiles
 the kernels for gfx950 and checks that no instruction touches a load's
 registers before the wait that retires it (a copy made earlier copies a
@@ -24,6 +24,9 @@ def test_gemm_lds_waits(tmp_path):
     import lds_wait_check
     res = lds_wait_check.check_file(str(out), "k_q4gemm_p")
     assert res, "no pipelined GEMM kernel found in the assembly"
+    res2 = lds_wait_check.check_file(str(out), "k_q4gemm2d")
+    assert len(res2) == 2, "expected both layouts of the DMA-fed gate/up"
+    res.update(res2)
     bad = {f: h for f, h in res.items() if h}
     assert not bad, bad
 
