@@ -272,28 +272,29 @@ __host__ __device__ __forceinline__ void static_for(F &&f) {
 //   X(j)      256 rows x 128 B of bf16 (16-byte chunks XOR-swizzled by
 //             row), two slots: one step ahead (X is read from L2);
 //   Wraw(j)   the raw Q4 bytes of both matrices (nibble words, scales),
-//             three slots: two steps ahead, since the weights' first
-//             touch comes from HBM.
-// Each step the 512 threads dequantize Wraw(j) (one 32-block each) into the
-// bf16 weight tile; all LDS reads of the loop are asm and pinned after the
-// waits, and the barriers carry no vmcnt wait.  K % 64 == 0.
-// At 512 x 3840 -> 2 x 15360: 159.6 us against 162-164 us for the
+//             two slots: fetched two steps before their tile is
+//             multiplied (dequantized one step before).
+// Each step the 512 threads dequantize the next step's Wraw (one 32-block
+// each) into the other of two bf16 weight tiles while the current one is
+// multiplied, so a step has one barrier; all LDS reads of the loop are asm
+// and pinned after the waits.  K % 64 == 0.
+// At 512 x 3840 -> 2 x 15360: 137.8 us against 162-164 us for the
 // register-staged k_q4gemm<2> (128-token tiles, operands one step ahead),
-// which still serves K % 64 != 0.
+// which still serves K % 64 != 0, and 159.6 us for this kernel with one
+// tile, dequantized between two barriers per step.
 template <bool REP>
 struct Gemm2dCfg {
-    static constexpr int BT = 256, GK = 64, SX = 2, SW = 3;
+    static constexpr int BT = 256, GK = 64, SX = 2, SW = 2;
     static constexpr int LROW = GK * 2 + 16;               // weight tile row stride (padded)
     static constexpr int XSLOT = BT * GK * 2;              // 32 KB of X per step
     static constexpr int QSLOT = 2 * 128 * 2 * 16;         // nibble words per step, [m][blk][row]
     static constexpr int SWORDS = REP ? 2 * 128 : 2 * 128 * 2;   // scale words, REP [m][row] else [m][blk][row]
     static constexpr int SSLOT = SWORDS * 4;
     static constexpr int OFF_Q = SX * XSLOT, OFF_S = OFF_Q + SW * QSLOT, OFF_W = OFF_S + SW * SSLOT;
-    static constexpr int OFF_D = OFF_W + 2 * GN * LROW;    // 256 B written by waves without a scale load
+    static constexpr int WTILE = 2 * GN * LROW;             // bf16 tiles of both matrices
+    static constexpr int OFF_D = OFF_W + 2 * WTILE;        // 256 B written by waves without a scale load
     static constexpr int LDS = OFF_D + 256;
     static constexpr int NS = SWORDS / 64;                 // scale instructions (one per wave < NS)
-    static constexpr int PER = 6;                          // DMA instructions per wave and step: 4 X, 1 nibble, 1 scale/dummy
-    static constexpr int PER_W = 2;
     static_assert(NS <= 8, "one scale instruction per wave");
 };
 
@@ -369,7 +370,7 @@ __global__ __launch_bounds__(512) void k_q4gemm2d(GemmArgs a) {
     const uint32_t dq_q = smb + C::OFF_Q + tid * 16;
     const uint32_t dq_s = smb + C::OFF_S + (REP ? ((d_m << 7) | d_row) : tid) * 4;
     const uint32_t dq_w = C::OFF_W + (d_m * GN + d_row) * C::LROW + d_blk * 64;
-    auto dequant = [&](auto slot_) {
+    auto dequant = [&](auto slot_) {                           // Wraw slot SL -> bf16 tile SL
         constexpr int SL = decltype(slot_)::value;
         u32x4v q = lds_read<u32x4v, SL * C::QSLOT>(dq_q);
         uint32_t sw = lds_read<uint32_t, SL * C::SSLOT>(dq_s);
@@ -377,7 +378,7 @@ __global__ __launch_bounds__(512) void k_q4gemm2d(GemmArgs a) {
         lds_pin(q);
         lds_pin(sw);
         const float sc = f16_lo_to_f32(REP ? sw >> (16 * d_blk) : sw), ms = -8.0f * sc;
-        unsigned char *dst = sm + dq_w;
+        unsigned char *dst = sm + dq_w + SL * C::WTILE;
 #pragma unroll
         for (int w = 0; w < 4; ++w) *(u32x4v *)(dst + 16 * w) = dequant_word_bf16(REP ? q[w] ^ 0x88888888u : q[w], sc, ms);
     };
@@ -402,27 +403,29 @@ __global__ __launch_bounds__(512) void k_q4gemm2d(GemmArgs a) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) acc[m][i][j] = f32x4{0, 0, 0, 0};
 
-    // issue order Wraw(0), X(0), Wraw(1): at every step the wait for X(j)
-    // leaves exactly the PER_W younger instructions of Wraw(j+1) in flight
+    // Wraw(0) is dequantized into tile 0 first; then each step j waits for
+    // X(j) and Wraw(j+1) (issued together at step j-1), passes one barrier,
+    // issues X(j+1) and Wraw(j+2), dequantizes Wraw(j+1) into tile (j+1) % 2
+    // and multiplies tile j % 2 with X slot j % 2: the dequantization of
+    // the next step overlaps the other waves' MFMAs, with no second barrier.
     issue_w(0);
-    __asm__ volatile("" ::: "memory");
+    wait_vm_lgkm0<0>();
+    bare_barrier();                                            // every wave's share of Wraw(0)
+    dequant(std::integral_constant<int, 0>{});
     issue_x(0);
     __asm__ volatile("" ::: "memory");
     issue_w(1);
     __asm__ volatile("" ::: "memory");
 
-    // step j: X slot j % 2 (XS), Wraw slot j % 3 (WS)
-    auto step = [&](uint32_t j, auto xs_, auto ws_) {
-        constexpr int XS = decltype(xs_)::value;
-        wait_vm_lgkm0<C::PER_W>();                             // X(j) and Wraw(j) landed
-        bare_barrier();                                        // ... for every wave; step j-1's reads done
+    auto step = [&](uint32_t j, auto xs_) {
+        constexpr int XS = decltype(xs_)::value;               // == j % 2: X slot and tile of step j
+        wait_vm_lgkm0<0>();                                    // X(j), Wraw(j+1); this wave's tile writes
+        bare_barrier();                                        // ... every wave's; step j-1's reads done
         issue_x(j + 1);                                        // into the X slot step j-1 read
         __asm__ volatile("" ::: "memory");
         issue_w(j + 2);                                        // into the Wraw slot step j-1 dequantized
         __asm__ volatile("" ::: "memory");
-        dequant(ws_);
-        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this thread's tile writes done
-        bare_barrier();                                        // ... every thread's (no vmcnt wait)
+        dequant(std::integral_constant<int, 1 - XS>{});        // Wraw(j+1) -> tile (j+1) % 2
         static_for<2>([&](auto kk_) {
             constexpr int KK = decltype(kk_)::value;
             bf16x8 af[4], bfm[NMAT][4];
@@ -432,7 +435,7 @@ __global__ __launch_bounds__(512) void k_q4gemm2d(GemmArgs a) {
             });
             static_for<NMAT * 4>([&](auto i_) {
                 constexpr int I = decltype(i_)::value, M = I / 4, NT = I % 4;
-                bfm[M][NT] = lds_read<bf16x8, M * GN * C::LROW + NT * 16 * C::LROW + KK * 64>(wa);
+                bfm[M][NT] = lds_read<bf16x8, XS * C::WTILE + M * GN * C::LROW + NT * 16 * C::LROW + KK * 64>(wa);
             });
             lds_wait();
 #pragma unroll
@@ -452,24 +455,12 @@ __global__ __launch_bounds__(512) void k_q4gemm2d(GemmArgs a) {
             __builtin_amdgcn_sched_barrier(0);                 // one K half's fragments live at a time
         });
     };
-    // six steps per iteration cover every (X slot, Wraw slot) pair
-    using I0 = std::integral_constant<int, 0>;
-    using I1 = std::integral_constant<int, 1>;
-    using I2 = std::integral_constant<int, 2>;
     uint32_t j = 0;
-    for (; j + 6 <= steps; j += 6) {
-        step(j, I0{}, I0{});
-        step(j + 1, I1{}, I1{});
-        step(j + 2, I0{}, I2{});
-        step(j + 3, I1{}, I0{});
-        step(j + 4, I0{}, I1{});
-        step(j + 5, I1{}, I2{});
+    for (; j + 1 < steps; j += 2) {
+        step(j, std::integral_constant<int, 0>{});
+        step(j + 1, std::integral_constant<int, 1>{});
     }
-    if (j < steps) step(j, I0{}, I0{});
-    if (j + 1 < steps) step(j + 1, I1{}, I1{});
-    if (j + 2 < steps) step(j + 2, I0{}, I2{});
-    if (j + 3 < steps) step(j + 3, I1{}, I0{});
-    if (j + 4 < steps) step(j + 4, I0{}, I1{});
+    if (j < steps) step(j, std::integral_constant<int, 0>{});
     wait_vm_lgkm0<0>();                                        // no DMA may land after the workgroup ends
 
     // epilogue: lane holds rows (tokens) (lane>>4)*4 + i, column (feature) lane & 15
