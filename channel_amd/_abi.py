@@ -35,6 +35,7 @@ PROTOTYPES = {
     "chn_init": (c_int, [c_int, P(c_void_p)]),
     "chn_destroy": (None, [c_void_p]),
     "chn_last_error": (ctypes.c_char_p, [c_void_p]),
+    "chn_device_name": (ctypes.c_char_p, [c_void_p]),
     "chn_alloc": (c_int, [c_void_p, c_size, P(c_void_p)]),
     "chn_free": (c_int, [c_void_p, c_void_p]),
     "chn_upload": (c_int, [c_void_p, c_void_p, c_void_p, c_size]),
@@ -96,6 +97,8 @@ PROTOTYPES = {
     "chn_kv_read": (c_int, [c_void_p, c_u32, c_u32, c_u32, c_void_p, c_void_p]),
     "chn_kv_write": (c_int, [c_void_p, c_u32, c_u32, c_u32, c_void_p, c_void_p]),
     "chn_model_read_state": (c_int, [c_void_p, c_void_p, c_void_p]),
+    "chn_model_read_logits": (c_int, [c_void_p, c_void_p]),
+    "chn_model_replay": (c_int, [c_void_p, c_int, c_void_p, c_void_p]),
     "chn_synth_q4": (c_int, [c_void_p, c_void_p, c_u32, c_u32, c_u64, c_f32, c_f32]),
     "chn_synth_q8": (c_int, [c_void_p, c_void_p, c_u32, c_u32, c_u64, c_f32, c_f32]),
     "chn_synth_normal": (c_int, [c_void_p, c_void_p, c_size, c_u64, c_f32]),

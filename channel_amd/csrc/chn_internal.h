@@ -13,6 +13,7 @@
 
 struct chn_ctx {
     int device = 0;
+    std::string name;           // the device's marketing name and gfx target
     hipStream_t stream = nullptr;
     hipEvent_t t0 = nullptr, t1 = nullptr;
     std::string err;

@@ -240,6 +240,17 @@ static int alloc_runtime(chn_model *m) {
     if (!rc) rc = chn_fill_u32(m->ctx, m->gen, 0, 16);
     if (!rc) rc = chn_fill_u32(m->ctx, m->qflags, 0, c.num_layers);
     if (!rc) rc = chn_fill_u32(m->ctx, m->qprev, 0, (size_t)c.num_layers * H);
+    // the state the reference's Server.init zeroes through its UMA slices
+    // (src/server.zig:76-81: buf_logits, buf_x, the prefill's buf_x and
+    // buf_normed_x) starts at zero here, so reads before the first step see
+    // what they would see there
+    if (!rc) rc = chn_fill_u32(m->ctx, m->x, 0, H);
+    if (!rc) rc = chn_fill_u32(m->ctx, m->x2, 0, H);
+    if (!rc) rc = chn_fill_u32(m->ctx, m->normed, 0, H);
+    if (!rc) rc = chn_fill_u32(m->ctx, m->logits, 0, V);
+    if (!rc) rc = chn_fill_u32(m->ctx, m->topk_vals, 0, 64);
+    if (!rc) rc = chn_fill_u32(m->ctx, m->px, 0, (size_t)T * H);
+    if (!rc) rc = chn_fill_u32(m->ctx, m->pn, 0, (size_t)T * H);
     return rc;
 }
 
@@ -950,6 +961,41 @@ extern "C" int chn_kv_write(chn_model *m, uint32_t layer, uint32_t slot_begin, u
     CHN_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
     if (k_in) CHN_HIP(m->ctx, hipMemcpy(l.kc + slot_begin * row, k_in, n * row * 4, hipMemcpyHostToDevice));
     if (v_in) CHN_HIP(m->ctx, hipMemcpy(l.vc + slot_begin * row, v_in, n * row * 4, hipMemcpyHostToDevice));
+    return CHN_OK;
+}
+
+// GpuEngine.submitPreRecorded(cmd_buf_decode) (src/gpu/kernels.zig:189-194,
+// as src/model/bench.zig:12-15 calls it): one more run of the recorded decode
+// step on the inputs already on the device -- the stream x, the slot lists
+// and the step parameters the last decode call left there -- then a wait, as
+// the reference waits on its fence.
+extern "C" int chn_model_replay(chn_model *m, int with_logits, uint32_t *topk_ids, float *topk_vals) {
+    if (!m) return CHN_E_INVALID;
+    chn_ctx *ctx = m->ctx;
+    hipStream_t s = ctx->stream;
+    const bool wl = with_logits != 0;
+    CHN_REQUIRE(ctx, wl || (!topk_ids && !topk_vals), "the step without logits has no top-64");
+    if (m->use_graph) {
+        CHN_HIP(ctx, hipGraphLaunch(m->exec[wl ? 1 : 0], s));
+    } else {
+        int rc = record_decode(m, wl);
+        if (rc) return rc;
+    }
+    if (topk_ids) CHN_HIP(ctx, hipMemcpyAsync(m->h_ids, m->topk_ids, 64 * 4, hipMemcpyDeviceToHost, s));
+    if (topk_vals) CHN_HIP(ctx, hipMemcpyAsync(m->h_vals, m->topk_vals, 64 * 4, hipMemcpyDeviceToHost, s));
+    CHN_HIP(ctx, hipStreamSynchronize(s));
+    if (topk_ids) std::memcpy(topk_ids, m->h_ids, 64 * 4);
+    if (topk_vals) std::memcpy(topk_vals, m->h_vals, 64 * 4);
+    return CHN_OK;
+}
+
+// Reads of buf_logits through asSlice (src/gpu/model_gpu.zig:30-216; zeroed
+// by src/server.zig:77): the logits of the last step or prefill that
+// computed them (vocab floats, fp32).
+extern "C" int chn_model_read_logits(chn_model *m, float *logits_out) {
+    if (!m || !logits_out) return m ? set_err(m->ctx, CHN_E_INVALID, "logits_out is NULL") : CHN_E_INVALID;
+    CHN_HIP(m->ctx, hipStreamSynchronize(m->ctx->stream));
+    CHN_HIP(m->ctx, hipMemcpy(logits_out, m->logits, (size_t)m->cfg.vocab_size * 4, hipMemcpyDeviceToHost));
     return CHN_OK;
 }
 

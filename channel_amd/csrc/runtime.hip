@@ -81,6 +81,14 @@ extern "C" int chn_init(int device, chn_ctx **out) {
     if (e != hipSuccess) return hip_fail(nullptr, e, "hipSetDevice");
     chn_ctx *ctx = new chn_ctx();
     ctx->device = device;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess) {
+        // some runtimes leave the marketing name empty: the gfx target stands alone then
+        ctx->name = prop.name;
+        if (prop.gcnArchName[0]) ctx->name += ctx->name.empty() ? std::string(prop.gcnArchName)
+                                                                : " (" + std::string(prop.gcnArchName) + ")";
+    }
+    if (ctx->name.empty()) ctx->name = "HIP device " + std::to_string(device);
     e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreate(&ctx->t0);
     if (e == hipSuccess) e = hipEventCreate(&ctx->t1);
@@ -131,6 +139,8 @@ extern "C" void chn_destroy(chn_ctx *ctx) {
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
+
+extern "C" const char *chn_device_name(const chn_ctx *ctx) { return ctx ? ctx->name.c_str() : ""; }
 
 extern "C" const char *chn_last_error(const chn_ctx *ctx) {
     return ctx ? ctx->err.c_str() : g_init_err.c_str();

@@ -75,6 +75,11 @@ class Context:
         self._bufs = []
         self._recs = []
 
+    @property
+    def device_name(self):
+        """GpuContext.device_name: the device's name and gfx target."""
+        return lib.chn_device_name(self.handle).decode()
+
     # -- plumbing -----------------------------------------------------
     def _check(self, fn, rc):
         if rc != 0:

@@ -229,6 +229,22 @@ class Model:
             self.handle, x.ctypes.data_as(c_void_p), nx.ctypes.data_as(c_void_p)))
         return x, nx
 
+    def read_logits(self):
+        """The fp32 logits of the last step or prefill that computed them."""
+        lg = np.zeros(self.config.vocab_size, np.float32)
+        self._check("chn_model_read_logits", lib.chn_model_read_logits(self.handle, lg.ctypes.data_as(c_void_p)))
+        return lg
+
+    def replay(self, with_logits=True):
+        """submitPreRecorded(cmd_buf_decode): the recorded step once more on
+        the inputs already on the device; returns (ids, vals) or None."""
+        ids = np.zeros(64, np.uint32) if with_logits else None
+        vals = np.zeros(64, np.float32) if with_logits else None
+        self._check("chn_model_replay", lib.chn_model_replay(
+            self.handle, 1 if with_logits else 0, None if ids is None else ids.ctypes.data_as(c_void_p),
+            None if vals is None else vals.ctypes.data_as(c_void_p)))
+        return (ids, vals) if with_logits else None
+
     def close(self):
         if self.handle is not None:
             lib.chn_model_destroy(self.handle)

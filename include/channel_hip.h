@@ -53,6 +53,11 @@ int chn_device_count(int *count);
  * create one stream.  CHN_E_NO_DEVICE when no device is visible. */
 int chn_init(int device, chn_ctx **out);
 
+/* GpuContext.device_name (src/gpu/context.zig:17-107; checked by the
+ * reference's context test, src/gpu.zig:24-30): the bound device's name and
+ * gfx target, never empty for a live context ("" for NULL). */
+const char *chn_device_name(const chn_ctx *ctx);
+
 /* GpuContext.deinit (src/gpu/context.zig:109). Waits for queued work. */
 void chn_destroy(chn_ctx *ctx);
 
@@ -490,8 +495,27 @@ int chn_kv_write(chn_model *m, uint32_t layer, uint32_t slot_begin, uint32_t n, 
                  const float *v_in);
 
 /* Reads of buf_x / buf_normed_x (src/server/decode.zig:13,
- * src/model/memory_inject.zig:56): hidden state and last normed row. */
+ * src/model/memory_inject.zig:56): hidden state and last normed row.  Both
+ * start at zero when the model is created (what src/server.zig:76-81 sets
+ * them to). */
 int chn_model_read_state(chn_model *m, float *x_out, float *normed_out);
+
+/* Reads of buf_logits (src/gpu/model_gpu.zig:30-216; zeroed by
+ * src/server.zig:77): the fp32 logits (vocab floats, host) of the last decode
+ * step or prefill that computed them; zero at creation. */
+int chn_model_read_logits(chn_model *m, float *logits_out);
+
+/* GpuEngine.submitPreRecorded(cmd_buf_decode) (src/gpu/kernels.zig:189-194,
+ * called by src/model/bench.zig:12-15): runs the recorded decode step once
+ * more on the inputs already on the device -- the stream x as the last step
+ * left it, and the slot lists, clock and slot_idx of the last decode call --
+ * and waits for it, as the reference waits on its fence.  with_logits != 0
+ * runs the logits step (cmd_buf_decode) and, when topk_ids / topk_vals
+ * (host, 64 each) are set, returns its top-64; 0 runs the step without
+ * logits (topk pointers must be NULL).  The same kernels as chn_decode_step,
+ * so the results equal a chn_decode_step call with x = the device stream and
+ * the same lists. */
+int chn_model_replay(chn_model *m, int with_logits, uint32_t *topk_ids, float *topk_vals);
 
 /* ======================================================================
  * Seeded synthetic inputs (no reference counterpart: benchmark and test

@@ -55,7 +55,7 @@ def test_prefill_then_decode(pair):
     _, Xn, lg_o, ids_o, vals_o = OM.prefill(W, kc, vc, toks, np.arange(n), 0, 0, bf16_gemm=True,
                                             window=1024)
     assert rel_err(lg, lg_o) < 1e-2
-    assert_topk_valid(ids, vals, lg_o, 1e-2)
+    assert_topk_valid(ids, vals, lg_o, 1e-2, "prefill 40 tokens")
     kv = _kv_all(m, n)
     for i in range(CFG["num_layers"]):
         assert rel_err(kv[i][0], kc[i][: n * kvd].reshape(n, kvd)) < 1e-2
@@ -76,7 +76,7 @@ def test_prefill_then_decode(pair):
         t_gpu, ids_g, vals_g = m.forward_token(x_in, clock, clock, active, sliding)
         x_o, nx_o, lg_o, ids_o, vals_o = OM.decode_step(W, kc, vc, x_in, clock, clock, active, sliding)
         assert t_gpu == ids_g[0]
-        assert_topk_valid(ids_g, vals_g, lg_o, 1e-3)
+        assert_topk_valid(ids_g, vals_g, lg_o, 1e-3, f"decode clock {clock}")
         x_g, nx_g = m.read_state()
         assert rel_err(x_g, x_o) < 1e-3
         assert rel_err(nx_g, nx_o) < 1e-3
@@ -138,7 +138,7 @@ def test_prefill_after_previous_slots(pair):
     lg, ids, vals = m.prefill_batch(toks, slots, 30, 30, embed_bf16=W.embed_bf16)
     _, _, lg_o, _, _ = OM.prefill(W, kc, vc, toks, slots, 30, 30, bf16_gemm=True)
     assert rel_err(lg, lg_o) < 1e-2
-    assert_topk_valid(ids, vals, lg_o, 1e-2)
+    assert_topk_valid(ids, vals, lg_o, 1e-2, "prefill after 30 previous slots")
 
 
 def test_model_errors(pair):
@@ -238,6 +238,53 @@ def test_eager_launches_match_graph(ctx):
             xg, ng = mg.read_state()
             xe, ne = me.read_state()
             assert np.array_equal(xg, xe) and np.array_equal(ng, ne)
+
+
+@pytest.mark.parametrize("graph", [True, False])
+def test_replay_equals_decode_step(ctx, graph):
+    """chn_model_replay (submitPreRecorded(cmd_buf_decode), as
+    src/model/bench.zig:12-15 calls it) runs the recorded step again on the
+    inputs the last call left on the device.  It must equal, bit for bit,
+    chn_decode_step fed with the device's stream x and the same lists:
+    top-64, state, logits and the K/V row written; likewise the step without
+    logits.  Also: the device state starts at zero, as src/server.zig:76-81
+    leaves it, and the context reports a device name (src/gpu.zig:24-30)."""
+    cfg = dict(CFG, num_layers=2, layer_full=[0, 1])
+    kvd = CFG["num_kv_heads"] * CFG["head_dim"]
+    assert ctx.device_name
+    say(f"replay vs decode_step, graph={graph} on {ctx.device_name}")
+    with Model.synthetic(ctx, cfg, 61) as ma, Model.synthetic(ctx, cfg, 61) as mb:
+        ma.set_graph(graph)
+        mb.set_graph(graph)
+        x0, n0 = ma.read_state()
+        assert not x0.any() and not n0.any() and not ma.read_logits().any()
+        clock = 37
+        active, sliding = OM.slot_lists(clock, WINDOW)
+        x_in = np.random.default_rng(61).standard_normal(cfg["hidden_size"]).astype(np.float32)
+        ta, ida, va = ma.forward_token(x_in, clock, clock, active, sliding)
+        tb, idb, vb = mb.forward_token(x_in, clock, clock, active, sliding)
+        assert np.array_equal(ida, idb) and np.array_equal(va, vb)
+        for with_logits in (True, False, True):
+            x_dev, _ = mb.read_state()
+            out = ma.replay(with_logits)
+            _, idb, vb = mb.forward_token(x_dev, clock, clock, active, sliding, topk=with_logits)
+            if with_logits:
+                assert np.array_equal(out[0], idb) and np.array_equal(out[1].view(np.uint32), vb.view(np.uint32))
+                assert np.array_equal(ma.read_logits().view(np.uint32), mb.read_logits().view(np.uint32))
+            xa, na = ma.read_state()
+            xb, nb = mb.read_state()
+            assert np.array_equal(xa, xb) and np.array_equal(na, nb)
+            assert not np.array_equal(xa, x_dev)        # the step ran on the device's stream
+            for layer in range(2):
+                ka, va_ = ma.kv_read(layer, clock, 1)
+                kb, vb_ = mb.kv_read(layer, clock, 1)
+                assert np.array_equal(ka, kb) and np.array_equal(va_, vb_)
+                assert ka.shape == (1, kvd)
+        with pytest.raises(ca.ChannelError):
+            lib = ca.lib
+            import ctypes
+            ids = np.zeros(64, np.uint32)
+            ma._check("chn_model_replay", lib.chn_model_replay(ma.handle, 0, ids.ctypes.data_as(ctypes.c_void_p), None))
 
 
 def ring_lists(clock, window):
@@ -353,7 +400,7 @@ def test_global_head_shape_model(ctx):
             say(f"global-shape decode clock={clock}")
             t_gpu, ids_g, vals_g = m.forward_token(x_in, clock, clock, active, sliding)
             x_o, nx_o, lg_o, _, _ = OM.decode_step(W, kc, vc, x_in, clock, clock, active, sliding)
-            assert_topk_valid(ids_g, vals_g, lg_o, 1e-3)
+            assert_topk_valid(ids_g, vals_g, lg_o, 1e-3, f"global-shape decode clock {clock}")
             x_g, _ = m.read_state()
             assert rel_err(x_g, x_o) < 1e-3
             tok = int(ids_g[0])
@@ -455,6 +502,81 @@ def test_quiescence_gating_matches_oracle(ctx):
                 k_o, v_o = kv_o[s][i]
                 assert np.array_equal(k == 0, k_o == 0), (s, i)      # the same rows written
                 assert rel_err(k, k_o) < 1e-3 and rel_err(v, v_o) < 1e-3, (s, i)
+
+
+def _gated_greedy_oracle(W, thresh, tok0, n):
+    """n greedy steps from clock 0 through the oracle's gated composition:
+    its tokens, per step its outputs and the relative top-2 margin."""
+    qs = OM.QuiescenceState(CFG_Q, thresh)
+    kc, vc = OM.new_caches(CFG_Q, 4096)
+    toks, outs, margins = [], [], []
+    tok = tok0
+    for clock in range(n):
+        act, sl = OM.slot_lists(clock, 16)
+        out = OM.decode_step(W, kc, vc, W.embed([tok])[0], clock, clock, act, sl, with_logits=True, qstate=qs)
+        vals = out[4].astype(np.float64)
+        margins.append((vals[0] - vals[1]) / np.max(np.abs(vals)))
+        tok = int(out[3][0])
+        toks.append(tok)
+        outs.append(out)
+    return qs, toks, outs, margins, kc, vc
+
+
+def test_gated_greedy_matches_token_loop_and_oracle(ctx):
+    """chn_decode_greedy with quiescence gating on (every greedy step
+    computes logits, so layers from num_layers / 3 on are gated): its tokens,
+    state and K/V rows equal the gated token loop (chn_decode_token with the
+    same lists) bit for bit, and both follow the oracle's gated greedy run:
+    the same tokens, the stream and normed row within 1e-3 at every step,
+    and the same layers quiescent (a quiescent layer writes no K/V row).
+    The threshold is chosen from the oracle's own gate values along the
+    greedy run: at least 5% away from every one of them, with both outcomes
+    present, and every step's argmax ahead of the runner-up by at least 2e-3
+    of the largest value, so rounding can flip neither a gate nor a token."""
+    layers, embed, final = OM.random_model(CFG_Q, 41)
+    W = OM.Weights(CFG_Q, layers, embed, final)
+    n, tok0 = 8, 17
+    best = None
+    for thresh in np.geomspace(1e-3, 10.0, 41):
+        qs, toks, outs, margins, kc, vc = _gated_greedy_oracle(W, thresh, tok0, n)
+        gates = [g for step in qs.log for g in step]
+        gm = min((abs(np.log(g[2] / thresh)) for g in gates if g[2] > 0), default=np.inf)
+        skips = sum(1 for g in gates if not g[1])
+        runs = len(gates) - skips
+        if gm > 0.05 and min(margins) >= 2e-3 and skips >= 2 and runs >= 2:
+            if best is None or min(skips, runs) > best[0]:
+                best = (min(skips, runs), float(thresh), qs, toks, outs, kc, vc)
+    assert best is not None
+    _, thresh, qs, toks_o, outs, kc_o, vc_o = best
+    kvd = CFG_Q["num_kv_heads"] * CFG_Q["head_dim"]
+    say(f"gated greedy: threshold {thresh:.3g}; quiescent layers per step: "
+        f"{[[g[0] for g in step if not g[1]] for step in qs.log]}")
+    cfg = dict(CFG_Q, quiescence_thresh=thresh)
+    with Model.create(ctx, cfg, layers, embed, final) as mg, Model.create(ctx, cfg, layers, embed, final) as mh:
+        say("decode_greedy 8 gated steps")
+        toks_g = mg.decode_greedy(tok0, 0, n)
+        tok, want = tok0, []
+        for clock in range(n):
+            act, sl = OM.slot_lists(clock, 16)
+            say(f"gated token loop clock={clock} tok={tok}")
+            tok, ids, vals = mh.forward_token_id(tok, clock, clock, act, sl)
+            want.append(tok)
+            x_o, n_o, lg_o, _, _ = outs[clock]
+            x_h, n_h = mh.read_state()
+            assert rel_err(x_h, x_o) < 1e-3 and rel_err(n_h, n_o) < 1e-3, clock
+            assert_topk_valid(ids, vals, lg_o, 1e-3, f"gated greedy step {clock}")
+        assert list(toks_g) == want == toks_o
+        xg, ng = mg.read_state()
+        xh, nh = mh.read_state()
+        assert np.array_equal(xg, xh) and np.array_equal(ng, nh)
+        for i in range(CFG_Q["num_layers"]):
+            kg, vg = mg.kv_read(i, 0, n)
+            kh, vh = mh.kv_read(i, 0, n)
+            assert np.array_equal(kg, kh) and np.array_equal(vg, vh), i
+            k_o = kc_o[i][: n * kvd].reshape(n, kvd)
+            v_o = vc_o[i][: n * kvd].reshape(n, kvd)
+            assert np.array_equal(np.all(kg == 0, axis=1), np.all(k_o == 0, axis=1)), i   # same rows written
+            assert rel_err(kg, k_o) < 1e-3 and rel_err(vg, v_o) < 1e-3, i
 
 
 def test_prefill_window_option(ctx):

@@ -11,9 +11,12 @@ sliding window 512, theta 1e4 (sliding) / 1e6 (full).
   (1e-3), starting from the GPU's caches.  The decode steps run the fused
   norm prologues at K = 3840, down at K = 15360 and the attention with
   fused RoPE for 16 heads.
-* All 48 layers: chn_decode_greedy against the same steps driven token by
-  token (bit for bit), and every step's top-64 against the oracle's Q8
-  logits of the downloaded final normed row.
+* Two layers over full 4096-slot rings, decoding across the ring's wrap at
+  clock 3968 with ~3968-entry global lists, against the oracle in fp32.
+* All 48 layers after the benchmark's 512-token prompt: chn_decode_greedy
+  against the same steps driven token by token (bit for bit), and every
+  step's top-64 against the oracle's Q8 logits of the downloaded final
+  normed row.
 
 The synthetic weights are regenerated on the host by the oracle's
 restatement of the generator (bit-exact, tests/test_gpu_golden.py); the
@@ -110,28 +113,84 @@ def test_12b_layers_prefill_512_then_decode(two_layers):
         tok = int(ids_g[0])
 
 
+def test_12b_layers_decode_full_ring_across_wrap(two_layers):
+    """Decode at the 12B layer dims over full rings: every one of the 4096
+    slots of both layers holds K/V rows (the same random rows on both
+    sides), then four steps at clocks 3966..3969 through chn_decode_token
+    with the lists of the ring restatement (oracle/ring.py, no anchors):
+    3967 and 3968 entries in the global list, the window wrapping at 3968
+    (clocks 3968 and 3969 take slots 0 and 1, and the list runs 2..3967,
+    0, 1), the sliding list the newest 512.  Against the oracle in fp32:
+    x, the normed row and the K/V rows written within 1e-3, the top-64
+    valid.  This is the model's attention with fused RoPE on ~3968-entry
+    lists, which the chunked greedy tests compare only with other HIP paths."""
+    from oracle.ring import Ring
+    from oracle import ring as OR
+    W, m = two_layers
+    kvd = CFG2["num_kv_heads"] * CFG2["head_dim"]
+    rng = np.random.default_rng(3968)
+    kc, vc = OM.new_caches(CFG2)
+    for i in range(2):
+        k = (rng.standard_normal((4096, kvd)) * 0.05).astype(np.float32)
+        v = rng.standard_normal((4096, kvd)).astype(np.float32)
+        say(f"fill all 4096 slots of layer {i}")
+        m.kv_write(i, 0, k, v)
+        kc[i][:] = k.ravel()
+        vc[i][:] = v.ravel()
+    ring = Ring(1, 0)
+    clock0 = 3966
+    for c in range(clock0):
+        ring.activate_slot(0, c)
+    tok = 4242
+    for clock in range(clock0, clock0 + 4):
+        slot, active, sliding = OR.decode_lists(ring, clock, CFG2["sliding_window"])
+        active = np.asarray(active, np.uint32)
+        sliding = np.asarray(sliding, np.uint32)
+        assert len(active) >= 3967 and len(sliding) == 512
+        say(f"decode clock={clock} slot={slot} global {len(active)} entries (first {active[0]}, last "
+            f"{active[-1]}), sliding {len(sliding)}")
+        t_gpu, ids_g, vals_g = m.forward_token_id(tok, clock, slot, active, sliding)
+        x_o, nx_o, lg_o, _, _ = OM.decode_step(W, kc, vc, W.embed([tok])[0], clock, slot, active, sliding,
+                                               nthreads=NT)
+        x_g, nx_g = m.read_state()
+        ex, en = rel_err(x_g, x_o), rel_err(nx_g, nx_o)
+        say(f"  x {ex:.2e} (elementwise {elem_err(x_g, x_o):.2e}), normed {en:.2e}")
+        assert ex < 1e-3 and en < 1e-3
+        assert t_gpu == ids_g[0]
+        assert_topk_valid(ids_g, vals_g, lg_o, 1e-3, f"full-ring decode {clock}")
+        for i in range(2):
+            k_g, v_g = m.kv_read(i, slot, 1)
+            ek = rel_err(k_g[0], kc[i][slot * kvd:(slot + 1) * kvd])
+            ev = rel_err(v_g[0], vc[i][slot * kvd:(slot + 1) * kvd])
+            assert ek < 1e-3 and ev < 1e-3, (i, ek, ev)
+        if clock >= 3968:
+            assert slot == clock - 3968 and active[-1] == slot and active[0] == clock - 3967
+        tok = int(ids_g[0])
+
+
 def test_12b_48_layers_greedy(ctx):
     """The full 48-layer model: device-resident greedy steps equal the
     token-by-token steps bit for bit, and every step's top-64 is the top-64
     of the oracle's Q8 logits of that step's final normed row."""
-    cfg = OM.default_config(max_prefill_tokens=64)
+    cfg = OM.default_config(max_prefill_tokens=512)
     say("model_create_synthetic x2: 48 layers at 12B dims")
     with Model.synthetic(ctx, cfg, SEED) as mg, Model.synthetic(ctx, cfg, SEED) as mh:
         emb = embedding(ctx, mg)
         E8 = O.quantize_q8(emb, NT)
         del emb
-        prompt = np.random.default_rng(48).integers(0, cfg["vocab_size"], 64).astype(np.uint32)
-        slots = np.arange(64, dtype=np.uint32)
-        say("prefill 64 tokens on both")
+        n_prompt = 512                     # the benchmark's prompt
+        prompt = np.random.default_rng(48).integers(0, cfg["vocab_size"], n_prompt).astype(np.uint32)
+        slots = np.arange(n_prompt, dtype=np.uint32)
+        say("prefill 512 tokens on both")
         _, ids_g, vals_g = mg.prefill_batch(prompt, slots, 0, 0, logits=False)
         _, ids_h, vals_h = mh.prefill_batch(prompt, slots, 0, 0, logits=False)
         assert np.array_equal(ids_g, ids_h) and np.array_equal(vals_g, vals_h)
         n = 5
         say("decode_greedy 5 steps")
-        toks = mg.decode_greedy(int(ids_g[0]), 64, n)
+        toks = mg.decode_greedy(int(ids_g[0]), n_prompt, n)
         tok, want = int(ids_h[0]), []
         for i in range(n):
-            clock = 64 + i
+            clock = n_prompt + i
             slot, active, sliding = ring.decode_lists(clock, cfg["sliding_window"])
             say(f"token loop clock={clock}")
             tok, ids, vals = mh.forward_token_id(tok, clock, slot, active, sliding)
