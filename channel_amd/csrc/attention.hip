@@ -343,210 +343,234 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ Q
 #pragma unroll
             for (int f = 0; f < NF; ++f) q[h][f] = *(const f4 *)(Q + (size_t)(qh0 + h) * D + c * 4 + 64 * f);
     }
-    if (iters) issue(0, 0, sl[0], sl[1]);
+    // A split with a single chunk (every split of a list of at most 16 G
+    // entries, e.g. a 512-entry sliding window) loads and reduces that chunk
+    // only.  The rest of the kernel is instantiated once per form, so each
+    // form's waits count its own loads.
+    auto issue1 = [&](uint32_t pa) {    // chunk 0 alone, into buffer 0 (two-set shapes)
+        ok[0] = entry(0) < S;
+        const size_t ra = (size_t)(ok[0] ? pa : 0u) * kv_dim + dim0;
+#pragma unroll
+        for (int f = 0; f < NF; ++f) kr[0][f] = *(const f4 *)(Kc + ra + 64 * f);
+#pragma unroll
+        for (int f = 0; f < NF; ++f) vr[0][f] = *(const f4 *)(Vc + ra + 64 * f);
+    };
+    auto body = [&](auto single_) {
+    constexpr bool SINGLE = decltype(single_)::value;
+    if (SINGLE) issue1(sl[0]);
+    else if (iters) issue(0, 0, sl[0], sl[1]);
 
-    uint32_t new_slot = 0xFFFFFFFFu;
-    if (ROPE) {
-        new_slot = ra.step[1];
-        // items: GQA query heads (RMSNorm * q_norm), the new K head
-        // (* k_norm), the new V head (unit RMSNorm), into LDS
-#pragma unroll
-        for (int j = 0; j < NIT; ++j) {
-            const int it = wave + 4 * j;
-            if (it < GQA + 2) {
-                float ss = 0.0f;
-#pragma unroll
-                for (int d = 0; d < DPL; ++d) ss += raw[j][d] * raw[j][d];
-                ss = wave_sum64(ss);
-                const float inv = 1.0f / sqrtf(ss / (float)D + ra.eps);
-                float *dst = it < GQA ? sh_q[it] : (it == GQA ? sh_k : sh_v);
-#pragma unroll
-                for (int d = 0; d < DPL; ++d) {
-                    const float n = raw[j][d] * inv;
-                    dst[lane + 64 * d] = it < GQA + 1 ? n * nwt[j][d] : n;
+        uint32_t new_slot = 0xFFFFFFFFu;
+        if (ROPE) {
+            new_slot = ra.step[1];
+            // items: GQA query heads (RMSNorm * q_norm), the new K head
+            // (* k_norm), the new V head (unit RMSNorm), into LDS
+    #pragma unroll
+            for (int j = 0; j < NIT; ++j) {
+                const int it = wave + 4 * j;
+                if (it < GQA + 2) {
+                    float ss = 0.0f;
+    #pragma unroll
+                    for (int d = 0; d < DPL; ++d) ss += raw[j][d] * raw[j][d];
+                    ss = wave_sum64(ss);
+                    const float inv = 1.0f / sqrtf(ss / (float)D + ra.eps);
+                    float *dst = it < GQA ? sh_q[it] : (it == GQA ? sh_k : sh_v);
+    #pragma unroll
+                    for (int d = 0; d < DPL; ++d) {
+                        const float n = raw[j][d] * inv;
+                        dst[lane + 64 * d] = it < GQA + 1 ? n * nwt[j][d] : n;
+                    }
                 }
             }
-        }
-        __syncthreads();
-        for (int it = wave; it < GQA + 1; it += 4)
-            wave_rope_lds(it < GQA ? sh_q[it] : sh_k, ra.rot, rcs, lane);
-        __syncthreads();
-        if (split == 0) {
-            float *kd = Kc + (size_t)new_slot * kv_dim + (size_t)kvh * D;
-            float *vd = Vc + (size_t)new_slot * kv_dim + (size_t)kvh * D;
-            for (int d = threadIdx.x; d < D; d += 256) {
-                kd[d] = sh_k[d];
-                vd[d] = sh_v[d];
+            __syncthreads();
+            for (int it = wave; it < GQA + 1; it += 4)
+                wave_rope_lds(it < GQA ? sh_q[it] : sh_k, ra.rot, rcs, lane);
+            __syncthreads();
+            if (split == 0) {
+                float *kd = Kc + (size_t)new_slot * kv_dim + (size_t)kvh * D;
+                float *vd = Vc + (size_t)new_slot * kv_dim + (size_t)kvh * D;
+                for (int d = threadIdx.x; d < D; d += 256) {
+                    kd[d] = sh_k[d];
+                    vd[d] = sh_v[d];
+                }
             }
+            if (!iters) {
+                write_empty();
+                return;
+            }
+    #pragma unroll
+            for (int h = 0; h < GQA; ++h)
+    #pragma unroll
+                for (int f = 0; f < NF; ++f) q[h][f] = *(const f4 *)&sh_q[h][c * 4 + 64 * f];
         }
-        if (!iters) {
-            write_empty();
-            return;
-        }
-#pragma unroll
-        for (int h = 0; h < GQA; ++h)
-#pragma unroll
-            for (int f = 0; f < NF; ++f) q[h][f] = *(const f4 *)&sh_q[h][c * 4 + 64 * f];
-    }
 
-    float M[GQA], L[GQA];
-    f4 acc[GQA][NF];
-#pragma unroll
-    for (int h = 0; h < GQA; ++h) {
-        M[h] = kNegBig;
-        L[h] = 0.0f;
-#pragma unroll
-        for (int f = 0; f < NF; ++f) acc[h][f] = f4{0, 0, 0, 0};
-    }
-    // One chunk of buffer b into the running state (fresh: the new token's
-    // row, in the rows that held it).  With two sets the rows that do not count (past the
-    // slot count, or, with ROPE, the new token's row: its cache row may
-    // predate split 0's write, so it is added from LDS after the loop) are
-    // masked with bit operations, not selects: given a select the compiler
-    // branches around the dot and copies the V rows into a second set of
-    // registers at the join, which costs registers the two-set shapes do not have.
-    // One set keeps the selects (its rows past the count hold zeros).
-    bool has_new = false;
-    auto reduce = [&](int b, uint32_t ps, bool fresh = false) {
-        bool use = fresh ? has_new : ok[b];
-        if constexpr (NSET == 2) {
-            if (ROPE && !fresh) {
-                has_new = has_new || (use && ps == new_slot);
-                use = use && ps != new_slot;
-            }
-        } else if (ROPE && use && ps == new_slot) {
-            // one set: the new token's row is replaced in place
-#pragma unroll
-            for (int f = 0; f < NF; ++f) {
-                kr[b][f] = *(const f4 *)&sh_k[c * 4 + 64 * f];
-                vr[b][f] = *(const f4 *)&sh_v[c * 4 + 64 * f];
-            }
-        }
-        uint32_t m = 0;
-        if constexpr (NSET == 2) {
-            m = opaque_mask(use);
-#pragma unroll
-            for (int f = 0; f < NF; ++f)
-                vr[b][f] = f4{mask_f(vr[b][f].x, m), mask_f(vr[b][f].y, m), mask_f(vr[b][f].z, m),
-                              mask_f(vr[b][f].w, m)};
-        }
-#pragma unroll
+        float M[GQA], L[GQA];
+        f4 acc[GQA][NF];
+    #pragma unroll
         for (int h = 0; h < GQA; ++h) {
-            float d = 0.0f;
-#pragma unroll
-            for (int f = 0; f < NF; ++f) {
-                d = fmaf(q[h][f].x, kr[b][f].x, d);
-                d = fmaf(q[h][f].y, kr[b][f].y, d);
-                d = fmaf(q[h][f].z, kr[b][f].z, d);
-                d = fmaf(q[h][f].w, kr[b][f].w, d);
-            }
-            float sc;
-            if constexpr (NSET == 2)
-                sc = __builtin_bit_cast(float, (__builtin_bit_cast(uint32_t, row16_sum(d) * scale) & m) |
-                                                   (__builtin_bit_cast(uint32_t, kNegBig) & ~m));
-            else
-                sc = use ? row16_sum(d) * scale : kNegBig;
-            const float mx = rows4_max(sc);
-            const float Mn = fmaxf(M[h], mx);
-            const float rs = expf(M[h] - Mn);
-            const float p = NSET == 2 ? mask_f(expf(sc - Mn), m) : (use ? expf(sc - Mn) : 0.0f);
-            const float psum = rows4_sum(p);
-#pragma unroll
-            for (int f = 0; f < NF; ++f) acc[h][f] = acc[h][f] * rs + p * vr[b][f];
-            L[h] = L[h] * rs + psum;
-            M[h] = Mn;
+            M[h] = kNegBig;
+            L[h] = 0.0f;
+    #pragma unroll
+            for (int f = 0; f < NF; ++f) acc[h][f] = f4{0, 0, 0, 0};
         }
-    };
-    // Pair pr = chunks 2 pr, 2 pr + 1 goes to set pr % NSET; once reduced,
-    // the set takes pair pr + NSET.  One straight-line body per pair count
-    // (the count is uniform over the workgroup): no branch between a load
-    // and its use, so each wait leaves the younger set in flight.  A chunk
-    // past `iters` in the last pair is masked by ok[].
-    if constexpr (NSET == 2) {
-        auto run = [&](auto np_) {
-            constexpr int NP = decltype(np_)::value;
-            if constexpr (NP > 1) issue(1, 2, sl[2 % NSL], sl[3 % NSL]);
-#pragma unroll
-            for (int pr = 0; pr < NP; ++pr) {
-                const int set = pr % 2;
-                reduce(2 * set, sl[(2 * pr) % NSL]);
-                reduce(2 * set + 1, sl[(2 * pr + 1) % NSL]);
-                if (pr + 2 < NP) issue(set, 2 * (pr + 2), sl[(2 * pr + 4) % NSL], sl[(2 * pr + 5) % NSL]);
+        // One chunk of buffer b into the running state (fresh: the new token's
+        // row, in the rows that held it).  With two sets the rows that do not count (past the
+        // slot count, or, with ROPE, the new token's row: its cache row may
+        // predate split 0's write, so it is added from LDS after the loop) are
+        // masked with bit operations, not selects: given a select the compiler
+        // branches around the dot and copies the V rows into a second set of
+        // registers at the join, which costs registers the two-set shapes do not have.
+        // One set keeps the selects (its rows past the count hold zeros).
+        bool has_new = false;
+        auto reduce = [&](int b, uint32_t ps, bool fresh = false) {
+            bool use = fresh ? has_new : ok[b];
+            if constexpr (NSET == 2) {
+                if (ROPE && !fresh) {
+                    has_new = has_new || (use && ps == new_slot);
+                    use = use && ps != new_slot;
+                }
+            } else if (ROPE && use && ps == new_slot) {
+                // one set: the new token's row is replaced in place
+    #pragma unroll
+                for (int f = 0; f < NF; ++f) {
+                    kr[b][f] = *(const f4 *)&sh_k[c * 4 + 64 * f];
+                    vr[b][f] = *(const f4 *)&sh_v[c * 4 + 64 * f];
+                }
+            }
+            uint32_t m = 0;
+            if constexpr (NSET == 2) {
+                m = opaque_mask(use);
+    #pragma unroll
+                for (int f = 0; f < NF; ++f)
+                    vr[b][f] = f4{mask_f(vr[b][f].x, m), mask_f(vr[b][f].y, m), mask_f(vr[b][f].z, m),
+                                  mask_f(vr[b][f].w, m)};
+            }
+    #pragma unroll
+            for (int h = 0; h < GQA; ++h) {
+                float d = 0.0f;
+    #pragma unroll
+                for (int f = 0; f < NF; ++f) {
+                    d = fmaf(q[h][f].x, kr[b][f].x, d);
+                    d = fmaf(q[h][f].y, kr[b][f].y, d);
+                    d = fmaf(q[h][f].z, kr[b][f].z, d);
+                    d = fmaf(q[h][f].w, kr[b][f].w, d);
+                }
+                float sc;
+                if constexpr (NSET == 2)
+                    sc = __builtin_bit_cast(float, (__builtin_bit_cast(uint32_t, row16_sum(d) * scale) & m) |
+                                                       (__builtin_bit_cast(uint32_t, kNegBig) & ~m));
+                else
+                    sc = use ? row16_sum(d) * scale : kNegBig;
+                const float mx = rows4_max(sc);
+                const float Mn = fmaxf(M[h], mx);
+                const float rs = expf(M[h] - Mn);
+                const float p = NSET == 2 ? mask_f(expf(sc - Mn), m) : (use ? expf(sc - Mn) : 0.0f);
+                const float psum = rows4_sum(p);
+    #pragma unroll
+                for (int f = 0; f < NF; ++f) acc[h][f] = acc[h][f] * rs + p * vr[b][f];
+                L[h] = L[h] * rs + psum;
+                M[h] = Mn;
             }
         };
-        const uint32_t np = (iters + 1) / 2;
-        if constexpr (kMaxChunks == 4) {
-            if (np <= 1) run(std::integral_constant<int, 1>{});
-            else run(std::integral_constant<int, 2>{});
+        // Pair pr = chunks 2 pr, 2 pr + 1 goes to set pr % NSET; once reduced,
+        // the set takes pair pr + NSET.  One straight-line body per pair count
+        // (the count is uniform over the workgroup): no branch between a load
+        // and its use, so each wait leaves the younger set in flight.  A chunk
+        // past `iters` in the last pair is masked by ok[].
+        if constexpr (NSET == 2 && SINGLE) {
+            reduce(0, sl[0]);
+        } else if constexpr (NSET == 2) {
+            auto run = [&](auto np_) {
+                constexpr int NP = decltype(np_)::value;
+                if constexpr (NP > 1) issue(1, 2, sl[2 % NSL], sl[3 % NSL]);
+    #pragma unroll
+                for (int pr = 0; pr < NP; ++pr) {
+                    const int set = pr % 2;
+                    reduce(2 * set, sl[(2 * pr) % NSL]);
+                    reduce(2 * set + 1, sl[(2 * pr + 1) % NSL]);
+                    if (pr + 2 < NP) issue(set, 2 * (pr + 2), sl[(2 * pr + 4) % NSL], sl[(2 * pr + 5) % NSL]);
+                }
+            };
+            const uint32_t np = (iters + 1) / 2;
+            if constexpr (kMaxChunks == 4) {
+                if (np <= 1) run(std::integral_constant<int, 1>{});
+                else run(std::integral_constant<int, 2>{});
+            } else {
+                static_assert(kMaxChunks == 8, "one body per pair count");
+                switch (np) {
+                case 1: run(std::integral_constant<int, 1>{}); break;
+                case 2: run(std::integral_constant<int, 2>{}); break;
+                case 3: run(std::integral_constant<int, 3>{}); break;
+                default: run(std::integral_constant<int, 4>{}); break;
+                }
+            }
         } else {
-            static_assert(kMaxChunks == 8, "one body per pair count");
-            switch (np) {
-            case 1: run(std::integral_constant<int, 1>{}); break;
-            case 2: run(std::integral_constant<int, 2>{}); break;
-            case 3: run(std::integral_constant<int, 3>{}); break;
-            default: run(std::integral_constant<int, 4>{}); break;
+            uint32_t pa = sl[0], pb = sl[1];
+    #pragma unroll 1
+            for (uint32_t t = 0; t < iters; t += 2) {
+                if (t > 0) issue(0, t, pa, pb);
+                const uint32_t na = slot_at(t + 2), nb = slot_at(t + 3);
+                reduce(0, pa);
+                if (t + 1 < iters) reduce(1, pb);
+                pa = na;
+                pb = nb;
             }
         }
-    } else {
-        uint32_t pa = sl[0], pb = sl[1];
-#pragma unroll 1
-        for (uint32_t t = 0; t < iters; t += 2) {
-            if (t > 0) issue(0, t, pa, pb);
-            const uint32_t na = slot_at(t + 2), nb = slot_at(t + 3);
-            reduce(0, pa);
-            if (t + 1 < iters) reduce(1, pb);
-            pa = na;
-            pb = nb;
+        // two sets: the new token's entry, from LDS, in the rows whose list
+        // entry it is
+        if (ROPE && NSET == 2 && __any(has_new)) {
+    #pragma unroll
+            for (int f = 0; f < NF; ++f) {
+                kr[0][f] = *(const f4 *)&sh_k[c * 4 + 64 * f];
+                vr[0][f] = *(const f4 *)&sh_v[c * 4 + 64 * f];
+            }
+            reduce(0, 0u, true);
         }
-    }
-    // two sets: the new token's entry, from LDS, in the rows whose list
-    // entry it is
-    if (ROPE && NSET == 2 && __any(has_new)) {
-#pragma unroll
-        for (int f = 0; f < NF; ++f) {
-            kr[0][f] = *(const f4 *)&sh_k[c * 4 + 64 * f];
-            vr[0][f] = *(const f4 *)&sh_v[c * 4 + 64 * f];
+        // rows of the wave hold different entries of the same columns
+    #pragma unroll
+        for (int h = 0; h < GQA; ++h)
+    #pragma unroll
+            for (int f = 0; f < NF; ++f) {
+                const f4 t = f4{rows4_sum(acc[h][f].x), rows4_sum(acc[h][f].y), rows4_sum(acc[h][f].z),
+                                rows4_sum(acc[h][f].w)};
+                if (r == 0) sh_acc[wave][h][c + 16 * f] = t;
+            }
+        if (lane < GQA) {
+            sh_m[wave][lane] = M[lane];
+            sh_l[wave][lane] = L[lane];
         }
-        reduce(0, 0u, true);
-    }
-    // rows of the wave hold different entries of the same columns
-#pragma unroll
-    for (int h = 0; h < GQA; ++h)
-#pragma unroll
-        for (int f = 0; f < NF; ++f) {
-            const f4 t = f4{rows4_sum(acc[h][f].x), rows4_sum(acc[h][f].y), rows4_sum(acc[h][f].z),
-                            rows4_sum(acc[h][f].w)};
-            if (r == 0) sh_acc[wave][h][c + 16 * f] = t;
-        }
-    if (lane < GQA) {
-        sh_m[wave][lane] = M[lane];
-        sh_l[wave][lane] = L[lane];
-    }
-    __syncthreads();
+        __syncthreads();
 
-    // workgroup partial for this split: [G][nq][D] sums, then [G][nq] maxima
-    // and [G][nq] denominators
-    float *wacc = ws;
-    float *wm = ws + (size_t)G * num_q_heads * D;
-    float *wl = wm + (size_t)G * num_q_heads;
-    for (int idx = threadIdx.x; idx < GQA * (D / 4); idx += 256) {
-        const int h = idx / (D / 4), col = idx % (D / 4);
-        float Mw = -1e9f;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) Mw = fmaxf(Mw, sh_m[w][h]);
-        f4 t = f4{0, 0, 0, 0};
-        float lw = 0.0f;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const float e = expf(sh_m[w][h] - Mw);
-            t += e * sh_acc[w][h][col];
-            lw += e * sh_l[w][h];
+        // workgroup partial for this split: [G][nq][D] sums, then [G][nq] maxima
+        // and [G][nq] denominators
+        float *wacc = ws;
+        float *wm = ws + (size_t)G * num_q_heads * D;
+        float *wl = wm + (size_t)G * num_q_heads;
+        for (int idx = threadIdx.x; idx < GQA * (D / 4); idx += 256) {
+            const int h = idx / (D / 4), col = idx % (D / 4);
+            float Mw = -1e9f;
+    #pragma unroll
+            for (int w = 0; w < 4; ++w) Mw = fmaxf(Mw, sh_m[w][h]);
+            f4 t = f4{0, 0, 0, 0};
+            float lw = 0.0f;
+    #pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float e = expf(sh_m[w][h] - Mw);
+                t += e * sh_acc[w][h][col];
+                lw += e * sh_l[w][h];
+            }
+            *(f4 *)(wacc + ((size_t)split * num_q_heads + qh0 + h) * D + 4 * col) = t;
+            if (col == 0) {
+                wm[(size_t)split * num_q_heads + qh0 + h] = Mw;
+                wl[(size_t)split * num_q_heads + qh0 + h] = lw;
+            }
         }
-        *(f4 *)(wacc + ((size_t)split * num_q_heads + qh0 + h) * D + 4 * col) = t;
-        if (col == 0) {
-            wm[(size_t)split * num_q_heads + qh0 + h] = Mw;
-            wl[(size_t)split * num_q_heads + qh0 + h] = lw;
-        }
+    };
+    if constexpr (NSET == 2) {
+        if (iters == 1) body(std::true_type{});
+        else body(std::false_type{});
+    } else {
+        body(std::false_type{});
     }
 }
 
