@@ -794,16 +794,20 @@ size_t prefill_frag_bytes(uint32_t num_kv_heads, uint32_t n_keys) {
     return (size_t)num_kv_heads * ((n_keys + kPaNK - 1) / kPaNK) * kPaChunkBytes;
 }
 
-// Pre-pass: grid (chunks c_lo .. c_lo + gridDim.x - 1, KV heads, 2): z = 0
-// writes the chunk's K planes, z = 1 its V^T planes; chunk blockIdx.x of KV
-// head kvh goes to F + (kvh * gridDim.x + blockIdx.x) * kPaChunkBytes.  Keys
-// at or past n_keys are zero.
+// Pre-pass: grid (KV heads, chunks c_lo .. c_lo + gridDim.y - 1, 2): z = 0
+// writes the chunk's K planes, z = 1 its V^T planes; chunk blockIdx.y of KV
+// head kvh = blockIdx.x goes to F + (kvh * gridDim.y + blockIdx.y) *
+// kPaChunkBytes.  Keys at or past n_keys are zero.  The KV head is the
+// fastest grid index here and in the attention (workgroup i runs on XCD
+// i % 8), so with eight KV heads every workgroup of one head runs on one
+// XCD and a head's fragments, read by all of its query tiles, stay in that
+// XCD's L2.
 __global__ __launch_bounds__(256) void k_prefill_frags(const float *__restrict__ Kc, const float *__restrict__ Vc,
                                                        const uint32_t *__restrict__ slots, uint32_t n_keys,
                                                        uint32_t c_lo, uint32_t kv_dim, unsigned char *__restrict__ F) {
     __shared__ f4 rows[kPaNK][64];                         // the chunk's K or V rows, 256 floats each
     const int tid = threadIdx.x;
-    const uint32_t c = c_lo + blockIdx.x, kvh = blockIdx.y;
+    const uint32_t c = c_lo + blockIdx.y, kvh = blockIdx.x;
     const bool is_v = blockIdx.z != 0;
     {
         const int key = tid >> 3, part = tid & 7;           // 8 threads per row
@@ -818,7 +822,7 @@ __global__ __launch_bounds__(256) void k_prefill_frags(const float *__restrict__
         }
     }
     __syncthreads();
-    unsigned char *Fc = F + ((size_t)kvh * gridDim.x + blockIdx.x) * kPaChunkBytes + (is_v ? 2 * kPaPlane : 0);
+    unsigned char *Fc = F + ((size_t)kvh * gridDim.y + blockIdx.y) * kPaChunkBytes + (is_v ? 2 * kPaPlane : 0);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         const int item = tid + 256 * u, f = item >> 6, l = item & 63;   // fragment f, lane l
@@ -859,15 +863,15 @@ __global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, c = lane & 15;
-    const uint32_t kvh = blockIdx.y;
+    const uint32_t kvh = blockIdx.x;
     // this lane's query: column c of the wave's 16 rows
     const int qi = wave * 16 + c;
-    const uint32_t tq = blockIdx.x * TQ + qi / GQA, head = kvh * GQA + qi % GQA;
+    const uint32_t tq = blockIdx.y * TQ + qi / GQA, head = kvh * GQA + qi % GQA;
     const uint32_t tqc = min(tq, n_tok - 1);
     const uint32_t Sq = num_prev + tqc + 1;                        // keys [startq, Sq)
     const uint32_t startq = (window > 0 && Sq > window) ? Sq - window : 0;
     // the workgroup's key range: from its first token's start to its last token
-    const uint32_t t_first = blockIdx.x * TQ, t_last = min(t_first + TQ - 1, n_tok - 1);
+    const uint32_t t_first = blockIdx.y * TQ, t_last = min(t_first + TQ - 1, n_tok - 1);
     const uint32_t S_first = num_prev + t_first + 1, S_end = num_prev + t_last + 1;
     const uint32_t k_first = (window > 0 && S_first > window) ? S_first - window : 0;
     // key split (gridDim.z parts): part z walks its share of the whole
@@ -1126,7 +1130,7 @@ int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const f
         const uint32_t k_lo = (window > 0 && num_prev + 1 > window) ? num_prev + 1 - window : 0;
         const uint32_t c_lo = k_lo / kPaNK, c_hi = (n_keys + kPaNK - 1) / kPaNK, nfch = c_hi - c_lo;
         if (!frag || frag_bytes < (size_t)num_kv * nfch * kPaChunkBytes) return CHN_E_UNSUPPORTED;
-        k_prefill_frags<<<dim3(nfch, num_kv, 2), 256, 0, st>>>(kc, vc, slots, n_keys, c_lo, kv_dim, frag);
+        k_prefill_frags<<<dim3(num_kv, nfch, 2), 256, 0, st>>>(kc, vc, slots, n_keys, c_lo, kv_dim, frag);
         const uint32_t tq = 64 / gqa;
         const uint32_t tiles = (n_tok + tq - 1) / tq;
         // Causal tiles differ in length (the last one walks every key): while
@@ -1138,7 +1142,7 @@ int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const f
         const uint32_t wgs = tiles * (num_q_heads / gqa);
         uint32_t nparts = ws ? 512 / (wgs ? wgs : 1) : 1;
         nparts = nparts < 1 ? 1 : (nparts > kPaParts ? kPaParts : nparts);
-        const dim3 mgrid(tiles, num_q_heads / gqa, nparts);
+        const dim3 mgrid(num_q_heads / gqa, tiles, nparts);
 #define CHN_PATTN_MF(G) \
     k_prefill_attn_mf<G><<<mgrid, 256, 0, st>>>(q, frag, c_lo, nfch, num_prev, n_tok, num_q_heads, scale, window, out, \
                                                 outb, ws)
