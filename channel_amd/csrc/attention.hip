@@ -45,10 +45,15 @@ size_t attn_ws_bytes(uint32_t num_q_heads, uint32_t head_dim, uint32_t max_slots
     return (size_t)dec_splits(max_slots) * num_q_heads * ((size_t)head_dim + 2) * 4;
 }
 
-// Prefill key split: up to kPaParts workgroups per query tile; the
-// workspace holds each part's sums [n_tok][heads][D] and (max,
-// denominator) pairs.
-constexpr uint32_t kPaParts = 2;   // 4 measured slower at 512 tokens (20.65 against 20.28 ms)
+// Prefill key split: a query tile's key chunks are cut into parts of about
+// kPaPartChunks chunks, at most kPaParts parts (one workgroup each), so the
+// causal tiles' walks come out about equally long; the workspace holds each
+// part's sums [n_tok][heads][D] and (max, denominator) pairs.
+constexpr uint32_t kPaParts = 4;
+constexpr uint32_t kPaPartChunks = 4;
+// Waves per prefill attention workgroup, 16 query rows each: eight waves
+// (128 query rows) share every 64 KB chunk the workgroup copies into LDS.
+constexpr int kPaWaves = 8;
 size_t prefill_attn_ws_bytes(uint32_t n_tok, uint32_t num_q_heads, uint32_t head_dim) {
     return kPaParts * (size_t)n_tok * num_q_heads * ((size_t)head_dim + 2) * 4;
 }
@@ -849,36 +854,88 @@ __global__ __launch_bounds__(256) void k_prefill_frags(const float *__restrict__
     }
 }
 
-// F: the pre-pass output for chunks c_lo .. c_lo + nfch - 1.
+// The key chunks [cf, ce) a query tile of TQ tokens walks (from its first
+// token's window start to its last token's key) and the number of parts it
+// is cut into (maxparts = 1: none).
+struct PaGeom {
+    uint32_t TQ, n_tok, num_prev, window, maxparts;
+};
+__host__ __device__ inline void pa_chunks(const PaGeom &g, uint32_t tile, uint32_t &cf, uint32_t &ce) {
+    const uint32_t t_first = tile * g.TQ;
+    const uint32_t t_last = t_first + g.TQ - 1 < g.n_tok - 1 ? t_first + g.TQ - 1 : g.n_tok - 1;
+    const uint32_t S_first = g.num_prev + t_first + 1, S_end = g.num_prev + t_last + 1;
+    const uint32_t k_first = (g.window > 0 && S_first > g.window) ? S_first - g.window : 0;
+    cf = k_first / kPaNK;
+    ce = (S_end + kPaNK - 1) / kPaNK;
+}
+__host__ __device__ inline uint32_t pa_parts(const PaGeom &g, uint32_t tile) {
+    uint32_t cf, ce;
+    pa_chunks(g, tile, cf, ce);
+    const uint32_t np = (ce - cf + kPaPartChunks - 1) / kPaPartChunks;
+    return np < 1 ? 1 : (np > g.maxparts ? g.maxparts : np);
+}
+
+// F: the pre-pass output for chunks c_lo .. c_lo + nfch - 1.  Grid (KV
+// heads, work items): item `it` of a KV head is part `part` of query tile
+// `tile`, the tiles' parts numbered in tile order; every wave finds its
+// item's tile with a prefix sum of the tiles' part counts over the lanes.
 template <int GQA>
-__global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict__ Q,
+__global__ __launch_bounds__(64 * kPaWaves) void k_prefill_attn_mf(const float *__restrict__ Q,
                                                          const unsigned char *__restrict__ F, uint32_t c_lo,
                                                          uint32_t nfch, uint32_t num_prev, uint32_t n_tok,
                                                          uint32_t num_q_heads, float scale, uint32_t window,
                                                          float *__restrict__ out, __bf16 *__restrict__ outb,
-                                                         float *__restrict__ ws) {
-    constexpr int D = 256, NK = kPaNK, TQ = 64 / GQA;
+                                                         float *__restrict__ ws, uint32_t maxparts) {
+    constexpr int D = 256, NK = kPaNK, TQ = 16 * kPaWaves / GQA;
     __shared__ __attribute__((aligned(16))) unsigned char ring[2][kPaChunkBytes];   // two chunks in flight
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, c = lane & 15;
     const uint32_t kvh = blockIdx.x;
+    // the work item's query tile and key part
+    const PaGeom geo{(uint32_t)TQ, n_tok, num_prev, window, maxparts};
+    const uint32_t ntiles = (n_tok + TQ - 1) / TQ;
+    uint32_t tile = 0, part = 0, nparts = 1;
+    {
+        const uint32_t it = blockIdx.y;
+        uint32_t base = 0;
+        for (uint32_t t0 = 0; t0 < ntiles; t0 += 64) {
+            const uint32_t t = t0 + lane;
+            const uint32_t np = t < ntiles ? pa_parts(geo, t) : 0u;
+            uint32_t incl = np;                                    // inclusive prefix sum over the lanes
+#pragma unroll
+            for (int d = 1; d < 64; d *= 2) {
+                const uint32_t v = (uint32_t)__shfl_up((int)incl, d, 64);
+                incl += lane >= d ? v : 0u;
+            }
+            const uint32_t total = (uint32_t)__shfl((int)incl, 63, 64);
+            if (it < base + total) {
+                const uint32_t r = it - base;
+                const uint64_t hit = __ballot(r < incl && r >= incl - np);
+                const int L = __builtin_ctzll(hit);
+                tile = t0 + L;
+                nparts = (uint32_t)__shfl((int)np, L, 64);
+                part = r - ((uint32_t)__shfl((int)incl, L, 64) - nparts);
+                break;
+            }
+            base += total;
+        }
+        tile = __builtin_amdgcn_readfirstlane(tile);
+        part = __builtin_amdgcn_readfirstlane(part);
+        nparts = __builtin_amdgcn_readfirstlane(nparts);
+    }
     // this lane's query: column c of the wave's 16 rows
     const int qi = wave * 16 + c;
-    const uint32_t tq = blockIdx.y * TQ + qi / GQA, head = kvh * GQA + qi % GQA;
+    const uint32_t tq = tile * TQ + qi / GQA, head = kvh * GQA + qi % GQA;
     const uint32_t tqc = min(tq, n_tok - 1);
     const uint32_t Sq = num_prev + tqc + 1;                        // keys [startq, Sq)
     const uint32_t startq = (window > 0 && Sq > window) ? Sq - window : 0;
-    // the workgroup's key range: from its first token's start to its last token
-    const uint32_t t_first = blockIdx.y * TQ, t_last = min(t_first + TQ - 1, n_tok - 1);
-    const uint32_t S_first = num_prev + t_first + 1, S_end = num_prev + t_last + 1;
-    const uint32_t k_first = (window > 0 && S_first > window) ? S_first - window : 0;
-    // key split (gridDim.z parts): part z walks its share of the whole
-    // 32-key chunks over [k_first, S_end); the parts' partial states meet in
-    // k_prefill_attn_merge
-    const uint32_t nparts = gridDim.z, part = blockIdx.z;
-    const uint32_t cf = k_first / NK, ce = (S_end + NK - 1) / NK;
+    // the tile's 32-key chunks [cf, ce) (from its first token's window start
+    // to its last token), cut into nparts parts; the parts' partial states
+    // meet in k_prefill_attn_merge
+    uint32_t cf, ce;
+    pa_chunks(geo, tile, cf, ce);
     const uint32_t per = (ce - cf + nparts - 1) / nparts;
     const uint32_t c_begin = min(ce, cf + part * per), c_stop = min(ce, c_begin + per);
 
@@ -899,13 +956,14 @@ __global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict
         }
     }
 
-    // chunk cc into ring stage st: wave w copies fragments 16 w .. 16 w + 15
+    // chunk cc into ring stage st: wave w copies fragments NFR w .. NFR w + NFR - 1
     const unsigned char *Fk = F + (size_t)kvh * nfch * kPaChunkBytes + lane * 16;
     auto issue = [&](uint32_t cc, int st) {
         const unsigned char *src = Fk + (size_t)(cc - c_lo) * kPaChunkBytes;
+        constexpr int NFR = 64 / kPaWaves;                     // fragments per wave
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int fr = wave * 16 + i;
+        for (int i = 0; i < NFR; ++i) {
+            const int fr = wave * NFR + i;
             __builtin_amdgcn_global_load_lds(src + fr * kPaFrag, (lds_t *)(ring[st] + fr * kPaFrag), 16, 0, 0);
         }
     };
@@ -1020,7 +1078,7 @@ __global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict
 #pragma unroll
         for (int dt = 0; dt < 16; ++dt) *(f4 *)(ws + part * nrow * D + orow + 16 * dt) = o[dt];
         if (g == 0) {
-            float *ml = ws + nparts * nrow * D + 2 * (part * nrow + (size_t)tq * num_q_heads + head);
+            float *ml = ws + maxparts * nrow * D + 2 * (part * nrow + (size_t)tq * num_q_heads + head);
             ml[0] = m;
             ml[1] = l;
         }
@@ -1032,14 +1090,18 @@ __global__ __launch_bounds__(256) void k_prefill_attn_mf(const float *__restrict
 }
 
 // The key-split parts' states of each (token, head) rescaled to their
-// common maximum and normalised; four values per thread.
-__global__ __launch_bounds__(256) void k_prefill_attn_merge(const float *__restrict__ ws, uint32_t nparts,
-                                                            size_t nrow, uint32_t D, float *__restrict__ out,
-                                                            __bf16 *__restrict__ outb) {
+// common maximum and normalised; four values per thread.  Rows of tiles
+// that were not split were written by the attention itself.
+__global__ __launch_bounds__(256) void k_prefill_attn_merge(const float *__restrict__ ws, PaGeom geo,
+                                                            uint32_t num_q_heads, size_t nrow, uint32_t D,
+                                                            float *__restrict__ out, __bf16 *__restrict__ outb) {
     const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;   // element of [token][head][D]
     if (i >= nrow * D) return;
     const size_t row = i / D;
-    const float *ml = ws + nparts * nrow * D;
+    const uint32_t nparts = pa_parts(geo, (uint32_t)(row / num_q_heads) / geo.TQ);
+    if (nparts < 2) return;
+    const uint32_t np_stride = geo.maxparts;   // the workspace holds maxparts parts
+    const float *ml = ws + np_stride * nrow * D;
     float mx = -INFINITY;
     for (uint32_t p = 0; p < nparts; ++p) mx = fmaxf(mx, ml[2 * (p * nrow + row)]);
     f4 t = f4{0, 0, 0, 0};
@@ -1131,21 +1193,24 @@ int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const f
         const uint32_t c_lo = k_lo / kPaNK, c_hi = (n_keys + kPaNK - 1) / kPaNK, nfch = c_hi - c_lo;
         if (!frag || frag_bytes < (size_t)num_kv * nfch * kPaChunkBytes) return CHN_E_UNSUPPORTED;
         k_prefill_frags<<<dim3(num_kv, nfch, 2), 256, 0, st>>>(kc, vc, slots, n_keys, c_lo, kv_dim, frag);
-        const uint32_t tq = 64 / gqa;
+        const uint32_t tq = 16 * kPaWaves / gqa;
         const uint32_t tiles = (n_tok + tq - 1) / tq;
-        // Causal tiles differ in length (the last one walks every key): while
-        // the tiles fill fewer than two workgroups per CU, each tile's keys
-        // are split between up to kPaParts workgroups, which shortens the
-        // longest walk and fills the part (512 tokens: 128 tiles of up to 16
-        // chunks -> 256 of up to 8: 76 -> 44 us per layer, plus 5.6 us of
-        // merge).
-        const uint32_t wgs = tiles * (num_q_heads / gqa);
-        uint32_t nparts = ws ? 512 / (wgs ? wgs : 1) : 1;
-        nparts = nparts < 1 ? 1 : (nparts > kPaParts ? kPaParts : nparts);
-        const dim3 mgrid(num_q_heads / gqa, tiles, nparts);
-#define CHN_PATTN_MF(G) \
-    k_prefill_attn_mf<G><<<mgrid, 256, 0, st>>>(q, frag, c_lo, nfch, num_prev, n_tok, num_q_heads, scale, window, out, \
-                                                outb, ws)
+        // Causal tiles differ in length (the last one walks every key): each
+        // tile's chunks are cut into parts of about kPaPartChunks chunks (at
+        // most kPaParts), so the longest walk is about that long and the
+        // short tiles run whole (512 tokens: 16 tiles of 1..16 chunks -> 40
+        // parts of at most 4 chunks per KV head).
+        const PaGeom geo{tq, n_tok, num_prev, window, ws ? kPaParts : 1u};
+        uint32_t items = 0, split_tiles = 0;
+        for (uint32_t t = 0; t < tiles; ++t) {
+            const uint32_t np = pa_parts(geo, t);
+            items += np;
+            split_tiles += np > 1 ? 1u : 0u;
+        }
+        const dim3 mgrid(num_q_heads / gqa, items);
+#define CHN_PATTN_MF(G)                                                                                  \
+    k_prefill_attn_mf<G><<<mgrid, 64 * kPaWaves, 0, st>>>(q, frag, c_lo, nfch, num_prev, n_tok, num_q_heads, scale, \
+                                                         window, out, outb, ws, geo.maxparts)
         switch (gqa) {
         case 1: CHN_PATTN_MF(1); break;
         case 2: CHN_PATTN_MF(2); break;
@@ -1153,9 +1218,10 @@ int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const f
         default: CHN_PATTN_MF(8); break;
         }
 #undef CHN_PATTN_MF
-        if (nparts > 1) {
+        if (split_tiles) {
             const size_t nrow = (size_t)n_tok * num_q_heads, nq4 = nrow * head_dim / 4;
-            k_prefill_attn_merge<<<(unsigned)((nq4 + 255) / 256), 256, 0, st>>>(ws, nparts, nrow, head_dim, out, outb);
+            k_prefill_attn_merge<<<(unsigned)((nq4 + 255) / 256), 256, 0, st>>>(ws, geo, num_q_heads, nrow, head_dim,
+                                                                                  out, outb);
         }
         return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
     }
