@@ -939,6 +939,21 @@ __global__ __launch_bounds__(64 * kPaWaves) void k_prefill_attn_mf(const float *
     const uint32_t per = (ce - cf + nparts - 1) / nparts;
     const uint32_t c_begin = min(ce, cf + part * per), c_stop = min(ce, c_begin + per);
 
+    // chunk cc into ring stage st: wave w copies fragments NFR w .. NFR w + NFR - 1
+    const unsigned char *Fk = F + (size_t)kvh * nfch * kPaChunkBytes + lane * 16;
+    auto issue = [&](uint32_t cc, int st) {
+        const unsigned char *src = Fk + (size_t)(cc - c_lo) * kPaChunkBytes;
+        constexpr int NFR = 64 / kPaWaves;                     // fragments per wave
+#pragma unroll
+        for (int i = 0; i < NFR; ++i) {
+            const int fr = wave * NFR + i;
+            __builtin_amdgcn_global_load_lds(src + fr * kPaFrag, (lds_t *)(ring[st] + fr * kPaFrag), 16, 0, 0);
+        }
+    };
+
+    // the first chunk's copy goes out before Q's loads, so the two overlap
+    if (c_begin < c_stop) issue(c_begin, 0);
+
     // Q^T operand: lane holds query c, dims 32 j + 8 g .. +8, as hi / lo bf16
     pbf16x8 qh[8], ql[8];
     {
@@ -956,25 +971,12 @@ __global__ __launch_bounds__(64 * kPaWaves) void k_prefill_attn_mf(const float *
         }
     }
 
-    // chunk cc into ring stage st: wave w copies fragments NFR w .. NFR w + NFR - 1
-    const unsigned char *Fk = F + (size_t)kvh * nfch * kPaChunkBytes + lane * 16;
-    auto issue = [&](uint32_t cc, int st) {
-        const unsigned char *src = Fk + (size_t)(cc - c_lo) * kPaChunkBytes;
-        constexpr int NFR = 64 / kPaWaves;                     // fragments per wave
-#pragma unroll
-        for (int i = 0; i < NFR; ++i) {
-            const int fr = wave * NFR + i;
-            __builtin_amdgcn_global_load_lds(src + fr * kPaFrag, (lds_t *)(ring[st] + fr * kPaFrag), 16, 0, 0);
-        }
-    };
-
     f4 o[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[i] = f4{0, 0, 0, 0};
     float m = -INFINITY, l = 0.0f;
 
     const uint32_t sm0 = lds_addr(ring[0]) + lane * 16;
-    if (c_begin < c_stop) issue(c_begin, 0);
     for (uint32_t cc = c_begin; cc < c_stop; ++cc) {
         const int st = (cc - c_begin) & 1;
         wait_vm_lgkm0<0>();                                        // this wave's share of chunk cc landed
