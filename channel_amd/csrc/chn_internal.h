@@ -228,9 +228,9 @@ int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const f
 size_t xbytes_bytes(uint32_t nb);
 int launch_gemv_q8(hipStream_t st, const uint32_t *W, const float *x, float *y, uint32_t M, uint32_t nb,
                    uint32_t *xp_ws);
-// Q8R (Q8_0 repacked for aligned streaming: [rows * nb][32] codes, then the
-// f32 scales) and the Q8 matvec over it (identical results to
-// launch_gemv_q8 on the same weights).
+// Q8R (Q8_0 repacked for coalesced streaming: [rows][2][nb] 16-byte code
+// halves, then the [rows * nb] f32 scales) and the Q8 matvec over it
+// (identical results to launch_gemv_q8 on the same weights).
 int launch_q8_repack(hipStream_t st, const uint32_t *W, uint32_t rows, uint32_t nb, void *dst);
 int launch_gemv_q8r(hipStream_t st, const void *R, const float *x, float *y, uint32_t M, uint32_t nb,
                     uint32_t *xp_ws, bool planes_ready = false);

@@ -150,16 +150,19 @@ __global__ __launch_bounds__(256) void k_q8mv(const uint32_t *__restrict__ W, co
     }
 }
 
-// Q8R: the Q8_0 blocks repacked for aligned streaming, codes first ([rows *
-// nb][32] int8, two 16-byte words per block, order kept), then the f32
-// scales ([rows * nb]); 36 bytes per block as before.
+// Q8R: the Q8_0 blocks repacked for coalesced streaming, codes first, then
+// the f32 scales ([rows * nb]); 36 bytes per block as before.  The codes of
+// a row are its blocks' first 16-byte halves in block order, then their
+// second halves ([rows][2][nb] 16-byte words), so the lanes of a wave that
+// take consecutive blocks read one contiguous run per half.
 __global__ __launch_bounds__(256) void k_repack_q8(const uint32_t *__restrict__ src, u32x4q *__restrict__ D,
-                                                   float *__restrict__ S, size_t nblk) {
+                                                   float *__restrict__ S, size_t nblk, uint32_t nb) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nblk) return;
     const uint32_t *p = src + i * 9;
-    D[2 * i] = u32x4q{p[1], p[2], p[3], p[4]};
-    D[2 * i + 1] = u32x4q{p[5], p[6], p[7], p[8]};
+    const size_t row = i / nb, h0 = row * 2 * nb + (i - row * nb);
+    D[h0] = u32x4q{p[1], p[2], p[3], p[4]};
+    D[h0 + nb] = u32x4q{p[5], p[6], p[7], p[8]};
     S[i] = __builtin_bit_cast(float, p[0]);
 }
 
@@ -167,21 +170,23 @@ int launch_q8_repack(hipStream_t st, const uint32_t *W, uint32_t rows, uint32_t 
     const size_t nblk = (size_t)rows * nb;
     if (!nblk) return CHN_OK;
     k_repack_q8<<<(unsigned)((nblk + 255) / 256), 256, 0, st>>>(W, (u32x4q *)dst,
-                                                               (float *)((unsigned char *)dst + nblk * 32), nblk);
+                                                               (float *)((unsigned char *)dst + nblk * 32), nblk, nb);
     return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
 }
 
 // The Q8 matvec over Q8R: lane l owns blocks l and l + 64 of each row (K <=
-// 4096) and reads them straight from the stream (two 16-byte codes words and
-// the scale), no LDS; RPW rows per group, the next group in flight while
-// one is reduced.  Per block and row the arithmetic, its order and the
-// reduction are k_q8mv's, so the two give identical results.
+// 4096) and reads them straight from the stream (its two 16-byte codes words
+// and the scale), no LDS; RPW rows per group, the next group in flight while
+// one is reduced.  Every load is unconditional (indices clamped into the
+// matrix; a lane past the row's blocks adds nothing, rows past M are not
+// stored).  Per block and row the arithmetic, its order and the reduction
+// are k_q8mv's, so the two give identical results.
 template <int RPW>
 __global__ __launch_bounds__(256) void k_q8rmv(const u32x4q *__restrict__ D, const float *__restrict__ S,
                                                const uint32_t *__restrict__ xp, float *__restrict__ y, uint32_t M,
                                                uint32_t nb) {
     constexpr int LV = RPW == 1 ? 0 : (RPW == 2 ? 1 : 2);
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     uint32_t P[2][XB_WORDS];
     float xs[2];
 #pragma unroll
@@ -201,15 +206,14 @@ __global__ __launch_bounds__(256) void k_q8rmv(const u32x4q *__restrict__ D, con
     auto load = [&](Grp &q, uint32_t g) {
 #pragma unroll
         for (int r = 0; r < RPW; ++r) {
-            const uint32_t row = g * RPW + r;
+            const uint32_t row = min(g * RPW + r, M - 1);
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
-                const uint32_t b = c * 64 + lane;
-                const bool ok = row < M && b < nb;
-                const size_t i = (size_t)(ok ? row : 0) * nb + (ok ? b : 0);
-                q.d[r][c][0] = ok ? __builtin_nontemporal_load(D + 2 * i) : u32x4q{0, 0, 0, 0};
-                q.d[r][c][1] = ok ? __builtin_nontemporal_load(D + 2 * i + 1) : u32x4q{0, 0, 0, 0};
-                q.s[r][c] = ok ? __builtin_nontemporal_load(S + i) : 0.0f;
+                const uint32_t b = min(c * 64 + lane, nb - 1);
+                const size_t h0 = (size_t)row * 2 * nb + b;
+                q.d[r][c][0] = __builtin_nontemporal_load(D + h0);
+                q.d[r][c][1] = __builtin_nontemporal_load(D + h0 + nb);
+                q.s[r][c] = __builtin_nontemporal_load(S + (size_t)row * nb + b);
             }
         }
     };

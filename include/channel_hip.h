@@ -331,9 +331,10 @@ int chn_batch_causal_attn(chn_ctx *ctx, const float *q, const float *k_cache, co
 int chn_gemv_q8(chn_ctx *ctx, const uint32_t *W, const float *x, float *y, uint32_t M, uint32_t K);
 
 /* Q8R: the Q8_0 blocks of W [rows x K] repacked into dst (rows * K / 32 * 36
- * bytes, 16-byte aligned) for aligned streaming: the 32 codes of every
- * block in order, then the f32 scales.  The model holds its tied embedding
- * this way.  Counterpart of chn_q4_repack for the logits table; the
+ * bytes, 16-byte aligned) for coalesced streaming: per row, the first 16
+ * codes of each of its blocks in block order, then the last 16 codes of
+ * each; after all rows, the f32 scales in block order.  The model holds its
+ * tied embedding this way.  Counterpart of chn_q4_repack for the logits table; the
  * reference keeps the Q8_0 layout (src/quant.zig:54-98). */
 int chn_q8_repack(chn_ctx *ctx, const uint32_t *W, uint32_t rows, uint32_t K, void *dst);
 

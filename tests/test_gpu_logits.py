@@ -41,9 +41,10 @@ def test_gemv_q8(ctx, M, K):
 
 @pytest.mark.parametrize("M,K", [(262144, 3840), (1001, 128), (7, 4096)])
 def test_gemv_q8r_matches_q8(ctx, M, K):
-    """The model's logits run on Q8R (the Q8_0 blocks repacked: codes, then
-    the f32 scales).  The repack keeps every byte, and the Q8R matvec gives
-    the reference-layout matvec's results bit for bit."""
+    """The model's logits run on Q8R (the Q8_0 blocks repacked: per row the
+    blocks' first 16 codes, then their last 16, then all f32 scales).  The
+    repack keeps every byte, and the Q8R matvec gives the reference-layout
+    matvec's results bit for bit."""
     nb = K // 32
     W = synth_q8_dev(ctx, M, K, 300 + M % 89)
     R = ctx.alloc(ca.q8_bytes(M, K))
@@ -56,7 +57,8 @@ def test_gemv_q8r_matches_q8(ctx, M, K):
     assert np.array_equal(ctx.download(y1, np.uint32, M), ctx.download(y2, np.uint32, M))
     Wh = ctx.download(W, np.uint32, M * nb * 9).reshape(M * nb, 9)
     Rh = ctx.download(R, np.uint32, M * nb * 9)
-    assert np.array_equal(Rh[: M * nb * 8].reshape(M * nb, 8), Wh[:, 1:])
+    codes = Rh[: M * nb * 8].reshape(M, 2, nb, 4).transpose(0, 2, 1, 3).reshape(M * nb, 8)
+    assert np.array_equal(codes, Wh[:, 1:])
     assert np.array_equal(Rh[M * nb * 8:], Wh[:, 0])
     if M <= 4096:
         want = oracle.gemv_q8(Wh.ravel(), f32_host(ctx, x, K), M, K)
