@@ -191,11 +191,11 @@ __global__ __launch_bounds__(256) void k_q8rmv(const u32x4q *__restrict__ D, con
     float xs[2];
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-        const uint32_t b = c * 64 + lane;
-        const bool ok = b < nb;
+        const uint32_t b = c * 64 + lane, bc = min(b, nb - 1);
+        const uint32_t keep = b < nb ? ~0u : 0u;
 #pragma unroll
-        for (int i = 0; i < XB_WORDS; ++i) P[c][i] = ok ? xp[(size_t)i * nb + b] : 0u;
-        xs[c] = ok ? ((const float *)(xp + (size_t)XB_WORDS * nb))[b] : 0.0f;
+        for (int i = 0; i < XB_WORDS; ++i) P[c][i] = xp[(size_t)i * nb + bc] & keep;
+        xs[c] = __builtin_bit_cast(float, xp[(size_t)XB_WORDS * nb + bc] & keep);
     }
     const uint32_t ngroups = (M + RPW - 1) / RPW;
     const uint32_t gstride = gridDim.x * 4;
@@ -219,7 +219,7 @@ __global__ __launch_bounds__(256) void k_q8rmv(const u32x4q *__restrict__ D, con
     };
     uint32_t g = blockIdx.x * 4 + wave;
     Grp nx;
-    if (g < ngroups) load(nx, g);
+    load(nx, g < ngroups ? g : ngroups - 1);   // unconditional: a wave past the groups never uses it
     for (; g < ngroups; g += gstride) {
         const Grp cur = nx;
         if (g + gstride < ngroups) load(nx, g + gstride);

@@ -115,16 +115,21 @@ constexpr int kSegWords = kMaxBlocksPerWave * 5; // LDS words per stream
 // XIN (WPR == 1, K <= 4096): the workgroup converts x to digit planes in LDS
 // itself (the same planes as k_xplanes), so the call is one launch; x's
 // loads are issued before the first weights, the conversion runs while
-// those are in flight.
-template <int MODE, int RPW, int WPR, bool XIN>
+// those are in flight.  A row segment is NJ 16-byte loads per lane
+// (NJ = ceil(chunks / 64), chosen by the host), every one unconditional:
+// indices past the segment or the matrix are clamped into it and their
+// data is never used, so the compiler's waits for x leave the weights in
+// flight.
+template <int MODE, int RPW, int WPR, bool XIN, int NJ>
 __global__ __launch_bounds__(256) void k_q4mv(MatvecArgs a, const float *__restrict__ x) {
     constexpr int NMAT = (MODE == MV_MLP) ? 2 : 1;
     constexpr int V = RPW * NMAT;
     constexpr int G = 4 / WPR;
     constexpr int LV = (V == 1) ? 0 : (V == 2) ? 1 : (V == 4) ? 2 : 3;
     static_assert(V == 1 || V == 2 || V == 4 || V == 8, "V must be a power of two <= 8");
+    static_assert(NJ >= 1 && NJ <= 3, "a wave's segment is at most 128 blocks");
 
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int grp = wave / WPR, part = wave % WPR;
     const uint32_t nb = a.nb;
 
@@ -143,43 +148,44 @@ __global__ __launch_bounds__(256) void k_q4mv(MatvecArgs a, const float *__restr
     uint32_t *L = seg[wave];
 
     // XIN: x's values, four threads per 32-block (eight values each), two passes
+    // (loads clamped into x, values past it zeroed)
     float xv[XIN ? 2 : 1][8];
     if (XIN) {
 #pragma unroll
         for (int ps = 0; ps < 2; ++ps) {
             const uint32_t b = ps * 64 + (threadIdx.x >> 2), w = threadIdx.x & 3;
-            if (b < nb) {
-                const float4 t0 = *(const float4 *)(x + (size_t)b * 32 + w * 8);
-                const float4 t1 = *(const float4 *)(x + (size_t)b * 32 + w * 8 + 4);
-                xv[ps][0] = t0.x; xv[ps][1] = t0.y; xv[ps][2] = t0.z; xv[ps][3] = t0.w;
-                xv[ps][4] = t1.x; xv[ps][5] = t1.y; xv[ps][6] = t1.z; xv[ps][7] = t1.w;
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) xv[ps][i] = 0.0f;
-            }
+            const uint32_t bc = min(b, nb - 1);
+            const float4 t0 = *(const float4 *)(x + (size_t)bc * 32 + w * 8);
+            const float4 t1 = *(const float4 *)(x + (size_t)bc * 32 + w * 8 + 4);
+            const float z = b < nb ? 1.0f : 0.0f;
+            xv[ps][0] = t0.x * z; xv[ps][1] = t0.y * z; xv[ps][2] = t0.z * z; xv[ps][3] = t0.w * z;
+            xv[ps][4] = t1.x * z; xv[ps][5] = t1.y * z; xv[ps][6] = t1.z * z; xv[ps][7] = t1.w * z;
         }
     }
 
     const uint32_t ngroups = (a.M + RPW - 1) / RPW;
     const uint32_t gstride = gridDim.x * G;
-    u32x4 pf[V][3];
+    u32x4 pf[V][NJ];
+    // clamps: the last chunk of the segment (a wave without blocks reads
+    // the row's first chunk), the last row of the matrix
+    const uint32_t c_last = chunks ? chunks - 1 : 0u;
+    const uint32_t kb_ld = nblk ? kb0 : 0u;
 
     auto load = [&](uint32_t g) {
 #pragma unroll
         for (int s = 0; s < V; ++s) {
-            const uint32_t row = g * RPW + s / NMAT;
-            const uint32_t *base = row_base<MODE>(a, row < a.M ? row : 0, s % NMAT) + (size_t)kb0 * 5;
+            const uint32_t row = min(g * RPW + s / NMAT, a.M - 1);
+            const uint32_t *base = row_base<MODE>(a, row, s % NMAT) + (size_t)kb_ld * 5;
 #pragma unroll
-            for (int j = 0; j < 3; ++j) {
-                const uint32_t c = lane + 64 * j;
-                if (row < a.M && c < chunks)
-                    pf[s][j] = __builtin_nontemporal_load((const u32x4 *)base + c);
+            for (int j = 0; j < NJ; ++j) {
+                const uint32_t c = min(lane + 64 * j, c_last);
+                pf[s][j] = __builtin_nontemporal_load((const u32x4 *)base + c);
             }
         }
     };
 
     uint32_t g = blockIdx.x * G + grp;
-    if (g < ngroups) load(g);
+    load(g < ngroups ? g : ngroups - 1);    // unconditional: a wave past the groups never uses it
 
     // this lane's two blocks of activation planes
     uint32_t P[2][XP_WORDS];
@@ -218,7 +224,7 @@ __global__ __launch_bounds__(256) void k_q4mv(MatvecArgs a, const float *__restr
 #pragma unroll
             for (int s = 0; s < V; ++s)
 #pragma unroll
-                for (int j = 0; j < 3; ++j) {
+                for (int j = 0; j < NJ; ++j) {
                     const uint32_t c = lane + 64 * j;
                     if (c < chunks) *(u32x4 *)(L + s * kSegWords + 4 * c) = pf[s][j];
                 }
@@ -306,16 +312,29 @@ static MvShape pick_shape(int mode, uint32_t M, uint32_t nb) {
     return s;
 }
 
-template <int MODE, int WPR, bool XIN>
-static bool launch_wpr(int rpw, const MatvecArgs &a, const float *x, uint32_t grid, hipStream_t st) {
+template <int MODE, int WPR, bool XIN, int NJ>
+static bool launch_nj(int rpw, const MatvecArgs &a, const float *x, uint32_t grid, hipStream_t st) {
     constexpr int NMAT = MODE == MV_MLP ? 2 : 1;
     switch (rpw) {
-    case 1: k_q4mv<MODE, 1, WPR, XIN><<<grid, 256, 0, st>>>(a, x); return true;
-    case 2: k_q4mv<MODE, 2, WPR, XIN><<<grid, 256, 0, st>>>(a, x); return true;
+    case 1: k_q4mv<MODE, 1, WPR, XIN, NJ><<<grid, 256, 0, st>>>(a, x); return true;
+    case 2: k_q4mv<MODE, 2, WPR, XIN, NJ><<<grid, 256, 0, st>>>(a, x); return true;
     case 4:
-        if constexpr (4 * NMAT <= 8) { k_q4mv<MODE, 4, WPR, XIN><<<grid, 256, 0, st>>>(a, x); return true; }
+        if constexpr (4 * NMAT <= 8) { k_q4mv<MODE, 4, WPR, XIN, NJ><<<grid, 256, 0, st>>>(a, x); return true; }
         return false;
     }
+    return false;
+}
+
+// NJ: 16-byte loads per lane for the widest wave segment (the kernel's
+// per-wave block count, rounded as it rounds it)
+template <int MODE, int WPR, bool XIN>
+static bool launch_wpr(int rpw, const MatvecArgs &a, const float *x, uint32_t grid, hipStream_t st) {
+    const uint32_t per = (((a.nb + WPR - 1) / WPR) + 3) / 4 * 4;
+    const uint32_t chunks = (per < a.nb ? per : a.nb) * 5 / 4;
+    const uint32_t nj = (chunks + 63) / 64;
+    if (nj <= 1) return launch_nj<MODE, WPR, XIN, 1>(rpw, a, x, grid, st);
+    if (nj == 2) return launch_nj<MODE, WPR, XIN, 2>(rpw, a, x, grid, st);
+    if (nj == 3) return launch_nj<MODE, WPR, XIN, 3>(rpw, a, x, grid, st);
     return false;
 }
 
