@@ -341,11 +341,15 @@ __global__ __launch_bounds__(256) void k_topk_tile(const float *__restrict__ log
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const uint32_t base = blockIdx.x * kTile + wave * 256;
     uint64_t k[4];
+    float lv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) lv[u] = logits[min(base + 64 * u + lane, V - 1)];   // all in flight
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         const uint32_t idx = base + 64 * u + lane;
         // padding keys (0) sort below every real key
-        k[u] = idx < V ? topk_key(30.0f * tanhf(logits[idx] * (1.0f / 30.0f)), idx) : 0ull;
+        const uint64_t key = topk_key(30.0f * tanhf(lv[u] * (1.0f / 30.0f)), idx);
+        k[u] = idx < V ? key : 0ull;
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) k[u] = wave_sort64_desc(k[u], lane);
