@@ -815,16 +815,18 @@ __global__ __launch_bounds__(256) void k_prefill_frags(const float *__restrict__
     const uint32_t c = c_lo + blockIdx.y, kvh = blockIdx.x;
     const bool is_v = blockIdx.z != 0;
     {
+        // every load unconditional (a key past n_keys reads the last key's
+        // row and stores zeros), so the eight row loads fly together
         const int key = tid >> 3, part = tid & 7;           // 8 threads per row
         const uint32_t kp = c * kPaNK + key;
         const bool ok = kp < n_keys;
-        const uint32_t slot = ok ? slots[kp] : 0u;
+        const uint32_t slot = slots[min(kp, n_keys - 1)];
         const f4 *src = (const f4 *)((is_v ? Vc : Kc) + (size_t)slot * kv_dim + (size_t)kvh * 256);
+        f4 r[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int idx = part + 8 * i;
-            rows[key][idx] = ok ? src[idx] : f4{0, 0, 0, 0};
-        }
+        for (int i = 0; i < 8; ++i) r[i] = src[part + 8 * i];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) rows[key][part + 8 * i] = ok ? r[i] : f4{0, 0, 0, 0};
     }
     __syncthreads();
     unsigned char *Fc = F + ((size_t)kvh * gridDim.y + blockIdx.y) * kPaChunkBytes + (is_v ? 2 * kPaPlane : 0);
