@@ -645,7 +645,8 @@ def bench_attn(ctx, args):
                    "slots": S, "bytes_per_step": nbytes},
         "roofline": {"kernel": "k_attn_decode + k_attn_merge", "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": None, "algorithmic_bytes_per_launch": nbytes,
+                     "traffic": load_traffic("k_attn_decode + k_attn_merge", "4096 slots") if S == 4096 else None,
+                     "algorithmic_bytes_per_launch": nbytes,
                      "avg_launch_ms": gpu_ms / args.steps,
                      "recorded": {"ms_per_step": rec_ms, "achieved": nbytes / (rec_ms * 1e-3) / 1e9,
                                   "frac": nbytes / (rec_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}},
