@@ -405,12 +405,20 @@ __global__ __launch_bounds__(1024) void k_topk_merge(const uint64_t *__restrict_
     }
     __syncthreads();
     const uint64_t T = thr;
-    // gather the prefixes at or above T: wave w takes selected lists w, w + 16, ...
+    // gather the prefixes at or above T: wave w takes selected lists w, w +
+    // 16, ...; the four lists' loads go out together (a wave past nsel
+    // reads list sel[0] and drops it)
+    uint64_t keys[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t i = wave + 16 * q;
+        keys[q] = cand[(size_t)sel[i < nsel ? i : 0u] * kTopK + lane];
+    }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const uint32_t i = wave + 16 * q;
         if (i >= nsel) continue;                                    // uniform per wave
-        const uint64_t key = cand[(size_t)sel[i] * kTopK + lane];
+        const uint64_t key = keys[q];
         const uint64_t above = __ballot(key >= T);                   // a prefix: the list is sorted
         const uint32_t cnt = __popcll(above);
         uint32_t off = 0;
