@@ -292,10 +292,8 @@ struct Gemm2dCfg {
     static constexpr int SSLOT = SWORDS * 4;
     static constexpr int OFF_Q = SX * XSLOT, OFF_S = OFF_Q + SW * QSLOT, OFF_W = OFF_S + SW * SSLOT;
     static constexpr int WTILE = 2 * GN * LROW;             // bf16 tiles of both matrices
-    static constexpr int OFF_D = OFF_W + 2 * WTILE;        // 256 B written by waves without a scale load
-    static constexpr int LDS = OFF_D + 256;
-    static constexpr int NS = SWORDS / 64;                 // scale instructions (one per wave < NS)
-    static_assert(NS <= 8, "one scale instruction per wave");
+    static constexpr int LDS = OFF_W + 2 * WTILE;
+    static constexpr int NS = SWORDS / 64;                 // scale instructions per step
 };
 
 template <bool REP>
@@ -311,58 +309,68 @@ __global__ __launch_bounds__(512) void k_q4gemm2d(GemmArgs a) {
     const uint32_t K = a.K, nb = K / 32, steps = K / C::GK;
     const uint32_t smb = lds_addr(sm);
 
-    // ---- X by DMA: 32 one-KB instructions per step, four per wave
+    // ---- every DMA is issued by waves 4-7 (the second wave of each SIMD),
+    // while waves 0-3 dequantize: X as 32 one-KB instructions per step, eight
+    // per issuing wave; the raw weights as eight one-KB nibble instructions
+    // (two per issuing wave) and NS scale instructions.  (Issuing them from
+    // all eight waves stalled every wave on the CU's address rate right after
+    // the barrier: 134-135 against 136-139 µs.)
     // (a dependent constant inside a DMA builtin's arguments makes the host
     // pass drop the kernel's launch stub: local copies)
     constexpr uint32_t GK = C::GK;
     const __bf16 *Xb = a.X;
-    uint32_t xe[4];                                            // element offsets (n_tok * K < 2^32)
+    const int dw = (wave - 4) & 3;                             // issuing wave 0..3 (waves 4-7)
+    uint32_t xe[8];                                            // element offsets (n_tok * K < 2^32)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int q = (i * 8 + wave) * 64 + lane;              // chunk position in the slot
+    for (int i = 0; i < 8; ++i) {
+        const int q = (i * 4 + dw) * 64 + lane;                // chunk position in the slot
         const int r = q >> 3, c = (q & 7) ^ ((r ^ (r >> 3)) & 7);
         xe[i] = (t0 + r < a.n_tok ? t0 + r : a.n_tok - 1) * K + c * 8;
     }
     auto issue_x = [&](uint32_t j) {                           // X(j) -> slot j % SX (j clamped)
+        if (wave < 4) return;                                  // wave-uniform
         const uint32_t jj = j < steps ? j : steps - 1;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 8; ++i)
             __builtin_amdgcn_global_load_lds(Xb + (xe[i] + jj * GK),
-                                             (lds_t *)(sm + (j % C::SX) * C::XSLOT + (i * 8 + wave) * 1024), 16, 0,
+                                             (lds_t *)(sm + (j % C::SX) * C::XSLOT + (i * 4 + dw) * 1024), 16, 0,
                                              0);
     };
-    // ---- raw weights by DMA: nibble chunk `tid` ([m][blk][row]); scale
-    // instruction `wave` (waves >= NS load 256 B of X into a dummy area)
-    const unsigned char *wq_g, *ws_g;
-    uint32_t ws_lds, ws_slot, ws_step;
-    const uint32_t wq_step = REP ? 32 : 40;
-    {
-        const int m = tid >> 8, blk = (tid >> 7) & 1, row = tid & 127;
+    const unsigned char *wq_g[2], *ws_g[2];
+    const uint32_t wq_step = REP ? 32 : 40, ws_step = REP ? 4 : 40;
+    constexpr int NSW = (C::NS + 3) / 4;                       // scale instructions per issuing wave
+    static_assert(NSW <= 2, "two scale instructions per issuing wave at most");
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int ch = (2 * dw + k) * 64 + lane;               // nibble chunk [m][blk][row]
+        const int m = ch >> 8, blk = (ch >> 7) & 1, row = ch & 127;
         const uint32_t n = n0 + row < a.M ? n0 + row : a.M - 1;
         const unsigned char *W = (const unsigned char *)(m == 0 ? a.W0 : a.W1);
-        wq_g = REP ? W + ((size_t)n * nb + blk) * 16 : W + ((size_t)n * nb + blk) * 20 + 4;
-        if (wave < C::NS) {
-            const int sq = wave * 64 + lane;                   // REP [m][row], else [m][blk][row]
-            const int sm_ = REP ? sq >> 7 : sq >> 8, sblk = REP ? 0 : (sq >> 7) & 1, srow = sq & 127;
-            const uint32_t ns = n0 + srow < a.M ? n0 + srow : a.M - 1;
-            const unsigned char *Ws = (const unsigned char *)(sm_ == 0 ? a.W0 : a.W1);
-            ws_g = REP ? Ws + (size_t)a.M * nb * 16 + (size_t)ns * nb * 2 : Ws + ((size_t)ns * nb + sblk) * 20;
-            ws_lds = C::OFF_S + wave * 256;
-            ws_slot = C::SSLOT;
-            ws_step = REP ? 4 : 40;
-        } else {
-            ws_g = (const unsigned char *)a.X + (lane * 4) % 128;
-            ws_lds = C::OFF_D;
-            ws_slot = 0;
-            ws_step = 0;
-        }
+        wq_g[k] = REP ? W + ((size_t)n * nb + blk) * 16 : W + ((size_t)n * nb + blk) * 20 + 4;
+    }
+#pragma unroll
+    for (int k = 0; k < NSW; ++k) {
+        const int si = dw * NSW + k;                           // scale instruction
+        const int sq = (si < C::NS ? si : 0) * 64 + lane;      // REP [m][row], else [m][blk][row]
+        const int sm_ = REP ? sq >> 7 : sq >> 8, sblk = REP ? 0 : (sq >> 7) & 1, srow = sq & 127;
+        const uint32_t ns = n0 + srow < a.M ? n0 + srow : a.M - 1;
+        const unsigned char *Ws = (const unsigned char *)(sm_ == 0 ? a.W0 : a.W1);
+        ws_g[k] = REP ? Ws + (size_t)a.M * nb * 16 + (size_t)ns * nb * 2 : Ws + ((size_t)ns * nb + sblk) * 20;
     }
     auto issue_w = [&](uint32_t j) {                           // Wraw(j) -> slot j % SW (j clamped)
+        if (wave < 4) return;
         const uint32_t jj = j < steps ? j : steps - 1;
-        __builtin_amdgcn_global_load_lds(wq_g + (size_t)jj * wq_step,
-                                         (lds_t *)(sm + C::OFF_Q + (j % C::SW) * C::QSLOT + wave * 1024), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(ws_g + (size_t)jj * ws_step,
-                                         (lds_t *)(sm + ws_lds + (j % C::SW) * ws_slot), 4, 0, 0);
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+            __builtin_amdgcn_global_load_lds(wq_g[k] + (size_t)jj * wq_step,
+                                             (lds_t *)(sm + C::OFF_Q + (j % C::SW) * C::QSLOT + (2 * dw + k) * 1024),
+                                             16, 0, 0);
+#pragma unroll
+        for (int k = 0; k < NSW; ++k)
+            if (dw * NSW + k < C::NS)
+                __builtin_amdgcn_global_load_lds(ws_g[k] + (size_t)jj * ws_step,
+                                                 (lds_t *)(sm + C::OFF_S + (j % C::SW) * C::SSLOT + (dw * NSW + k) * 256),
+                                                 4, 0, 0);
     };
 
     // ---- dequantization by waves 0-3, the first wave of each SIMD: thread
