@@ -70,6 +70,10 @@ struct GemmArgs {
     // Register-staged kernel only: Yb != NULL writes the result as bf16 to
     // Yb ([n_tok][M]) instead of Y (the next contraction's input).
     __bf16 *Yb = nullptr;
+    // Pipelined kernel, K split in two: with Y2, the second half is stored
+    // to Y2 ([n_tok][M]) and the first to Y, both plainly (the consumer adds
+    // them); without it, both halves add into Y, which starts at zero.
+    float *Y2 = nullptr;
 };
 
 typedef uint32_t u32x4g __attribute__((ext_vector_type(4)));
@@ -850,8 +854,11 @@ __global__ __launch_bounds__(512) void k_q4gemm_p(GemmArgs a, uint32_t n_ct, uin
                 acc[m][mt][nt] += *(const f32x4 *)(red + ((((rw * NMAT + m) * 4 + mt) * NTW + nt) * 64 + lane) * 4);
 
     // epilogue: lane holds tokens (lane>>4)*4 + i of each 16-row tile, feature
-    // lane & 15.  Split K: the two halves add into Y, which starts at zero
-    // (two addends from zero give the same sum in either order).
+    // lane & 15.  Split K: the halves go to Y and Y2, or add into Y, which
+    // starts at zero (two addends from zero give the same sum in either
+    // order, and the same as their sum formed by the consumer).
+    float *Yo = ks && a.Y2 ? a.Y2 : Yp;
+    const bool plain = ksplit == 1 || a.Y2;
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
@@ -863,8 +870,8 @@ __global__ __launch_bounds__(512) void k_q4gemm_p(GemmArgs a, uint32_t n_ct, uin
                 if (t < a.n_tok && n < Mloc) {
                     float v = acc[0][mt][nt][i];
                     if (NMAT == 2) v = gelu_tanh(v) * acc[NMAT - 1][mt][nt][i];
-                    float *y = Yp + (size_t)t * Mloc + n;
-                    if (ksplit == 1) *y = v;
+                    float *y = Yo + (size_t)t * Mloc + n;
+                    if (plain) *y = v;
                     else unsafeAtomicAdd(y, v);
                 }
             }
@@ -895,15 +902,19 @@ static void launch_to_bf16(hipStream_t st, const float *X, __bf16 *xb, size_t n,
 //    (half the LDS fragment reads per MFMA of 128 x 64 tiles; 15360 x 3840:
 //    97 us against 135 us, q/k/v 8192 x 3840: 54 against 69 us; 128 such
 //    workgroups lose to 256 of 128 x 64);
-//  * for long K (>= 8192) 128 x 128 tiles with K split in two, whose larger
-//    per-step work pays for itself over the longer loop;
+//  * for long K 128 x 128 tiles with K split in two, whose larger per-step
+//    work pays for itself over the longer loop: K >= 8192 when the halves
+//    add into Y by atomics, K >= 4096 when they are stored to two buffers
+//    (the atomic epilogue of two halves costs about as much as the plain
+//    stores of four; at 512 tokens, 12B o_proj 4096 -> 3840 in 128 x 128
+//    halves saves ~4 us a layer against 128 x 64 tiles over all of K);
 //  * else 128-token x 64-feature tiles when they give at least ~200
 //    workgroups, otherwise the same tiles with K split in two.
 enum class PipeShape { BN64, BN64_K2, BN128, BN128_K2 };
-static PipeShape pipe_shape(uint32_t n_tok, uint32_t M, uint32_t K) {
+static PipeShape pipe_shape(uint32_t n_tok, uint32_t M, uint32_t K, bool halves = false) {
     const uint32_t tt = (n_tok + 127) / 128;
     if (((M + 127) / 128) * tt >= 256) return PipeShape::BN128;
-    if (K >= 8192 && 2 * ((M + 127) / 128) * tt >= 192) return PipeShape::BN128_K2;
+    if (K >= (halves ? 4096u : 8192u) && 2 * ((M + 127) / 128) * tt >= 192) return PipeShape::BN128_K2;
     if (((M + 63) / 64) * tt >= 192 || K < 128) return PipeShape::BN64;
     return PipeShape::BN64_K2;
 }
@@ -917,14 +928,20 @@ static void launch_pipe(hipStream_t st, const GemmArgs &a, PipeShape ps) {
 }
 
 int launch_q4gemm(chn_ctx *ctx, int nmat, const float *X, const uint32_t *W0, const uint32_t *W1, float *Y,
-                  uint32_t n_tok, uint32_t M, uint32_t K, __bf16 *xb, bool repacked, __bf16 *Yb, bool y_zeroed) {
+                  uint32_t n_tok, uint32_t M, uint32_t K, __bf16 *xb, bool repacked, __bf16 *Yb, float *Y2,
+                  bool *y2_written) {
     const size_t n = X ? (size_t)n_tok * K : 0;
     GemmArgs a{xb, W0, W1, Y, n_tok, M, K};
+    if (y2_written) *y2_written = false;
     if (nmat == 1 && K % 64 == 0) {
         if (Yb) return set_err(ctx, CHN_E_UNSUPPORTED, "bf16 output needs the two-matrix contraction");
-        const PipeShape ps = pipe_shape(n_tok, M, K);
+        const PipeShape ps = pipe_shape(n_tok, M, K, Y2 != nullptr);
         const bool split = ps == PipeShape::BN64_K2 || ps == PipeShape::BN128_K2;
-        const bool zero = split && !y_zeroed;
+        if (split && Y2) {
+            a.Y2 = Y2;
+            if (y2_written) *y2_written = true;
+        }
+        const bool zero = split && !a.Y2;
         if (n || zero) {
             launch_to_bf16(ctx->stream, X, xb, n, zero ? Y : nullptr, zero ? (size_t)n_tok * M : 0);
             CHN_LAUNCHED(ctx, "k_to_bf16");

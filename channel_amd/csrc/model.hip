@@ -50,7 +50,7 @@ struct chn_model {
     uint64_t *topk_ws;
     // prefill buffers
     uint32_t max_tok = 0;
-    float *px, *pn, *pq, *pk, *pv, *pmlp, *pact, *pattn_ws;
+    float *px, *pn, *pq, *pk, *pv, *pmlp, *pmlp2, *pact, *pattn_ws;
     unsigned char *pfrag;   // prefill attention: the keys' bf16 operand fragments
     size_t pfrag_bytes;
     float2 *prope;       // prefill (cos, sin) per token: [2 kinds][T][rot / 2]
@@ -206,6 +206,7 @@ static int alloc_runtime(chn_model *m) {
     M_ALLOC(m->pk, (size_t)T * kvd * 4);
     M_ALLOC(m->pv, (size_t)T * kvd * 4);
     M_ALLOC(m->pmlp, (size_t)T * H * 4);
+    M_ALLOC(m->pmlp2, (size_t)T * H * 4);
     M_ALLOC(m->pattn_ws, prefill_attn_ws_bytes(T, c.num_heads, md.D));
     // every key of a prefill (at most the ring plus the batch) for the KV
     // heads of the widest 256-dim layer
@@ -880,8 +881,8 @@ extern "C" int chn_prefill(chn_model *m, const uint32_t *tokens, uint32_t n, con
     } while (0)
     // Every contraction reads bf16 activations that their producer wrote
     // directly: the norm chains and the attention into pxb, gate/up into the
-    // act buffer (as bf16).  The chain after o_proj also clears pmlp, which
-    // down's split-K halves then add into.
+    // act buffer (as bf16).  Where down splits K, its halves go to pmlp and
+    // pmlp2 and the closing norm chain adds them.
     __bf16 *xb = m->pxb;
     __bf16 *actb = (__bf16 *)m->pact;
     // the prompt's rotation angles, once per kind (sliding / full layers)
@@ -893,7 +894,7 @@ extern "C" int chn_prefill(chn_model *m, const uint32_t *tokens, uint32_t n, con
         const auto &l = m->L[i];
         const float theta = l.full ? c.rope_theta_full : c.rope_theta;
         if (i == 0)
-            P_(launch_rmsnorm_chain(s, m->px, nullptr, nullptr, l.in_norm, xb, nullptr, H, n, eps, 1.0f, false, false));
+            P_(launch_rmsnorm_chain(s, m->px, nullptr, nullptr, l.in_norm, xb, nullptr, H, n, eps, 1.0f, false));
         const uint32_t D = l.D, nkv = l.nkv, qd = l.qd, kvd = l.kvd, gqa = l.gqa;
         P_(launch_q4gemm_qkv(ctx, nullptr, l.Wq, l.Wk, l.Wv, m->pq, m->pk, m->pv, n, qd, kvd, H, xb));
         P_(launch_batch_qkv_rope(s, m->pq, m->pk, m->pv, l.q_norm, l.k_norm, m->pq, l.kc, l.vc, m->pslots,
@@ -904,15 +905,16 @@ extern "C" int chn_prefill(chn_model *m, const uint32_t *tokens, uint32_t n, con
         const uint32_t pwin = c.prefill_window ? c.prefill_window : 1024u;
         P_(launch_prefill_attn(s, m->pq, l.kc, l.vc, m->pslots, n, num_prev_slots, nq, D, kvd, gqa, 1.0f,
                                l.full ? 0u : pwin, nullptr, xb, m->pattn_ws, m->pfrag, m->pfrag_bytes));
-        P_(launch_q4gemm(ctx, 1, nullptr, l.Wo, nullptr, m->pmlp, n, H, qd, xb, true));
+        bool halves = false;
+        P_(launch_q4gemm(ctx, 1, nullptr, l.Wo, nullptr, m->pmlp, n, H, qd, xb, true, nullptr, m->pmlp2, &halves));
         P_(launch_rmsnorm_chain(s, m->px, m->pmlp, l.has_post_attn ? l.post_attn : nullptr, l.pre_ffn, xb, nullptr,
-                                H, n, eps, 1.0f, true, true));
+                                H, n, eps, 1.0f, true, halves ? m->pmlp2 : nullptr));
         P_(launch_q4gemm(ctx, 2, nullptr, l.Wg, l.Wu, nullptr, n, I, H, xb, true, actb));
-        P_(launch_q4gemm(ctx, 1, nullptr, l.Wd, nullptr, m->pmlp, n, H, I, actb, true, nullptr, true));
+        P_(launch_q4gemm(ctx, 1, nullptr, l.Wd, nullptr, m->pmlp, n, H, I, actb, true, nullptr, m->pmlp2, &halves));
         const bool last = i + 1 == c.num_layers;
         const float *next_norm = last ? m->final_norm : m->L[i + 1].in_norm;
         P_(launch_rmsnorm_chain(s, m->px, m->pmlp, l.has_post_ffn ? l.post_ffn : nullptr, next_norm, xb,
-                                last ? m->pn : nullptr, H, n, eps, l.scalar, true, false));
+                                last ? m->pn : nullptr, H, n, eps, l.scalar, true, halves ? m->pmlp2 : nullptr));
         if ((i + 1) % 4 == 0 || i + 1 == c.num_layers) {
             if (i + 1 == c.num_layers && (logits_out || topk_ids)) {
                 CHN_HIP(ctx, hipMemcpyAsync(m->normed, m->pn + (size_t)(n - 1) * H, H * 4, hipMemcpyDeviceToDevice, s));
