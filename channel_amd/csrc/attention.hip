@@ -1110,15 +1110,34 @@ __global__ __launch_bounds__(256) void k_prefill_attn_merge(const float *__restr
     if (nparts < 2) return;
     const uint32_t np_stride = geo.maxparts;   // the workspace holds maxparts parts
     const float *ml = ws + np_stride * nrow * D;
+    // every part's state is requested at once (parts past nparts reload the
+    // last one and are left out below), then combined in part order
+    float mp[kPaParts], lp[kPaParts];
+    f4 v[kPaParts];
+#pragma unroll
+    for (uint32_t p = 0; p < kPaParts; ++p) {
+        const uint32_t pc = p < nparts ? p : nparts - 1;
+        const float2 m2 = *(const float2 *)(ml + 2 * (pc * nrow + row));
+        mp[p] = m2.x;
+        lp[p] = m2.y;
+        v[p] = *(const f4 *)(ws + pc * nrow * D + i);
+    }
+    // (an opaque use of every loaded value: otherwise the compiler sinks
+    // the loads of the later parts into the branches that use them, and
+    // each waits on its own round trip)
+#pragma unroll
+    for (uint32_t p = 0; p < kPaParts; ++p) __asm__ volatile("" : "+v"(mp[p]), "+v"(lp[p]), "+v"(v[p]));
     float mx = -INFINITY;
-    for (uint32_t p = 0; p < nparts; ++p) mx = fmaxf(mx, ml[2 * (p * nrow + row)]);
+#pragma unroll
+    for (uint32_t p = 0; p < kPaParts; ++p) mx = p < nparts ? fmaxf(mx, mp[p]) : mx;
     f4 t = f4{0, 0, 0, 0};
     float den = 0.0f;
-    for (uint32_t p = 0; p < nparts; ++p) {
-        const float mp = ml[2 * (p * nrow + row)], lp = ml[2 * (p * nrow + row) + 1];
-        const float a = mp == -INFINITY ? 0.0f : __expf(mp - mx);
-        t += *(const f4 *)(ws + p * nrow * D + i) * a;
-        den += lp * a;
+#pragma unroll
+    for (uint32_t p = 0; p < kPaParts; ++p) {
+        if (p >= nparts) break;
+        const float a = mp[p] == -INFINITY ? 0.0f : __expf(mp[p] - mx);
+        t += v[p] * a;
+        den += lp[p] * a;
     }
     store_out4(out, outb, i, t * (1.0f / (den + 1e-9f)));
 }
