@@ -635,13 +635,25 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ ws
     for (uint32_t jb = j0; jb < nsplit; jb += 16 * U) {
         float mj[U], lj[U];
         f4 aj[U];
+        // every load unconditional (a split past nsplit reads split jb's
+        // state again and is masked below), and each value given an opaque
+        // use, so the compiler neither branches around a load nor sinks it
+        // into its use: the U partials cost one memory round trip
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const uint32_t j = jb + 16 * u;
-            const bool v = j < nsplit;
-            mj[u] = v ? wm[(size_t)j * num_q_heads] : kNegBig;
-            lj[u] = v ? wl[(size_t)j * num_q_heads] : 0.0f;
-            aj[u] = v ? *(const f4 *)(wacc + j * stride) : f4{0, 0, 0, 0};
+            const uint32_t j = jb + 16 * u < nsplit ? jb + 16 * u : jb;
+            mj[u] = wm[(size_t)j * num_q_heads];
+            lj[u] = wl[(size_t)j * num_q_heads];
+            aj[u] = *(const f4 *)(wacc + j * stride);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) __asm__ volatile("" : "+v"(mj[u]), "+v"(lj[u]), "+v"(aj[u]));
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const bool v = jb + 16 * u < nsplit;
+            mj[u] = v ? mj[u] : kNegBig;
+            lj[u] = v ? lj[u] : 0.0f;
+            aj[u] = v ? aj[u] : f4{0, 0, 0, 0};
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
