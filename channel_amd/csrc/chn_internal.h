@@ -89,15 +89,15 @@ int mv_mlp(chn_ctx *ctx, const uint32_t *Wg, const uint32_t *Wu, const float *x,
            uint32_t *ws, bool planes_ready = false);
 int launch_rmsnorm(hipStream_t s, float *x, const float *r, const float *w, float *y, uint32_t dim, uint32_t rows,
                    float eps, float scalar, bool add);
-// The prefill's norm chain per token row: the branch is r, or r + r2 when
-// r2 != NULL (the two K halves of a split contraction); with post_w, r' =
-// rmsnorm(branch) * post_w (else r' = branch); with add, x = (x + r') *
-// scalar (written back); y = rmsnorm(x) * w as bf16 into yb and, if y !=
-// NULL, as fp32.  The same arithmetic, in the same order, as
-// launch_rmsnorm's two passes.
+// The prefill's norm chain per token row: the branch is the sum of the
+// nparts (1, 2 or 4) partial outputs r + p * pstride of a split
+// contraction, added in index order; with post_w, r' = rmsnorm(branch) *
+// post_w (else r' = branch); with add, x = (x + r') * scalar (written
+// back); y = rmsnorm(x) * w as bf16 into yb and, if y != NULL, as fp32.
+// The same arithmetic, in the same order, as launch_rmsnorm's two passes.
 int launch_rmsnorm_chain(hipStream_t s, float *x, const float *r, const float *post_w, const float *w, __bf16 *yb,
                          float *y, uint32_t dim, uint32_t rows, float eps, float scalar, bool add,
-                         const float *r2 = nullptr);
+                         uint32_t nparts = 1, size_t pstride = 0);
 // Digit planes of x (nb 32-blocks) into xp (xplanes_bytes(nb)).
 int launch_xplanes(hipStream_t s, const float *x, uint32_t *xp, uint32_t nb);
 
@@ -253,12 +253,18 @@ int launch_quantize(hipStream_t st, int q8, const uint16_t *src, uint32_t *dst, 
 // W0/W1 in the reference Q4 layout, or in Q4R with repacked.  X (fp32) is
 // converted into xb; with X == NULL, xb already holds the bf16 activations.
 // Yb (two-matrix form only): the result goes to Yb as bf16 instead of Y.
-// Y2 (single matrix): a shape that splits K in two stores the halves to Y
-// and Y2 (their sum is the result; *y2_written tells) instead of clearing
-// Y and adding both into it.
+// po (single matrix): a shape that splits K may store its partial sums to
+// Y + p * po->stride, p < po->max_parts (1, 2 or 4), with plain stores
+// instead of clearing Y and adding into it; po->parts tells how many it
+// wrote (their sum, in index order, is the result).
+struct PartialOut {
+    size_t stride = 0;         // elements between partial outputs
+    uint32_t max_parts = 1;
+    uint32_t parts = 1;        // set by the launch
+};
 int launch_q4gemm(chn_ctx *ctx, int nmat, const float *X, const uint32_t *W0, const uint32_t *W1, float *Y,
                   uint32_t n_tok, uint32_t M, uint32_t K, __bf16 *xb, bool repacked, __bf16 *Yb = nullptr,
-                  float *Y2 = nullptr, bool *y2_written = nullptr);
+                  PartialOut *po = nullptr);
 // q, k, v (Q4R) over the same activations in one launch (X == NULL: xb
 // already holds them).
 int launch_q4gemm_qkv(chn_ctx *ctx, const float *X, const uint32_t *Wq, const uint32_t *Wk, const uint32_t *Wv,

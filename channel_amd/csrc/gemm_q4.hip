@@ -70,10 +70,11 @@ struct GemmArgs {
     // Register-staged kernel only: Yb != NULL writes the result as bf16 to
     // Yb ([n_tok][M]) instead of Y (the next contraction's input).
     __bf16 *Yb = nullptr;
-    // Pipelined kernel, K split in two: with Y2, the second half is stored
-    // to Y2 ([n_tok][M]) and the first to Y, both plainly (the consumer adds
-    // them); without it, both halves add into Y, which starts at zero.
-    float *Y2 = nullptr;
+    // Split K: with ypart, split p stores its partial sums to Y + p * ypart
+    // ([n_tok][M] each, plain stores; the consumer adds them); without it
+    // (the pipelined kernel's two halves) both add into Y, which starts at
+    // zero.
+    size_t ypart = 0;
 };
 
 typedef uint32_t u32x4g __attribute__((ext_vector_type(4)));
@@ -508,6 +509,188 @@ __global__ __launch_bounds__(512) void k_q4gemm2d(GemmArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Single-matrix contraction on 256-token x 128-feature tiles: the fused
+// gate/up's pipeline with one matrix, eight waves (wr, wc) of 64 tokens x 64
+// features, every operand by DMA (waves 4-7 issue, waves 0-3 dequantize),
+// one barrier per K step of 64, each weight dequantized once per 256
+// tokens.  K is split ksplit ways (work items), split ks storing its sums to
+// Y + ks * ypart with plain stores; the consumer adds them.
+template <bool REP>
+struct Gemm2sCfg {
+    static constexpr int BT = 256, GK = 64, SX = 2, SW = 2;
+    static constexpr int LROW = GK * 2 + 16;
+    static constexpr int XSLOT = BT * GK * 2;              // 32 KB of X per step
+    static constexpr int QSLOT = GN * 2 * 16;              // nibble words per step, [blk][row]
+    static constexpr int SWORDS = REP ? GN : 2 * GN;       // REP [row] (both blocks' f16 scales), else [blk][row]
+    static constexpr int SSLOT = SWORDS * 4;
+    static constexpr int OFF_Q = SX * XSLOT, OFF_S = OFF_Q + SW * QSLOT, OFF_W = OFF_S + SW * SSLOT;
+    static constexpr int WTILE = GN * LROW;
+    static constexpr int LDS = OFF_W + 2 * WTILE;
+    static constexpr int NS = SWORDS / 64;                 // scale instructions per step
+};
+
+template <bool REP>
+__global__ __launch_bounds__(512) void k_q4gemm2s(GemmArgs a, uint32_t n_ft, uint32_t n_tt, uint32_t ksplit) {
+    using C = Gemm2sCfg<REP>;
+    __shared__ __attribute__((aligned(16))) unsigned char sm[C::LDS];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr = wave >> 1, wc = wave & 1;
+    // work items (split, feature tile, token tile), token tile fastest; the
+    // items are dealt to the XCDs in contiguous runs (workgroup i runs on
+    // XCD i % 8), so the token tiles of a feature block share one L2
+    const uint32_t nwork = n_ft * n_tt * ksplit, per = (nwork + 7) / 8;
+    const uint32_t work = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    if (work >= nwork) return;                             // uniform, before any barrier
+    const uint32_t tt = work % n_tt, ft = (work / n_tt) % n_ft, ks = work / (n_tt * n_ft);
+    const uint32_t n0 = ft * GN, t0 = tt * C::BT;
+    const uint32_t K = a.K, nb = K / 32, kper = K / ksplit, steps = kper / C::GK, kb0 = ks * kper / 32;
+    const uint32_t smb = lds_addr(sm);
+
+    constexpr uint32_t GK = C::GK;
+    const __bf16 *Xb = a.X + ks * kper;
+    const int dw = (wave - 4) & 3;                             // issuing wave 0..3 (waves 4-7)
+    uint32_t xe[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int q = (i * 4 + dw) * 64 + lane;
+        const int r = q >> 3, c = (q & 7) ^ ((r ^ (r >> 3)) & 7);
+        xe[i] = (t0 + r < a.n_tok ? t0 + r : a.n_tok - 1) * K + c * 8;
+    }
+    auto issue_x = [&](uint32_t j) {
+        if (wave < 4) return;
+        const uint32_t jj = j < steps ? j : steps - 1;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            __builtin_amdgcn_global_load_lds(Xb + (xe[i] + jj * GK),
+                                             (lds_t *)(sm + (j % C::SX) * C::XSLOT + (i * 4 + dw) * 1024), 16, 0,
+                                             0);
+    };
+    const unsigned char *W = (const unsigned char *)a.W0;
+    const unsigned char *wq_g, *ws_g;
+    const uint32_t wq_step = REP ? 32 : 40, ws_step = REP ? 4 : 40;
+    {
+        const int ch = dw * 64 + lane;                         // nibble chunk [blk][row]
+        const int blk = ch >> 7, row = ch & 127;
+        const uint32_t n = n0 + row < a.M ? n0 + row : a.M - 1;
+        wq_g = REP ? W + ((size_t)n * nb + kb0 + blk) * 16 : W + ((size_t)n * nb + kb0 + blk) * 20 + 4;
+        const int sq = (dw < C::NS ? dw : 0) * 64 + lane;      // REP [row], else [blk][row]
+        const int sblk = REP ? 0 : sq >> 7, srow = sq & 127;
+        const uint32_t ns = n0 + srow < a.M ? n0 + srow : a.M - 1;
+        ws_g = REP ? W + (size_t)a.M * nb * 16 + ((size_t)ns * nb + kb0) * 2 : W + ((size_t)ns * nb + kb0 + sblk) * 20;
+    }
+    auto issue_w = [&](uint32_t j) {
+        if (wave < 4) return;
+        const uint32_t jj = j < steps ? j : steps - 1;
+        __builtin_amdgcn_global_load_lds(wq_g + (size_t)jj * wq_step,
+                                         (lds_t *)(sm + C::OFF_Q + (j % C::SW) * C::QSLOT + dw * 1024), 16, 0, 0);
+        if (dw < C::NS)
+            __builtin_amdgcn_global_load_lds(ws_g + (size_t)jj * ws_step,
+                                             (lds_t *)(sm + C::OFF_S + (j % C::SW) * C::SSLOT + dw * 256), 4, 0, 0);
+    };
+
+    const int d_blk = (tid >> 7) & 1, d_row = tid & 127;
+    const uint32_t dq_q = smb + C::OFF_Q + (tid & 255) * 16;
+    const uint32_t dq_s = smb + C::OFF_S + (REP ? d_row : (tid & 255)) * 4;
+    const uint32_t dq_w = C::OFF_W + d_row * C::LROW + d_blk * 64;
+    auto dequant = [&](auto slot_) {
+        constexpr int SL = decltype(slot_)::value;
+        if (wave >= 4) return;
+        u32x4v q0 = lds_read<u32x4v, SL * C::QSLOT>(dq_q);
+        uint32_t s0 = lds_read<uint32_t, SL * C::SSLOT>(dq_s);
+        lds_wait();
+        lds_pin(q0);
+        lds_pin(s0);
+        const float sc0 = f16_lo_to_f32(REP ? s0 >> (16 * d_blk) : s0), ms0 = -8.0f * sc0;
+        unsigned char *dst = sm + dq_w + SL * C::WTILE;
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+            *(u32x4v *)(dst + 16 * w) = dequant_word_bf16(REP ? q0[w] ^ 0x88888888u : q0[w], sc0, ms0);
+    };
+
+    uint32_t xa[2][4];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            const int r = wr * 64 + mt * 16 + (lane & 15);
+            const int c = (4 * kk + (lane >> 4)) ^ ((r ^ (r >> 3)) & 7);
+            xa[kk][mt] = smb + r * 128 + c * 16;
+        }
+    const uint32_t wa = smb + C::OFF_W + (wc * 64 + (lane & 15)) * C::LROW + (lane >> 4) * 16;
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
+
+    issue_w(0);
+    wait_vm_lgkm0<0>();
+    bare_barrier();
+    dequant(std::integral_constant<int, 0>{});
+    issue_x(0);
+    __asm__ volatile("" ::: "memory");
+    issue_w(1);
+    __asm__ volatile("" ::: "memory");
+
+    auto step = [&](uint32_t j, auto xs_) {
+        constexpr int XS = decltype(xs_)::value;
+        wait_vm_lgkm0<0>();
+        bare_barrier();
+        issue_x(j + 1);
+        __asm__ volatile("" ::: "memory");
+        issue_w(j + 2);
+        __asm__ volatile("" ::: "memory");
+        dequant(std::integral_constant<int, 1 - XS>{});
+        static_for<2>([&](auto kk_) {
+            constexpr int KK = decltype(kk_)::value;
+            bf16x8 af[4], bfm[4];
+            static_for<4>([&](auto mt_) {
+                constexpr int MT = decltype(mt_)::value;
+                af[MT] = lds_read<bf16x8, XS * C::XSLOT>(xa[KK][MT]);
+            });
+            static_for<4>([&](auto nt_) {
+                constexpr int NT = decltype(nt_)::value;
+                bfm[NT] = lds_read<bf16x8, XS * C::WTILE + NT * 16 * C::LROW + KK * 64>(wa);
+            });
+            lds_wait();
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) lds_pin(af[mt]);
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt) lds_pin(bfm[nt]);
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < 4; ++nt)
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bfm[nt], acc[mt][nt], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+    uint32_t j = 0;
+    for (; j + 1 < steps; j += 2) {
+        step(j, std::integral_constant<int, 0>{});
+        step(j + 1, std::integral_constant<int, 1>{});
+    }
+    if (j < steps) step(j, std::integral_constant<int, 0>{});
+    wait_vm_lgkm0<0>();
+
+    float *Yp = a.Y + ks * a.ypart;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+            const uint32_t n = n0 + wc * 64 + nt * 16 + (lane & 15);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t t = t0 + wr * 64 + mt * 16 + (lane >> 4) * 4 + i;
+                if (t < a.n_tok && n < a.M) Yp[(size_t)t * a.M + n] = acc[mt][nt][i];
+            }
+        }
+}
+
+// ---------------------------------------------------------------------------
 // Pipelined contraction for K % 64 == 0 (every prefill shape of the model).
 //
 // A workgroup owns 128 tokens x BN features (per matrix) and walks K in steps
@@ -854,11 +1037,11 @@ __global__ __launch_bounds__(512) void k_q4gemm_p(GemmArgs a, uint32_t n_ct, uin
                 acc[m][mt][nt] += *(const f32x4 *)(red + ((((rw * NMAT + m) * 4 + mt) * NTW + nt) * 64 + lane) * 4);
 
     // epilogue: lane holds tokens (lane>>4)*4 + i of each 16-row tile, feature
-    // lane & 15.  Split K: the halves go to Y and Y2, or add into Y, which
-    // starts at zero (two addends from zero give the same sum in either
-    // order, and the same as their sum formed by the consumer).
-    float *Yo = ks && a.Y2 ? a.Y2 : Yp;
-    const bool plain = ksplit == 1 || a.Y2;
+    // lane & 15.  Split K: the halves go to Y and Y + ypart, or add into Y,
+    // which starts at zero (two addends from zero give the same sum in
+    // either order, and the same as their sum formed by the consumer).
+    float *Yo = Yp + (a.ypart ? ks * a.ypart : 0);
+    const bool plain = ksplit == 1 || a.ypart;
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
@@ -927,21 +1110,46 @@ static void launch_pipe(hipStream_t st, const GemmArgs &a, PipeShape ps) {
     else launch_gemm_p<1, 128, REP, 4>(st, a, 2);
 }
 
+// Four-way split of a long K on 256-token x 128-feature tiles (the
+// single-matrix 256-token kernel) where its work items fill the CUs once and
+// the caller takes four partial outputs: at 512 tokens the 12B down
+// projection 15360 -> 3840, 81 against 89 us for 128 x 128 halves; the
+// consumer's two extra partial reads cost ~3 us, so shorter K stays on the
+// pipelined kernel (o_proj 4096 -> 3840: 29 against 31 us).
+static bool split4_fits(uint32_t n_tok, uint32_t M, uint32_t K) {
+    const uint32_t items = ((M + GN - 1) / GN) * ((n_tok + 255) / 256) * 4;
+    return K >= 8192 && K % 256 == 0 && n_tok > 256 && items >= 192 && items <= 256;
+}
+
 int launch_q4gemm(chn_ctx *ctx, int nmat, const float *X, const uint32_t *W0, const uint32_t *W1, float *Y,
-                  uint32_t n_tok, uint32_t M, uint32_t K, __bf16 *xb, bool repacked, __bf16 *Yb, float *Y2,
-                  bool *y2_written) {
+                  uint32_t n_tok, uint32_t M, uint32_t K, __bf16 *xb, bool repacked, __bf16 *Yb, PartialOut *po) {
     const size_t n = X ? (size_t)n_tok * K : 0;
     GemmArgs a{xb, W0, W1, Y, n_tok, M, K};
-    if (y2_written) *y2_written = false;
+    if (po) po->parts = 1;
+    if (nmat == 1 && K % 64 == 0 && po && po->max_parts >= 4 && split4_fits(n_tok, M, K)) {
+        if (Yb) return set_err(ctx, CHN_E_UNSUPPORTED, "bf16 output needs the two-matrix contraction");
+        if (n) {
+            launch_to_bf16(ctx->stream, X, xb, n, nullptr, 0);
+            CHN_LAUNCHED(ctx, "k_to_bf16");
+        }
+        a.ypart = po->stride;
+        po->parts = 4;
+        const uint32_t n_ft = (M + GN - 1) / GN, n_tt = (n_tok + 255) / 256, per = (n_ft * n_tt * 4 + 7) / 8;
+        if (repacked) k_q4gemm2s<true><<<8 * per, 512, 0, ctx->stream>>>(a, n_ft, n_tt, 4);
+        else k_q4gemm2s<false><<<8 * per, 512, 0, ctx->stream>>>(a, n_ft, n_tt, 4);
+        CHN_LAUNCHED(ctx, "k_q4gemm2s");
+        return CHN_OK;
+    }
     if (nmat == 1 && K % 64 == 0) {
         if (Yb) return set_err(ctx, CHN_E_UNSUPPORTED, "bf16 output needs the two-matrix contraction");
-        const PipeShape ps = pipe_shape(n_tok, M, K, Y2 != nullptr);
+        const bool halves_ok = po && po->max_parts >= 2;
+        const PipeShape ps = pipe_shape(n_tok, M, K, halves_ok);
         const bool split = ps == PipeShape::BN64_K2 || ps == PipeShape::BN128_K2;
-        if (split && Y2) {
-            a.Y2 = Y2;
-            if (y2_written) *y2_written = true;
+        if (split && halves_ok) {
+            a.ypart = po->stride;
+            po->parts = 2;
         }
-        const bool zero = split && !a.Y2;
+        const bool zero = split && !a.ypart;
         if (n || zero) {
             launch_to_bf16(ctx->stream, X, xb, n, zero ? Y : nullptr, zero ? (size_t)n_tok * M : 0);
             CHN_LAUNCHED(ctx, "k_to_bf16");

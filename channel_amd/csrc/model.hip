@@ -50,7 +50,7 @@ struct chn_model {
     uint64_t *topk_ws;
     // prefill buffers
     uint32_t max_tok = 0;
-    float *px, *pn, *pq, *pk, *pv, *pmlp, *pmlp2, *pact, *pattn_ws;
+    float *px, *pn, *pq, *pk, *pv, *pmlp, *pact, *pattn_ws;
     unsigned char *pfrag;   // prefill attention: the keys' bf16 operand fragments
     size_t pfrag_bytes;
     float2 *prope;       // prefill (cos, sin) per token: [2 kinds][T][rot / 2]
@@ -205,8 +205,7 @@ static int alloc_runtime(chn_model *m) {
     M_ALLOC(m->pq, (size_t)T * qd * 4);
     M_ALLOC(m->pk, (size_t)T * kvd * 4);
     M_ALLOC(m->pv, (size_t)T * kvd * 4);
-    M_ALLOC(m->pmlp, (size_t)T * H * 4);
-    M_ALLOC(m->pmlp2, (size_t)T * H * 4);
+    M_ALLOC(m->pmlp, (size_t)4 * T * H * 4);          // up to four partial outputs of a split contraction
     M_ALLOC(m->pattn_ws, prefill_attn_ws_bytes(T, c.num_heads, md.D));
     // every key of a prefill (at most the ring plus the batch) for the KV
     // heads of the widest 256-dim layer
@@ -881,8 +880,8 @@ extern "C" int chn_prefill(chn_model *m, const uint32_t *tokens, uint32_t n, con
     } while (0)
     // Every contraction reads bf16 activations that their producer wrote
     // directly: the norm chains and the attention into pxb, gate/up into the
-    // act buffer (as bf16).  Where down splits K, its halves go to pmlp and
-    // pmlp2 and the closing norm chain adds them.
+    // act buffer (as bf16).  Where o_proj and down split K, their partial
+    // sums go to pmlp + p * max_tok * H and the next norm chain adds them.
     __bf16 *xb = m->pxb;
     __bf16 *actb = (__bf16 *)m->pact;
     // the prompt's rotation angles, once per kind (sliding / full layers)
@@ -905,16 +904,18 @@ extern "C" int chn_prefill(chn_model *m, const uint32_t *tokens, uint32_t n, con
         const uint32_t pwin = c.prefill_window ? c.prefill_window : 1024u;
         P_(launch_prefill_attn(s, m->pq, l.kc, l.vc, m->pslots, n, num_prev_slots, nq, D, kvd, gqa, 1.0f,
                                l.full ? 0u : pwin, nullptr, xb, m->pattn_ws, m->pfrag, m->pfrag_bytes));
-        bool halves = false;
-        P_(launch_q4gemm(ctx, 1, nullptr, l.Wo, nullptr, m->pmlp, n, H, qd, xb, true, nullptr, m->pmlp2, &halves));
+        const size_t pstride = (size_t)m->max_tok * H;
+        PartialOut po_o{pstride, 2};
+        P_(launch_q4gemm(ctx, 1, nullptr, l.Wo, nullptr, m->pmlp, n, H, qd, xb, true, nullptr, &po_o));
         P_(launch_rmsnorm_chain(s, m->px, m->pmlp, l.has_post_attn ? l.post_attn : nullptr, l.pre_ffn, xb, nullptr,
-                                H, n, eps, 1.0f, true, halves ? m->pmlp2 : nullptr));
+                                H, n, eps, 1.0f, true, po_o.parts, pstride));
         P_(launch_q4gemm(ctx, 2, nullptr, l.Wg, l.Wu, nullptr, n, I, H, xb, true, actb));
-        P_(launch_q4gemm(ctx, 1, nullptr, l.Wd, nullptr, m->pmlp, n, H, I, actb, true, nullptr, m->pmlp2, &halves));
+        PartialOut po_d{pstride, 4};
+        P_(launch_q4gemm(ctx, 1, nullptr, l.Wd, nullptr, m->pmlp, n, H, I, actb, true, nullptr, &po_d));
         const bool last = i + 1 == c.num_layers;
         const float *next_norm = last ? m->final_norm : m->L[i + 1].in_norm;
         P_(launch_rmsnorm_chain(s, m->px, m->pmlp, l.has_post_ffn ? l.post_ffn : nullptr, next_norm, xb,
-                                last ? m->pn : nullptr, H, n, eps, l.scalar, true, halves ? m->pmlp2 : nullptr));
+                                last ? m->pn : nullptr, H, n, eps, l.scalar, true, po_d.parts, pstride));
         if ((i + 1) % 4 == 0 || i + 1 == c.num_layers) {
             if (i + 1 == c.num_layers && (logits_out || topk_ids)) {
                 CHN_HIP(ctx, hipMemcpyAsync(m->normed, m->pn + (size_t)(n - 1) * H, H * 4, hipMemcpyDeviceToDevice, s));

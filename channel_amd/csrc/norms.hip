@@ -61,22 +61,33 @@ int launch_rmsnorm(hipStream_t s, float *x, const float *r, const float *w, floa
 // fp32.  The per-thread partial sums, their reduction and every product
 // are those of the two k_rmsnorm passes, so x and y are bit-identical to
 // them (r' is formed where it is added, never stored).  POST needs ADD.
-// R2: the branch is r + r2 (the two K halves of a split contraction, added
-// here instead of through atomics into one zeroed buffer: a + b either way).
-template <bool POST, bool ADD, bool R2>
-__global__ __launch_bounds__(256) void k_rmsnorm_chain(float *__restrict__ x, const float *__restrict__ r,
-                                                       const float *__restrict__ r2, const float *__restrict__ pw,
-                                                       const float *__restrict__ w, __bf16 *__restrict__ yb,
-                                                       float *__restrict__ y, uint32_t dim, float eps, float scalar) {
+// NP: the branch is the sum of NP partial outputs r + p * ps of a split
+// contraction, added here in index order instead of through atomics into
+// one zeroed buffer.
+template <int NP>
+__device__ __forceinline__ f4n branch_sum(const f4n (&v)[NP]) {
+    f4n b = v[0];
+#pragma unroll
+    for (int p = 1; p < NP; ++p) b = b + v[p];
+    return b;
+}
+template <bool POST, bool ADD, int NP>
+__global__ __launch_bounds__(256) void k_rmsnorm_chain(float *__restrict__ x, const float *__restrict__ r, size_t ps,
+                                                       const float *__restrict__ pw, const float *__restrict__ w,
+                                                       __bf16 *__restrict__ yb, float *__restrict__ y, uint32_t dim,
+                                                       float eps, float scalar) {
     __shared__ float sh[4];
     const size_t off = (size_t)blockIdx.x * dim;
     f4n *xr = (f4n *)(x + off);
-    const f4n *rr = (const f4n *)(r + off);
-    const f4n *rr2 = (const f4n *)(r2 + off);
     const f4n *pwr = (const f4n *)pw;
     const f4n *wr = (const f4n *)w;
     const uint32_t dv = dim / 4;
-    auto branch = [&](uint32_t i) { return R2 ? rr[i] + rr2[i] : rr[i]; };
+    auto branch = [&](uint32_t i) {
+        f4n v[NP];
+#pragma unroll
+        for (int p = 0; p < NP; ++p) v[p] = ((const f4n *)(r + p * ps + off))[i];
+        return branch_sum<NP>(v);
+    };
     float inv_r = 1.0f;
     if (POST) {
         float ss = 0.0f;
@@ -114,35 +125,34 @@ __global__ __launch_bounds__(256) void k_rmsnorm_chain(float *__restrict__ x, co
 // memory round trip instead of three, and each element is read once.
 // Thread i handles float4s i, i + 256, ... in that order, so every sum and
 // product is the loop form's.
-template <bool POST, bool ADD, bool R2>
-__global__ __launch_bounds__(256) void k_rmsnorm_chain_r(float *__restrict__ x, const float *__restrict__ r,
-                                                         const float *__restrict__ r2, const float *__restrict__ pw,
-                                                         const float *__restrict__ w, __bf16 *__restrict__ yb,
-                                                         float *__restrict__ y, uint32_t dim, float eps,
-                                                         float scalar) {
+template <bool POST, bool ADD, int NP>
+__global__ __launch_bounds__(256) void k_rmsnorm_chain_r(float *__restrict__ x, const float *__restrict__ r, size_t ps,
+                                                         const float *__restrict__ pw, const float *__restrict__ w,
+                                                         __bf16 *__restrict__ yb, float *__restrict__ y, uint32_t dim,
+                                                         float eps, float scalar) {
     constexpr int NPT = 4;
     __shared__ float sh[4];
     const size_t off = (size_t)blockIdx.x * dim;
     f4n *xr = (f4n *)(x + off);
-    const f4n *rr = (const f4n *)(r + off);
-    const f4n *rr2 = (const f4n *)(r2 + off);
     const f4n *pwr = (const f4n *)pw;
     const f4n *wr = (const f4n *)w;
     const uint32_t dv = dim / 4;
-    f4n xv[NPT], rv[NPT], r2v[NPT], pv[NPT], wv[NPT];
+    f4n xv[NPT], rv[NPT], pv[NPT], wv[NPT];
+    f4n rp[NPT][NP];
 #pragma unroll
     for (int k = 0; k < NPT; ++k) {
         const uint32_t i = threadIdx.x + 256 * k;
         const bool ok = i < dv;
         xv[k] = ok ? xr[i] : f4n{0, 0, 0, 0};
-        if (ADD) rv[k] = ok ? rr[i] : f4n{0, 0, 0, 0};
-        if (R2) r2v[k] = ok ? rr2[i] : f4n{0, 0, 0, 0};
+        if (ADD)
+#pragma unroll
+            for (int p = 0; p < NP; ++p) rp[k][p] = ok ? ((const f4n *)(r + p * ps + off))[i] : f4n{0, 0, 0, 0};
         if (POST) pv[k] = ok ? pwr[i] : f4n{0, 0, 0, 0};
         wv[k] = ok ? wr[i] : f4n{0, 0, 0, 0};
     }
-    if (R2)
+    if (ADD)
 #pragma unroll
-        for (int k = 0; k < NPT; ++k) rv[k] = rv[k] + r2v[k];
+        for (int k = 0; k < NPT; ++k) rv[k] = branch_sum<NP>(rp[k]);
     float inv_r = 1.0f;
     if (POST) {
         float ss = 0.0f;
@@ -190,19 +200,18 @@ __global__ __launch_bounds__(256) void k_rmsnorm_chain_r(float *__restrict__ x, 
 // cache), so the compiler's waits leave the next row's loads outstanding.
 // Per row, every sum and product is k_rmsnorm_chain_r's.
 constexpr uint32_t kChainGrid = 256;
-template <bool POST, bool ADD, bool R2>
-__global__ __launch_bounds__(256) void k_rmsnorm_chain_p(float *__restrict__ x, const float *__restrict__ r,
-                                                         const float *__restrict__ r2, const float *__restrict__ pw,
-                                                         const float *__restrict__ w, __bf16 *__restrict__ yb,
-                                                         float *__restrict__ y, uint32_t dim, uint32_t rows, float eps,
-                                                         float scalar) {
+template <bool POST, bool ADD, int NP>
+__global__ __launch_bounds__(256) void k_rmsnorm_chain_p(float *__restrict__ x, const float *__restrict__ r, size_t ps,
+                                                         const float *__restrict__ pw, const float *__restrict__ w,
+                                                         __bf16 *__restrict__ yb, float *__restrict__ y, uint32_t dim,
+                                                         uint32_t rows, float eps, float scalar) {
     constexpr int NPT = 4;
     __shared__ float sh[4];
     const f4n *pwr = (const f4n *)pw;
     const f4n *wr = (const f4n *)w;
     const uint32_t dv = dim / 4;
     struct Row {
-        f4n x[NPT], r[NPT], r2[R2 ? NPT : 1];
+        f4n x[NPT], r[NPT][ADD ? NP : 1];
     };
     f4n pv[NPT], wv[NPT];
     uint32_t idx[NPT];
@@ -218,13 +227,12 @@ __global__ __launch_bounds__(256) void k_rmsnorm_chain_p(float *__restrict__ x, 
     };
     auto load = [&](uint32_t row, Row &d) {
         const f4n *xr = (const f4n *)(x + (size_t)row * dim);
-        const f4n *rr = (const f4n *)(r + (size_t)row * dim);
-        const f4n *rr2 = (const f4n *)(r2 + (size_t)row * dim);
 #pragma unroll
         for (int k = 0; k < NPT; ++k) {
             d.x[k] = xr[idx[k]];
-            if (ADD) d.r[k] = rr[idx[k]];
-            if (R2) d.r2[k] = rr2[idx[k]];
+            if (ADD)
+#pragma unroll
+                for (int p = 0; p < NP; ++p) d.r[k][p] = ((const f4n *)(r + p * ps + (size_t)row * dim))[idx[k]];
         }
     };
     uint32_t row = blockIdx.x;
@@ -242,8 +250,12 @@ __global__ __launch_bounds__(256) void k_rmsnorm_chain_p(float *__restrict__ x, 
 #pragma unroll
         for (int k = 0; k < NPT; ++k) {
             xv[k] = mask4(d.x[k], okm[k]);
-            if (ADD) rv[k] = mask4(d.r[k], okm[k]);
-            if (R2) rv[k] = rv[k] + mask4(d.r2[k], okm[k]);
+            if (ADD) {
+                f4n v[NP];
+#pragma unroll
+                for (int p = 0; p < NP; ++p) v[p] = mask4(d.r[k][p], okm[k]);
+                rv[k] = branch_sum<NP>(v);
+            }
         }
         float inv_r = 1.0f;
         if (POST) {
@@ -297,24 +309,32 @@ __global__ __launch_bounds__(256) void k_rmsnorm_chain_p(float *__restrict__ x, 
     }
 }
 
-template <bool POST, bool ADD, bool R2>
-static void launch_chain_kind(hipStream_t s, float *x, const float *r, const float *r2, const float *post_w,
+template <bool POST, bool ADD, int NP>
+static void launch_chain_kind(hipStream_t s, float *x, const float *r, size_t ps, const float *post_w,
                               const float *w, __bf16 *yb, float *y, uint32_t dim, uint32_t rows, float eps,
                               float scalar) {
     if (dim <= 4096 && rows > kChainGrid)
-        k_rmsnorm_chain_p<POST, ADD, R2><<<kChainGrid, 256, 0, s>>>(x, r, r2, post_w, w, yb, y, dim, rows, eps, scalar);
+        k_rmsnorm_chain_p<POST, ADD, NP><<<kChainGrid, 256, 0, s>>>(x, r, ps, post_w, w, yb, y, dim, rows, eps, scalar);
     else if (dim <= 4096)
-        k_rmsnorm_chain_r<POST, ADD, R2><<<rows, 256, 0, s>>>(x, r, r2, post_w, w, yb, y, dim, eps, scalar);
-    else k_rmsnorm_chain<POST, ADD, R2><<<rows, 256, 0, s>>>(x, r, r2, post_w, w, yb, y, dim, eps, scalar);
+        k_rmsnorm_chain_r<POST, ADD, NP><<<rows, 256, 0, s>>>(x, r, ps, post_w, w, yb, y, dim, eps, scalar);
+    else k_rmsnorm_chain<POST, ADD, NP><<<rows, 256, 0, s>>>(x, r, ps, post_w, w, yb, y, dim, eps, scalar);
+}
+
+template <int NP>
+static void launch_chain_np(hipStream_t s, float *x, const float *r, size_t ps, const float *post_w, const float *w,
+                            __bf16 *yb, float *y, uint32_t dim, uint32_t rows, float eps, float scalar) {
+    if (post_w) launch_chain_kind<true, true, NP>(s, x, r, ps, post_w, w, yb, y, dim, rows, eps, scalar);
+    else launch_chain_kind<false, true, NP>(s, x, r, ps, post_w, w, yb, y, dim, rows, eps, scalar);
 }
 
 int launch_rmsnorm_chain(hipStream_t s, float *x, const float *r, const float *post_w, const float *w, __bf16 *yb,
-                         float *y, uint32_t dim, uint32_t rows, float eps, float scalar, bool add, const float *r2) {
-    if (!add) launch_chain_kind<false, false, false>(s, x, r, r2, post_w, w, yb, y, dim, rows, eps, scalar);
-    else if (post_w && r2) launch_chain_kind<true, true, true>(s, x, r, r2, post_w, w, yb, y, dim, rows, eps, scalar);
-    else if (post_w) launch_chain_kind<true, true, false>(s, x, r, r2, post_w, w, yb, y, dim, rows, eps, scalar);
-    else if (r2) launch_chain_kind<false, true, true>(s, x, r, r2, post_w, w, yb, y, dim, rows, eps, scalar);
-    else launch_chain_kind<false, true, false>(s, x, r, r2, post_w, w, yb, y, dim, rows, eps, scalar);
+                         float *y, uint32_t dim, uint32_t rows, float eps, float scalar, bool add, uint32_t nparts,
+                         size_t pstride) {
+    if (!add) launch_chain_kind<false, false, 1>(s, x, r, 0, post_w, w, yb, y, dim, rows, eps, scalar);
+    else if (nparts == 4) launch_chain_np<4>(s, x, r, pstride, post_w, w, yb, y, dim, rows, eps, scalar);
+    else if (nparts == 2) launch_chain_np<2>(s, x, r, pstride, post_w, w, yb, y, dim, rows, eps, scalar);
+    else if (nparts == 1) launch_chain_np<1>(s, x, r, 0, post_w, w, yb, y, dim, rows, eps, scalar);
+    else return CHN_E_UNSUPPORTED;
     return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
 }
 
