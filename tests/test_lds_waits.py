@@ -27,6 +27,9 @@ def test_gemm_lds_waits(tmp_path):
     res2 = lds_wait_check.check_file(str(out), "k_q4gemm2d")
     assert len(res2) == 2, "expected both layouts of the DMA-fed gate/up"
     res.update(res2)
+    res3 = lds_wait_check.check_file(str(out), "k_q4gemm2s")
+    assert len(res3) == 2, "expected both layouts of the 256-token single-matrix contraction"
+    res.update(res3)
     bad = {f: h for f, h in res.items() if h}
     assert not bad, bad
 
