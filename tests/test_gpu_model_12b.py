@@ -113,6 +113,37 @@ def test_12b_layers_prefill_512_then_decode(two_layers):
         tok = int(ids_g[0])
 
 
+def test_12b_layers_prefill_ragged_tiles(two_layers):
+    """A 300-token prefill at the 12B layer dims: every contraction's last
+    token tile is ragged (300 = 256 + 44 for the 256-token tiles of gate/up
+    and of down, whose K is split four ways; 2 x 128 + 44 for q/k/v and o)
+    and the attention's last query tile holds 44 of its 64 tokens.  Against
+    the oracle's bf16-operand model as the 512-token test: logits, every
+    K/V row of both layers and the last normed row."""
+    W, m = two_layers
+    n = 300
+    kvd = CFG2["num_kv_heads"] * CFG2["head_dim"]
+    toks = np.random.default_rng(300).integers(0, CFG2["vocab_size"], n).astype(np.uint32)
+    slots = np.arange(n, dtype=np.uint32)
+    say("prefill 300 tokens at 12B dims")
+    lg, ids, vals = m.prefill_batch(toks, slots, 0, 0)
+    kc, vc = OM.new_caches(CFG2)
+    _, Xn, lg_o, _, _ = OM.prefill(W, kc, vc, toks, slots, 0, 0, bf16_gemm=True, window=1024, nthreads=NT)
+    e = rel_err(lg, lg_o)
+    say(f"  prefill logits: normwise {e:.2e}, elementwise {elem_err(lg, lg_o):.2e}")
+    assert e < 1e-2
+    assert_topk_valid(ids, vals, lg_o, 1e-2, "prefill 300")
+    for i in range(2):
+        k, v = m.kv_read(i, 0, n)
+        ek = rel_err(k, kc[i][: n * kvd].reshape(n, kvd))
+        ev = rel_err(v, vc[i][: n * kvd].reshape(n, kvd))
+        tail = rel_err(k[256:], kc[i][256 * kvd: n * kvd].reshape(n - 256, kvd))
+        say(f"  layer {i} K/V rows: {ek:.2e} / {ev:.2e}; K rows 256..299 {tail:.2e}")
+        assert ek < 1e-2 and ev < 1e-2 and tail < 1e-2
+    _, normed = m.read_state()
+    assert rel_err(normed, Xn[n - 1]) < 1e-2
+
+
 def test_12b_layers_decode_full_ring_across_wrap(two_layers):
     """Decode at the 12B layer dims over full rings: every one of the 4096
     slots of both layers holds K/V rows (the same random rows on both
