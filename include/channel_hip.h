@@ -223,9 +223,11 @@ int chn_batch_gemm_q4(chn_ctx *ctx, const uint32_t *W, const float *X, float *Y,
 int chn_batch_fused_mlp_q4(chn_ctx *ctx, const uint32_t *Wg, const uint32_t *Wu,
                            const float *X, float *Y, uint32_t n_tok, uint32_t M, uint32_t K);
 
-/* The same contractions over Q4R weights (chn_q4_repack), launched as
- * chn_prefill launches them: chn_batch_gemm_q4r as the o and down
- * projections (src/gpu/batch_dispatch.zig:108-109,129-130),
+/* The same contractions over Q4R weights (chn_q4_repack), the ones
+ * chn_prefill runs (which keeps the K-split partial sums of o and down in
+ * separate buffers for its norm chains to add; these entries return their
+ * sum in Y): chn_batch_gemm_q4r as the o and down projections
+ * (src/gpu/batch_dispatch.zig:108-109,129-130),
  * chn_batch_qkv_q4r as q, k and v in one launch over the same activations
  * (:70-81), chn_batch_fused_mlp_q4r as gate/up with the product written as
  * fp32 (Y) or as bf16 bits (Y_bf16, the form the down projection reads;
