@@ -117,9 +117,10 @@ def test_12b_layers_prefill_ragged_tiles(two_layers):
     """A 300-token prefill at the 12B layer dims: every contraction's last
     token tile is ragged (300 = 256 + 44 for the 256-token tiles of gate/up
     and of down, whose K is split four ways; 2 x 128 + 44 for q/k/v and o)
-    and the attention's last query tile holds 44 of its 64 tokens.  Against
-    the oracle's bf16-operand model as the 512-token test: logits, every
-    K/V row of both layers and the last normed row."""
+    and the attention's last query tile holds 44 of its 64 tokens; then a
+    second chunk of 212 tokens over those 300 slots.  Against the oracle's
+    bf16-operand model as the 512-token test: logits, every K/V row of both
+    layers and the last normed row."""
     W, m = two_layers
     n = 300
     kvd = CFG2["num_kv_heads"] * CFG2["head_dim"]
@@ -140,8 +141,32 @@ def test_12b_layers_prefill_ragged_tiles(two_layers):
         tail = rel_err(k[256:], kc[i][256 * kvd: n * kvd].reshape(n - 256, kvd))
         say(f"  layer {i} K/V rows: {ek:.2e} / {ev:.2e}; K rows 256..299 {tail:.2e}")
         assert ek < 1e-2 and ev < 1e-2 and tail < 1e-2
+        kc[i][: n * kvd] = k.ravel()          # the second chunk starts from the GPU's caches
+        vc[i][: n * kvd] = v.ravel()
     _, normed = m.read_state()
     assert rel_err(normed, Xn[n - 1]) < 1e-2
+
+    # a second chunk of 212 tokens over the 300 previous slots: the key list's
+    # 32-key chunk 9 holds 12 previous and 20 new keys, and every contraction
+    # runs one ragged token tile (212 < 256)
+    n2 = 212
+    toks2 = np.random.default_rng(212).integers(0, CFG2["vocab_size"], n2).astype(np.uint32)
+    slots2 = np.arange(n + n2, dtype=np.uint32)
+    say("prefill 212 more tokens after 300 previous slots")
+    lg2, ids2, vals2 = m.prefill_batch(toks2, slots2, n, n)
+    _, Xn2, lg2_o, _, _ = OM.prefill(W, kc, vc, toks2, slots2, n, n, bf16_gemm=True, window=1024, nthreads=NT)
+    e2 = rel_err(lg2, lg2_o)
+    say(f"  second chunk logits: normwise {e2:.2e}")
+    assert e2 < 1e-2
+    assert_topk_valid(ids2, vals2, lg2_o, 1e-2, "prefill 212 after 300")
+    for i in range(2):
+        k, v = m.kv_read(i, n, n2)
+        ek = rel_err(k, kc[i][n * kvd:(n + n2) * kvd].reshape(n2, kvd))
+        ev = rel_err(v, vc[i][n * kvd:(n + n2) * kvd].reshape(n2, kvd))
+        say(f"  layer {i} new K/V rows: {ek:.2e} / {ev:.2e}")
+        assert ek < 1e-2 and ev < 1e-2
+    _, normed = m.read_state()
+    assert rel_err(normed, Xn2[n2 - 1]) < 1e-2
 
 
 def test_12b_layers_decode_full_ring_across_wrap(two_layers):
