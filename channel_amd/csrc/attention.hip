@@ -816,16 +816,18 @@ size_t prefill_frag_bytes(uint32_t num_kv_heads, uint32_t n_keys) {
 }
 
 // Pre-pass: grid (KV heads, chunks c_lo .. c_lo + gridDim.y - 1, 2): z = 0
-// writes the chunk's K planes, z = 1 its V^T planes; chunk blockIdx.y of KV
-// head kvh = blockIdx.x goes to F + (kvh * gridDim.y + blockIdx.y) *
-// kPaChunkBytes.  Keys at or past n_keys are zero.  The KV head is the
+// writes the chunk's K planes, z = 1 its V^T planes; chunk c_lo + blockIdx.y
+// of KV head kvh = blockIdx.x goes to F + (kvh * nfch + blockIdx.y) *
+// kPaChunkBytes (nfch chunks per head, of which the grid may cover the
+// first ones only).  Keys at or past n_keys are zero.  The KV head is the
 // fastest grid index here and in the attention (workgroup i runs on XCD
 // i % 8), so with eight KV heads every workgroup of one head runs on one
 // XCD and a head's fragments, read by all of its query tiles, stay in that
 // XCD's L2.
 __global__ __launch_bounds__(256) void k_prefill_frags(const float *__restrict__ Kc, const float *__restrict__ Vc,
                                                        const uint32_t *__restrict__ slots, uint32_t n_keys,
-                                                       uint32_t c_lo, uint32_t kv_dim, unsigned char *__restrict__ F) {
+                                                       uint32_t c_lo, uint32_t nfch, uint32_t kv_dim,
+                                                       unsigned char *__restrict__ F) {
     __shared__ f4 rows[kPaNK][64];                         // the chunk's K or V rows, 256 floats each
     const int tid = threadIdx.x;
     const uint32_t c = c_lo + blockIdx.y, kvh = blockIdx.x;
@@ -845,7 +847,7 @@ __global__ __launch_bounds__(256) void k_prefill_frags(const float *__restrict__
         for (int i = 0; i < 8; ++i) rows[key][part + 8 * i] = ok ? r[i] : f4{0, 0, 0, 0};
     }
     __syncthreads();
-    unsigned char *Fc = F + ((size_t)kvh * gridDim.y + blockIdx.y) * kPaChunkBytes + (is_v ? 2 * kPaPlane : 0);
+    unsigned char *Fc = F + ((size_t)kvh * nfch + blockIdx.y) * kPaChunkBytes + (is_v ? 2 * kPaPlane : 0);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         const int item = tid + 256 * u, f = item >> 6, l = item & 63;   // fragment f, lane l
@@ -1220,18 +1222,36 @@ int launch_rope_decode_attn(chn_ctx *ctx, const float *q_in, const float *k_in, 
                               out, ws, xp, &ra, skip);
 }
 
+// The key chunks [c_lo, c_hi) whose operand fragments a prefill's attention
+// reads: from the first token's window start to the last key.
+static void pa_frag_span(uint32_t n_tok, uint32_t num_prev, uint32_t window, uint32_t &c_lo, uint32_t &c_hi) {
+    const uint32_t n_keys = num_prev + n_tok;
+    const uint32_t k_lo = (window > 0 && num_prev + 1 > window) ? num_prev + 1 - window : 0;
+    c_lo = k_lo / kPaNK;
+    c_hi = (n_keys + kPaNK - 1) / kPaNK;
+}
+
+bool prefill_frags_fusable(uint32_t num_prev, uint32_t head_dim, uint32_t gqa) {
+    return head_dim == 256 && (gqa == 1 || gqa == 2 || gqa == 4 || gqa == 8) && num_prev % kPaNK == 0;
+}
+
 int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const float *vc, const uint32_t *slots,
                         uint32_t n_tok, uint32_t num_prev, uint32_t num_q_heads, uint32_t head_dim, uint32_t kv_dim,
                         uint32_t gqa, float scale, uint32_t window, float *out, __bf16 *outb, float *ws,
-                        unsigned char *frag, size_t frag_bytes) {
+                        unsigned char *frag, size_t frag_bytes, bool new_frags_ready) {
     if (head_dim == 256 && (gqa == 1 || gqa == 2 || gqa == 4 || gqa == 8)) {
-        // the keys' operand fragments, chunks c_lo .. c_hi - 1 (from the
-        // first token's window start to the last key)
+        // the keys' operand fragments, chunks c_lo .. c_hi - 1; those of the
+        // new tokens' chunks may be written already (by the rope kernel)
         const uint32_t num_kv = num_q_heads / gqa, n_keys = num_prev + n_tok;
-        const uint32_t k_lo = (window > 0 && num_prev + 1 > window) ? num_prev + 1 - window : 0;
-        const uint32_t c_lo = k_lo / kPaNK, c_hi = (n_keys + kPaNK - 1) / kPaNK, nfch = c_hi - c_lo;
+        uint32_t c_lo, c_hi;
+        pa_frag_span(n_tok, num_prev, window, c_lo, c_hi);
+        const uint32_t nfch = c_hi - c_lo;
         if (!frag || frag_bytes < (size_t)num_kv * nfch * kPaChunkBytes) return CHN_E_UNSUPPORTED;
-        k_prefill_frags<<<dim3(num_kv, nfch, 2), 256, 0, st>>>(kc, vc, slots, n_keys, c_lo, kv_dim, frag);
+        if (new_frags_ready && !prefill_frags_fusable(num_prev, head_dim, gqa)) return CHN_E_UNSUPPORTED;
+        const uint32_t c_pre = new_frags_ready ? num_prev / kPaNK : c_hi;   // pre-pass chunks [c_lo, c_pre)
+        if (c_pre > c_lo)
+            k_prefill_frags<<<dim3(num_kv, c_pre - c_lo, 2), 256, 0, st>>>(kc, vc, slots, n_keys, c_lo, nfch,
+                                                                         kv_dim, frag);
         const uint32_t tq = 16 * kPaWaves / gqa;
         const uint32_t tiles = (n_tok + tq - 1) / tq;
         // Causal tiles differ in length (the last one walks every key): each
@@ -1410,43 +1430,53 @@ int launch_qkv_rope(hipStream_t st, const float *q_in, const float *k_in, const 
 // pairs (d, d + rot/2) through its own LDS row (a wave reads only what it
 // wrote, so no workgroup barrier is needed).
 template <int DV>
-__device__ __forceinline__ void norm_rope_head4(const float *__restrict__ in, const float *__restrict__ w,
-                                                float *__restrict__ out, uint32_t rot, float eps, float *buf,
-                                                const float2 *__restrict__ cs, int lane) {
-    constexpr int D = 256 * DV;
-    const uint32_t half = rot / 2;
+struct RopeRow {   // this lane's inputs of one head row: values, norm weights, angles
     f4 v[DV], wv[DV];
     float2 t[DV][4];
+};
+template <int DV>
+__device__ __forceinline__ void rope_row_load(const float *__restrict__ in, const float *__restrict__ w,
+                                              const float2 *__restrict__ cs, uint32_t rot, int lane, RopeRow<DV> &r) {
+    const uint32_t half = rot / 2;
 #pragma unroll
     for (int j = 0; j < DV; ++j) {
-        v[j] = *(const f4 *)(in + 4 * lane + 256 * j);
-        wv[j] = *(const f4 *)(w + 4 * lane + 256 * j);
+        r.v[j] = *(const f4 *)(in + 4 * lane + 256 * j);
+        r.wv[j] = *(const f4 *)(w + 4 * lane + 256 * j);
     }
-    // the angles too, with the inputs (after the LDS step below the compiler
-    // may not move loads up past its memory clobber)
+    // the angles too, with the inputs (after the LDS step of rope_row_math
+    // the compiler may not move loads up past its memory clobber)
 #pragma unroll
     for (int j = 0; j < DV; ++j)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const uint32_t d = 4 * lane + 256 * j + e;
             const uint32_t p = d < half ? d : d - half;
-            t[j][e] = cs[d < rot ? p : 0u];
+            r.t[j][e] = cs[d < rot ? p : 0u];
         }
+}
+// RMSNorm (weights wv) and rotation of the row; o gets this lane's values.
+template <int DV>
+__device__ __forceinline__ void rope_row_math(const RopeRow<DV> &r, uint32_t rot, float eps, float *buf, int lane,
+                                              f4 (&o)[DV]) {
+    constexpr int D = 256 * DV;
+    const uint32_t half = rot / 2;
+    f4 v[DV];
     float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < DV; ++j) ss += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
+    for (int j = 0; j < DV; ++j)
+        ss += (r.v[j].x * r.v[j].x + r.v[j].y * r.v[j].y) + (r.v[j].z * r.v[j].z + r.v[j].w * r.v[j].w);
     ss = wave_sum64(ss);
     const float inv = 1.0f / sqrtf(ss / (float)D + eps);
 #pragma unroll
     for (int j = 0; j < DV; ++j) {
-        v[j] = (v[j] * inv) * wv[j];
+        v[j] = (r.v[j] * inv) * r.wv[j];
         *(f4 *)(buf + 4 * lane + 256 * j) = v[j];
     }
     __builtin_amdgcn_wave_barrier();
     __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
     for (int j = 0; j < DV; ++j) {
-        f4 o = v[j];
+        o[j] = v[j];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             // branch-free (a branch would let the compiler sink the angle
@@ -1455,11 +1485,21 @@ __device__ __forceinline__ void norm_rope_head4(const float *__restrict__ in, co
             const uint32_t d = 4 * lane + 256 * j + e;
             const uint32_t p = d < half ? d : d - half;              // the pair's index
             const float v0 = buf[p], v1 = buf[p + half];
-            const float r = d < half ? v0 * t[j][e].x - v1 * t[j][e].y : v0 * t[j][e].y + v1 * t[j][e].x;
-            o[e] = d < rot ? r : o[e];
+            const float rr = d < half ? v0 * r.t[j][e].x - v1 * r.t[j][e].y : v0 * r.t[j][e].y + v1 * r.t[j][e].x;
+            o[j][e] = d < rot ? rr : o[j][e];
         }
-        *(f4 *)(out + 4 * lane + 256 * j) = o;
     }
+}
+template <int DV>
+__device__ __forceinline__ void norm_rope_head4(const float *__restrict__ in, const float *__restrict__ w,
+                                                float *__restrict__ out, uint32_t rot, float eps, float *buf,
+                                                const float2 *__restrict__ cs, int lane) {
+    RopeRow<DV> r;
+    rope_row_load<DV>(in, w, cs, rot, lane, r);
+    f4 o[DV];
+    rope_row_math<DV>(r, rot, eps, buf, lane, o);
+#pragma unroll
+    for (int j = 0; j < DV; ++j) *(f4 *)(out + 4 * lane + 256 * j) = o[j];
 }
 
 template <int DV>
@@ -1502,10 +1542,142 @@ __global__ __launch_bounds__(256) void k_batch_qkv_rope4(const float *__restrict
     for (int j = 0; j < DV; ++j) *(f4 *)(vo + 4 * lane + 256 * j) = vv[j] * inv;
 }
 
+// k_batch_qkv_rope4<1> that also writes the new keys' attention operand
+// fragments (the layout of k_prefill_frags), so that no pre-pass reads the
+// new K/V rows back.  The new tokens' keys start a chunk (num_prev is a
+// multiple of 32): chunk c0 + cc holds tokens 32 cc .. 32 cc + 31, keys
+// past n_tok are zero.  Grid: nkw = 5 * num_kv * (new chunks) workgroups,
+// one per (KV head, new chunk, part) with the KV head fastest, first (each
+// is a longer chain than a query workgroup, so they start first), then
+// n_tok * ceil(num_q / 4) workgroups of four query heads as
+// k_batch_qkv_rope4.  Parts 0..3 are the K rows of the chunk's four 8-key
+// quarters (two keys per wave), part 4 its V rows (eight per wave).
+//  * K: RMSNorm + RoPE of each key's row; the even lane 2 m of the row,
+//    given its odd neighbour's four values, holds dims 8 m .. 8 m + 7 - one
+//    16-byte item of a K fragment - and stores its bf16 high and low parts;
+//  * V: unit RMSNorm of each row; wave w takes the keys of V^T positions
+//    8 w .. 8 w + 7, so each lane holds four V^T fragment items whole.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void k_batch_qkv_rope_frags(
+    const float *__restrict__ q_in, const float *__restrict__ k_in, const float *__restrict__ v_in,
+    const float *__restrict__ qw, const float *__restrict__ kw, float *__restrict__ q_out,
+    float *__restrict__ k_cache, float *__restrict__ v_cache, const uint32_t *__restrict__ slots,
+    uint32_t slot_offset, uint32_t n_tok, uint32_t num_q, uint32_t num_kv, uint32_t rot, int k_eq_v, float eps,
+    const float2 *__restrict__ tab, unsigned char *__restrict__ F, uint32_t c0, uint32_t c_lo, uint32_t nfch,
+    uint32_t nkw) {
+    constexpr int D = 256;
+    __shared__ __attribute__((aligned(16))) float buf[4][D];  // per-wave rotation rows (query and K paths)
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const size_t q_dim = (size_t)num_q * D, kv_dim = (size_t)num_kv * D;
+    if (blockIdx.x >= nkw) {
+        const uint32_t qb = (num_q + 3) / 4, wq = blockIdx.x - nkw;
+        const uint32_t t = wq / qb, head = (wq % qb) * 4 + wave;
+        if (head >= num_q) return;                          // whole waves; no workgroup barrier follows
+        norm_rope_head4<1>(q_in + t * q_dim + (size_t)head * D, qw, q_out + t * q_dim + (size_t)head * D, rot,
+                           eps, buf[wave], tab + (size_t)t * (rot / 2), lane);
+        return;
+    }
+    const uint32_t j = blockIdx.x;
+    const uint32_t h = j % num_kv, r = j / num_kv, cc = r / 5, part = r % 5;
+    const bool is_v = part == 4;                             // uniform over the workgroup
+    unsigned char *Fc = F + ((size_t)h * nfch + (c0 + cc - c_lo)) * kPaChunkBytes + (is_v ? 2 * kPaPlane : 0);
+    // K: keys 8 part + 2 w, + 1 of the chunk in wave w (two keys: the query
+    // workgroups share this kernel's register budget, and their occupancy
+    // matters more); key k of this wave: its token (clamped into the
+    // prompt) and whether it exists
+    const uint32_t t0 = cc * kPaNK + 8 * part + 2 * wave;
+    auto tok = [&](int k) { return t0 + k < n_tok ? t0 + k : n_tok - 1; };
+    auto has = [&](int k) { return t0 + k < n_tok; };
+    if (!is_v) {
+        RopeRow<1> in[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+            rope_row_load<1>(k_in + tok(k) * kv_dim + (size_t)h * D, kw, tab + (size_t)tok(k) * (rot / 2), rot, lane,
+                             in[k]);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            f4 o[1];
+            rope_row_math<1>(in[k], rot, eps, buf[wave], lane, o);
+            if (has(k)) {
+                const uint32_t slot = slots[slot_offset + tok(k)];
+                *(f4 *)(k_cache + (size_t)slot * kv_dim + (size_t)h * D + 4 * lane) = o[0];
+            }
+            // dims 8 m .. 8 m + 7 at the even lane 2 m
+            const f4 x = has(k) ? o[0] : f4{0.0f, 0.0f, 0.0f, 0.0f};
+            const f4 y = {__shfl_xor(x.x, 1, 64), __shfl_xor(x.y, 1, 64), __shfl_xor(x.z, 1, 64),
+                          __shfl_xor(x.w, 1, 64)};
+            if ((lane & 1) == 0) {
+                const int key = 8 * part + 2 * wave + k, m = lane >> 1;
+                const int f = 8 * (key >> 4) + (m >> 2), l = (key & 15) + 16 * (m & 3);
+                pu32x4 hi, lo;
+                put_hilo(hi, lo, 0, x.x, x.y);
+                put_hilo(hi, lo, 1, x.z, x.w);
+                put_hilo(hi, lo, 2, y.x, y.y);
+                put_hilo(hi, lo, 3, y.z, y.w);
+                *(pu32x4 *)(Fc + (f * 64 + l) * 16) = hi;
+                *(pu32x4 *)(Fc + kPaPlane + (f * 64 + l) * 16) = lo;
+            }
+        }
+        return;
+    }
+    // V: wave w takes the eight keys of chunk positions 8 w .. 8 w + 7 (the
+    // key order of a V^T fragment item), so lane c, which holds dims
+    // 4 c .. 4 c + 3 of every row, holds the four items of those dims whole
+    const float *vsrc = (k_eq_v ? k_in : v_in) + (size_t)h * D + 4 * lane;
+    const uint32_t tv0 = cc * kPaNK;
+    auto vtok = [&](int i) {
+        const uint32_t t = tv0 + vt_key(8 * wave + i);
+        return t < n_tok ? t : n_tok - 1;
+    };
+    auto vhas = [&](int i) { return tv0 + vt_key(8 * wave + i) < n_tok; };
+    f4 vn[8];   // the eight rows, normalised in place
+#pragma unroll
+    for (int i = 0; i < 8; ++i) vn[i] = *(const f4 *)(vsrc + vtok(i) * kv_dim);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float ss = (vn[i].x * vn[i].x + vn[i].y * vn[i].y) + (vn[i].z * vn[i].z + vn[i].w * vn[i].w);
+        ss = wave_sum64(ss);
+        const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+        vn[i] = vn[i] * inv;
+        if (vhas(i)) {
+            const uint32_t slot = slots[slot_offset + vtok(i)];
+            *(f4 *)(v_cache + (size_t)slot * kv_dim + (size_t)h * D + 4 * lane) = vn[i];
+        }
+        vn[i] = vhas(i) ? vn[i] : f4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    // item (dt, l) of the V^T planes: dims 16 dt + (l & 15), positions 8 (l >> 4) .. + 7
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int d = 4 * lane + e, gi = (d >> 4) * 64 + (d & 15) + 16 * wave;
+        pu32x4 hi, lo;
+        put_hilo(hi, lo, 0, vn[0][e], vn[1][e]);
+        put_hilo(hi, lo, 1, vn[2][e], vn[3][e]);
+        put_hilo(hi, lo, 2, vn[4][e], vn[5][e]);
+        put_hilo(hi, lo, 3, vn[6][e], vn[7][e]);
+        *(pu32x4 *)(Fc + gi * 16) = hi;
+        *(pu32x4 *)(Fc + kPaPlane + gi * 16) = lo;
+    }
+}
+
 int launch_batch_qkv_rope(hipStream_t st, const float *q_in, const float *k_in, const float *v_in, const float *qw,
                           const float *kw, float *q_out, float *kc, float *vc, const uint32_t *slots,
                           uint32_t slot_offset, uint32_t start_clock, uint32_t n_tok, uint32_t num_q, uint32_t num_kv,
-                          uint32_t D, uint32_t rot, int k_eq_v, float theta, float eps, const float2 *tab) {
+                          uint32_t D, uint32_t rot, int k_eq_v, float theta, float eps, const float2 *tab,
+                          unsigned char *frag, size_t frag_bytes, uint32_t window) {
+    if (frag) {
+        // with the new keys' attention fragments (slot_offset = the number
+        // of previous keys)
+        const uint32_t num_prev = slot_offset;
+        if (!tab || D != 256 || num_prev % kPaNK || !num_kv || num_q % num_kv) return CHN_E_UNSUPPORTED;
+        uint32_t c_lo, c_hi;
+        pa_frag_span(n_tok, num_prev, window, c_lo, c_hi);
+        const uint32_t nfch = c_hi - c_lo, c0 = num_prev / kPaNK, nnew = c_hi - c0;
+        if (frag_bytes < (size_t)num_kv * nfch * kPaChunkBytes) return CHN_E_UNSUPPORTED;
+        const uint32_t nqw = n_tok * ((num_q + 3) / 4), nkw = 5 * num_kv * nnew;
+        k_batch_qkv_rope_frags<<<nkw + nqw, 256, 0, st>>>(q_in, k_in, v_in, qw, kw, q_out, kc, vc, slots,
+                                                         slot_offset, n_tok, num_q, num_kv, rot, k_eq_v, eps, tab,
+                                                         frag, c0, c_lo, nfch, nkw);
+        return hipGetLastError() == hipSuccess ? CHN_OK : CHN_E_HIP;
+    }
     if (tab && (D == 256 || D == 512)) {
         dim3 grid4((num_q + num_kv + 3) / 4, n_tok);
         if (D == 256)

@@ -194,11 +194,15 @@ int launch_qkv_rope(hipStream_t st, const float *q_in, const float *k_in, const 
                     const float *kw, float *q_out, float *kc, float *vc, const uint32_t *step, uint32_t num_q,
                     uint32_t num_kv, uint32_t D, uint32_t rot, int k_eq_v, float theta, float eps);
 // tab (or NULL): the prompt's (cos, sin) table from launch_rope_tab_batch
-// for this rot and theta.
+// for this rot and theta.  frag (or NULL): launch_prefill_attn's fragment
+// buffer for the same tokens, slot_offset previous keys and window; the
+// launch then also writes the new keys' fragments (needs tab, D 256 and
+// prefill_frags_fusable), and launch_prefill_attn is told so.
 int launch_batch_qkv_rope(hipStream_t st, const float *q_in, const float *k_in, const float *v_in, const float *qw,
                           const float *kw, float *q_out, float *kc, float *vc, const uint32_t *slots,
                           uint32_t slot_offset, uint32_t start_clock, uint32_t n_tok, uint32_t num_q, uint32_t num_kv,
-                          uint32_t D, uint32_t rot, int k_eq_v, float theta, float eps, const float2 *tab = nullptr);
+                          uint32_t D, uint32_t rot, int k_eq_v, float theta, float eps, const float2 *tab = nullptr,
+                          unsigned char *frag = nullptr, size_t frag_bytes = 0, uint32_t window = 0);
 int launch_rope_tab_batch(hipStream_t st, float2 *tab, uint32_t start_clock, uint32_t n_tok, uint32_t rot,
                           float theta);
 size_t attn_ws_bytes(uint32_t num_q_heads, uint32_t head_dim, uint32_t max_slots);
@@ -223,10 +227,13 @@ int launch_rope_decode_attn(chn_ctx *ctx, const float *q_in, const float *k_in, 
 // required at head_dim 256.
 size_t prefill_attn_ws_bytes(uint32_t n_tok, uint32_t num_q_heads, uint32_t head_dim);
 size_t prefill_frag_bytes(uint32_t num_kv_heads, uint32_t n_keys);
+// new_frags_ready: the fragments of the new tokens' key chunks were written
+// by launch_batch_qkv_rope; only the earlier keys' are built here.
+bool prefill_frags_fusable(uint32_t num_prev, uint32_t head_dim, uint32_t gqa);
 int launch_prefill_attn(hipStream_t st, const float *q, const float *kc, const float *vc, const uint32_t *slots,
                         uint32_t n_tok, uint32_t num_prev, uint32_t num_q_heads, uint32_t head_dim, uint32_t kv_dim,
                         uint32_t gqa, float scale, uint32_t window, float *out, __bf16 *outb, float *ws,
-                        unsigned char *frag, size_t frag_bytes);
+                        unsigned char *frag, size_t frag_bytes, bool new_frags_ready = false);
 size_t xbytes_bytes(uint32_t nb);
 int launch_gemv_q8(hipStream_t st, const uint32_t *W, const float *x, float *y, uint32_t M, uint32_t nb,
                    uint32_t *xp_ws);

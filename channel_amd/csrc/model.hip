@@ -896,14 +896,17 @@ extern "C" int chn_prefill(chn_model *m, const uint32_t *tokens, uint32_t n, con
             P_(launch_rmsnorm_chain(s, m->px, nullptr, nullptr, l.in_norm, xb, nullptr, H, n, eps, 1.0f, false));
         const uint32_t D = l.D, nkv = l.nkv, qd = l.qd, kvd = l.kvd, gqa = l.gqa;
         P_(launch_q4gemm_qkv(ctx, nullptr, l.Wq, l.Wk, l.Wv, m->pq, m->pk, m->pv, n, qd, kvd, H, xb));
-        P_(launch_batch_qkv_rope(s, m->pq, m->pk, m->pv, l.q_norm, l.k_norm, m->pq, l.kc, l.vc, m->pslots,
-                                 num_prev_slots, start_clock, n, nq, nkv, D, l.rot, (int)c.k_eq_v, theta, eps,
-                                 ptab[l.full ? 1 : 0]));
         // sliding layers see the last 1024 slots (shaders/batch_causal_attn.wgsl:53)
         // unless the config sets another prefill window
-        const uint32_t pwin = c.prefill_window ? c.prefill_window : 1024u;
-        P_(launch_prefill_attn(s, m->pq, l.kc, l.vc, m->pslots, n, num_prev_slots, nq, D, kvd, gqa, 1.0f,
-                               l.full ? 0u : pwin, nullptr, xb, m->pattn_ws, m->pfrag, m->pfrag_bytes));
+        const uint32_t pwin = c.prefill_window ? c.prefill_window : 1024u, win = l.full ? 0u : pwin;
+        // when the new keys start a 32-key chunk, the rope kernel also
+        // writes their attention operand fragments
+        const bool fuse = prefill_frags_fusable(num_prev_slots, D, gqa);
+        P_(launch_batch_qkv_rope(s, m->pq, m->pk, m->pv, l.q_norm, l.k_norm, m->pq, l.kc, l.vc, m->pslots,
+                                 num_prev_slots, start_clock, n, nq, nkv, D, l.rot, (int)c.k_eq_v, theta, eps,
+                                 ptab[l.full ? 1 : 0], fuse ? m->pfrag : nullptr, m->pfrag_bytes, win));
+        P_(launch_prefill_attn(s, m->pq, l.kc, l.vc, m->pslots, n, num_prev_slots, nq, D, kvd, gqa, 1.0f, win,
+                               nullptr, xb, m->pattn_ws, m->pfrag, m->pfrag_bytes, fuse));
         const size_t pstride = (size_t)m->max_tok * H;
         PartialOut po_o{pstride, 2};
         P_(launch_q4gemm(ctx, 1, nullptr, l.Wo, nullptr, m->pmlp, n, H, qd, xb, true, nullptr, &po_o));

@@ -595,3 +595,33 @@ def test_prefill_window_option(ctx):
     _, _, lg1024, _, _ = OM.prefill(W, kc, vc, toks, np.arange(40), 0, 0, bf16_gemm=True, window=1024)
     assert rel_err(lg, lg16) < 1e-2
     assert rel_err(lg16, lg1024) > 1e-2          # the window matters at 40 tokens
+
+
+def test_prefill_window_second_chunk(ctx):
+    """A second prefill chunk after 64 previous keys (whole 32-key chunks)
+    under prefill_window 16: the attention's first key chunk is an earlier
+    one (its operand fragments built from the caches) and the new keys'
+    fragments come with their RMSNorm + RoPE.  Logits, top-64 and the new
+    K/V rows against the oracle run through the same two chunks."""
+    cfg = dict(CFG, prefill_window=WINDOW, num_layers=2, layer_full=[0, 1])
+    layers, embed, final = OM.random_model(cfg, 56)
+    W = OM.Weights(cfg, layers, embed, final)
+    kvd = cfg["num_kv_heads"] * cfg["head_dim"]
+    toks = [int(t) for t in np.random.default_rng(56).integers(0, cfg["vocab_size"], 104)]
+    slots = np.arange(104, dtype=np.uint32)
+    kc, vc = OM.new_caches(cfg, 4096)
+    with Model.create(ctx, cfg, layers, embed, final) as m:
+        say("prefill chunk 1: 64 tokens, prefill_window 16")
+        m.prefill_batch(toks[:64], slots[:64], 0, 0, embed_bf16=W.embed_bf16, logits=False, topk=False)
+        OM.prefill(W, kc, vc, toks[:64], slots[:64], 0, 0, bf16_gemm=True, window=WINDOW)
+        say("prefill chunk 2: 40 tokens over 64 previous slots")
+        lg, ids, vals = m.prefill_batch(toks[64:], slots, 64, 64, embed_bf16=W.embed_bf16)
+        _, _, lg_o, _, _ = OM.prefill(W, kc, vc, toks[64:], slots, 64, 64, bf16_gemm=True, window=WINDOW)
+        kv = [m.kv_read(i, 64, 40) for i in range(cfg["num_layers"])]
+    assert rel_err(lg, lg_o) < 1e-2
+    assert_topk_valid(ids, vals, lg_o, 1e-2, "second prefill chunk, window 16")
+    for i, (k_g, v_g) in enumerate(kv):
+        ek = rel_err(k_g.ravel(), kc[i][64 * kvd:104 * kvd])
+        ev = rel_err(v_g.ravel(), vc[i][64 * kvd:104 * kvd])
+        say(f"  layer {i}: new K rows {ek:.2e}, V rows {ev:.2e}")
+        assert ek < 1e-2 and ev < 1e-2
