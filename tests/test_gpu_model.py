@@ -625,3 +625,47 @@ def test_prefill_window_second_chunk(ctx):
         ev = rel_err(v_g.ravel(), vc[i][64 * kvd:104 * kvd])
         say(f"  layer {i}: new K rows {ek:.2e}, V rows {ev:.2e}")
         assert ek < 1e-2 and ev < 1e-2
+
+
+def test_k_eq_v_model_prefill_then_decode(ctx):
+    """attention_k_eq_v with v_proj absent (src/gpu/model_gpu.zig:123): V's
+    projection is k_proj's and V is the raw K row under a unit RMSNorm, in
+    the prefill's RoPE + fragment kernel and in the decode step's fused
+    attention.  Prefill logits, every K/V row, then two decode steps from
+    the GPU's caches, against the oracle."""
+    cfg = dict(CFG, k_eq_v=1, num_layers=2, layer_full=[0, 1])
+    layers, embed, final = OM.random_model(cfg, 57)
+    for l in layers:
+        l["v_proj"] = None
+    W = OM.Weights(cfg, layers, embed, final)
+    kvd = cfg["num_kv_heads"] * cfg["head_dim"]
+    toks = [int(t) for t in np.random.default_rng(57).integers(0, cfg["vocab_size"], 40)]
+    n = len(toks)
+    kc, vc = OM.new_caches(cfg, 4096)
+    with Model.create(ctx, cfg, layers, embed, final) as m:
+        say("k_eq_v model: prefill 40 tokens")
+        lg, ids, vals = m.prefill_batch(toks, np.arange(n), 0, 0, embed_bf16=W.embed_bf16)
+        _, _, lg_o, _, _ = OM.prefill(W, kc, vc, toks, np.arange(n), 0, 0, bf16_gemm=True, window=1024)
+        assert rel_err(lg, lg_o) < 1e-2
+        assert_topk_valid(ids, vals, lg_o, 1e-2, "k_eq_v prefill")
+        for i in range(cfg["num_layers"]):
+            k_g, v_g = m.kv_read(i, 0, n)
+            assert rel_err(k_g, kc[i][: n * kvd].reshape(n, kvd)) < 1e-2
+            assert rel_err(v_g, vc[i][: n * kvd].reshape(n, kvd)) < 1e-2
+            kc[i][: n * kvd] = k_g.ravel()
+            vc[i][: n * kvd] = v_g.ravel()
+        tok = int(ids[0])
+        for clock in range(n, n + 2):
+            active, sliding = OM.slot_lists(clock, WINDOW)
+            x_in = W.embed([tok])[0]
+            say(f"k_eq_v model: decode clock={clock}")
+            _, ids_g, vals_g = m.forward_token(x_in, clock, clock, active, sliding)
+            x_o, nx_o, lg_o, _, _ = OM.decode_step(W, kc, vc, x_in, clock, clock, active, sliding)
+            assert_topk_valid(ids_g, vals_g, lg_o, 1e-3, f"k_eq_v decode clock {clock}")
+            x_g, _ = m.read_state()
+            assert rel_err(x_g, x_o) < 1e-3
+            for i in range(cfg["num_layers"]):
+                k_g, v_g = m.kv_read(i, clock, 1)
+                assert rel_err(k_g[0], kc[i][clock * kvd:(clock + 1) * kvd]) < 1e-3
+                assert rel_err(v_g[0], vc[i][clock * kvd:(clock + 1) * kvd]) < 1e-3
+            tok = int(ids_g[0])
