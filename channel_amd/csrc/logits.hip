@@ -27,8 +27,8 @@ __global__ __launch_bounds__(256) void k_xbytes(const float *__restrict__ x, uin
     float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     // NaN or Inf in the block: zero digits and a NaN scale (the products of
     // the reference's fp32 matvec would be non-finite)
-    uint32_t bad = !(fabsf(v.x) <= 3.4028235e38f) | !(fabsf(v.y) <= 3.4028235e38f) |
-                   !(fabsf(v.z) <= 3.4028235e38f) | !(fabsf(v.w) <= 3.4028235e38f);
+    uint32_t bad = (uint32_t)!(fabsf(v.x) <= 3.4028235e38f) | (uint32_t)!(fabsf(v.y) <= 3.4028235e38f) |
+                   (uint32_t)!(fabsf(v.z) <= 3.4028235e38f) | (uint32_t)!(fabsf(v.w) <= 3.4028235e38f);
     m = fmaxf(m, __shfl_xor(m, 1, 64));
     m = fmaxf(m, __shfl_xor(m, 2, 64));
     m = fmaxf(m, __shfl_xor(m, 4, 64));
