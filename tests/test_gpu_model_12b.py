@@ -120,7 +120,8 @@ def test_12b_layers_prefill_ragged_tiles(two_layers):
     and the attention's last query tile holds 44 of its 64 tokens; then a
     second chunk of 212 tokens over those 300 slots.  Against the oracle's
     bf16-operand model as the 512-token test: logits, every K/V row of both
-    layers and the last normed row."""
+    layers and the last normed row; then a third chunk of 100 tokens after
+    the 512 slots (the new keys start a 32-key chunk)."""
     W, m = two_layers
     n = 300
     kvd = CFG2["num_kv_heads"] * CFG2["head_dim"]
@@ -165,8 +166,32 @@ def test_12b_layers_prefill_ragged_tiles(two_layers):
         ev = rel_err(v, vc[i][n * kvd:(n + n2) * kvd].reshape(n2, kvd))
         say(f"  layer {i} new K/V rows: {ek:.2e} / {ev:.2e}")
         assert ek < 1e-2 and ev < 1e-2
+        kc[i][n * kvd:(n + n2) * kvd] = k.ravel()
+        vc[i][n * kvd:(n + n2) * kvd] = v.ravel()
     _, normed = m.read_state()
     assert rel_err(normed, Xn2[n2 - 1]) < 1e-2
+
+    # a third chunk of 100 tokens after 512 previous slots (whole 32-key
+    # chunks): the new keys' operand fragments come with their RoPE, the 16
+    # earlier chunks' from the caches
+    n0, n3 = n + n2, 100
+    toks3 = np.random.default_rng(100).integers(0, CFG2["vocab_size"], n3).astype(np.uint32)
+    slots3 = np.arange(n0 + n3, dtype=np.uint32)
+    say("prefill 100 more tokens after 512 previous slots")
+    lg3, ids3, vals3 = m.prefill_batch(toks3, slots3, n0, n0)
+    _, Xn3, lg3_o, _, _ = OM.prefill(W, kc, vc, toks3, slots3, n0, n0, bf16_gemm=True, window=1024, nthreads=NT)
+    e3 = rel_err(lg3, lg3_o)
+    say(f"  third chunk logits: normwise {e3:.2e}")
+    assert e3 < 1e-2
+    assert_topk_valid(ids3, vals3, lg3_o, 1e-2, "prefill 100 after 512")
+    for i in range(2):
+        k, v = m.kv_read(i, n0, n3)
+        ek = rel_err(k, kc[i][n0 * kvd:(n0 + n3) * kvd].reshape(n3, kvd))
+        ev = rel_err(v, vc[i][n0 * kvd:(n0 + n3) * kvd].reshape(n3, kvd))
+        say(f"  layer {i} new K/V rows: {ek:.2e} / {ev:.2e}")
+        assert ek < 1e-2 and ev < 1e-2
+    _, normed = m.read_state()
+    assert rel_err(normed, Xn3[n3 - 1]) < 1e-2
 
 
 def test_12b_layers_decode_full_ring_across_wrap(two_layers):
